@@ -1,0 +1,147 @@
+"""ctypes binding of the C ABI in include/llk/llk_abi.h.
+
+Loads ``dslcompiler_amd/libllk_gfx950.so`` from the package directory.  There
+is no fallback: if the library is missing, :func:`lib` raises, so nothing can
+silently run a CPU path instead of the HIP kernels.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libllk_gfx950.so"
+
+LLK_OK = 0
+LLK_ERR_INVALID_ARGUMENT = -1
+LLK_ERR_SHAPE = -2
+LLK_ERR_DTYPE = -3
+LLK_ERR_LAYOUT = -4
+LLK_ERR_HIP = -5
+LLK_ERR_NO_DEVICE = -6
+LLK_ERR_UNSUPPORTED_ARCH = -7
+LLK_ERR_OUT_OF_MEMORY = -8
+LLK_ERR_SCRATCH = -9
+LLK_ERR_DEVICE_MISMATCH = -10
+LLK_ERR_NOT_FOUND = -11
+
+LLK_BF16, LLK_FP16, LLK_FP32 = 0, 1, 2
+LLK_PACK_KEEP_HOST = 1
+
+STATUS_NAMES = {
+    0: "LLK_OK", -1: "LLK_ERR_INVALID_ARGUMENT", -2: "LLK_ERR_SHAPE", -3: "LLK_ERR_DTYPE",
+    -4: "LLK_ERR_LAYOUT", -5: "LLK_ERR_HIP", -6: "LLK_ERR_NO_DEVICE",
+    -7: "LLK_ERR_UNSUPPORTED_ARCH", -8: "LLK_ERR_OUT_OF_MEMORY", -9: "LLK_ERR_SCRATCH",
+    -10: "LLK_ERR_DEVICE_MISMATCH", -11: "LLK_ERR_NOT_FOUND",
+}
+
+
+class Tensor2D(C.Structure):
+    """Tensor2D (JitCache.h:30-36)."""
+    _fields_ = [("data", C.c_void_p), ("dim0", C.c_int64), ("dim1", C.c_int64),
+                ("stride0", C.c_int64), ("stride1", C.c_int64)]
+
+
+class KernelContext(C.Structure):
+    """KernelContext (JitCache.h:59-62) plus the HIP stream."""
+    _fields_ = [("scratch", C.c_void_p), ("scratch_size", C.c_size_t), ("stream", C.c_void_p)]
+
+
+class ScheduleEntry(C.Structure):
+    """ScheduleEntry (ScheduleLoader.h:23-31)."""
+    _fields_ = [("BM", C.c_int64), ("BN", C.c_int64), ("BK", C.c_int64), ("VM", C.c_int64),
+                ("VN", C.c_int64), ("vector_width", C.c_int64), ("num_threads", C.c_int64),
+                ("grain_size", C.c_int64), ("parallel_axis", C.c_char * 8)]
+
+
+class LLKError(RuntimeError):
+    """A negative llk_status, with the library's message."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+
+
+P = C.c_void_p
+PP = C.POINTER(C.c_void_p)
+T2 = C.POINTER(Tensor2D)
+CTX = C.POINTER(KernelContext)
+
+# name -> (restype, argtypes); every function declared in include/llk/llk_abi.h.
+SIGNATURES = {
+    "llk_last_error": (C.c_char_p, []),
+    "llk_abi_version": (C.c_int, []),
+    "llk_device_info": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int),
+                                  C.POINTER(C.c_int)]),
+    "llk_pack_weights": (C.c_int, [T2, C.c_int64, C.c_uint, PP]),
+    "llk_pack_weights_device": (C.c_int, [T2, C.c_int64, P, PP]),
+    "llk_repack": (C.c_int, [P, T2]),
+    "llk_packed_weights_free": (None, [P]),
+    "llk_packed_weights_k_blocks": (C.c_int64, [P]),
+    "llk_packed_weights_n": (C.c_int64, [P]),
+    "llk_packed_weights_block_size": (C.c_int64, [P]),
+    "llk_packed_weights_bk": (C.c_int64, [P]),
+    "llk_packed_weights_dtype": (C.c_int, [P]),
+    "llk_packed_weights_k": (C.c_int64, [P]),
+    "llk_packed_weights_host_data": (C.c_void_p, [P]),
+    "llk_packed_weights_device_data": (C.c_void_p, [P]),
+    "llk_packed_weights_device_bytes": (C.c_size_t, [P]),
+    "llk_pack_device_bytes": (C.c_size_t, [C.c_int64, C.c_int64]),
+    "llk_pack_device_layout": (C.c_int, [T2, P]),
+    "llk_swiglu_bf16": (C.c_int, [T2, P, P, T2, C.c_int, CTX]),
+    "llk_swiglu_scratch_size": (C.c_size_t, [C.c_int64, C.c_int64, C.c_int64]),
+    "llk_gemm_bf16": (C.c_int, [T2, P, T2, C.c_int, CTX]),
+    "llk_mlp_bf16": (C.c_int, [T2, P, P, P, T2, T2, CTX]),
+    "llk_classify_m": (C.c_int, [C.c_int64]),
+    "llk_num_tiles": (C.c_int64, [C.c_int64, C.c_int64]),
+    "llk_tile_size": (C.c_int64, [C.c_int64, C.c_int64, C.c_int64]),
+    "llk_num_inner_tiles": (C.c_int64, [C.c_int64, C.c_int64]),
+    "llk_kernel_key_hash": (C.c_uint64, [C.c_uint8, C.c_uint8, C.c_uint8, C.c_int64, C.c_int64,
+                                         C.c_int64, C.c_uint8, C.c_uint8, C.c_uint8, C.c_uint16,
+                                         C.c_uint64, C.c_uint64]),
+    "llk_select_schedule": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int,
+                                      C.POINTER(ScheduleEntry), C.POINTER(C.c_int)]),
+    "llk_fill_normal_bf16": (C.c_int, [C.c_uint64, C.c_uint64, C.c_float, P, C.c_int64,
+                                       C.c_int]),
+    "llk_set_tunable": (C.c_int, [C.c_char_p, C.c_int64]),
+    "llk_get_tunable": (C.c_int, [C.c_char_p, C.POINTER(C.c_int64)]),
+}
+
+_LIB: C.CDLL | None = None
+
+
+def lib() -> C.CDLL:
+    """The loaded library (raises FileNotFoundError if it was never built)."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise FileNotFoundError(
+                f"{LIB_PATH} is missing: build it with `python -m dslcompiler_amd.build` "
+                "(there is no CPU fallback)")
+        # torch ships its own HIP runtime under the same SONAME
+        # (libamdhip64.so.7).  Loading torch first makes this library bind to
+        # that one copy, so both share device memory, streams and events.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        l = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(l, name)
+            f.restype = res
+            f.argtypes = args
+        _LIB = l
+    return _LIB
+
+
+def check(status: int) -> None:
+    """Raises LLKError for a negative status."""
+    if status != LLK_OK:
+        msg = lib().llk_last_error()
+        raise LLKError(status, msg.decode() if msg else "")
+
+
+def tensor2d(ptr: int, dim0: int, dim1: int, stride0: int | None = None,
+             stride1: int = 1) -> Tensor2D:
+    return Tensor2D(ptr, dim0, dim1, dim1 if stride0 is None else stride0, stride1)

@@ -1,0 +1,76 @@
+// common.h -- shared device definitions for the gfx950 kernels.
+//
+// Packed weight layout on the device ("MFMA operand order")
+// ---------------------------------------------------------
+// A bf16 weight matrix W[K, N] (row-major in the reference: PackedWeights.cpp
+// copies rows k of length N) is stored transposed into 16 KiB blocks:
+//
+//   N_pad = ceil(N / 128) * 128,  K_pad = ceil(K / 64) * 64
+//   block (nb, kb), nb < N_pad/128, kb < K_pad/64, at byte (nb*KB + kb)*16384
+//   inside a block: 16 sub-blocks of 1 KiB, sub-block s = kh*8 + n16
+//       (kh in {0,1} selects k half [32*kh, 32*kh+32), n16 in 0..7)
+//   inside a sub-block: 64 lane slots of 16 bytes, slot l holds the 8 bf16
+//       W[k][n] for n = nb*128 + n16*16 + (l % 16),
+//                   k = kb*64 + kh*32 + (l / 16)*8 + t,  t = 0..7
+//   entries outside [K, N] are zero.
+//
+// A 1 KiB sub-block is exactly the A operand of one
+// v_mfma_f32_16x16x32_bf16 (16 rows n x 32 k) in lane order, so one
+// contiguous 1 KiB wave load (global or LDS) yields a ready operand with no
+// bank conflicts, and a 16 KiB block streams contiguously from HBM.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace llk_gfx950 {
+
+constexpr int kPackN = 128;           // n per packed block
+constexpr int kPackK = 64;            // k per packed block
+constexpr int kSubBytes = 1024;       // one MFMA operand
+constexpr int kBlockBytes = 16384;    // kPackN * kPackK * 2
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// IEEE round-to-nearest-even f32 -> bf16 (what arith.truncf produces);
+// NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t b = __float_as_uint(f);
+  if ((b & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((b >> 16) | 0x40u);
+  b += 0x7fffu + ((b >> 16) & 1u);
+  return static_cast<uint16_t>(b >> 16);
+}
+
+// SwiGLU epilogue of the fused reference path: g * (1 / (1 + exp(-g))) * u
+// with the accurate expf and IEEE division.
+__device__ __forceinline__ float swiglu_act(float g, float u) {
+  float e = expf(-g);
+  float den = 1.0f + e;
+  float sig = 1.0f / den;
+  return (g * sig) * u;
+}
+
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Maps a linear workgroup id to a tile id so that the tiles processed
+// concurrently on one XCD are contiguous in tile order.  Workgroups are
+// dispatched round-robin over the 8 XCDs (bid % 8 picks the XCD), so
+// bid -> (xcd = bid % 8, local = bid / 8) -> xcd's contiguous range.
+__device__ __forceinline__ int xcd_remap(int bid, int total) {
+  constexpr int kXcd = 8;
+  int xcd = bid % kXcd;
+  int local = bid / kXcd;
+  int base = total / kXcd, extra = total % kXcd;
+  return xcd * base + (xcd < extra ? xcd : extra) + local;
+}
+
+}  // namespace llk_gfx950

@@ -1,0 +1,63 @@
+// pack.hip -- repack a row-major bf16 W[K, N] (device memory) into the
+// MFMA-ordered packed payload described in common.h.  One thread produces
+// one 16-byte lane slot (8 consecutive k of one n); entries outside [K, N]
+// are written as zero, so the whole payload is defined.
+#include "common.h"
+
+namespace llk_gfx950 {
+
+__global__ __launch_bounds__(256) void pack_weights_kernel(const uint16_t* __restrict__ w,
+                                                           int64_t ld, int K, int N, int KB,
+                                                           int64_t slots, uint4* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= slots) return;
+  // slot index = ((nb*KB + kb)*16 + s)*64 + l
+  const int l = (int)(idx & 63);
+  const int s = (int)((idx >> 6) & 15);
+  const int64_t blk = idx >> 10;
+  const int kb = (int)(blk % KB);
+  const int nb = (int)(blk / KB);
+  const int kh = s >> 3, n16 = s & 7;
+  const int n = nb * kPackN + n16 * 16 + (l & 15);
+  const int k0 = kb * kPackK + kh * 32 + (l >> 4) * 8;
+  uint16_t e[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int k = k0 + t;
+    e[t] = (n < N && k < K) ? w[(int64_t)k * ld + n] : (uint16_t)0;
+  }
+  uint4 v;
+  v.x = e[0] | ((uint32_t)e[1] << 16);
+  v.y = e[2] | ((uint32_t)e[3] << 16);
+  v.z = e[4] | ((uint32_t)e[5] << 16);
+  v.w = e[6] | ((uint32_t)e[7] << 16);
+  out[idx] = v;
+}
+
+}  // namespace llk_gfx950
+
+hipError_t llk_launch_pack(const uint16_t* w, int64_t ld, int K, int N, int KB, int NB,
+                           void* out, hipStream_t s) {
+  using namespace llk_gfx950;
+  const int64_t slots = (int64_t)NB * KB * 1024;
+  const int64_t blocks = (slots + 255) / 256;
+  hipLaunchKernelGGL(pack_weights_kernel, dim3((unsigned)blocks), dim3(256), 0, s, w, ld, K, N,
+                     KB, slots, static_cast<uint4*>(out));
+  return hipGetLastError();
+}
+
+// Fills `n` 32-bit words with zero (used instead of hipMemsetAsync so the
+// call is safe inside captured HIP graphs).
+__global__ void llk_zero_words_kernel(unsigned* p, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+hipError_t llk_launch_zero(void* p, size_t bytes, hipStream_t s) {
+  int64_t n = (int64_t)(bytes / 4);
+  if (n == 0) return hipSuccess;
+  int64_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(llk_zero_words_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                     static_cast<unsigned*>(p), n);
+  return hipGetLastError();
+}

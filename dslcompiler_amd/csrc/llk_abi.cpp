@@ -1,0 +1,556 @@
+// llk_abi.cpp -- C ABI of the gfx950 backend (include/llk/llk_abi.h):
+// argument validation, packed-weight handles, workspace management and
+// kernel dispatch.  Kernels live in kernels/*.hip.
+#include "llk/llk_abi.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "runtime/kernel_key.h"
+#include "runtime/packed_layout.h"
+#include "runtime/schedule.h"
+#include "runtime/tunables.h"
+
+// Kernel launchers (kernels/*.hip).
+hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
+                           const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
+                           int NB, bool out_bf16, bool xvec, bool yvec, hipStream_t s);
+hipError_t llk_launch_decode(const uint16_t* x, int64_t ldx, const void* wg, const void* wu,
+                             void* y, int64_t ldy, int M, int N, int K, int KB, int NB, int S,
+                             void* ws, bool out_bf16, bool xvec, bool yvec, hipStream_t s);
+size_t llk_decode_workspace_bytes(int M, int N_pad, int NB, int S);
+hipError_t llk_launch_pack(const uint16_t* w, int64_t ld, int K, int N, int KB, int NB, void* out,
+                           hipStream_t s);
+hipError_t llk_launch_zero(void* p, size_t bytes, hipStream_t s);
+
+struct llk_packed_weights {
+  // Reference metadata (PackedWeights.h:13-19).
+  int64_t K_blocks = 0, N = 0, block_size = 0, BK = 0;
+  int dtype = LLK_BF16;
+  // Backend fields.
+  int64_t K = 0;
+  std::vector<uint16_t> host;  // reference layout, when kept
+  void* dev = nullptr;
+  size_t dev_bytes = 0;
+  int device = -1;
+  int64_t KB = 0, NB = 0;  // device layout blocks (64 k, 128 n)
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int fail_hip(hipError_t e, const char* what) {
+  return fail(LLK_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr int kMaxDevices = 64;
+
+struct DeviceState {
+  std::mutex mu;
+  int checked = 0;  // 0 unknown, 1 gfx950, -1 other
+  char arch[64] = {0};
+  int cu_count = 0, lds = 0, clock_khz = 0;
+  void* ws = nullptr;  // library-owned workspace (counters zeroed)
+  size_t ws_bytes = 0;
+};
+DeviceState g_dev[kMaxDevices];
+
+// Current device, verified to be gfx950.
+int current_device(int* dev) {
+  int d = 0;
+  hipError_t e = hipGetDevice(&d);
+  if (e != hipSuccess) return fail(LLK_ERR_NO_DEVICE, "hipGetDevice: %s", hipGetErrorString(e));
+  if (d < 0 || d >= kMaxDevices) return fail(LLK_ERR_NO_DEVICE, "device index %d out of range", d);
+  DeviceState& st = g_dev[d];
+  std::lock_guard<std::mutex> lk(st.mu);
+  if (st.checked == 0) {
+    hipDeviceProp_t p;
+    e = hipGetDeviceProperties(&p, d);
+    if (e != hipSuccess) return fail_hip(e, "hipGetDeviceProperties");
+    std::snprintf(st.arch, sizeof(st.arch), "%s", p.gcnArchName);
+    st.cu_count = p.multiProcessorCount;
+    st.lds = static_cast<int>(p.sharedMemPerBlock);
+    st.clock_khz = p.clockRate;
+    st.checked = std::strncmp(p.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+  }
+  *dev = d;
+  if (st.checked != 1)
+    return fail(LLK_ERR_UNSUPPORTED_ARCH, "device %d is %s, this library is built for gfx950", d,
+                st.arch);
+  return LLK_OK;
+}
+
+int check_tensor(const llk_tensor2d* t, const char* name) {
+  if (!t) return fail(LLK_ERR_INVALID_ARGUMENT, "%s is NULL", name);
+  if (t->dim0 < 0 || t->dim1 < 0)
+    return fail(LLK_ERR_SHAPE, "%s has negative dimension (%lld, %lld)", name,
+                (long long)t->dim0, (long long)t->dim1);
+  if (t->dim0 > 0 && t->dim1 > 0 && !t->data)
+    return fail(LLK_ERR_INVALID_ARGUMENT, "%s.data is NULL", name);
+  if (t->dim0 > 0 && t->dim1 > 0) {
+    if (t->stride1 != 1)
+      return fail(LLK_ERR_LAYOUT, "%s.stride1 is %lld; only unit inner stride is supported", name,
+                  (long long)t->stride1);
+    if (t->dim0 > 1 && t->stride0 < t->dim1)
+      return fail(LLK_ERR_LAYOUT, "%s.stride0 (%lld) < dim1 (%lld)", name, (long long)t->stride0,
+                  (long long)t->dim1);
+  }
+  return LLK_OK;
+}
+
+int check_packed(const llk_packed_weights* w, const char* name, int dev) {
+  if (!w) return fail(LLK_ERR_INVALID_ARGUMENT, "%s is NULL", name);
+  if (!w->dev) return fail(LLK_ERR_INVALID_ARGUMENT, "%s has no device payload", name);
+  if (w->device != dev)
+    return fail(LLK_ERR_DEVICE_MISMATCH, "%s was packed for device %d, current device is %d",
+                name, w->device, dev);
+  return LLK_OK;
+}
+
+constexpr int64_t kMaxDim = (int64_t)1 << 30;
+
+bool x_vec_ok(const llk_tensor2d* x) {
+  return (reinterpret_cast<uintptr_t>(x->data) % 16 == 0) && (x->stride0 % 8 == 0) &&
+         (x->dim1 % 8 == 0);
+}
+bool y_vec_ok(const llk_tensor2d* y, bool bf16) {
+  const uintptr_t align = bf16 ? 8 : 16;
+  return (reinterpret_cast<uintptr_t>(y->data) % align == 0) && (y->stride0 % 4 == 0);
+}
+
+// Split count for the decode kernel: enough workgroups to keep every CU
+// streaming, at least `min_kb` 64-k steps per split, no empty splits.
+int decode_splits(int64_t KB, int64_t NB) {
+  int64_t forced = llk::tunable("decode_splits");
+  int64_t S;
+  if (forced > 0) {
+    S = std::min<int64_t>(forced, KB);
+  } else {
+    const int64_t target_wgs = llk::tunable("decode_target_wgs");
+    const int64_t min_kb = std::max<int64_t>(1, llk::tunable("decode_min_kb"));
+    int64_t kbps = std::max<int64_t>(min_kb, (KB * NB + target_wgs - 1) / target_wgs);
+    kbps = std::min<int64_t>(kbps, KB);
+    S = (KB + kbps - 1) / kbps;
+  }
+  if (S < 1) S = 1;
+  const int64_t kbps = (KB + S - 1) / S;
+  return static_cast<int>((KB + kbps - 1) / kbps);
+}
+
+// Workspace: the caller's (ctx->scratch) if given, else the library's own
+// per-device buffer, grown on demand and zeroed when (re)allocated.
+int get_workspace(int dev, size_t need, llk_kernel_context* ctx, void** out) {
+  *out = nullptr;
+  if (need == 0) return LLK_OK;
+  if (ctx && ctx->scratch) {
+    if (ctx->scratch_size < need)
+      return fail(LLK_ERR_SCRATCH, "scratch_size %zu < required %zu bytes", ctx->scratch_size,
+                  need);
+    if (reinterpret_cast<uintptr_t>(ctx->scratch) % 256 != 0)
+      return fail(LLK_ERR_SCRATCH, "scratch must be 256-byte aligned");
+    *out = ctx->scratch;
+    return LLK_OK;
+  }
+  DeviceState& st = g_dev[dev];
+  std::lock_guard<std::mutex> lk(st.mu);
+  if (st.ws_bytes < need) {
+    if (st.ws) {
+      hipError_t e = hipDeviceSynchronize();
+      if (e != hipSuccess) return fail_hip(e, "hipDeviceSynchronize");
+      hipFree(st.ws);
+      st.ws = nullptr;
+      st.ws_bytes = 0;
+    }
+    size_t bytes = std::max(need, (size_t)1 << 20);
+    hipError_t e = hipMalloc(&st.ws, bytes);
+    if (e != hipSuccess) {
+      st.ws = nullptr;
+      return fail(LLK_ERR_OUT_OF_MEMORY, "hipMalloc(%zu) for workspace: %s", bytes,
+                  hipGetErrorString(e));
+    }
+    e = hipMemset(st.ws, 0, bytes);
+    if (e != hipSuccess) return fail_hip(e, "hipMemset(workspace)");
+    st.ws_bytes = bytes;
+  }
+  *out = st.ws;
+  return LLK_OK;
+}
+
+hipStream_t stream_of(const llk_kernel_context* ctx) {
+  return ctx ? static_cast<hipStream_t>(ctx->stream) : nullptr;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* llk_last_error(void) { return g_error.c_str(); }
+
+int llk_abi_version(void) { return LLK_ABI_VERSION; }
+
+int llk_device_info(char* arch_name, int cap, int* cu_count, int* lds_bytes, int* clock_khz) {
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (dev < 0) return rc;
+  DeviceState& st = g_dev[dev];
+  if (arch_name && cap > 0) std::snprintf(arch_name, cap, "%s", st.arch);
+  if (cu_count) *cu_count = st.cu_count;
+  if (lds_bytes) *lds_bytes = st.lds;
+  if (clock_khz) *clock_khz = st.clock_khz;
+  return rc;
+}
+
+// ---------------------------------------------------------------------------
+// Packed weights
+// ---------------------------------------------------------------------------
+
+static int check_weight_input(const llk_tensor2d* w, int64_t bk) {
+  int rc = check_tensor(w, "w");
+  if (rc) return rc;
+  if (bk <= 0) return fail(LLK_ERR_INVALID_ARGUMENT, "BK must be positive (got %lld)", (long long)bk);
+  if (w->dim0 > kMaxDim || w->dim1 > kMaxDim)
+    return fail(LLK_ERR_SHAPE, "weight dimensions too large");
+  return LLK_OK;
+}
+
+static void fill_meta(llk_packed_weights* pw, int64_t K, int64_t N, int64_t bk) {
+  pw->K = K;
+  pw->N = N;
+  pw->BK = bk;
+  pw->K_blocks = (K + bk - 1) / bk;
+  pw->block_size = bk * N * 2;
+  pw->dtype = LLK_BF16;
+  pw->KB = llk::deviceBlocksK(K);
+  pw->NB = llk::deviceBlocksN(N);
+}
+
+int llk_pack_weights(const llk_tensor2d* w, int64_t bk, unsigned flags,
+                     llk_packed_weights** out) {
+  if (!out) return fail(LLK_ERR_INVALID_ARGUMENT, "out is NULL");
+  *out = nullptr;
+  int rc = check_weight_input(w, bk);
+  if (rc) return rc;
+  int dev;
+  rc = current_device(&dev);
+  if (rc) return rc;
+  auto* pw = new (std::nothrow) llk_packed_weights();
+  if (!pw) return fail(LLK_ERR_OUT_OF_MEMORY, "handle allocation");
+  fill_meta(pw, w->dim0, w->dim1, bk);
+  const uint16_t* src = static_cast<const uint16_t*>(w->data);
+  try {
+    if (flags & LLK_PACK_KEEP_HOST) {
+      pw->host.resize(static_cast<size_t>(pw->K_blocks * bk * pw->N));
+      if (!pw->host.empty()) llk::packReferenceLayout(src, pw->K, pw->N, w->stride0, bk, pw->host.data());
+    }
+    pw->dev_bytes = llk::deviceLayoutBytes(pw->K, pw->N);
+    if (pw->dev_bytes == 0) {
+      // Empty matrix: keep a small zeroed payload so the handle is usable.
+      hipError_t e = hipMalloc(&pw->dev, 256);
+      if (e == hipSuccess) e = hipMemset(pw->dev, 0, 256);
+      if (e != hipSuccess) {
+        llk_packed_weights_free(pw);
+        return fail_hip(e, "hipMalloc(empty payload)");
+      }
+    } else {
+      std::vector<uint8_t> staging(pw->dev_bytes);
+      llk::packDeviceLayout(src, pw->K, pw->N, w->stride0, staging.data());
+      hipError_t e = hipMalloc(&pw->dev, pw->dev_bytes);
+      if (e != hipSuccess) {
+        pw->dev = nullptr;
+        llk_packed_weights_free(pw);
+        return fail(LLK_ERR_OUT_OF_MEMORY, "hipMalloc(%zu): %s", pw->dev_bytes, hipGetErrorString(e));
+      }
+      e = hipMemcpy(pw->dev, staging.data(), pw->dev_bytes, hipMemcpyHostToDevice);
+      if (e != hipSuccess) {
+        llk_packed_weights_free(pw);
+        return fail_hip(e, "hipMemcpy(packed weights)");
+      }
+    }
+  } catch (const std::bad_alloc&) {
+    llk_packed_weights_free(pw);
+    return fail(LLK_ERR_OUT_OF_MEMORY, "host allocation while packing");
+  }
+  pw->device = dev;
+  *out = pw;
+  return LLK_OK;
+}
+
+int llk_pack_weights_device(const llk_tensor2d* w, int64_t bk, void* stream,
+                            llk_packed_weights** out) {
+  if (!out) return fail(LLK_ERR_INVALID_ARGUMENT, "out is NULL");
+  *out = nullptr;
+  int rc = check_weight_input(w, bk);
+  if (rc) return rc;
+  int dev;
+  rc = current_device(&dev);
+  if (rc) return rc;
+  auto* pw = new (std::nothrow) llk_packed_weights();
+  if (!pw) return fail(LLK_ERR_OUT_OF_MEMORY, "handle allocation");
+  fill_meta(pw, w->dim0, w->dim1, bk);
+  pw->dev_bytes = llk::deviceLayoutBytes(pw->K, pw->N);
+  if (pw->dev_bytes > 0) {
+    hipError_t e = hipMalloc(&pw->dev, pw->dev_bytes);
+    if (e != hipSuccess) {
+      pw->dev = nullptr;
+      llk_packed_weights_free(pw);
+      return fail(LLK_ERR_OUT_OF_MEMORY, "hipMalloc(%zu): %s", pw->dev_bytes, hipGetErrorString(e));
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    e = llk_launch_pack(static_cast<const uint16_t*>(w->data), w->stride0, (int)pw->K, (int)pw->N,
+                        (int)pw->KB, (int)pw->NB, pw->dev, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+      llk_packed_weights_free(pw);
+      return fail_hip(e, "pack kernel");
+    }
+  }
+  pw->device = dev;
+  *out = pw;
+  return LLK_OK;
+}
+
+int llk_repack(llk_packed_weights* pw, const llk_tensor2d* w) {
+  if (!pw) return fail(LLK_ERR_INVALID_ARGUMENT, "handle is NULL");
+  int rc = check_weight_input(w, pw->BK);
+  if (rc) return rc;
+  if (w->dim0 != pw->K || w->dim1 != pw->N)
+    return fail(LLK_ERR_SHAPE, "repack shape (%lld, %lld) differs from packed (%lld, %lld)",
+                (long long)w->dim0, (long long)w->dim1, (long long)pw->K, (long long)pw->N);
+  llk_packed_weights* fresh = nullptr;
+  int dev_saved = 0;
+  hipGetDevice(&dev_saved);
+  if (pw->device >= 0) hipSetDevice(pw->device);
+  rc = llk_pack_weights(w, pw->BK, pw->host.empty() ? 0u : LLK_PACK_KEEP_HOST, &fresh);
+  hipSetDevice(dev_saved);
+  if (rc) return rc;
+  if (pw->dev) hipFree(pw->dev);
+  pw->host.swap(fresh->host);
+  pw->dev = fresh->dev;
+  pw->dev_bytes = fresh->dev_bytes;
+  pw->device = fresh->device;
+  fresh->dev = nullptr;
+  llk_packed_weights_free(fresh);
+  return LLK_OK;
+}
+
+void llk_packed_weights_free(llk_packed_weights* pw) {
+  if (!pw) return;
+  if (pw->dev) hipFree(pw->dev);
+  delete pw;
+}
+
+int64_t llk_packed_weights_k_blocks(const llk_packed_weights* pw) { return pw ? pw->K_blocks : 0; }
+int64_t llk_packed_weights_n(const llk_packed_weights* pw) { return pw ? pw->N : 0; }
+int64_t llk_packed_weights_block_size(const llk_packed_weights* pw) { return pw ? pw->block_size : 0; }
+int64_t llk_packed_weights_bk(const llk_packed_weights* pw) { return pw ? pw->BK : 0; }
+int llk_packed_weights_dtype(const llk_packed_weights* pw) { return pw ? pw->dtype : -1; }
+int64_t llk_packed_weights_k(const llk_packed_weights* pw) { return pw ? pw->K : 0; }
+const void* llk_packed_weights_host_data(const llk_packed_weights* pw) {
+  return (pw && !pw->host.empty()) ? pw->host.data() : nullptr;
+}
+const void* llk_packed_weights_device_data(const llk_packed_weights* pw) { return pw ? pw->dev : nullptr; }
+size_t llk_packed_weights_device_bytes(const llk_packed_weights* pw) { return pw ? pw->dev_bytes : 0; }
+
+size_t llk_pack_device_bytes(int64_t K, int64_t N) {
+  if (K < 0 || N < 0) return 0;
+  return llk::deviceLayoutBytes(K, N);
+}
+
+int llk_pack_device_layout(const llk_tensor2d* w, void* out) {
+  int rc = check_tensor(w, "w");
+  if (rc) return rc;
+  if (!out) return fail(LLK_ERR_INVALID_ARGUMENT, "out is NULL");
+  llk::packDeviceLayout(static_cast<const uint16_t*>(w->data), w->dim0, w->dim1, w->stride0,
+                        static_cast<uint8_t*>(out));
+  return LLK_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Kernels
+// ---------------------------------------------------------------------------
+
+size_t llk_swiglu_scratch_size(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  if (M > llk::tunable("decode_max_m")) return 0;
+  const int64_t NB = llk::deviceBlocksN(N), KB = llk::deviceBlocksK(K);
+  const int S = decode_splits(KB, NB);
+  return llk_decode_workspace_bytes((int)M, (int)(NB * 128), (int)NB, S);
+}
+
+int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
+                    const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
+                    llk_kernel_context* ctx) {
+  int rc;
+  if ((rc = check_tensor(x, "x")) || (rc = check_tensor(y, "y"))) return rc;
+  if (y_dtype != LLK_BF16 && y_dtype != LLK_FP32)
+    return fail(LLK_ERR_DTYPE, "y_dtype %d unsupported (bf16 or f32)", y_dtype);
+  if (!wg || !wu) return fail(LLK_ERR_INVALID_ARGUMENT, "packed weights handle is NULL");
+  const int64_t M = x->dim0, K = x->dim1, N = wg->N;
+  // FusedSwiGLUOp::verify (LLKOps.cpp:42-83) checks, same order.
+  if (y->dim0 != M) return fail(LLK_ERR_SHAPE, "M dimension mismatch: X=%lld vs init=%lld", (long long)M, (long long)y->dim0);
+  if (wg->N != y->dim1) return fail(LLK_ERR_SHAPE, "N dimension mismatch: Wg=%lld vs init=%lld", (long long)wg->N, (long long)y->dim1);
+  if (K != wg->K) return fail(LLK_ERR_SHAPE, "K dimension mismatch between X=%lld and Wg=%lld", (long long)K, (long long)wg->K);
+  if (K != wu->K) return fail(LLK_ERR_SHAPE, "K dimension mismatch between X=%lld and Wu=%lld", (long long)K, (long long)wu->K);
+  if (wg->N != wu->N) return fail(LLK_ERR_SHAPE, "N dimension mismatch between Wg=%lld and Wu=%lld", (long long)wg->N, (long long)wu->N);
+  if (M > kMaxDim) return fail(LLK_ERR_SHAPE, "M too large");
+  if (M == 0 || N == 0) return LLK_OK;
+  if (K == 0) return fail(LLK_ERR_SHAPE, "K must be >= 1 (empty reduction)");
+  int dev;
+  if ((rc = current_device(&dev))) return rc;
+  if ((rc = check_packed(wg, "wg", dev)) || (rc = check_packed(wu, "wu", dev))) return rc;
+
+  const bool bf16 = y_dtype == LLK_BF16;
+  const bool xvec = x_vec_ok(x), yvec = y_vec_ok(y, bf16);
+  hipStream_t s = stream_of(ctx);
+  hipError_t e;
+  if (M <= llk::tunable("decode_max_m")) {
+    const int S = decode_splits(std::max<int64_t>(wg->KB, 1), wg->NB);
+    void* ws = nullptr;
+    size_t need = llk_decode_workspace_bytes((int)M, (int)(wg->NB * 128), (int)wg->NB, S);
+    if ((rc = get_workspace(dev, need, ctx, &ws))) return rc;
+    e = llk_launch_decode(static_cast<const uint16_t*>(x->data), x->stride0, wg->dev, wu->dev,
+                          y->data, y->stride0, (int)M, (int)N, (int)K, (int)wg->KB, (int)wg->NB, S,
+                          ws, bf16, xvec, yvec, s);
+  } else {
+    e = llk_launch_tile(1, static_cast<const uint16_t*>(x->data), x->stride0, wg->dev, wu->dev,
+                        y->data, y->stride0, (int)M, (int)N, (int)K, (int)wg->KB, (int)wg->NB, bf16,
+                        xvec, yvec, s);
+  }
+  if (e != hipSuccess) return fail_hip(e, "swiglu launch");
+  return LLK_OK;
+}
+
+int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor2d* c,
+                  int c_dtype, llk_kernel_context* ctx) {
+  int rc;
+  if ((rc = check_tensor(a, "a")) || (rc = check_tensor(c, "c"))) return rc;
+  if (c_dtype != LLK_BF16 && c_dtype != LLK_FP32)
+    return fail(LLK_ERR_DTYPE, "c_dtype %d unsupported (bf16 or f32)", c_dtype);
+  if (!b) return fail(LLK_ERR_INVALID_ARGUMENT, "packed weights handle is NULL");
+  const int64_t M = a->dim0, K = a->dim1, N = b->N;
+  // micro.mma verifier (MicroOps.cpp:246-291): lhs [M,K], rhs [K,N], acc [M,N].
+  if (K != b->K) return fail(LLK_ERR_SHAPE, "K mismatch: a=%lld vs b=%lld", (long long)K, (long long)b->K);
+  if (c->dim0 != M || c->dim1 != N)
+    return fail(LLK_ERR_SHAPE, "c shape (%lld, %lld) != (%lld, %lld)", (long long)c->dim0,
+                (long long)c->dim1, (long long)M, (long long)N);
+  if (M > kMaxDim) return fail(LLK_ERR_SHAPE, "M too large");
+  if (M == 0 || N == 0) return LLK_OK;
+  if (K == 0) return fail(LLK_ERR_SHAPE, "K must be >= 1 (empty reduction)");
+  int dev;
+  if ((rc = current_device(&dev))) return rc;
+  if ((rc = check_packed(b, "b", dev))) return rc;
+  const bool bf16 = c_dtype == LLK_BF16;
+  hipError_t e = llk_launch_tile(0, static_cast<const uint16_t*>(a->data), a->stride0, b->dev,
+                                 nullptr, c->data, c->stride0, (int)M, (int)N, (int)K, (int)b->KB,
+                                 (int)b->NB, bf16, x_vec_ok(a), y_vec_ok(c, bf16), stream_of(ctx));
+  if (e != hipSuccess) return fail_hip(e, "gemm launch");
+  return LLK_OK;
+}
+
+int llk_mlp_bf16(const llk_tensor2d* x, const llk_packed_weights* wg, const llk_packed_weights* wu,
+                 const llk_packed_weights* wd, llk_tensor2d* y, llk_tensor2d* z,
+                 llk_kernel_context* ctx) {
+  if (!wd) return fail(LLK_ERR_INVALID_ARGUMENT, "wd is NULL");
+  if (wg && wd->K != wg->N)
+    return fail(LLK_ERR_SHAPE, "Wd rows (%lld) != SwiGLU N (%lld)", (long long)wd->K, (long long)wg->N);
+  int rc = llk_swiglu_bf16(x, wg, wu, y, LLK_BF16, ctx);
+  if (rc) return rc;
+  return llk_gemm_bf16(y, wd, z, LLK_BF16, ctx);
+}
+
+// ---------------------------------------------------------------------------
+// Shape specialisation, tiling, keys, schedules
+// ---------------------------------------------------------------------------
+
+int llk_classify_m(int64_t M) { return llk::classifyM(M); }
+
+int llk_set_tunable(const char* name, int64_t value) {
+  if (!name || !llk::setTunable(name, value))
+    return fail(LLK_ERR_INVALID_ARGUMENT, "unknown tunable %s", name ? name : "(null)");
+  return LLK_OK;
+}
+
+int llk_get_tunable(const char* name, int64_t* value) {
+  if (!name || !value) return fail(LLK_ERR_INVALID_ARGUMENT, "NULL argument");
+  if (!llk::setTunable(name, llk::tunable(name)))
+    return fail(LLK_ERR_INVALID_ARGUMENT, "unknown tunable %s", name);
+  *value = llk::tunable(name);
+  return LLK_OK;
+}
+
+int64_t llk_num_tiles(int64_t dim, int64_t tile) {
+  if (tile == 0) return 1;
+  return (dim + tile - 1) / tile;
+}
+int64_t llk_tile_size(int64_t dim, int64_t tile, int64_t idx) {
+  int64_t start = idx * tile;
+  if (start >= dim) return 0;
+  int64_t rem = dim - start;
+  return rem < tile ? rem : tile;
+}
+int64_t llk_num_inner_tiles(int64_t outer, int64_t inner) {
+  if (inner == 0) return 1;
+  return (outer + inner - 1) / inner;
+}
+
+uint64_t llk_kernel_key_hash(uint8_t operation, uint8_t input_type, uint8_t output_type,
+                             int64_t m_bucket, int64_t n, int64_t k, uint8_t weight_layout,
+                             uint8_t isa, uint8_t math_mode, uint16_t thread_count,
+                             uint64_t compiler_version, uint64_t schedule_version) {
+  llk::KernelKey key;
+  key.operation = static_cast<llk::OperationKind>(operation);
+  key.input_type = static_cast<llk::DType>(input_type);
+  key.output_type = static_cast<llk::DType>(output_type);
+  key.M_bucket = m_bucket;
+  key.N = n;
+  key.K = k;
+  key.weight_layout = static_cast<llk::Layout>(weight_layout);
+  key.isa = static_cast<llk::Isa>(isa);
+  key.math_mode = static_cast<llk::MathMode>(math_mode);
+  key.thread_count = thread_count;
+  key.compiler_version = compiler_version;
+  key.schedule_version = schedule_version;
+  return key.hash();
+}
+
+int llk_select_schedule(const char* db_path, const char* op_name, int m_bucket,
+                        llk_schedule_entry* out, int* n_matches) {
+  if (!db_path || !op_name || !out) return fail(LLK_ERR_INVALID_ARGUMENT, "NULL argument");
+  bool ok = false;
+  std::vector<llk::ScheduleEntry> m = llk::loadScheduleDB(db_path, m_bucket, op_name, &ok);
+  llk::ScheduleEntry se = llk::selectBest(m);
+  out->BM = se.BM;
+  out->BN = se.BN;
+  out->BK = se.BK;
+  out->VM = se.VM;
+  out->VN = se.VN;
+  out->vector_width = se.vector_width;
+  out->num_threads = se.num_threads;
+  out->grain_size = se.grain_size;
+  std::snprintf(out->parallel_axis, sizeof(out->parallel_axis), "%s", se.parallel_axis.c_str());
+  if (n_matches) *n_matches = static_cast<int>(m.size());
+  if (!ok) return fail(LLK_ERR_NOT_FOUND, "cannot read or parse schedule DB %s", db_path);
+  return LLK_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,22 @@
+// packed_layout.h -- host-side packers for weight matrices.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+namespace llk {
+
+// Reference host layout (PackedWeights.cpp:5-33): [K_blocks][BK][N] bf16,
+// zero-padded, rows copied from w + k*stride0.  `out` holds
+// ceil(K/BK)*BK*N elements.
+void packReferenceLayout(const uint16_t* w, int64_t K, int64_t N, int64_t stride0, int64_t BK,
+                         uint16_t* out);
+
+// Device payload layout (MFMA operand order, 128 n x 64 k blocks of 16 KiB,
+// 1 KiB sub-blocks of 16 n x 32 k in v_mfma_f32_16x16x32_bf16 lane order).
+int64_t deviceBlocksN(int64_t N);  // ceil(N / 128)
+int64_t deviceBlocksK(int64_t K);  // ceil(K / 64)
+size_t deviceLayoutBytes(int64_t K, int64_t N);
+void packDeviceLayout(const uint16_t* w, int64_t K, int64_t N, int64_t stride0, uint8_t* out);
+
+}  // namespace llk

@@ -1,0 +1,246 @@
+"""Host-side mirror of the reference operator surface for this path.
+
+- :class:`PackedWeights` mirrors ``PackedWeights`` / ``packWeightMatrix`` /
+  ``repack`` (PackedWeights.h:13-49) over the C ABI handle.
+- :func:`fused_swiglu` is ``llk.fused_swiglu`` (LLKOps.td:13-67) executed by
+  the gfx950 kernels: X[M,K] bf16, packed Wg/Wu [K,N], result bf16 (the
+  reference op's result type) or fp32 (the pre-truncf value).
+- :func:`matmul` is the micro.mma / llk.matmul contract (MicroOps.td:196-222,
+  LLKOps.td:210-255) with fp32 accumulation.
+- :func:`mlp` composes SwiGLU and the down projection.
+
+torch tensors only carry device memory and the current stream; all compute
+goes through ``libllk_gfx950.so``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from ._lib import (LLK_BF16, LLK_FP32, LLK_PACK_KEEP_HOST, KernelContext, check, lib,
+                   tensor2d)
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _stream_handle(stream=None) -> int:
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+def _ctx(stream=None, scratch=None) -> KernelContext:
+    ctx = KernelContext(None, 0, _stream_handle(stream))
+    if scratch is not None:
+        ctx.scratch = scratch.data_ptr()
+        ctx.scratch_size = scratch.numel() * scratch.element_size()
+    return ctx
+
+
+def _t2d(t) -> _lib.Tensor2D:
+    if t.dim() != 2:
+        raise ValueError("expected a 2-D tensor")
+    return tensor2d(t.data_ptr(), t.shape[0], t.shape[1], t.stride(0), t.stride(1))
+
+
+def _out_dtype_code(dtype) -> int:
+    torch = _torch()
+    if dtype == torch.bfloat16:
+        return LLK_BF16
+    if dtype == torch.float32:
+        return LLK_FP32
+    raise ValueError(f"unsupported output dtype {dtype}")
+
+
+class PackedWeights:
+    """Packed bf16 weight matrix [K, N] resident on the current device.
+
+    Metadata (``K_blocks``, ``N``, ``block_size``, ``BK``, ``dtype``) equals the
+    reference's packWeightMatrix exactly (PackedWeights.cpp:5-15).
+    """
+
+    def __init__(self, handle: int):
+        self._h = C.c_void_p(handle)
+
+    # -- construction -------------------------------------------------------
+    @classmethod
+    def from_host(cls, w: np.ndarray, bk: int = 64, keep_host: bool = False) -> "PackedWeights":
+        """packWeightMatrix from a host bf16 matrix given as uint16 bits."""
+        w = np.ascontiguousarray(w, dtype=np.uint16)
+        if w.ndim != 2:
+            raise ValueError("w must be 2-D")
+        t = tensor2d(w.ctypes.data, w.shape[0], w.shape[1])
+        out = C.c_void_p()
+        check(lib().llk_pack_weights(C.byref(t), bk, LLK_PACK_KEEP_HOST if keep_host else 0,
+                                     C.byref(out)))
+        return cls(out.value)
+
+    @classmethod
+    def from_device(cls, w, bk: int = 64, stream=None) -> "PackedWeights":
+        """Packs a torch bf16 [K, N] CUDA tensor with the device pack kernel."""
+        torch = _torch()
+        if w.dtype != torch.bfloat16 or not w.is_cuda:
+            raise ValueError("w must be a CUDA bfloat16 tensor")
+        out = C.c_void_p()
+        check(lib().llk_pack_weights_device(C.byref(_t2d(w)), bk, _stream_handle(stream),
+                                            C.byref(out)))
+        return cls(out.value)
+
+    def repack(self, w: np.ndarray) -> None:
+        """repack (PackedWeights.cpp:35-37) with new host contents."""
+        w = np.ascontiguousarray(w, dtype=np.uint16)
+        t = tensor2d(w.ctypes.data, w.shape[0], w.shape[1])
+        check(lib().llk_repack(self._h, C.byref(t)))
+
+    def free(self) -> None:
+        if self._h is not None and self._h.value:
+            lib().llk_packed_weights_free(self._h)
+        self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.free()
+
+    # -- metadata -----------------------------------------------------------
+    @property
+    def handle(self) -> C.c_void_p:
+        if self._h is None:
+            raise ValueError("packed weights were freed")
+        return self._h
+
+    @property
+    def K_blocks(self) -> int:
+        return lib().llk_packed_weights_k_blocks(self.handle)
+
+    @property
+    def N(self) -> int:
+        return lib().llk_packed_weights_n(self.handle)
+
+    @property
+    def K(self) -> int:
+        return lib().llk_packed_weights_k(self.handle)
+
+    @property
+    def block_size(self) -> int:
+        return lib().llk_packed_weights_block_size(self.handle)
+
+    @property
+    def BK(self) -> int:
+        return lib().llk_packed_weights_bk(self.handle)
+
+    @property
+    def dtype(self) -> int:
+        return lib().llk_packed_weights_dtype(self.handle)
+
+    @property
+    def device_bytes(self) -> int:
+        return lib().llk_packed_weights_device_bytes(self.handle)
+
+    def host_data(self) -> np.ndarray | None:
+        """The reference host layout [K_blocks][BK][N] (uint16), if kept."""
+        p = lib().llk_packed_weights_host_data(self.handle)
+        if not p:
+            return None
+        n = self.K_blocks * self.BK * self.N
+        buf = (C.c_uint16 * n).from_address(p)
+        return np.frombuffer(buf, dtype=np.uint16).reshape(self.K_blocks, self.BK, self.N).copy()
+
+
+def pack_device_layout(w: np.ndarray) -> np.ndarray:
+    """Host computation of the device payload bytes for bf16 bits ``w`` [K, N]."""
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    nbytes = lib().llk_pack_device_bytes(w.shape[0], w.shape[1])
+    out = np.zeros(nbytes, dtype=np.uint8)
+    t = tensor2d(w.ctypes.data, w.shape[0], w.shape[1])
+    check(lib().llk_pack_device_layout(C.byref(t), out.ctypes.data))
+    return out
+
+
+def fused_swiglu(x, wg: PackedWeights, wu: PackedWeights, out=None, out_dtype=None,
+                 stream=None, scratch=None):
+    """Y = SiLU(X Wg) * (X Wu) on the current device (asynchronous)."""
+    torch = _torch()
+    if out is None:
+        out = torch.empty((x.shape[0], wg.N), dtype=out_dtype or torch.bfloat16, device=x.device)
+    check(lib().llk_swiglu_bf16(C.byref(_t2d(x)), wg.handle, wu.handle, C.byref(_t2d(out)),
+                                _out_dtype_code(out.dtype), C.byref(_ctx(stream, scratch))))
+    return out
+
+
+def matmul(a, b: PackedWeights, out=None, out_dtype=None, stream=None):
+    """C = A B (micro.mma, fp32 accumulation) on the current device."""
+    torch = _torch()
+    if out is None:
+        out = torch.empty((a.shape[0], b.N), dtype=out_dtype or torch.float32, device=a.device)
+    check(lib().llk_gemm_bf16(C.byref(_t2d(a)), b.handle, C.byref(_t2d(out)),
+                              _out_dtype_code(out.dtype), C.byref(_ctx(stream))))
+    return out
+
+
+def mlp(x, wg: PackedWeights, wu: PackedWeights, wd: PackedWeights, y=None, z=None,
+        stream=None):
+    """Y = SwiGLU(X) (bf16), Z = Y Wd (bf16); returns (y, z)."""
+    torch = _torch()
+    if y is None:
+        y = torch.empty((x.shape[0], wg.N), dtype=torch.bfloat16, device=x.device)
+    if z is None:
+        z = torch.empty((x.shape[0], wd.N), dtype=torch.bfloat16, device=x.device)
+    check(lib().llk_mlp_bf16(C.byref(_t2d(x)), wg.handle, wu.handle, wd.handle,
+                             C.byref(_t2d(y)), C.byref(_t2d(z)), C.byref(_ctx(stream))))
+    return y, z
+
+
+def fill_normal_bf16(seed: int, stream: int, shape, sigma: float = 1.0,
+                     threads: int = 0) -> np.ndarray:
+    """Deterministic bf16 bits of sigma * N(0, 1) (splitmix64 + Box-Muller)."""
+    out = np.empty(shape, dtype=np.uint16)
+    check(lib().llk_fill_normal_bf16(seed, stream, sigma, out.ctypes.data, out.size, threads))
+    return out
+
+
+def swiglu_scratch_size(M: int, N: int, K: int) -> int:
+    return int(lib().llk_swiglu_scratch_size(M, N, K))
+
+
+def classify_m(M: int) -> int:
+    return int(lib().llk_classify_m(M))
+
+
+def set_tunable(name: str, value: int) -> None:
+    check(lib().llk_set_tunable(name.encode(), value))
+
+
+def get_tunable(name: str) -> int:
+    v = C.c_int64()
+    check(lib().llk_get_tunable(name.encode(), C.byref(v)))
+    return v.value
+
+
+def select_schedule(db_path: str, op_name: str, m_bucket: int):
+    """(entry, n_matches, status) of the reference lookup semantics."""
+    e = _lib.ScheduleEntry()
+    n = C.c_int()
+    st = lib().llk_select_schedule(db_path.encode(), op_name.encode(), m_bucket, C.byref(e),
+                                   C.byref(n))
+    return e, n.value, st
+
+
+def device_info():
+    name = C.create_string_buffer(64)
+    cu, lds, clk = C.c_int(), C.c_int(), C.c_int()
+    st = lib().llk_device_info(name, 64, C.byref(cu), C.byref(lds), C.byref(clk))
+    return {"status": st, "arch": name.value.decode(), "cu_count": cu.value,
+            "lds_bytes": lds.value, "clock_khz": clk.value}

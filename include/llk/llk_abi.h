@@ -1,0 +1,245 @@
+/*
+ * llk_abi.h -- C ABI of the MI355X (gfx950) backend for DSLCompiler's fused
+ * SwiGLU / micro.mma hot path.
+ *
+ * Plain C: pointers, sizes and status codes; no torch or C++ types.  Every
+ * entry point is declared next to the reference interface it replaces
+ * (paths relative to the skg7on/DSLCompiler tree).
+ *
+ * Conventions
+ *   - Return value: LLK_OK (0) on success, a negative llk_status on error.
+ *     llk_last_error() returns a thread-local, human-readable message for the
+ *     most recent failing call on the calling thread.
+ *   - Launch entry points are stream-ordered and asynchronous: they enqueue
+ *     on ctx->stream (NULL = the default stream) and return without waiting.
+ *     All tensor data pointers passed to them are device pointers on the
+ *     current HIP device.
+ *   - A packed-weights handle is immutable after packing and may be shared by
+ *     launches on any stream of the device it was packed for.  Freeing it
+ *     while launches that use it are still queued is the caller's error.
+ *   - Element types: bf16 inputs; outputs bf16 or fp32 as requested.  Tensors
+ *     are 2-D with unit inner stride (stride1 == 1); stride0 is the row
+ *     stride in elements and must be >= dim1.
+ */
+#ifndef LLK_ABI_H
+#define LLK_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LLK_ABI_VERSION 1
+
+/* Status codes.  The reference returns errors as llvm::Expected /
+ * StringError (JitCache.cpp:200-224); this ABI uses negative integers. */
+typedef enum llk_status {
+  LLK_OK = 0,
+  LLK_ERR_INVALID_ARGUMENT = -1, /* null pointer, bad enum value          */
+  LLK_ERR_SHAPE = -2,            /* dimension mismatch (LLKOps.cpp:42-83)  */
+  LLK_ERR_DTYPE = -3,            /* unsupported element type               */
+  LLK_ERR_LAYOUT = -4,           /* stride1 != 1, stride0 < dim1, alignment */
+  LLK_ERR_HIP = -5,              /* a HIP runtime call failed              */
+  LLK_ERR_NO_DEVICE = -6,        /* no HIP device visible                  */
+  LLK_ERR_UNSUPPORTED_ARCH = -7, /* current device is not gfx950           */
+  LLK_ERR_OUT_OF_MEMORY = -8,    /* host or device allocation failed       */
+  LLK_ERR_SCRATCH = -9,          /* caller scratch too small / misaligned  */
+  LLK_ERR_DEVICE_MISMATCH = -10, /* handle packed for another device       */
+  LLK_ERR_NOT_FOUND = -11        /* schedule DB file missing or invalid    */
+} llk_status;
+
+/* Element types: values of llk::DType (KernelKey.h:22). */
+typedef enum llk_dtype { LLK_BF16 = 0, LLK_FP16 = 1, LLK_FP32 = 2 } llk_dtype;
+
+/* Tensor2D (JitCache.h:30-36): same fields, same order, same meaning. */
+typedef struct llk_tensor2d {
+  void* data;
+  int64_t dim0;
+  int64_t dim1;
+  int64_t stride0;
+  int64_t stride1;
+} llk_tensor2d;
+
+/* KernelContext (JitCache.h:59-62) plus the HIP stream to launch on.
+ * scratch/scratch_size: optional caller-owned device workspace; when
+ * scratch is NULL the library uses a workspace it owns per device.  The
+ * required size is given by llk_swiglu_scratch_size(). */
+typedef struct llk_kernel_context {
+  void* scratch;
+  size_t scratch_size;
+  void* stream; /* hipStream_t */
+} llk_kernel_context;
+
+/* Opaque packed-weights handle (PackedWeights, PackedWeights.h:13-43). */
+typedef struct llk_packed_weights llk_packed_weights;
+
+/* ----------------------------------------------------------------------- */
+/* Library / target                                                         */
+/* ----------------------------------------------------------------------- */
+
+/* Thread-local message of the last failing call ("" if none). */
+const char* llk_last_error(void);
+
+/* LLK_ABI_VERSION of the loaded library. */
+int llk_abi_version(void);
+
+/* Device query (replaces CpuFeatures::detect / bestIsa,
+ * lib/Target/X86/TargetAVX2.cpp:33-92).  Fills arch_name (NUL-terminated,
+ * at most cap bytes), compute-unit count, LDS bytes per workgroup and the
+ * peak engine clock in kHz of the current device.  Returns
+ * LLK_ERR_UNSUPPORTED_ARCH (after filling the fields) when the device is not
+ * gfx950. */
+int llk_device_info(char* arch_name, int cap, int* cu_count, int* lds_bytes,
+                    int* clock_khz);
+
+/* ----------------------------------------------------------------------- */
+/* Packed weights (PackedWeights.h:46-49, PackedWeights.cpp:5-37)           */
+/* ----------------------------------------------------------------------- */
+
+/* Pack flags. */
+#define LLK_PACK_KEEP_HOST 1u /* also keep the reference host layout       */
+
+/* packWeightMatrix (PackedWeights.cpp:5-33).  `w` is a bf16 [K, N] matrix in
+ * HOST memory (stride1 == 1).  Metadata follows the reference exactly:
+ * N = dim1, BK = bk, K_blocks = ceil(K / BK), block_size = BK * N * 2,
+ * dtype = BF16.  The device payload (on the current device) is laid out in
+ * MFMA operand order: see llk_pack_device_layout.  With LLK_PACK_KEEP_HOST
+ * the handle also owns the reference's host buffer [K_blocks][BK][N]
+ * (zero-padded), readable through llk_packed_weights_host_data. */
+int llk_pack_weights(const llk_tensor2d* w_host, int64_t bk, unsigned flags,
+                     llk_packed_weights** out);
+
+/* Same as llk_pack_weights for a bf16 [K, N] matrix already in DEVICE memory;
+ * the repack runs as a kernel on `stream` and this call waits for it.
+ * LLK_PACK_KEEP_HOST is not accepted here. */
+int llk_pack_weights_device(const llk_tensor2d* w_dev, int64_t bk,
+                            void* stream, llk_packed_weights** out);
+
+/* repack (PackedWeights.cpp:35-37): re-pack new host contents into an
+ * existing handle, keeping its BK.  The shape must be unchanged. */
+int llk_repack(llk_packed_weights* pw, const llk_tensor2d* w_host);
+
+/* Destroys the handle and frees host and device buffers.  NULL is a no-op. */
+void llk_packed_weights_free(llk_packed_weights* pw);
+
+/* Metadata getters (PackedWeights.h:13-19 fields), exact reference values. */
+int64_t llk_packed_weights_k_blocks(const llk_packed_weights* pw);
+int64_t llk_packed_weights_n(const llk_packed_weights* pw);
+int64_t llk_packed_weights_block_size(const llk_packed_weights* pw);
+int64_t llk_packed_weights_bk(const llk_packed_weights* pw);
+int llk_packed_weights_dtype(const llk_packed_weights* pw);
+/* The logical K (rows of the packed matrix); not a reference field. */
+int64_t llk_packed_weights_k(const llk_packed_weights* pw);
+/* Reference host layout, or NULL when LLK_PACK_KEEP_HOST was not given. */
+const void* llk_packed_weights_host_data(const llk_packed_weights* pw);
+/* Device payload pointer and size in bytes. */
+const void* llk_packed_weights_device_data(const llk_packed_weights* pw);
+size_t llk_packed_weights_device_bytes(const llk_packed_weights* pw);
+
+/* Host-side implementation of the device payload layout, for inspection
+ * (no HIP call): writes the device layout of bf16 [K, N] `w_host` into
+ * `out`, which must hold llk_pack_device_bytes(K, N) bytes. */
+size_t llk_pack_device_bytes(int64_t K, int64_t N);
+int llk_pack_device_layout(const llk_tensor2d* w_host, void* out);
+
+/* ----------------------------------------------------------------------- */
+/* Kernels                                                                  */
+/* ----------------------------------------------------------------------- */
+
+/* Fused SwiGLU  Y = SiLU(X Wg) * (X Wu).
+ * Replaces the JIT'd kernel `KernelFn(x, wg, wu, init, result)`
+ * (JitCache.h:79-81) produced from llk.fused_swiglu (LLKOps.td:13-67) by
+ * FuseDoubleContraction (FuseDoubleContraction.cpp:109-199).
+ * x: bf16 [M, K] device; wg, wu: packed [K, N] handles; y: [M, N] device of
+ * y_dtype LLK_BF16 (truncf RNE of the fp32 result, the reference op's result
+ * type) or LLK_FP32 (the pre-truncf value).  fp32 accumulation, exact exp.
+ * M == 0 is valid and launches nothing (edge_cases.cpp:84-97). */
+int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
+                    const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
+                    llk_kernel_context* ctx);
+
+/* Device workspace bytes llk_swiglu_bf16 needs for an M x N problem when the
+ * caller supplies ctx->scratch (0 when none is needed). */
+size_t llk_swiglu_scratch_size(int64_t M, int64_t N, int64_t K);
+
+/* micro.mma matmul  C = A B  (MicroOps.td:196-222, MicroOps.cpp:246-291;
+ * llk.matmul, LLKOps.td:210-255, accumulator f32).
+ * a: bf16 [M, K] device; b: packed [K, N] handle; c: [M, N] device of
+ * c_dtype LLK_FP32 or LLK_BF16 (RNE of the fp32 sum). */
+int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b,
+                  llk_tensor2d* c, int c_dtype, llk_kernel_context* ctx);
+
+/* MLP block: Y = SwiGLU(X; Wg, Wu) in bf16, then Z = Y Wd (fp32 accumulate,
+ * bf16 result).  wd is a packed [N, K_out] handle.  y is a caller-owned
+ * bf16 [M, N] device buffer that receives the intermediate.  No reference
+ * op (the reference has no lowering for llk.matmul: LLKToLinalg.cpp:621-646);
+ * composed from the two entry points above. */
+int llk_mlp_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
+                 const llk_packed_weights* wu, const llk_packed_weights* wd,
+                 llk_tensor2d* y, llk_tensor2d* z, llk_kernel_context* ctx);
+
+/* ----------------------------------------------------------------------- */
+/* Shape specialisation and schedules                                       */
+/* ----------------------------------------------------------------------- */
+
+/* classifyM (ScheduleLoader.cpp:19-29). */
+int llk_classify_m(int64_t M);
+
+/* TilingUtils.h:28-50. */
+int64_t llk_num_tiles(int64_t dim, int64_t tile);
+int64_t llk_tile_size(int64_t dim, int64_t tile, int64_t idx);
+int64_t llk_num_inner_tiles(int64_t outer, int64_t inner);
+
+/* KernelKey::hash (KernelKey.h:60-86) over the twelve fields. */
+uint64_t llk_kernel_key_hash(uint8_t operation, uint8_t input_type,
+                             uint8_t output_type, int64_t m_bucket, int64_t n,
+                             int64_t k, uint8_t weight_layout, uint8_t isa,
+                             uint8_t math_mode, uint16_t thread_count,
+                             uint64_t compiler_version,
+                             uint64_t schedule_version);
+
+/* ScheduleEntry (ScheduleLoader.h:23-31). */
+typedef struct llk_schedule_entry {
+  int64_t BM, BN, BK, VM, VN, vector_width, num_threads, grain_size;
+  char parallel_axis[8];
+} llk_schedule_entry;
+
+/* loadScheduleDB + selectBest (ScheduleLoader.cpp:31-98,
+ * ScheduleSelection.cpp:46-67): entries whose "operation" equals op_name and
+ * whose shape.M_bucket equals m_bucket (shape.N and shape.K must be present
+ * but are not compared), first match wins; with no match, the built-in
+ * default {8,32,32,1,4,8,4,1,"n"}.  Returns LLK_OK, or LLK_ERR_NOT_FOUND
+ * when the file cannot be read or parsed (out = default, like the
+ * reference's warn-and-fall-back), and sets *n_matches. */
+int llk_select_schedule(const char* db_path, const char* op_name,
+                        int m_bucket, llk_schedule_entry* out, int* n_matches);
+
+/* ----------------------------------------------------------------------- */
+/* Synthetic inputs (no reference counterpart; used by llk-bench)          */
+/* ----------------------------------------------------------------------- */
+
+/* Fills HOST buffer out[0..n) with bf16 bits of sigma * N(0,1): counter-based
+ * splitmix64 streams (s0 = seed ^ stream * 0x9E3779B97F4A7C15) and
+ * Box-Muller, scaled in fp32 and rounded to nearest even.  threads <= 0 uses
+ * every hardware thread.  Deterministic for a given (seed, stream, n). */
+int llk_fill_normal_bf16(uint64_t seed, uint64_t stream, float sigma,
+                         uint16_t* out, int64_t n, int threads);
+
+/* ----------------------------------------------------------------------- */
+/* Backend knobs (no reference counterpart)                                 */
+/* ----------------------------------------------------------------------- */
+
+/* Named integer knobs of the dispatch heuristics: "decode_max_m" (largest M
+ * sent to the split-K decode kernel), "decode_splits" (force the k-split
+ * count, 0 = heuristic), "decode_target_wgs", "decode_min_kb".  Returns
+ * LLK_OK or LLK_ERR_INVALID_ARGUMENT for an unknown name. */
+int llk_set_tunable(const char* name, int64_t value);
+int llk_get_tunable(const char* name, int64_t* value);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* LLK_ABI_H */
