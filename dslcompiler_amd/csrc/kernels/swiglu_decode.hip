@@ -236,18 +236,26 @@ static hipError_t launch_dec_mt(const DecodeArgs& a, bool out_bf16, bool xvec, b
 
 }  // namespace llk_gfx950
 
-// Workspace bytes for the split-K decode path: partials + counters.
+// Split-K workspace layout: a fixed region of kDecodeMaxCounters arrival
+// counters at offset 0 (zero before first use; every launch leaves the
+// counters it used at zero), then the fp32 partials.  The counters never
+// move, so partials of an earlier, larger launch can never land on them.
+constexpr int kDecodeMaxCounters = 16384;
+constexpr size_t kDecodeCounterBytes = kDecodeMaxCounters * sizeof(unsigned);
+
+int llk_decode_max_counters() { return kDecodeMaxCounters; }
+
 size_t llk_decode_workspace_bytes(int M, int N_pad, int NB, int S) {
   if (S <= 1) return 0;
+  (void)NB;
   int mt = (M + 15) / 16;
   size_t part = (size_t)S * 2 * (mt * 16) * N_pad * sizeof(float);
-  part = (part + 255) & ~(size_t)255;
-  return part + (size_t)NB * sizeof(unsigned);
+  return kDecodeCounterBytes + part;
 }
 
 // Internal: called by the host dispatch layer.  `ws` must hold
-// llk_decode_workspace_bytes(M, N_pad, NB, S) bytes, its counter region
-// zeroed before first use (the kernel leaves it zeroed).
+// llk_decode_workspace_bytes(M, N_pad, NB, S) bytes with its counter region
+// zeroed, and NB <= kDecodeMaxCounters when S > 1.
 hipError_t llk_launch_decode(const uint16_t* x, int64_t ldx, const void* wg, const void* wu,
                              void* y, int64_t ldy, int M, int N, int K, int KB, int NB, int S,
                              void* ws, bool out_bf16, bool xvec, bool yvec, hipStream_t s) {
@@ -270,11 +278,9 @@ hipError_t llk_launch_decode(const uint16_t* x, int64_t ldx, const void* wg, con
   a.part = nullptr;
   a.counter = nullptr;
   if (a.S > 1) {
-    int mt = (M + 15) / 16;
-    size_t part = (size_t)a.S * 2 * (mt * 16) * a.n_pad * sizeof(float);
-    part = (part + 255) & ~(size_t)255;
-    a.part = static_cast<float*>(ws);
-    a.counter = reinterpret_cast<unsigned*>(static_cast<uint8_t*>(ws) + part);
+    if (NB > kDecodeMaxCounters || ws == nullptr) return hipErrorInvalidValue;
+    a.counter = static_cast<unsigned*>(ws);
+    a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kDecodeCounterBytes);
   }
   const int mt = (M + 15) / 16;
   switch (mt) {

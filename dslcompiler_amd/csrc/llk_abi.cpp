@@ -28,6 +28,7 @@ hipError_t llk_launch_decode(const uint16_t* x, int64_t ldx, const void* wg, con
                              void* y, int64_t ldy, int M, int N, int K, int KB, int NB, int S,
                              void* ws, bool out_bf16, bool xvec, bool yvec, hipStream_t s);
 size_t llk_decode_workspace_bytes(int M, int N_pad, int NB, int S);
+int llk_decode_max_counters();
 hipError_t llk_launch_pack(const uint16_t* w, int64_t ld, int K, int N, int KB, int NB, void* out,
                            hipStream_t s);
 hipError_t llk_launch_zero(void* p, size_t bytes, hipStream_t s);
@@ -141,6 +142,7 @@ bool y_vec_ok(const llk_tensor2d* y, bool bf16) {
 // Split count for the decode kernel: enough workgroups to keep every CU
 // streaming, at least `min_kb` 64-k steps per split, no empty splits.
 int decode_splits(int64_t KB, int64_t NB) {
+  if (NB > llk_decode_max_counters()) return 1;  // one arrival counter per n-block
   int64_t forced = llk::tunable("decode_splits");
   int64_t S;
   if (forced > 0) {
