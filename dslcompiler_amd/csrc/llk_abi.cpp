@@ -23,7 +23,8 @@
 // Kernel launchers (kernels/*.hip).
 hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                            const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
-                           int NB, bool out_bf16, bool xvec, bool yvec, hipStream_t s);
+                           int NB, bool out_bf16, bool xvec, bool yvec, int load_override,
+                           hipStream_t s);
 hipError_t llk_launch_decode(const uint16_t* x, int64_t ldx, const void* wg, const void* wu,
                              void* y, int64_t ldy, int M, int N, int K, int KB, int NB, int S,
                              void* ws, bool out_bf16, bool xvec, bool yvec, hipStream_t s);
@@ -436,7 +437,7 @@ int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
   } else {
     e = llk_launch_tile(1, static_cast<const uint16_t*>(x->data), x->stride0, wg->dev, wu->dev,
                         y->data, y->stride0, (int)M, (int)N, (int)K, (int)wg->KB, (int)wg->NB, bf16,
-                        xvec, yvec, s);
+                        xvec, yvec, (int)llk::tunable("tile_load"), s);
   }
   if (e != hipSuccess) return fail_hip(e, "swiglu launch");
   return LLK_OK;
@@ -464,7 +465,8 @@ int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor
   const bool bf16 = c_dtype == LLK_BF16;
   hipError_t e = llk_launch_tile(0, static_cast<const uint16_t*>(a->data), a->stride0, b->dev,
                                  nullptr, c->data, c->stride0, (int)M, (int)N, (int)K, (int)b->KB,
-                                 (int)b->NB, bf16, x_vec_ok(a), y_vec_ok(c, bf16), stream_of(ctx));
+                                 (int)b->NB, bf16, x_vec_ok(a), y_vec_ok(c, bf16),
+                                 (int)llk::tunable("tile_load"), stream_of(ctx));
   if (e != hipSuccess) return fail_hip(e, "gemm launch");
   return LLK_OK;
 }

@@ -16,7 +16,10 @@ struct Knob {
 // decode_splits:     force the decode k-split count (0 = heuristic).
 // decode_target_wgs: workgroups the decode heuristic aims for.
 // decode_min_kb:     fewest 64-k steps per decode split.
+// tile_load:         force the tile kernel's operand path (-1 = automatic,
+//                    0 = direct-to-LDS, 1 = staged 16-byte, 2 = staged scalar).
 Knob g_knobs[] = {
+    {"tile_load", {-1}},
     {"decode_max_m", {64}},
     {"decode_splits", {0}},
     {"decode_target_wgs", {1536}},

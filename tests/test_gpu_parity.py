@@ -88,6 +88,28 @@ def test_swiglu_config1_prefill_path(llk, gpu, orc):
         llk.set_tunable("decode_max_m", old)
 
 
+@pytest.mark.parametrize("path", [0, 1, 2])
+@pytest.mark.parametrize("M,K,N", [(320, 512, 392), (300, 1024, 256), (513, 128, 200)])
+def test_tile_load_paths(llk, gpu, orc, path, M, K, N):
+    """The prefill/GEMM tile kernel's three operand paths (direct-to-LDS,
+    staged 16-byte, staged element-wise) on ragged M and N edge tiles."""
+    print(f"case tile load path={path} M={M} K={K} N={N}", flush=True)
+    old = llk.get_tunable("tile_load")
+    llk.set_tunable("tile_load", path)
+    try:
+        x, wg, wu = swiglu_inputs(M, K, N, seed=path + 1)
+        _check_swiglu(llk, gpu, orc, x, wg, wu, f"path{path}")
+        s = 1.0 / np.sqrt(K)
+        a = normal_bf16(9, 0, (M, K), s)
+        b = normal_bf16(9, 1, (K, N), s)
+        cf_ref, _ = orc.gemm(a, b)
+        pb = llk.PackedWeights.from_host(b)
+        cf = from_dev(llk.matmul(to_dev(gpu, a), pb, out_dtype=gpu.float32))
+        assert_parity(cf, cf_ref, f"gemm path{path}")
+    finally:
+        llk.set_tunable("tile_load", old)
+
+
 @pytest.mark.parametrize("splits", [1, 2, 3, 16])
 def test_swiglu_decode_splits(llk, gpu, orc, splits):
     print(f"case swiglu decode splits={splits}", flush=True)
