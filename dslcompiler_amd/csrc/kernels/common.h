@@ -7,17 +7,18 @@
 //
 //   N_pad = ceil(N / 128) * 128,  K_pad = ceil(K / 64) * 64
 //   block (nb, kb), nb < N_pad/128, kb < K_pad/64, at byte (nb*KB + kb)*16384
-//   inside a block: 16 sub-blocks of 1 KiB, sub-block s = kh*8 + n16
-//       (kh in {0,1} selects k half [32*kh, 32*kh+32), n16 in 0..7)
+//   inside a block: 16 sub-blocks of 1 KiB, sub-block s = kq*4 + n32
+//       (kq in 0..3 selects k quarter [16*kq, 16*kq+16), n32 in 0..3)
 //   inside a sub-block: 64 lane slots of 16 bytes, slot l holds the 8 bf16
-//       W[k][n] for n = nb*128 + n16*16 + (l % 16),
-//                   k = kb*64 + kh*32 + (l / 16)*8 + t,  t = 0..7
+//       W[k][n] for n = nb*128 + n32*32 + (l % 32),
+//                   k = kb*64 + kq*16 + (l / 32)*8 + t,  t = 0..7
 //   entries outside [K, N] are zero.
 //
-// A 1 KiB sub-block is exactly the A operand of one
-// v_mfma_f32_16x16x32_bf16 (16 rows n x 32 k) in lane order, so one
-// contiguous 1 KiB wave load (global or LDS) yields a ready operand with no
-// bank conflicts, and a 16 KiB block streams contiguously from HBM.
+// A 1 KiB sub-block is exactly the A operand of one v_mfma_f32_32x32x16_bf16
+// (32 rows n x 16 k) in lane order, so one contiguous 1 KiB wave load (global
+// or LDS) yields a ready operand with no bank conflicts, and a 16 KiB block
+// streams contiguously from HBM.  (On gfx950 the 32x32x16 bf16 MFMA issues
+// twice the flops per cycle of the 16x16x32 one.)
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -32,8 +33,14 @@ constexpr int kBlockBytes = 16384;    // kPackN * kPackK * 2
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Buffer resource word 3 for raw (untyped) buffer access on gfx950.
+constexpr int kBufferWord3 = 0x00020000;
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
@@ -57,8 +64,11 @@ __device__ __forceinline__ float swiglu_act(float g, float u) {
   return (g * sig) * u;
 }
 
-__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+// D[32x32] += A[32x16] B[16x32].  Lane l supplies A row l%32 / B column
+// l%32, k values 8*(l/32) .. +8; it receives D column l%32, rows
+// 8*(r/4) + 4*(l/32) + r%4 for r = 0..15.
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 // Maps a linear workgroup id to a tile id so that the tiles processed
@@ -71,6 +81,32 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
   int local = bid / kXcd;
   int base = total / kXcd, extra = total % kXcd;
   return xcd * base + (xcd < extra ? xcd : extra) + local;
+}
+
+// Stores 4 consecutive n of output row m (bf16 or fp32), bounds-checked.
+template <bool OUT_BF16>
+__device__ __forceinline__ void store4(void* y, int64_t ldy, int M, int N, int m, int n,
+                                       const float (&v)[4], bool vec_ok) {
+  if (m >= M || n >= N) return;
+  if (OUT_BF16) {
+    uint16_t* dst = reinterpret_cast<uint16_t*>(y) + (size_t)m * ldy + n;
+    if (vec_ok && n + 4 <= N) {
+      u16x4 h = {f32_to_bf16_rne(v[0]), f32_to_bf16_rne(v[1]), f32_to_bf16_rne(v[2]),
+                 f32_to_bf16_rne(v[3])};
+      *reinterpret_cast<u16x4*>(dst) = h;
+    } else {
+      for (int r = 0; r < 4; ++r)
+        if (n + r < N) dst[r] = f32_to_bf16_rne(v[r]);
+    }
+  } else {
+    float* dst = reinterpret_cast<float*>(y) + (size_t)m * ldy + n;
+    if (vec_ok && n + 4 <= N) {
+      *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+    } else {
+      for (int r = 0; r < 4; ++r)
+        if (n + r < N) dst[r] = v[r];
+    }
+  }
 }
 
 }  // namespace llk_gfx950

@@ -17,9 +17,9 @@ __global__ __launch_bounds__(256) void pack_weights_kernel(const uint16_t* __res
   const int64_t blk = idx >> 10;
   const int kb = (int)(blk % KB);
   const int nb = (int)(blk / KB);
-  const int kh = s >> 3, n16 = s & 7;
-  const int n = nb * kPackN + n16 * 16 + (l & 15);
-  const int k0 = kb * kPackK + kh * 32 + (l >> 4) * 8;
+  const int kq = s >> 2, n32 = s & 3;
+  const int n = nb * kPackN + n32 * 32 + (l & 31);
+  const int k0 = kb * kPackK + kq * 16 + (l >> 5) * 8;
   uint16_t e[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
@@ -43,6 +43,37 @@ hipError_t llk_launch_pack(const uint16_t* w, int64_t ld, int K, int N, int KB, 
   const int64_t blocks = (slots + 255) / 256;
   hipLaunchKernelGGL(pack_weights_kernel, dim3((unsigned)blocks), dim3(256), 0, s, w, ld, K, N,
                      KB, slots, static_cast<uint4*>(out));
+  return hipGetLastError();
+}
+
+// Copies X[M, K] (any row stride, any alignment) into a dense [M, ldo]
+// buffer, ldo a multiple of 64, zero-filling columns K .. ldo-1: the layout
+// the direct-to-LDS tile kernel reads.  One thread per 8 output columns.
+__global__ __launch_bounds__(256) void pad_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                       int M, int K, uint16_t* __restrict__ out,
+                                                       int64_t ldo) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per_row = ldo / 8;
+  if (idx >= (int64_t)M * per_row) return;
+  const int64_t m = idx / per_row;
+  const int c0 = (int)(idx % per_row) * 8;
+  uint16_t e[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) e[t] = (c0 + t < K) ? x[m * ldx + c0 + t] : (uint16_t)0;
+  uint4 v;
+  v.x = e[0] | ((uint32_t)e[1] << 16);
+  v.y = e[2] | ((uint32_t)e[3] << 16);
+  v.z = e[4] | ((uint32_t)e[5] << 16);
+  v.w = e[6] | ((uint32_t)e[7] << 16);
+  *reinterpret_cast<uint4*>(out + m * ldo + c0) = v;
+}
+
+hipError_t llk_launch_pad_rows(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* out,
+                               int64_t ldo, hipStream_t s) {
+  const int64_t threads = (int64_t)M * (ldo / 8);
+  if (threads == 0) return hipSuccess;
+  hipLaunchKernelGGL(pad_rows_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, x,
+                     ldx, M, K, out, ldo);
   return hipGetLastError();
 }
 

@@ -1,269 +1,263 @@
-// swiglu_decode.hip -- bandwidth-bound fused SwiGLU for small M (decode).
+// swiglu_decode.hip -- bandwidth-bound kernels for small M (decode).
 //
-// Y = SiLU(X Wg) * (X Wu) for M <= 16 * MT rows.  The weights dominate the
-// traffic (2*K*N bf16 read once), so the kernel is an HBM stream over the
-// packed payload: every wave load is one contiguous 1 KiB MFMA operand.
-// X (at most 64 rows) is tiny and served from L2.
+// NMAT = 2: fused SwiGLU  Y = SiLU(X Wg) * (X Wu);   NMAT = 1: C = X W.
+// For M <= 32 * MT rows the weights dominate the traffic (K*N bf16 per
+// matrix, read once), so the kernel is an HBM stream over the packed
+// payload: every wave load is one contiguous 1 KiB MFMA operand
+// (v_mfma_f32_32x32x16_bf16 A operand); X (at most 64 rows) is tiny and
+// served from L2.
 //
-// Grid: (NB n-blocks of 128) x S k-splits.  Workgroup = 4 waves; wave w owns
-// n16 groups {2w, 2w+1} of the block for both Wg and Wu, so a lane's gate and
-// up partial sums describe the same (m, n) pairs.  Each k step (64 k) a wave
-// issues 8 independent 1 KiB loads per step, UNROLL steps at a time.
-//
-// With S > 1 each workgroup writes fp32 partial sums to a workspace; the last
-// workgroup of an n-block to finish (device-scope counter) adds the S
-// partials in split order -- a fixed order, so results are deterministic --
-// and applies the SiLU(g)*u epilogue (FuseDoubleContraction.cpp:175-199).
-// It then resets the counter, so the workspace needs zeroing only once.
+// Grid: (4 * NB column groups of 32 n) x S k-splits.  A workgroup of KS
+// waves owns one 32-column group of every matrix; its k range is divided
+// among the waves, each streaming its part with UNROLL 64-k steps of loads
+// in flight.  The waves' partial sums meet in LDS, in wave order (a fixed
+// order, so results are deterministic).  With S == 1 the workgroup then
+// applies the epilogue (FuseDoubleContraction.cpp:175-199 for SwiGLU) and
+// stores Y.  With S > 1 it writes fp32 partials to a workspace and a second
+// kernel adds the S partials in split order and applies the epilogue -- the
+// kernel boundary orders the two, so no device-scope fences are needed.
 #include "common.h"
 
 namespace llk_gfx950 {
 
-struct DecodeArgs {
+struct SkinnyArgs {
   const uint16_t* x;  // [M, K]
-  const uint8_t* wg;  // packed
-  const uint8_t* wu;  // packed
+  const uint8_t* w0;  // packed (Wg, or B for GEMM)
+  const uint8_t* w1;  // packed (Wu), NMAT == 2
   void* y;            // [M, N]
-  float* part;        // [S][2][MT*16][N_pad] fp32 partials (S > 1)
-  unsigned* counter;  // [NB] arrival counters (S > 1), zero between calls
+  float* part;        // [S][NMAT][MT*32][n_pad] fp32 partials (S > 1)
   int64_t ldx, ldy;
   int M, N, K, KB, NB, S, kb_per_split, n_pad;
+  bool yvec;
 };
 
-constexpr int kDecThreads = 256;
-
-template <int MT, bool OUT_BF16, bool XVEC>
-__device__ __forceinline__ void load_x_frag(const DecodeArgs& a, int kb, int kh, int lane,
-                                            bf16x8 (&xf)[MT]) {
+template <int MT, bool XVEC>
+__device__ __forceinline__ void load_x_frags(const SkinnyArgs& a, int kb, int lane,
+                                             bf16x8 (&xf)[4][MT]) {
 #pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    int m = t * 16 + (lane & 15);
-    int kk = kb * 64 + kh * 32 + (lane >> 4) * 8;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (m < a.M) {
-      const uint16_t* src = a.x + (size_t)m * a.ldx + kk;
-      if (XVEC) {
-        if (kk + 8 <= a.K) v = *reinterpret_cast<const uint4*>(src);
-      } else {
-        uint16_t e[8];
+  for (int kq = 0; kq < 4; ++kq)
 #pragma unroll
-        for (int q = 0; q < 8; ++q) e[q] = (kk + q < a.K) ? src[q] : (uint16_t)0;
-        v.x = e[0] | ((uint32_t)e[1] << 16);
-        v.y = e[2] | ((uint32_t)e[3] << 16);
-        v.z = e[4] | ((uint32_t)e[5] << 16);
-        v.w = e[6] | ((uint32_t)e[7] << 16);
+    for (int t = 0; t < MT; ++t) {
+      const int m = t * 32 + (lane & 31);
+      const int kk = kb * 64 + kq * 16 + (lane >> 5) * 8;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (m < a.M) {
+        const uint16_t* src = a.x + (size_t)m * a.ldx + kk;
+        if (XVEC) {
+          if (kk + 8 <= a.K) v = *reinterpret_cast<const uint4*>(src);
+        } else {
+          uint16_t e[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) e[q] = (kk + q < a.K) ? src[q] : (uint16_t)0;
+          v.x = e[0] | ((uint32_t)e[1] << 16);
+          v.y = e[2] | ((uint32_t)e[3] << 16);
+          v.z = e[4] | ((uint32_t)e[5] << 16);
+          v.w = e[6] | ((uint32_t)e[7] << 16);
+        }
       }
+      xf[kq][t] = *reinterpret_cast<bf16x8*>(&v);
     }
-    xf[t] = *reinterpret_cast<bf16x8*>(&v);
-  }
 }
 
-template <bool OUT_BF16>
-__device__ __forceinline__ void store_y4(const DecodeArgs& a, int m, int n, const float (&v)[4],
-                                         bool yvec) {
-  if (m >= a.M || n >= a.N) return;
-  if (OUT_BF16) {
-    uint16_t* dst = reinterpret_cast<uint16_t*>(a.y) + (size_t)m * a.ldy + n;
-    if (yvec && n + 4 <= a.N) {
-      u16x4 h = {f32_to_bf16_rne(v[0]), f32_to_bf16_rne(v[1]), f32_to_bf16_rne(v[2]),
-                 f32_to_bf16_rne(v[3])};
-      *reinterpret_cast<u16x4*>(dst) = h;
-    } else {
-      for (int r = 0; r < 4; ++r)
-        if (n + r < a.N) dst[r] = f32_to_bf16_rne(v[r]);
-    }
-  } else {
-    float* dst = reinterpret_cast<float*>(a.y) + (size_t)m * a.ldy + n;
-    if (yvec && n + 4 <= a.N) {
-      *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
-    } else {
-      for (int r = 0; r < 4; ++r)
-        if (n + r < a.N) dst[r] = v[r];
-    }
-  }
-}
-
-template <int MT, bool OUT_BF16, bool XVEC, bool YVEC, int UNROLL>
-__global__ __launch_bounds__(kDecThreads) void swiglu_decode_kernel(DecodeArgs a) {
+template <int NMAT, int MT, int KS, bool OUT_BF16, bool XVEC, int UNROLL>
+__global__ __launch_bounds__(KS * 64) void skinny_kernel(SkinnyArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float red[];  // [KS][NMAT][MT][16][64]
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int nb = blockIdx.x % a.NB;
-  const int split = blockIdx.x / a.NB;
-  const int kb_begin = split * a.kb_per_split;
-  const int kb_end = min(a.KB, kb_begin + a.kb_per_split);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ngroups = a.NB * 4;
+  const int grp = blockIdx.x % ngroups;  // 32-column group
+  const int split = blockIdx.x / ngroups;
+  const int nb = grp >> 2, n32 = grp & 3;
 
-  // acc[mat][g][t]: mat 0 gate / 1 up, g = n16 group 2*wave+g, t = m16 group
-  f32x4 acc[2][2][MT];
-#pragma unroll
-  for (int p = 0; p < 2; ++p)
-#pragma unroll
-    for (int g = 0; g < 2; ++g)
-#pragma unroll
-      for (int t = 0; t < MT; ++t) acc[p][g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // k range of this workgroup, then of this wave (contiguous chunks).
+  const int kb0 = split * a.kb_per_split;
+  const int kb1 = min(a.KB, kb0 + a.kb_per_split);
+  const int span = kb1 > kb0 ? kb1 - kb0 : 0;
+  const int per_wave = (span + KS - 1) / KS;
+  const int wb0 = kb0 + wave * per_wave;
+  const int wb1 = min(kb1, wb0 + per_wave);
 
-  const size_t col_base = (size_t)nb * a.KB * kBlockBytes;
-  const uint8_t* wbase[2] = {a.wg + col_base, a.wu + col_base};
+  f32x16 acc[NMAT][MT];
+#pragma unroll
+  for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[p][t][r] = 0.0f;
 
-  int kb = kb_begin;
-  for (; kb + UNROLL <= kb_end; kb += UNROLL) {
-    u32x4 w[UNROLL][2][2][2];  // [step][mat][kh][g]
+  // Sub-block (kq, n32) of block (nb, kb): + kb*16K + (kq*4 + n32)*1K.
+  const size_t panel = (size_t)nb * a.KB * kBlockBytes + n32 * kSubBytes + lane * 16;
+  const uint8_t* wbase[2] = {a.w0 + panel, (NMAT == 2 ? a.w1 : a.w0) + panel};
+
+  int kb = wb0;
+  for (; kb + UNROLL <= wb1; kb += UNROLL) {
+    u32x4 w[UNROLL][NMAT][4];
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u)
 #pragma unroll
-      for (int p = 0; p < 2; ++p)
+      for (int p = 0; p < NMAT; ++p)
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
+        for (int kq = 0; kq < 4; ++kq)
+          w[u][p][kq] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+              wbase[p] + (size_t)(kb + u) * kBlockBytes + kq * 4 * kSubBytes));
 #pragma unroll
-          for (int g = 0; g < 2; ++g) {
-            const uint8_t* src = wbase[p] + (size_t)(kb + u) * kBlockBytes +
-                                 (kh * 8 + wave * 2 + g) * kSubBytes + lane * 16;
-            w[u][p][kh][g] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
-          }
+    for (int u = 0; u < UNROLL; ++u) {
+      bf16x8 xf[4][MT];
+      load_x_frags<MT, XVEC>(a, kb + u, lane, xf);
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u)
+      for (int kq = 0; kq < 4; ++kq)
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        bf16x8 xf[MT];
-        load_x_frag<MT, OUT_BF16, XVEC>(a, kb + u, kh, lane, xf);
+        for (int p = 0; p < NMAT; ++p) {
+          const bf16x8 wop = *reinterpret_cast<const bf16x8*>(&w[u][p][kq]);
 #pragma unroll
-        for (int p = 0; p < 2; ++p)
-#pragma unroll
-          for (int g = 0; g < 2; ++g) {
-            bf16x8 wop = *reinterpret_cast<bf16x8*>(&w[u][p][kh][g]);
-#pragma unroll
-            for (int t = 0; t < MT; ++t) acc[p][g][t] = mfma16(wop, xf[t], acc[p][g][t]);
-          }
-      }
-  }
-  for (; kb < kb_end; ++kb) {  // remainder steps
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-      bf16x8 xf[MT];
-      load_x_frag<MT, OUT_BF16, XVEC>(a, kb, kh, lane, xf);
-#pragma unroll
-      for (int p = 0; p < 2; ++p)
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          const uint8_t* src = wbase[p] + (size_t)kb * kBlockBytes +
-                               (kh * 8 + wave * 2 + g) * kSubBytes + lane * 16;
-          u32x4 wv = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
-          bf16x8 wop = *reinterpret_cast<bf16x8*>(&wv);
-#pragma unroll
-          for (int t = 0; t < MT; ++t) acc[p][g][t] = mfma16(wop, xf[t], acc[p][g][t]);
+          for (int t = 0; t < MT; ++t) acc[p][t] = mfma32(wop, xf[kq][t], acc[p][t]);
         }
     }
   }
-
-  // Lane holds n = nb*128 + (2*wave+g)*16 + 4*(lane/16) + r, m = t*16 + lane%16.
-  const int nq = 4 * (lane >> 4);
-  const int mr = lane & 15;
-
-  if (a.S == 1) {
+  for (; kb < wb1; ++kb) {  // remainder steps
+    bf16x8 xf[4][MT];
+    load_x_frags<MT, XVEC>(a, kb, lane, xf);
 #pragma unroll
-    for (int g = 0; g < 2; ++g)
+    for (int kq = 0; kq < 4; ++kq)
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        float v[4];
+      for (int p = 0; p < NMAT; ++p) {
+        const u32x4 wv = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+            wbase[p] + (size_t)kb * kBlockBytes + kq * 4 * kSubBytes));
+        const bf16x8 wop = *reinterpret_cast<const bf16x8*>(&wv);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = swiglu_act(acc[0][g][t][r], acc[1][g][t][r]);
-        store_y4<OUT_BF16>(a, t * 16 + mr, nb * 128 + (2 * wave + g) * 16 + nq, v, YVEC);
+        for (int t = 0; t < MT; ++t) acc[p][t] = mfma32(wop, xf[kq][t], acc[p][t]);
       }
-    return;
   }
 
-  // ---- split-K: publish partials, last arrival reduces in split order
-  constexpr int kRows = MT * 16;
+  // ---- reduce the KS waves' partial sums in LDS, in wave order ----------
+  if (KS > 1) {
 #pragma unroll
-  for (int p = 0; p < 2; ++p)
+    for (int p = 0; p < NMAT; ++p)
 #pragma unroll
-    for (int g = 0; g < 2; ++g)
+      for (int t = 0; t < MT; ++t)
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const int m = t * 16 + mr;
-        if (m >= a.M) continue;
-        const int n = nb * 128 + (2 * wave + g) * 16 + nq;
-        float* dst = a.part + (((size_t)split * 2 + p) * kRows + m) * a.n_pad + n;
-        *reinterpret_cast<f32x4*>(dst) = acc[p][g][t];
-      }
-  __threadfence();
-  __syncthreads();
-  __shared__ unsigned last;
-  if (threadIdx.x == 0) {
-    unsigned prev = atomicAdd(&a.counter[nb], 1u);
-    last = (prev == (unsigned)(a.S - 1)) ? 1u : 0u;
+        for (int r = 0; r < 16; ++r)
+          red[(((wave * NMAT + p) * MT + t) * 16 + r) * 64 + lane] = acc[p][t][r];
+    __syncthreads();
   }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
 
-  // 128 n x kRows m of this block: thread handles 4 consecutive n of a row.
-  for (int e = threadIdx.x; e < kRows * 32; e += kDecThreads) {
-    const int m = e / 32;
-    const int n = nb * 128 + (e % 32) * 4;
-    if (m >= a.M) continue;
-    f32x4 gs = {0.f, 0.f, 0.f, 0.f}, us = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < a.S; ++s) {
-      const float* pg = a.part + (((size_t)s * 2 + 0) * kRows + m) * a.n_pad + n;
-      const float* pu = a.part + (((size_t)s * 2 + 1) * kRows + m) * a.n_pad + n;
-      gs += *reinterpret_cast<const f32x4*>(pg);
-      us += *reinterpret_cast<const f32x4*>(pu);
+  // Thread e handles (t, g, ln): rows m = t*32 + ln%32 of this group and the
+  // 4 consecutive columns n = 8g + 4*(ln/32) + 0..3 (accumulator r = 4g+q).
+  const int n_group0 = nb * kPackN + n32 * 32;
+  for (int e = threadIdx.x; e < MT * 4 * 64; e += KS * 64) {
+    const int ln = e & 63;
+    const int g = (e >> 6) & 3;
+    const int t = e >> 8;
+    float sum[NMAT][4];
+#pragma unroll
+    for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float s = 0.0f;
+        if (KS > 1) {
+          for (int w2 = 0; w2 < KS; ++w2)
+            s += red[(((w2 * NMAT + p) * MT + t) * 16 + 4 * g + q) * 64 + ln];
+        } else {
+          s = acc[p][t][4 * g + q];  // KS == 1: e == lane for t = g = 0 only
+        }
+        sum[p][q] = s;
+      }
+    const int m = t * 32 + (ln & 31);
+    const int n = n_group0 + 8 * g + 4 * (ln >> 5);
+    if (a.S > 1) {
+      if (n < a.n_pad) {
+#pragma unroll
+        for (int p = 0; p < NMAT; ++p) {
+          float* dst = a.part + (((size_t)split * NMAT + p) * (MT * 32) + m) * a.n_pad + n;
+          *reinterpret_cast<f32x4*>(dst) = f32x4{sum[p][0], sum[p][1], sum[p][2], sum[p][3]};
+        }
+      }
+    } else {
+      float v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        v[q] = (NMAT == 2) ? swiglu_act(sum[0][q], sum[1][q]) : sum[0][q];
+      store4<OUT_BF16>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
     }
-    float v[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) v[r] = swiglu_act(gs[r], us[r]);
-    store_y4<OUT_BF16>(a, m, n, v, YVEC);
   }
-  if (threadIdx.x == 0) a.counter[nb] = 0u;
 }
 
-template <int MT, bool OUT_BF16, bool XVEC, bool YVEC>
-static hipError_t launch_dec_t(const DecodeArgs& a, hipStream_t s) {
-  dim3 grid(a.NB * a.S), block(kDecThreads);
-  hipLaunchKernelGGL((swiglu_decode_kernel<MT, OUT_BF16, XVEC, YVEC, 2>), grid, block, 0, s, a);
+// Adds the S partials in split order and applies the epilogue: thread
+// handles 4 consecutive n of one row.
+template <int NMAT, bool OUT_BF16>
+__global__ __launch_bounds__(256) void skinny_reduce_kernel(SkinnyArgs a, int rows) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int quads = a.n_pad / 4;
+  if (e >= (int64_t)a.M * quads) return;
+  const int m = (int)(e / quads);
+  const int n = (int)(e % quads) * 4;
+  f32x4 s[NMAT];
+#pragma unroll
+  for (int p = 0; p < NMAT; ++p) s[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < a.S; ++sp)
+#pragma unroll
+    for (int p = 0; p < NMAT; ++p)
+      s[p] += *reinterpret_cast<const f32x4*>(a.part + (((size_t)sp * NMAT + p) * rows + m) * a.n_pad + n);
+  float v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) v[q] = (NMAT == 2) ? swiglu_act(s[0][q], s[1][q]) : s[0][q];
+  store4<OUT_BF16>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
+}
+
+template <int NMAT, int MT, int KS, bool OUT_BF16, bool XVEC>
+static hipError_t launch_skinny_t(const SkinnyArgs& a, hipStream_t s) {
+  auto fn = skinny_kernel<NMAT, MT, KS, OUT_BF16, XVEC, 2>;
+  const size_t lds = KS > 1 ? (size_t)KS * NMAT * MT * 16 * 64 * sizeof(float) : 0;
+  static bool attr_set = false;  // per instantiation; benign race (idempotent)
+  if (!attr_set && lds > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  attr_set = true;
+  hipLaunchKernelGGL(fn, dim3(a.NB * 4 * a.S), dim3(KS * 64), lds, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.S == 1) return e;
+  const int64_t threads = (int64_t)a.M * (a.n_pad / 4);
+  hipLaunchKernelGGL((skinny_reduce_kernel<NMAT, OUT_BF16>), dim3((unsigned)((threads + 255) / 256)),
+                     dim3(256), 0, s, a, MT * 32);
   return hipGetLastError();
 }
 
-template <int MT>
-static hipError_t launch_dec_mt(const DecodeArgs& a, bool out_bf16, bool xvec, bool yvec,
-                                hipStream_t s) {
-  if (out_bf16) {
-    if (xvec) return yvec ? launch_dec_t<MT, true, true, true>(a, s) : launch_dec_t<MT, true, true, false>(a, s);
-    return yvec ? launch_dec_t<MT, true, false, true>(a, s) : launch_dec_t<MT, true, false, false>(a, s);
-  }
-  if (xvec) return yvec ? launch_dec_t<MT, false, true, true>(a, s) : launch_dec_t<MT, false, true, false>(a, s);
-  return yvec ? launch_dec_t<MT, false, false, true>(a, s) : launch_dec_t<MT, false, false, false>(a, s);
+// KS (waves per workgroup) keeps the LDS reduction buffer at 64 KiB.
+template <int NMAT, int MT>
+static hipError_t launch_skinny_mt(const SkinnyArgs& a, bool out_bf16, bool xvec, hipStream_t s) {
+  constexpr int KS = (NMAT * MT <= 2) ? 8 : 4;
+  if (out_bf16)
+    return xvec ? launch_skinny_t<NMAT, MT, KS, true, true>(a, s)
+                : launch_skinny_t<NMAT, MT, KS, true, false>(a, s);
+  return xvec ? launch_skinny_t<NMAT, MT, KS, false, true>(a, s)
+              : launch_skinny_t<NMAT, MT, KS, false, false>(a, s);
 }
 
 }  // namespace llk_gfx950
 
-// Split-K workspace layout: a fixed region of kDecodeMaxCounters arrival
-// counters at offset 0 (zero before first use; every launch leaves the
-// counters it used at zero), then the fp32 partials.  The counters never
-// move, so partials of an earlier, larger launch can never land on them.
-constexpr int kDecodeMaxCounters = 16384;
-constexpr size_t kDecodeCounterBytes = kDecodeMaxCounters * sizeof(unsigned);
+// Rows of the partial buffer for M rows (whole 32-row MFMA groups).
+static int skinny_rows(int M) { return (M + 31) / 32 * 32; }
 
-int llk_decode_max_counters() { return kDecodeMaxCounters; }
-
-size_t llk_decode_workspace_bytes(int M, int N_pad, int NB, int S) {
+size_t llk_skinny_workspace_bytes(int nmat, int M, int N_pad, int S) {
   if (S <= 1) return 0;
-  (void)NB;
-  int mt = (M + 15) / 16;
-  size_t part = (size_t)S * 2 * (mt * 16) * N_pad * sizeof(float);
-  return kDecodeCounterBytes + part;
+  return (size_t)S * nmat * skinny_rows(M) * N_pad * sizeof(float);
 }
 
-// Internal: called by the host dispatch layer.  `ws` must hold
-// llk_decode_workspace_bytes(M, N_pad, NB, S) bytes with its counter region
-// zeroed, and NB <= kDecodeMaxCounters when S > 1.
-hipError_t llk_launch_decode(const uint16_t* x, int64_t ldx, const void* wg, const void* wu,
-                             void* y, int64_t ldy, int M, int N, int K, int KB, int NB, int S,
-                             void* ws, bool out_bf16, bool xvec, bool yvec, hipStream_t s) {
+// Internal: called by the host dispatch layer.  mode 1 = SwiGLU (w0 = Wg,
+// w1 = Wu), mode 0 = GEMM (w0 = B).  M <= 64.  `ws` must hold
+// llk_skinny_workspace_bytes(nmat, M, 128*NB, S) bytes when S > 1.
+hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const void* w0,
+                             const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
+                             int NB, int S, void* ws, bool out_bf16, bool xvec, bool yvec,
+                             hipStream_t s) {
   using namespace llk_gfx950;
-  DecodeArgs a;
+  if (M < 1 || M > 64) return hipErrorInvalidValue;
+  SkinnyArgs a;
   a.x = x;
-  a.wg = static_cast<const uint8_t*>(wg);
-  a.wu = static_cast<const uint8_t*>(wu);
+  a.w0 = static_cast<const uint8_t*>(w0);
+  a.w1 = static_cast<const uint8_t*>(w1);
   a.y = y;
   a.ldx = ldx;
   a.ldy = ldy;
@@ -275,19 +269,13 @@ hipError_t llk_launch_decode(const uint16_t* x, int64_t ldx, const void* wg, con
   a.S = S < 1 ? 1 : S;
   a.kb_per_split = (KB + a.S - 1) / a.S;
   a.n_pad = NB * kPackN;
-  a.part = nullptr;
-  a.counter = nullptr;
-  if (a.S > 1) {
-    if (NB > kDecodeMaxCounters || ws == nullptr) return hipErrorInvalidValue;
-    a.counter = static_cast<unsigned*>(ws);
-    a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kDecodeCounterBytes);
-  }
-  const int mt = (M + 15) / 16;
-  switch (mt) {
-    case 1: return launch_dec_mt<1>(a, out_bf16, xvec, yvec, s);
-    case 2: return launch_dec_mt<2>(a, out_bf16, xvec, yvec, s);
-    case 3: return launch_dec_mt<3>(a, out_bf16, xvec, yvec, s);
-    case 4: return launch_dec_mt<4>(a, out_bf16, xvec, yvec, s);
-    default: return hipErrorInvalidValue;
-  }
+  a.yvec = yvec;
+  a.part = static_cast<float*>(ws);
+  if (a.S > 1 && ws == nullptr) return hipErrorInvalidValue;
+  const int mt = (M + 31) / 32;
+  if (mode == 1)
+    return mt == 1 ? launch_skinny_mt<2, 1>(a, out_bf16, xvec, s)
+                   : launch_skinny_mt<2, 2>(a, out_bf16, xvec, s);
+  return mt == 1 ? launch_skinny_mt<1, 1>(a, out_bf16, xvec, s)
+                 : launch_skinny_mt<1, 2>(a, out_bf16, xvec, s);
 }

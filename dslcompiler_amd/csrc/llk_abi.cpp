@@ -22,17 +22,18 @@
 
 // Kernel launchers (kernels/*.hip).
 hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
-                           const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
-                           int NB, bool out_bf16, bool xvec, bool yvec, int load_override,
-                           hipStream_t s);
-hipError_t llk_launch_decode(const uint16_t* x, int64_t ldx, const void* wg, const void* wu,
-                             void* y, int64_t ldy, int M, int N, int K, int KB, int NB, int S,
-                             void* ws, bool out_bf16, bool xvec, bool yvec, hipStream_t s);
-size_t llk_decode_workspace_bytes(int M, int N_pad, int NB, int S);
-int llk_decode_max_counters();
+                           const void* w1, void* y, int64_t ldy, int M, int N, int KB, int NB,
+                           bool out_bf16, bool yvec, hipStream_t s);
+bool llk_tile_x_fits(int M, int64_t ldx);
+hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const void* w0,
+                             const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
+                             int NB, int S, void* ws, bool out_bf16, bool xvec, bool yvec,
+                             hipStream_t s);
+size_t llk_skinny_workspace_bytes(int nmat, int M, int N_pad, int S);
+hipError_t llk_launch_pad_rows(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* out,
+                               int64_t ldo, hipStream_t s);
 hipError_t llk_launch_pack(const uint16_t* w, int64_t ld, int K, int N, int KB, int NB, void* out,
                            hipStream_t s);
-hipError_t llk_launch_zero(void* p, size_t bytes, hipStream_t s);
 
 struct llk_packed_weights {
   // Reference metadata (PackedWeights.h:13-19).
@@ -140,28 +141,10 @@ bool y_vec_ok(const llk_tensor2d* y, bool bf16) {
   return (reinterpret_cast<uintptr_t>(y->data) % align == 0) && (y->stride0 % 4 == 0);
 }
 
-// Split count for the decode kernel: enough workgroups to keep every CU
-// streaming, at least `min_kb` 64-k steps per split, no empty splits.
-int decode_splits(int64_t KB, int64_t NB) {
-  if (NB > llk_decode_max_counters()) return 1;  // one arrival counter per n-block
-  int64_t forced = llk::tunable("decode_splits");
-  int64_t S;
-  if (forced > 0) {
-    S = std::min<int64_t>(forced, KB);
-  } else {
-    const int64_t target_wgs = llk::tunable("decode_target_wgs");
-    const int64_t min_kb = std::max<int64_t>(1, llk::tunable("decode_min_kb"));
-    int64_t kbps = std::max<int64_t>(min_kb, (KB * NB + target_wgs - 1) / target_wgs);
-    kbps = std::min<int64_t>(kbps, KB);
-    S = (KB + kbps - 1) / kbps;
-  }
-  if (S < 1) S = 1;
-  const int64_t kbps = (KB + S - 1) / S;
-  return static_cast<int>((KB + kbps - 1) / kbps);
-}
-
 // Workspace: the caller's (ctx->scratch) if given, else the library's own
-// per-device buffer, grown on demand and zeroed when (re)allocated.
+// per-device buffer, grown on demand.  Launches that use the library's
+// buffer on different streams of one device must not overlap (pass a
+// scratch buffer per stream instead).
 int get_workspace(int dev, size_t need, llk_kernel_context* ctx, void** out) {
   *out = nullptr;
   if (need == 0) return LLK_OK;
@@ -180,7 +163,7 @@ int get_workspace(int dev, size_t need, llk_kernel_context* ctx, void** out) {
     if (st.ws) {
       hipError_t e = hipDeviceSynchronize();
       if (e != hipSuccess) return fail_hip(e, "hipDeviceSynchronize");
-      hipFree(st.ws);
+      (void)hipFree(st.ws);
       st.ws = nullptr;
       st.ws_bytes = 0;
     }
@@ -201,6 +184,79 @@ int get_workspace(int dev, size_t need, llk_kernel_context* ctx, void** out) {
 
 hipStream_t stream_of(const llk_kernel_context* ctx) {
   return ctx ? static_cast<hipStream_t>(ctx->stream) : nullptr;
+}
+
+// Launch plan of one contraction (SwiGLU: nmat 2, GEMM: nmat 1).
+struct Plan {
+  bool skinny = false;   // small-M bandwidth kernel
+  int S = 1;             // its k splits across workgroups
+  bool pad = false;      // tile path: copy X into a padded buffer first
+  int64_t chunk = 0;     // tile path: rows per launch (32-bit X offsets)
+  int64_t ld = 0;        // tile path: row stride of the X the kernel reads
+  size_t ws_bytes = 0;   // workspace the plan needs
+};
+
+// x == nullptr: plan for the worst case (X needs padding).
+Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const llk_tensor2d* x) {
+  Plan p;
+  if (M <= std::min<int64_t>(64, llk::tunable("decode_max_m"))) {
+    p.skinny = true;
+    const int64_t groups = NB * 4;
+    int64_t S = llk::tunable("decode_splits");
+    if (S <= 0) {
+      const int64_t target = std::max<int64_t>(1, llk::tunable("decode_target_wgs"));
+      const int64_t min_kb = std::max<int64_t>(1, llk::tunable("decode_min_kb"));
+      S = std::min((target + groups - 1) / groups, std::max<int64_t>(1, KB / min_kb));
+    }
+    S = std::max<int64_t>(1, std::min(S, KB));
+    const int64_t kbps = (KB + S - 1) / S;  // no empty splits
+    p.S = static_cast<int>((KB + kbps - 1) / kbps);
+    p.ws_bytes = llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), p.S);
+    return p;
+  }
+  p.pad = !(x && x_vec_ok(x) && K % 64 == 0);
+  p.ld = p.pad ? KB * 64 : x->stride0;
+  p.chunk = M;
+  if (!llk_tile_x_fits((int)std::min<int64_t>(M, kMaxDim), p.ld))
+    p.chunk = std::max<int64_t>(256, (((int64_t)1 << 31) - 1) / (p.ld * 2) / 256 * 256 - 256);
+  if (p.pad) p.ws_bytes = (size_t)std::min(p.chunk, M) * p.ld * 2;
+  return p;
+}
+
+int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w0,
+                    const llk_packed_weights* w1, llk_tensor2d* y, bool out_bf16,
+                    llk_kernel_context* ctx, int dev, const char* what) {
+  const int64_t M = x->dim0, K = x->dim1, N = w0->N;
+  const int nmat = mode == 1 ? 2 : 1;
+  const Plan p = plan_launch(nmat, M, K, w0->KB, w0->NB, x);
+  void* ws = nullptr;
+  int rc = get_workspace(dev, p.ws_bytes, ctx, &ws);
+  if (rc) return rc;
+  hipStream_t s = stream_of(ctx);
+  const bool yvec = y_vec_ok(y, out_bf16);
+  hipError_t e = hipSuccess;
+  if (p.skinny) {
+    e = llk_launch_skinny(mode, static_cast<const uint16_t*>(x->data), x->stride0, w0->dev,
+                          w1 ? w1->dev : nullptr, y->data, y->stride0, (int)M, (int)N, (int)K,
+                          (int)w0->KB, (int)w0->NB, p.S, ws, out_bf16, x_vec_ok(x), yvec, s);
+    if (e != hipSuccess) return fail_hip(e, what);
+    return LLK_OK;
+  }
+  const size_t ysz = out_bf16 ? 2 : 4;
+  for (int64_t m0 = 0; m0 < M && e == hipSuccess; m0 += p.chunk) {
+    const int rows = (int)std::min(p.chunk, M - m0);
+    const uint16_t* xp = static_cast<const uint16_t*>(x->data) + m0 * x->stride0;
+    if (p.pad) {
+      e = llk_launch_pad_rows(xp, x->stride0, rows, (int)K, static_cast<uint16_t*>(ws), p.ld, s);
+      if (e != hipSuccess) break;
+      xp = static_cast<const uint16_t*>(ws);
+    }
+    e = llk_launch_tile(mode, xp, p.ld, w0->dev, w1 ? w1->dev : nullptr,
+                        static_cast<uint8_t*>(y->data) + m0 * y->stride0 * ysz, y->stride0, rows,
+                        (int)N, (int)w0->KB, (int)w0->NB, out_bf16, yvec, s);
+  }
+  if (e != hipSuccess) return fail_hip(e, what);
+  return LLK_OK;
 }
 
 }  // namespace
@@ -341,12 +397,16 @@ int llk_repack(llk_packed_weights* pw, const llk_tensor2d* w) {
                 (long long)w->dim0, (long long)w->dim1, (long long)pw->K, (long long)pw->N);
   llk_packed_weights* fresh = nullptr;
   int dev_saved = 0;
-  hipGetDevice(&dev_saved);
-  if (pw->device >= 0) hipSetDevice(pw->device);
+  hipError_t e = hipGetDevice(&dev_saved);
+  if (e != hipSuccess) return fail_hip(e, "hipGetDevice");
+  if (pw->device >= 0 && pw->device != dev_saved) {
+    e = hipSetDevice(pw->device);
+    if (e != hipSuccess) return fail_hip(e, "hipSetDevice");
+  }
   rc = llk_pack_weights(w, pw->BK, pw->host.empty() ? 0u : LLK_PACK_KEEP_HOST, &fresh);
-  hipSetDevice(dev_saved);
+  if (pw->device >= 0 && pw->device != dev_saved) (void)hipSetDevice(dev_saved);
   if (rc) return rc;
-  if (pw->dev) hipFree(pw->dev);
+  if (pw->dev) (void)hipFree(pw->dev);
   pw->host.swap(fresh->host);
   pw->dev = fresh->dev;
   pw->dev_bytes = fresh->dev_bytes;
@@ -358,7 +418,7 @@ int llk_repack(llk_packed_weights* pw, const llk_tensor2d* w) {
 
 void llk_packed_weights_free(llk_packed_weights* pw) {
   if (!pw) return;
-  if (pw->dev) hipFree(pw->dev);
+  if (pw->dev) (void)hipFree(pw->dev);
   delete pw;
 }
 
@@ -394,10 +454,7 @@ int llk_pack_device_layout(const llk_tensor2d* w, void* out) {
 
 size_t llk_swiglu_scratch_size(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  if (M > llk::tunable("decode_max_m")) return 0;
-  const int64_t NB = llk::deviceBlocksN(N), KB = llk::deviceBlocksK(K);
-  const int S = decode_splits(KB, NB);
-  return llk_decode_workspace_bytes((int)M, (int)(NB * 128), (int)NB, S);
+  return plan_launch(2, M, K, llk::deviceBlocksK(K), llk::deviceBlocksN(N), nullptr).ws_bytes;
 }
 
 int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
@@ -408,39 +465,20 @@ int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
   if (y_dtype != LLK_BF16 && y_dtype != LLK_FP32)
     return fail(LLK_ERR_DTYPE, "y_dtype %d unsupported (bf16 or f32)", y_dtype);
   if (!wg || !wu) return fail(LLK_ERR_INVALID_ARGUMENT, "packed weights handle is NULL");
-  const int64_t M = x->dim0, K = x->dim1, N = wg->N;
-  // FusedSwiGLUOp::verify (LLKOps.cpp:42-83) checks, same order.
+  const int64_t M = x->dim0, K = x->dim1;
+  // FusedSwiGLUOp::verify (LLKOps.cpp:42-83) checks, same order and wording.
   if (y->dim0 != M) return fail(LLK_ERR_SHAPE, "M dimension mismatch: X=%lld vs init=%lld", (long long)M, (long long)y->dim0);
   if (wg->N != y->dim1) return fail(LLK_ERR_SHAPE, "N dimension mismatch: Wg=%lld vs init=%lld", (long long)wg->N, (long long)y->dim1);
   if (K != wg->K) return fail(LLK_ERR_SHAPE, "K dimension mismatch between X=%lld and Wg=%lld", (long long)K, (long long)wg->K);
   if (K != wu->K) return fail(LLK_ERR_SHAPE, "K dimension mismatch between X=%lld and Wu=%lld", (long long)K, (long long)wu->K);
   if (wg->N != wu->N) return fail(LLK_ERR_SHAPE, "N dimension mismatch between Wg=%lld and Wu=%lld", (long long)wg->N, (long long)wu->N);
   if (M > kMaxDim) return fail(LLK_ERR_SHAPE, "M too large");
-  if (M == 0 || N == 0) return LLK_OK;
+  if (M == 0 || wg->N == 0) return LLK_OK;
   if (K == 0) return fail(LLK_ERR_SHAPE, "K must be >= 1 (empty reduction)");
   int dev;
   if ((rc = current_device(&dev))) return rc;
   if ((rc = check_packed(wg, "wg", dev)) || (rc = check_packed(wu, "wu", dev))) return rc;
-
-  const bool bf16 = y_dtype == LLK_BF16;
-  const bool xvec = x_vec_ok(x), yvec = y_vec_ok(y, bf16);
-  hipStream_t s = stream_of(ctx);
-  hipError_t e;
-  if (M <= llk::tunable("decode_max_m")) {
-    const int S = decode_splits(std::max<int64_t>(wg->KB, 1), wg->NB);
-    void* ws = nullptr;
-    size_t need = llk_decode_workspace_bytes((int)M, (int)(wg->NB * 128), (int)wg->NB, S);
-    if ((rc = get_workspace(dev, need, ctx, &ws))) return rc;
-    e = llk_launch_decode(static_cast<const uint16_t*>(x->data), x->stride0, wg->dev, wu->dev,
-                          y->data, y->stride0, (int)M, (int)N, (int)K, (int)wg->KB, (int)wg->NB, S,
-                          ws, bf16, xvec, yvec, s);
-  } else {
-    e = llk_launch_tile(1, static_cast<const uint16_t*>(x->data), x->stride0, wg->dev, wu->dev,
-                        y->data, y->stride0, (int)M, (int)N, (int)K, (int)wg->KB, (int)wg->NB, bf16,
-                        xvec, yvec, (int)llk::tunable("tile_load"), s);
-  }
-  if (e != hipSuccess) return fail_hip(e, "swiglu launch");
-  return LLK_OK;
+  return run_contraction(1, x, wg, wu, y, y_dtype == LLK_BF16, ctx, dev, "swiglu");
 }
 
 int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor2d* c,
@@ -462,13 +500,7 @@ int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor
   int dev;
   if ((rc = current_device(&dev))) return rc;
   if ((rc = check_packed(b, "b", dev))) return rc;
-  const bool bf16 = c_dtype == LLK_BF16;
-  hipError_t e = llk_launch_tile(0, static_cast<const uint16_t*>(a->data), a->stride0, b->dev,
-                                 nullptr, c->data, c->stride0, (int)M, (int)N, (int)K, (int)b->KB,
-                                 (int)b->NB, bf16, x_vec_ok(a), y_vec_ok(c, bf16),
-                                 (int)llk::tunable("tile_load"), stream_of(ctx));
-  if (e != hipSuccess) return fail_hip(e, "gemm launch");
-  return LLK_OK;
+  return run_contraction(0, a, b, nullptr, c, c_dtype == LLK_BF16, ctx, dev, "gemm");
 }
 
 int llk_mlp_bf16(const llk_tensor2d* x, const llk_packed_weights* wg, const llk_packed_weights* wu,

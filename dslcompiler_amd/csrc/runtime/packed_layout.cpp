@@ -31,9 +31,9 @@ void packDeviceLayout(const uint16_t* w, int64_t K, int64_t N, int64_t stride0, 
   uint16_t* o = reinterpret_cast<uint16_t*>(out);
   std::memset(out, 0, deviceLayoutBytes(K, N));
   // Block (nb, kb) holds n in [128 nb, +128), k in [64 kb, +64).  Element
-  // (n, k) of a block sits in sub-block s = kh*8 + n16, lane
-  // l = g*16 + i, slot element t, where kk = k - 64 kb = 32 kh + 8 g + t and
-  // nn = n - 128 nb = 16 n16 + i.  Rows of W are read contiguously.
+  // (n, k) of a block sits in sub-block s = kq*4 + n32, lane l = h*32 + i,
+  // slot element t, where kk = k - 64 kb = 16 kq + 8 h + t and
+  // nn = n - 128 nb = 32 n32 + i.  Rows of W are read contiguously.
   for (int64_t nb = 0; nb < NB; ++nb)
     for (int64_t kb = 0; kb < KB; ++kb) {
       uint16_t* blk = o + (nb * KB + kb) * 8192;
@@ -41,9 +41,9 @@ void packDeviceLayout(const uint16_t* w, int64_t K, int64_t N, int64_t stride0, 
       const int64_t nend = std::min<int64_t>(128, N - nb * 128);
       for (int64_t kk = 0; kk < kend; ++kk) {
         const uint16_t* row = w + (kb * 64 + kk) * stride0 + nb * 128;
-        const int64_t kh = kk >> 5, g = (kk >> 3) & 3, t = kk & 7;
+        const int64_t kq = kk >> 4, h = (kk >> 3) & 1, t = kk & 7;
         for (int64_t nn = 0; nn < nend; ++nn) {
-          const int64_t s = kh * 8 + (nn >> 4), l = g * 16 + (nn & 15);
+          const int64_t s = kq * 4 + (nn >> 5), l = h * 32 + (nn & 31);
           blk[(s * 64 + l) * 8 + t] = row[nn];
         }
       }

@@ -13,7 +13,7 @@ void packReferenceLayout(const uint16_t* w, int64_t K, int64_t N, int64_t stride
                          uint16_t* out);
 
 // Device payload layout (MFMA operand order, 128 n x 64 k blocks of 16 KiB,
-// 1 KiB sub-blocks of 16 n x 32 k in v_mfma_f32_16x16x32_bf16 lane order).
+// 1 KiB sub-blocks of 32 n x 16 k in v_mfma_f32_32x32x16_bf16 lane order).
 int64_t deviceBlocksN(int64_t N);  // ceil(N / 128)
 int64_t deviceBlocksK(int64_t K);  // ceil(K / 64)
 size_t deviceLayoutBytes(int64_t K, int64_t N);

@@ -12,17 +12,14 @@ struct Knob {
   std::atomic<int64_t> value;
 };
 
-// decode_max_m:      largest M routed to the split-K decode kernel.
-// decode_splits:     force the decode k-split count (0 = heuristic).
-// decode_target_wgs: workgroups the decode heuristic aims for.
-// decode_min_kb:     fewest 64-k steps per decode split.
-// tile_load:         force the tile kernel's operand path (-1 = automatic,
-//                    0 = direct-to-LDS, 1 = staged 16-byte, 2 = staged scalar).
+// decode_max_m:      largest M (<= 64) routed to the small-M bandwidth kernel.
+// decode_splits:     force its cross-workgroup k-split count (0 = heuristic).
+// decode_target_wgs: workgroups the split heuristic aims for (1 per CU).
+// decode_min_kb:     fewest 64-k steps per split.
 Knob g_knobs[] = {
-    {"tile_load", {-1}},
     {"decode_max_m", {64}},
     {"decode_splits", {0}},
-    {"decode_target_wgs", {1536}},
+    {"decode_target_wgs", {256}},
     {"decode_min_kb", {2}},
 };
 

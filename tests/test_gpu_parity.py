@@ -88,26 +88,57 @@ def test_swiglu_config1_prefill_path(llk, gpu, orc):
         llk.set_tunable("decode_max_m", old)
 
 
-@pytest.mark.parametrize("path", [0, 1, 2])
-@pytest.mark.parametrize("M,K,N", [(320, 512, 392), (300, 1024, 256), (513, 128, 200)])
-def test_tile_load_paths(llk, gpu, orc, path, M, K, N):
-    """The prefill/GEMM tile kernel's three operand paths (direct-to-LDS,
-    staged 16-byte, staged element-wise) on ragged M and N edge tiles."""
-    print(f"case tile load path={path} M={M} K={K} N={N}", flush=True)
-    old = llk.get_tunable("tile_load")
-    llk.set_tunable("tile_load", path)
-    try:
-        x, wg, wu = swiglu_inputs(M, K, N, seed=path + 1)
-        _check_swiglu(llk, gpu, orc, x, wg, wu, f"path{path}")
-        s = 1.0 / np.sqrt(K)
-        a = normal_bf16(9, 0, (M, K), s)
-        b = normal_bf16(9, 1, (K, N), s)
-        cf_ref, _ = orc.gemm(a, b)
-        pb = llk.PackedWeights.from_host(b)
-        cf = from_dev(llk.matmul(to_dev(gpu, a), pb, out_dtype=gpu.float32))
-        assert_parity(cf, cf_ref, f"gemm path{path}")
-    finally:
-        llk.set_tunable("tile_load", old)
+@pytest.mark.parametrize("case", ["k_ragged", "odd_stride", "misaligned_base", "aligned"])
+def test_tile_x_layouts(llk, gpu, orc, case):
+    """The tile kernel reads X straight into LDS when rows are 16-byte
+    aligned and K % 64 == 0; otherwise X is first copied into a padded
+    buffer.  Both routes, on ragged M and N edge tiles, for SwiGLU and GEMM."""
+    print(f"case tile x layout {case}", flush=True)
+    M, N = 300, 392
+    K = {"k_ragged": 200, "odd_stride": 256, "misaligned_base": 256, "aligned": 320}[case]
+    x, wg, wu = swiglu_inputs(M, K, N, seed=len(case))
+    if case == "odd_stride":
+        xd = to_dev(gpu, x, stride0=K + 3)
+    elif case == "misaligned_base":
+        big = np.zeros((M, K + 8), np.uint16)
+        big[:, 1:K + 1] = x
+        xd = to_dev(gpu, big)[:, 1:K + 1]
+    else:
+        xd = to_dev(gpu, x)
+    yf_ref, _ = orc.swiglu(x, wg, wu)
+    pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
+    yf = from_dev(llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.float32))
+    assert_parity(yf, yf_ref, f"swiglu {case}")
+    s = 1.0 / np.sqrt(K)
+    b = normal_bf16(9, 1, (K, N), s)
+    cf_ref, _ = orc.gemm(x, b)
+    pb = llk.PackedWeights.from_host(b)
+    cf = from_dev(llk.matmul(xd, pb, out_dtype=gpu.float32))
+    assert_parity(cf, cf_ref, f"gemm {case}")
+
+
+@pytest.mark.parametrize("M", [1, 17, 40, 64])
+def test_gemm_small_m(llk, gpu, orc, M):
+    """Small-M GEMM (the down projection of decode-sized MLP blocks) runs on
+    the bandwidth kernel, with and without the cross-workgroup k split."""
+    print(f"case gemm small M={M}", flush=True)
+    K, N = 1536, 640
+    s = 1.0 / np.sqrt(K)
+    a = normal_bf16(4, 0, (M, K), s)
+    b = normal_bf16(4, 1, (K, N), s)
+    cf_ref, _ = orc.gemm(a, b)
+    pb = llk.PackedWeights.from_host(b)
+    ad = to_dev(gpu, a)
+    for splits in (0, 1, 3):
+        old = llk.get_tunable("decode_splits")
+        llk.set_tunable("decode_splits", splits)
+        try:
+            cf = from_dev(llk.matmul(ad, pb, out_dtype=gpu.float32))
+            cb = from_dev(llk.matmul(ad, pb, out_dtype=gpu.bfloat16))
+        finally:
+            llk.set_tunable("decode_splits", old)
+        assert_parity(cf, cf_ref, f"gemm small M={M} S={splits}")
+        assert np.array_equal(cb, to_bf16_bits(cf)), "bf16 != RNE(fp32)"
 
 
 @pytest.mark.parametrize("splits", [1, 2, 3, 16])
@@ -123,9 +154,9 @@ def test_swiglu_decode_splits(llk, gpu, orc, splits):
 
 
 def test_swiglu_decode_workspace_reuse(llk, gpu, orc):
-    """Regression: a large split-K decode call followed by smaller ones whose
-    partial/counter layout differs must not see stale workspace contents
-    (the arrival counters live at a fixed offset and stay zero)."""
+    """Regression: a large split-K decode call followed by smaller ones with a
+    different partial-sum layout in the shared workspace must not see stale
+    workspace contents."""
     print("case swiglu decode workspace reuse", flush=True)
     for (M, K, N, S) in [(64, 4096, 1376, 8), (8, 1024, 640, 2), (1, 256, 128, 2),
                          (33, 2048, 2000, 5), (3, 512, 96, 3)]:
