@@ -14,15 +14,20 @@
 // FuseDoubleContraction.cpp:155-173).  Wave tile: 128 m x 128 MFMA rows =
 // 4 x 4 MFMA tiles of 32 x 32, 256 fp32 accumulators per lane (AGPRs).
 //
-// K loop: 64 k per step, two LDS stages of 64 KiB (32 KiB weights + 32 KiB
-// X).  Operands go straight from memory into LDS (buffer_load_dwordx4 ...
-// lds), so step kb+1 streams in while the 64 MFMAs of step kb run.  LDS
-// holds every operand as a 1 KiB MFMA-ordered sub-block: every LDS read is
-// one contiguous 1 KiB wave access (no bank conflicts).
+// K loop: 32 k per stage, a ring of 4 LDS stages of 32 KiB (16 KiB weights
+// + 16 KiB X).  Operands go straight from memory into LDS
+// (buffer_load_dwordx4 ... lds) two to three stages ahead of the 32 MFMAs
+// per wave that consume them, and each stage's barrier sits between two
+// halves of the previous stage's MFMAs, so LDS reads never stall the MFMA
+// stream.  Weights sit in LDS as 1 KiB MFMA-ordered sub-blocks (contiguous,
+// conflict-free operand reads); X as XOR-swizzled 64-byte rows, so its loads
+// move whole rows and its operand reads are conflict-free too.
 //
 // X must be padded to whole 64-k steps with 16-byte aligned rows (the host
 // copies it into a padded buffer otherwise); rows >= M read as zero through
 // the buffer resource's range check.
+#include <type_traits>
+
 #include "common.h"
 
 namespace llk_gfx950 {
@@ -41,8 +46,27 @@ struct TileArgs {
 
 constexpr int kThreads = 256;
 constexpr int kTileM = 256;
-constexpr int kStageBytes = 65536;
-constexpr int kXOff = 32768;  // X sub-blocks inside a stage
+constexpr int kStageK = 32;           // k per pipeline stage
+constexpr int kStageBytes = 32768;    // 16 KiB weights + 16 KiB X
+constexpr int kXOff = 16384;          // X rows inside a stage
+constexpr int kStages = 4;            // LDS ring of stages
+constexpr int kLoadsPerStage = 8;     // buffer_load ... lds per wave per stage
+
+// s_waitcnt with vmcnt(n) (n < 64) and the other counters left alone.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Waits until at most `ahead` stages of this wave's loads are outstanding.
+__device__ __forceinline__ void wait_stages(int ahead) {
+  if (ahead >= 3) wait_vmcnt<3 * kLoadsPerStage>();
+  else if (ahead == 2) wait_vmcnt<2 * kLoadsPerStage>();
+  else if (ahead == 1) wait_vmcnt<kLoadsPerStage>();
+  else wait_vmcnt<0>();
+}
 
 // MODE 0: GEMM (C = X W);  MODE 1: fused SwiGLU.
 // OUT_BF16: store bf16 (RNE) instead of fp32.
@@ -63,21 +87,26 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   const int m0 = tm * kTileM;
 
   // ---- operand streams ----------------------------------------------------
-  // LDS weight slot b (0, 1) holds one packed n-block.  Waves 0-1 fill slot 0
-  // and waves 2-3 slot 1: wave w copies sub-blocks (w&1)*8 .. +8 of its
-  // slot's block, 8 KiB contiguous in the payload.  Every wave also copies
-  // the 8 X sub-blocks of k quarter kq = w (rows m0 + 32 i + lane%32).
+  // Stage t holds k range [32 t, 32 t + 32).
+  // Weights: LDS slot b (0, 1) holds the 8 sub-blocks (k quarters 2(t%2),
+  // 2(t%2)+1 of block (nb, t/2)) of one packed n-block, 8 KiB contiguous in
+  // the payload at t * 8 KiB of the n-block's panel.  Wave w fills
+  // sub-blocks (w&1)*4 .. +4 of slot w>>1.
+  // X: 256 rows of 32 k = 64 bytes, row r at kXOff + 64 r.  Inside a row the
+  // four 16-byte chunks c (8 k each) are stored at slot c ^ ((r >> 2) & 3),
+  // so the MFMA operand reads (32 rows, one chunk) hit distinct banks.  Wave
+  // w fills rows w*64 .. +64: each load instruction covers 16 full rows.
   const int wslot = wave >> 1;
   const uint8_t* wpanel;
-  bool wvalid = true;
   if (MODE == 1) {
     wpanel = (wslot ? a.w1 : a.w0) + (size_t)tn * a.KB * kBlockBytes;
   } else {
+    // An odd NB leaves the last tile without a second block; its wave pair
+    // streams block 0 instead and the results (n >= N) are never stored.
     const int nb = 2 * tn + wslot;
-    wvalid = nb < a.NB;
-    wpanel = a.w0 + (size_t)(wvalid ? nb : 0) * a.KB * kBlockBytes;
+    wpanel = a.w0 + (size_t)(nb < a.NB ? nb : 0) * a.KB * kBlockBytes;
   }
-  wpanel += (wave & 1) * 8 * kSubBytes;
+  wpanel += (wave & 1) * 4 * kSubBytes;
   const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(wpanel), (short)0, a.KB * kBlockBytes, kBufferWord3);
   const int w_voff = lane * 16;
@@ -87,24 +116,24 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.x) + (size_t)m0 * a.ldx, (short)0,
       (int)((int64_t)rows_left * a.ldx * 2), kBufferWord3);
-  const int x_voff = ((lane & 31) * (int)a.ldx + wave * 16 + (lane >> 5) * 8) * 2;
-  const int x_rowstep = 32 * (int)a.ldx * 2;
+  // Load slot p = lane of an instruction: row (lane/4) of 16, stored chunk
+  // lane%4 holding logical chunk (lane%4) ^ ((row >> 2) & 3).
+  const int x_rowstep = 16 * (int)a.ldx * 2;
+  const int x_voff =
+      (((lane >> 2) + wave * 64) * (int)a.ldx + (((lane & 3) ^ ((lane >> 4) & 3)) * 8)) * 2;
 
-  auto dma_issue = [&](int kb, int buf) {
-    uint8_t* st = smem + buf * kStageBytes;
-    if (MODE == 1 || wvalid) {
+  auto dma_issue = [&](int t, int buf) {
+    uint8_t* st = smem + buf * kStageBytes + (wave * 4) * kSubBytes;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wrsrc, (lds_ptr_t)(st + (wave * 8 + i) * kSubBytes),
-                                                 16, w_voff, kb * kBlockBytes + i * kSubBytes, 0,
-                                                 0);
-    }
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrsrc, (lds_ptr_t)(st + i * kSubBytes), 16, w_voff,
+                                               t * 8 * kSubBytes + i * kSubBytes, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
       // whole offset in the VGPR operand so the range check covers it
-      const int voff = x_voff + i * x_rowstep + kb * 128;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          xrsrc, (lds_ptr_t)(st + kXOff + (wave * 8 + i) * kSubBytes), 16, voff, 0, 0, 0);
+      const int voff = x_voff + i * x_rowstep + t * (kStageK * 2);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrsrc, (lds_ptr_t)(st + kXOff + i * kSubBytes), 16,
+                                               voff, 0, 0, 0);
     }
   };
 
@@ -116,64 +145,85 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // LDS byte offsets (within a stage) of the A operand i and B operand j of
-  // k quarter kq.
-  auto a_off = [&](int kq, int i) -> int {
-    if (MODE == 1) return (i >> 1) * kBlockBytes + (kq * 4 + wn * 2 + (i & 1)) * kSubBytes;
-    return wn * kBlockBytes + (kq * 4 + i) * kSubBytes;
+  // LDS byte offsets (within a stage, before the lane's own offset) of the
+  // A operand i and the B operand j of the stage's k quarter q (0, 1).
+  const int a_lane = lane * 16;
+  const int sw = ((lane & 31) >> 2) & 3;
+  const int b_lane[2] = {(lane & 31) * 64 + (((lane >> 5)) ^ sw) * 16,
+                         (lane & 31) * 64 + ((2 + (lane >> 5)) ^ sw) * 16};
+  auto a_off = [&](int q, int i) -> int {
+    if (MODE == 1) return (i >> 1) * 8 * kSubBytes + (q * 4 + wn * 2 + (i & 1)) * kSubBytes + a_lane;
+    return wn * 8 * kSubBytes + (q * 4 + i) * kSubBytes + a_lane;
   };
-  auto b_off = [&](int kq, int j) -> int { return kXOff + (kq * 8 + wm * 4 + j) * kSubBytes; };
+  auto b_off = [&](int q, int j) -> int { return kXOff + (wm * 128 + j * 32) * 64 + b_lane[q]; };
+  auto rd = [&](int buf, int off) {
+    return *reinterpret_cast<const bf16x8*>(smem + buf * kStageBytes + off);
+  };
 
-  if (MODE == 0 && !wvalid) {  // missing second block of an odd-NB GEMM: zeros
+  // Pipeline: every stage buffer starts free, so stages 0..kStages-1 are
+  // issued up front.  While stage t computes, the barrier for stage t+1
+  // sits between its two k quarters: after it, stage t's buffer is free for
+  // stage t + kStages and stage t+1's first operands are read during the
+  // MFMAs of stage t's second quarter.
+  const int T = a.KB * 2;  // stages
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        *reinterpret_cast<uint4*>(smem + s * kStageBytes + (wave * 8 + i) * kSubBytes + lane * 16) =
-            make_uint4(0, 0, 0, 0);
-  }
-  dma_issue(0, 0);
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's LDS DMA landed
+  for (int p = 0; p < kStages; ++p)
+    if (p < T) dma_issue(p, p);
+  wait_stages(min(kStages - 1, T - 1));
   __syncthreads();
 
-  for (int kb = 0; kb < a.KB; ++kb) {
-    const int cur = kb & 1;
-    if (kb + 1 < a.KB) dma_issue(kb + 1, cur ^ 1);
-    const uint8_t* st = smem + cur * kStageBytes + lane * 16;
-    auto rd = [&](int off) { return *reinterpret_cast<const bf16x8*>(st + off); };
-    // Operand schedule: the 8 operands of k quarter kq are in registers while
-    // the next quarter's 8 are read, one LDS read per two MFMAs.
-    bf16x8 acur[4], bcur[4], anxt[4], bnxt[4];
+  bf16x8 aq0[4], bq0[4], aq1[4], bq1[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bcur[j] = rd(b_off(0, j));
+  for (int j = 0; j < 4; ++j) bq0[j] = rd(0, b_off(0, j));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acur[i] = rd(a_off(0, i));
+  for (int i = 0; i < 4; ++i) aq0[i] = rd(0, a_off(0, i));
+
+  // One stage.  ISSUE: refill stage t's buffer with stage t + kStages.
+  // MORE: a stage t+1 follows (sync on it and prefetch its operands).
+  auto stage = [&](int t, auto ISSUE, auto MORE) {
+    constexpr bool kIssue = decltype(ISSUE)::value, kMore = decltype(MORE)::value;
+    const int buf = t % kStages;
+    // k quarter 0 of stage t; read quarter 1's operands meanwhile.
 #pragma unroll
-    for (int kq = 0; kq < 4; ++kq) {
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (kq < 3 && j == 0) bnxt[i] = rd(b_off(kq + 1, i));
-          if (kq < 3 && j == 2) anxt[i] = rd(a_off(kq + 1, i));
-          acc[i][j] = mfma32(acur[i], bcur[j], acc[i][j]);
-          if (kq < 3 && (j == 0 || j == 2)) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMAs
-          }
-        }
-      }
-      if (kq < 3) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          acur[q] = anxt[q];
-          bcur[q] = bnxt[q];
+      for (int j = 0; j < 4; ++j) {
+        if (j == 0) bq1[i] = rd(buf, b_off(1, i));
+        if (j == 2) aq1[i] = rd(buf, a_off(1, i));
+        acc[i][j] = mfma32(aq0[i], bq0[j], acc[i][j]);
+        if (j == 0 || j == 2) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMAs
         }
       }
     }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next stage landed
-    __syncthreads();
-  }
+    if constexpr (kMore) {
+      wait_lgkmcnt0();  // this wave's reads of stage t are complete
+      if constexpr (kIssue) wait_vmcnt<(kStages - 2) * kLoadsPerStage>();  // stage t+1 landed
+      else wait_stages(min(kStages - 2, T - 2 - t));
+      __syncthreads();  // ... for every wave; stage t's buffer is free
+      if constexpr (kIssue) dma_issue(t + kStages, buf);
+    }
+    const int nbuf = (t + 1) % kStages;
+    // k quarter 1 of stage t; read stage t+1's quarter-0 operands meanwhile.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (kMore && j == 0) bq0[i] = rd(nbuf, b_off(0, i));
+        if (kMore && j == 2) aq0[i] = rd(nbuf, a_off(0, i));
+        acc[i][j] = mfma32(aq1[i], bq1[j], acc[i][j]);
+        if (kMore && (j == 0 || j == 2)) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMAs
+        }
+      }
+    }
+  };
+  int t = 0;
+  for (; t + kStages < T; ++t) stage(t, std::true_type{}, std::true_type{});  // steady state
+  for (; t + 1 < T; ++t) stage(t, std::false_type{}, std::true_type{});       // drain
+  stage(t, std::false_type{}, std::false_type{});                             // last stage
 
   // ---- epilogue: lane holds m = base + lane%32, n = base + 8*(r/4) +
   // 4*(lane/32) + r%4 for its 16 values r of each 32 x 32 tile.
@@ -210,12 +260,12 @@ static hipError_t launch_t(const TileArgs& a, hipStream_t s) {
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       2 * kStageBytes);
+                                       kStages * kStageBytes);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
   dim3 grid(a.tiles_m * a.tiles_n), block(kThreads);
-  hipLaunchKernelGGL(fn, grid, block, 2 * kStageBytes, s, a);
+  hipLaunchKernelGGL(fn, grid, block, kStages * kStageBytes, s, a);
   return hipGetLastError();
 }
 
