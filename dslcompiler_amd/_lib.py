@@ -28,6 +28,7 @@ LLK_ERR_NOT_FOUND = -11
 
 LLK_BF16, LLK_FP16, LLK_FP32 = 0, 1, 2
 LLK_PACK_KEEP_HOST = 1
+LLK_PACK_HOST_ONLY = 2
 
 STATUS_NAMES = {
     0: "LLK_OK", -1: "LLK_ERR_INVALID_ARGUMENT", -2: "LLK_ERR_SHAPE", -3: "LLK_ERR_DTYPE",

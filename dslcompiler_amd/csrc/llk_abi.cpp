@@ -309,17 +309,24 @@ int llk_pack_weights(const llk_tensor2d* w, int64_t bk, unsigned flags,
   *out = nullptr;
   int rc = check_weight_input(w, bk);
   if (rc) return rc;
-  int dev;
-  rc = current_device(&dev);
-  if (rc) return rc;
+  const bool host_only = (flags & LLK_PACK_HOST_ONLY) != 0;
+  int dev = -1;
+  if (!host_only) {
+    rc = current_device(&dev);
+    if (rc) return rc;
+  }
   auto* pw = new (std::nothrow) llk_packed_weights();
   if (!pw) return fail(LLK_ERR_OUT_OF_MEMORY, "handle allocation");
   fill_meta(pw, w->dim0, w->dim1, bk);
   const uint16_t* src = static_cast<const uint16_t*>(w->data);
   try {
-    if (flags & LLK_PACK_KEEP_HOST) {
+    if (flags & (LLK_PACK_KEEP_HOST | LLK_PACK_HOST_ONLY)) {
       pw->host.resize(static_cast<size_t>(pw->K_blocks * bk * pw->N));
       if (!pw->host.empty()) llk::packReferenceLayout(src, pw->K, pw->N, w->stride0, bk, pw->host.data());
+    }
+    if (host_only) {
+      *out = pw;
+      return LLK_OK;
     }
     pw->dev_bytes = llk::deviceLayoutBytes(pw->K, pw->N);
     if (pw->dev_bytes == 0) {
@@ -396,15 +403,22 @@ int llk_repack(llk_packed_weights* pw, const llk_tensor2d* w) {
     return fail(LLK_ERR_SHAPE, "repack shape (%lld, %lld) differs from packed (%lld, %lld)",
                 (long long)w->dim0, (long long)w->dim1, (long long)pw->K, (long long)pw->N);
   llk_packed_weights* fresh = nullptr;
+  // A host-only handle repacks on the host; a device handle repacks on the
+  // device it was packed for.
+  const bool on_device = pw->dev != nullptr;
   int dev_saved = 0;
-  hipError_t e = hipGetDevice(&dev_saved);
-  if (e != hipSuccess) return fail_hip(e, "hipGetDevice");
-  if (pw->device >= 0 && pw->device != dev_saved) {
-    e = hipSetDevice(pw->device);
-    if (e != hipSuccess) return fail_hip(e, "hipSetDevice");
+  if (on_device) {
+    hipError_t e = hipGetDevice(&dev_saved);
+    if (e != hipSuccess) return fail_hip(e, "hipGetDevice");
+    if (pw->device != dev_saved) {
+      e = hipSetDevice(pw->device);
+      if (e != hipSuccess) return fail_hip(e, "hipSetDevice");
+    }
   }
-  rc = llk_pack_weights(w, pw->BK, pw->host.empty() ? 0u : LLK_PACK_KEEP_HOST, &fresh);
-  if (pw->device >= 0 && pw->device != dev_saved) (void)hipSetDevice(dev_saved);
+  const unsigned fl =
+      on_device ? (pw->host.empty() ? 0u : LLK_PACK_KEEP_HOST) : LLK_PACK_HOST_ONLY;
+  rc = llk_pack_weights(w, pw->BK, fl, &fresh);
+  if (on_device && pw->device != dev_saved) (void)hipSetDevice(dev_saved);
   if (rc) return rc;
   if (pw->dev) (void)hipFree(pw->dev);
   pw->host.swap(fresh->host);

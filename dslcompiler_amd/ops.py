@@ -19,8 +19,8 @@ import ctypes as C
 import numpy as np
 
 from . import _lib
-from ._lib import (LLK_BF16, LLK_FP32, LLK_PACK_KEEP_HOST, KernelContext, check, lib,
-                   tensor2d)
+from ._lib import (LLK_BF16, LLK_FP32, LLK_PACK_HOST_ONLY, LLK_PACK_KEEP_HOST, KernelContext,
+                   check, lib, tensor2d)
 
 
 def _torch():
@@ -69,15 +69,19 @@ class PackedWeights:
 
     # -- construction -------------------------------------------------------
     @classmethod
-    def from_host(cls, w: np.ndarray, bk: int = 64, keep_host: bool = False) -> "PackedWeights":
-        """packWeightMatrix from a host bf16 matrix given as uint16 bits."""
-        w = np.ascontiguousarray(w, dtype=np.uint16)
+    def from_host(cls, w: np.ndarray, bk: int = 64, keep_host: bool = False,
+                  host_only: bool = False) -> "PackedWeights":
+        """packWeightMatrix from a host bf16 matrix given as uint16 bits.
+        host_only: the reference's host packer alone (no device payload)."""
+        w = np.asarray(w, dtype=np.uint16)
         if w.ndim != 2:
             raise ValueError("w must be 2-D")
-        t = tensor2d(w.ctypes.data, w.shape[0], w.shape[1])
+        if w.strides[1] != 2:
+            w = np.ascontiguousarray(w)
+        t = tensor2d(w.ctypes.data, w.shape[0], w.shape[1], w.strides[0] // 2)
+        flags = (LLK_PACK_KEEP_HOST if keep_host else 0) | (LLK_PACK_HOST_ONLY if host_only else 0)
         out = C.c_void_p()
-        check(lib().llk_pack_weights(C.byref(t), bk, LLK_PACK_KEEP_HOST if keep_host else 0,
-                                     C.byref(out)))
+        check(lib().llk_pack_weights(C.byref(t), bk, flags, C.byref(out)))
         return cls(out.value)
 
     @classmethod

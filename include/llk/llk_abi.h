@@ -100,6 +100,9 @@ int llk_device_info(char* arch_name, int cap, int* cu_count, int* lds_bytes,
 
 /* Pack flags. */
 #define LLK_PACK_KEEP_HOST 1u /* also keep the reference host layout       */
+#define LLK_PACK_HOST_ONLY 2u /* host layout only: no device payload, no
+                                 HIP call (the reference's host-only packer);
+                                 kernels reject such a handle            */
 
 /* packWeightMatrix (PackedWeights.cpp:5-33).  `w` is a bf16 [K, N] matrix in
  * HOST memory (stride1 == 1).  Metadata follows the reference exactly:
