@@ -1,10 +1,13 @@
 """Benchmark of the fused SwiGLU hot path on one MI355X (BASELINE.json metric).
 
-Headline workload (value): prefill fused SwiGLU, M=2048, K=4096, N=11008,
-bf16 inputs, fp32 accumulation, bf16 output -> TFLOP/s (4*M*K*N per step).
-One step = one llk_swiglu_bf16 call over the resident inputs.  Also reported
-("extra"): the decode shape M=8, K=4096, N=14336 in HBM GB/s with rotated
-weight copies (so the 256 MB MALL cannot hold them), and the 4096^3 GEMM.
+Headline (value): prefill fused SwiGLU, M=2048, K=4096, N=11008 (BASELINE
+config 3), bf16 inputs, fp32 accumulation, bf16 output, in TFLOP/s with
+4*M*K*N flops per step.  One step = one llk_swiglu_bf16 call over inputs
+already resident in HBM; the average launch time comes from HIP events on
+the launch stream.  Reported in "extra": decode SwiGLU (config 4,
+M in {1, 8, 16}, K=4096, N=14336) in HBM GB/s with weights rotated over four
+copies (940 MB, beyond the 256 MB MALL); the 4096^3 GEMM (config 2); the
+MLP block (config 5) over its ragged M sweep.
 
 Prints ONE JSON line.  --gpus N with N > 1 exits: this path runs on one GPU.
 """
@@ -13,6 +16,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -23,18 +27,19 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 sys.path.insert(0, str(ROOT / "tests"))
 
-PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
-PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (published)
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E (published)
+PROFILE = ROOT / "profiles" / "swiglu_prefill_2048x4096x11008.md"
 
 PREFILL = dict(M=2048, K=4096, N=11008)
-DECODE = dict(M=8, K=4096, N=14336)
-GEMM = dict(M=4096, K=4096, N=4096)
+DECODE = dict(K=4096, N=14336)
+MLP = dict(K=5120, N=13824)
 
 
 def _time_loop(torch, fn, steps: int, warmup: int) -> float:
-    """Average ms per call measured with HIP events on the launch stream."""
-    for _ in range(warmup):
-        fn(0)
+    """Average ms per call, HIP events on the launch (current) stream."""
+    for i in range(warmup):
+        fn(i)
     torch.cuda.synchronize()
     s = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -58,66 +63,84 @@ def bench_prefill(torch, llk, steps, warmup):
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     ms = _time_loop(torch, lambda i: llk.fused_swiglu(xd, pg, pu, out=y), steps, warmup)
     flops = 4.0 * M * K * N
-    return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, flops=flops,
-                inputs=(x, wg, wu), y=y, packed=(pg, pu))
+    return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, inputs=(x, wg, wu), y=y)
 
 
-def bench_decode(torch, llk, steps, warmup, copies=4):
-    M, K, N = DECODE["M"], DECODE["K"], DECODE["N"]
+def _rand_w(torch, g, K, N):
+    return (torch.randn((K, N), generator=g, device="cuda") / np.sqrt(K)).to(torch.bfloat16)
+
+
+def bench_decode(torch, llk, M, steps, warmup, copies=4):
+    K, N = DECODE["K"], DECODE["N"]
     g = torch.Generator(device="cuda")
     g.manual_seed(42)
-    sets = []
-    for c in range(copies):  # distinct weights, 235 MB per set: > MALL
-        wg = (torch.randn((K, N), generator=g, device="cuda") / np.sqrt(K)).to(torch.bfloat16)
-        wu = (torch.randn((K, N), generator=g, device="cuda") / np.sqrt(K)).to(torch.bfloat16)
-        sets.append((llk.PackedWeights.from_device(wg), llk.PackedWeights.from_device(wu)))
-        del wg, wu
+    sets = [(llk.PackedWeights.from_device(_rand_w(torch, g, K, N)),
+             llk.PackedWeights.from_device(_rand_w(torch, g, K, N))) for _ in range(copies)]
     x = torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-    ms = _time_loop(torch, lambda i: llk.fused_swiglu(x, *sets[i % copies], out=y), steps,
-                    warmup)
+    ms = _time_loop(torch, lambda i: llk.fused_swiglu(x, *sets[i % copies], out=y), steps, warmup)
     nbytes = 2.0 * K * N * 2 + M * K * 2 + M * N * 2
-    return dict(ms=ms, gbs=nbytes / (ms * 1e-3) / 1e9, bytes=nbytes)
+    return dict(ms=ms, gbs=nbytes / (ms * 1e-3) / 1e9)
 
 
 def bench_gemm(torch, llk, steps, warmup):
-    M, K, N = GEMM["M"], GEMM["K"], GEMM["N"]
+    n = 4096
     g = torch.Generator(device="cuda")
     g.manual_seed(42)
-    a = (torch.randn((M, K), generator=g, device="cuda") / np.sqrt(K)).to(torch.bfloat16)
-    b = (torch.randn((K, N), generator=g, device="cuda") / np.sqrt(K)).to(torch.bfloat16)
-    pb = llk.PackedWeights.from_device(b)
-    c = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    a = _rand_w(torch, g, n, n)
+    pb = llk.PackedWeights.from_device(_rand_w(torch, g, n, n))
+    c = torch.empty((n, n), dtype=torch.float32, device="cuda")
     ms = _time_loop(torch, lambda i: llk.matmul(a, pb, out=c), steps, warmup)
-    return dict(ms=ms, tflops=2.0 * M * N * K / (ms * 1e-3) / 1e12)
+    return dict(ms=ms, tflops=2.0 * n ** 3 / (ms * 1e-3) / 1e12)
+
+
+def bench_mlp(torch, llk, steps, warmup):
+    """Config 5: Y = SwiGLU(X; K=5120, N=13824), Z = Y Wd; per M: us, TFLOP/s
+    (6*M*K*N) and GB/s over the compulsory bytes (weights + X + Y twice + Z)."""
+    K, N = MLP["K"], MLP["N"]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(42)
+    pg = llk.PackedWeights.from_device(_rand_w(torch, g, K, N))
+    pu = llk.PackedWeights.from_device(_rand_w(torch, g, K, N))
+    pd = llk.PackedWeights.from_device(_rand_w(torch, g, N, K))
+    out = {}
+    for M in (1, 17, 255, 1000, 4097):
+        x = torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        z = torch.empty((M, K), dtype=torch.bfloat16, device="cuda")
+        ms = _time_loop(torch, lambda i: llk.mlp(x, pg, pu, pd, y=y, z=z), max(5, steps // 2),
+                        warmup)
+        nbytes = 3.0 * K * N * 2 + M * K * 2 * 2 + M * N * 2 * 2
+        out[f"M{M}"] = {"us": round(ms * 1e3, 1),
+                        "tflops": round(6.0 * M * K * N / (ms * 1e-3) / 1e12, 1),
+                        "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    return out
 
 
 def cpu_baseline(x, wg, wu, budget_s: float = 12.0):
     """The oracle's AVX2 restatement of the reference fused kernel on a bounded
-    sample of the headline workload: the first `rows` rows of X (full K, N),
-    repeated for about `budget_s` seconds; best rate reported."""
+    sample of the headline workload: the first `rows` rows of X (full K and
+    N), best of up to 5 runs within about `budget_s` seconds."""
     import oracle
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     threads = max(1, min(threads, os.cpu_count() or 1))
     K, N = wg.shape
-    rows = 32  # one BM tile row
     t0 = time.perf_counter()
-    oracle.swiglu_avx2(x[:rows], wg, wu, threads)  # warm-up + estimate
+    oracle.swiglu_avx2(x[:32], wg, wu, threads)  # warm-up + estimate
     est = time.perf_counter() - t0
     rows = int(min(x.shape[0], max(32, 32 * round(budget_s / 3 / max(est, 1e-3)))))
     rows -= rows % 32
-    best = 0.0
+    best, reps = 0.0, 0
     t_end = time.perf_counter() + budget_s
-    reps = 0
     while reps < 1 or (time.perf_counter() < t_end and reps < 5):
         t = time.perf_counter()
         oracle.swiglu_avx2(x[:rows], wg, wu, threads)
-        dt = time.perf_counter() - t
-        best = max(best, 4.0 * rows * K * N / dt / 1e12)
+        best = max(best, 4.0 * rows * K * N / (time.perf_counter() - t) / 1e12)
         reps += 1
     return {"value": round(best, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"fused SwiGLU rows 0..{rows - 1} of M=2048 (K=4096, N=11008), "
-                      f"best of {reps} runs, AVX2 BM32/BN64/BK64/VM4/VN8 tiles"}
+            "sample": f"fused SwiGLU rows 0..{rows - 1} of M=2048 (K=4096, N=11008), best of "
+                      f"{reps} runs; AVX2 BM32/BN64/BK64/VM4/VN8 tiles, ThreadPool-style "
+                      f"dynamic tile queue"}
 
 
 def spot_parity(x, wg, wu, y_dev):
@@ -131,6 +154,15 @@ def spot_parity(x, wg, wu, y_dev):
     return parity(bf16_bits_to_f32(got), bf16_bits_to_f32(yb_ref))
 
 
+def profiled_traffic():
+    """HBM bytes per launch of the prefill kernel from the committed rocprofv3
+    summary (FETCH_SIZE and WRITE_SIZE, scaled by the copy-kernel factors)."""
+    if not PROFILE.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", PROFILE.read_text())
+    return float(m.group(1)) if m else None
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -138,6 +170,10 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--only", choices=["prefill", "decode8", "gemm", "mlp", "copy"],
+                    help="run one workload for --steps launches and print its timing only "
+                         "(for profiler runs); 'copy' is a 256 MiB device copy used to "
+                         "calibrate byte counters")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this hot path runs on one GPU; multi-GPU runs are not part of this "
@@ -148,20 +184,35 @@ def main() -> None:
     import dslcompiler_amd as llk
     torch.cuda.set_device(0)
 
+    if a.only:
+        if a.only == "prefill":
+            r = {"ms": bench_prefill(torch, llk, a.steps, a.warmup)["ms"]}
+        elif a.only == "decode8":
+            r = bench_decode(torch, llk, 8, a.steps, a.warmup)
+        elif a.only == "gemm":
+            r = bench_gemm(torch, llk, a.steps, a.warmup)
+        elif a.only == "mlp":
+            r = bench_mlp(torch, llk, a.steps, a.warmup)
+        else:
+            src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+            dst = torch.empty_like(src)
+            r = {"ms": _time_loop(torch, lambda i: dst.copy_(src), a.steps, a.warmup)}
+        print(json.dumps({"only": a.only, **r}), flush=True)
+        return
+
     pre = bench_prefill(torch, llk, a.steps, a.warmup)
     x, wg, wu = pre["inputs"]
     par = spot_parity(x, wg, wu, pre["y"])
     extra = {"prefill_parity_rows": {k: round(v, 6) for k, v in par.items()}}
     if not a.no_extra:
-        dec = bench_decode(torch, llk, a.steps, a.warmup)
+        for M in (1, 8, 16):
+            d = bench_decode(torch, llk, M, a.steps, a.warmup)
+            extra[f"decode_m{M}"] = {"us": round(d["ms"] * 1e3, 2), "gbs": round(d["gbs"], 1),
+                                     "hbm_frac": round(d["gbs"] / PEAK_HBM_GBS, 4)}
         gem = bench_gemm(torch, llk, max(10, a.steps // 2), a.warmup)
-        extra.update({
-            "decode_m8_gbs": round(dec["gbs"], 1),
-            "decode_m8_us": round(dec["ms"] * 1e3, 2),
-            "decode_m8_hbm_frac": round(dec["gbs"] / PEAK_HBM_GBS, 4),
-            "gemm_4096_tflops": round(gem["tflops"], 1),
-            "gemm_4096_mfma_frac": round(gem["tflops"] / PEAK_BF16_TFLOPS, 4),
-        })
+        extra["gemm_4096"] = {"us": round(gem["ms"] * 1e3, 1), "tflops": round(gem["tflops"], 1),
+                              "mfma_frac": round(gem["tflops"] / PEAK_BF16_TFLOPS, 4)}
+        extra["mlp_k5120_n13824"] = bench_mlp(torch, llk, a.steps, a.warmup)
     cpu = None if a.no_cpu_baseline else cpu_baseline(x, wg, wu)
 
     achieved = pre["tflops"]
@@ -178,11 +229,12 @@ def main() -> None:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (splitmix64/Box-Muller seed 42; X~N(0,1), W~N(0,1/sqrt(K)))",
-        "config": {"workload": "prefill fused SwiGLU M=2048 K=4096 N=11008, bf16 out",
+        "config": {"workload": "prefill fused SwiGLU M=2048 K=4096 N=11008, bf16 out "
+                               "(BASELINE config 3)",
                    "M": 2048, "K": 4096, "N": 11008, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": profiled_traffic()},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -112,10 +112,11 @@ def assert_parity(got, want, what: str = "") -> dict:
 # A bf16 result may differ from the oracle's RNE(fp32) by one ulp where the
 # oracle's fp32 value lies within this relative distance of the midpoint
 # between two bf16 neighbours: fp32 sums taken in a different order differ by
-# ~1e-6 relative, so such elements round either way.  At most this fraction
-# of elements may be boundary flips.
+# ~1e-6 relative (more for long reductions: K = 13824 in config 5), so such
+# elements round either way.  At most this fraction of elements may be
+# boundary flips; each one is verified individually.
 FLIP_MIDPOINT_REL = 1e-4
-FLIP_MAX_FRACTION = 1e-3
+FLIP_MAX_FRACTION = 1e-2
 
 
 def assert_parity_bf16(got_bits: np.ndarray, ref_f32: np.ndarray, what: str = "") -> dict:

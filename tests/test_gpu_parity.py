@@ -370,3 +370,34 @@ def test_errors(llk, gpu):
     with pytest.raises(llk.LLKError, match="LLK_ERR_SCRATCH"):
         llk.fused_swiglu(gpu.zeros((4, 1024), dtype=gpu.bfloat16, device="cuda"), big, big,
                          scratch=gpu.zeros(4, dtype=gpu.uint8, device="cuda"))
+
+
+GOLDEN = __import__("pathlib").Path(__file__).resolve().parent / "golden"
+
+
+@pytest.mark.parametrize("shape", [(32, 128, 256), (16, 512, 512), (32, 256, 127), (4, 8, 3)])
+def test_golden_reference_inputs_on_gpu(llk, gpu, orc, shape):
+    """The reference tests' own inputs (tests/golden, reproduced from their
+    mt19937 streams): the kernel's fp32 result against the reference's own
+    fp64 routine and against the oracle; bf16 result = RNE of it."""
+    print(f"case golden {shape}", flush=True)
+    g = np.load(GOLDEN / "ref_vectors.npz")
+    M, N, K = shape
+    t = f"vec_M{M}_N{N}_K{K}"
+    x, wg, wu, y64 = g[t + "_x"], g[t + "_wg"], g[t + "_wu"], g[t + "_y_fp64"]
+    yf = _run_swiglu(llk, gpu, x, wg, wu, gpu.float32)
+    p = parity(yf, y64)
+    assert p["rel_l2"] < 2e-6 and p["max_abs_over_rms"] < 2e-5, p
+    yf_ref, _ = orc.swiglu(x, wg, wu)
+    assert_parity(yf, yf_ref, f"golden {shape}")
+
+
+def test_golden_config1_samples_on_gpu(llk, gpu):
+    """BASELINE config 1 through the GPU against the committed oracle samples."""
+    print("case golden config1", flush=True)
+    s = np.load(GOLDEN / "config1_samples.npz")
+    x, wg, wu = swiglu_inputs(64, 512, 1376, seed=42)
+    yf = _run_swiglu(llk, gpu, x, wg, wu, gpu.float32).ravel()[s["index"]]
+    yb = _run_swiglu(llk, gpu, x, wg, wu, gpu.bfloat16).ravel()[s["index"]]
+    assert_parity(yf, s["y_fp32"], "config1 samples fp32")
+    assert np.mean(yb == s["y_bf16"]) > 0.99
