@@ -42,6 +42,12 @@ struct TileArgs {
   int KB;              // K_pad / 64
   int NB;              // N_pad / 128 (packed n-blocks)
   int tiles_m, tiles_n;
+  // k split across workgroups (S > 1): workgroup (tile, s) covers the 64-k
+  // blocks [s * kbs, min(KB, (s + 1) * kbs)) and writes its raw fp32
+  // accumulators to part[s][mat][M][n_pad]; split_reduce_kernel adds them
+  // in split order and applies the epilogue.
+  float* part;
+  int S, kbs, n_pad;
 };
 
 constexpr int kThreads = 256;
@@ -71,7 +77,8 @@ __device__ __forceinline__ void wait_stages(int ahead) {
 // MODE 0: GEMM (C = X W);  MODE 1: fused SwiGLU.
 // OUT_BF16: store bf16 (RNE) instead of fp32.
 // YVEC: Y rows allow a 4-element vector store (aligned base, ldy % 4 == 0).
-template <int MODE, bool OUT_BF16, bool YVEC>
+// SPLIT: store raw fp32 partial accumulators of k split s (see TileArgs).
+template <int MODE, bool OUT_BF16, bool YVEC, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
@@ -80,11 +87,18 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   const int wm = wave & 1;
   const int wn = wave >> 1;
 
-  const int total = a.tiles_m * a.tiles_n;
-  const int tile = xcd_remap(blockIdx.x, total);
-  const int tm = tile % a.tiles_m;  // m fastest: tiles sharing W columns
-  const int tn = tile / a.tiles_m;  // run together on one XCD
+  // Workgroup -> (split s, tile): tiles of one split are contiguous, so
+  // after the XCD remap the tiles that share X's k slice (and, m fastest,
+  // the tiles that share W columns) run on one XCD.
+  const int tiles = a.tiles_m * a.tiles_n;
+  const int idx = xcd_remap(blockIdx.x, tiles * (SPLIT ? a.S : 1));
+  const int split = SPLIT ? idx / tiles : 0;
+  const int tile = SPLIT ? idx - split * tiles : idx;
+  const int tm = tile % a.tiles_m;
+  const int tn = tile / a.tiles_m;
   const int m0 = tm * kTileM;
+  const int kb0 = SPLIT ? split * a.kbs : 0;
+  const int nkb = SPLIT ? min(a.KB - kb0, a.kbs) : a.KB;
 
   // ---- operand streams ----------------------------------------------------
   // Stage t holds k range [32 t, 32 t + 32).
@@ -106,16 +120,17 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
     const int nb = 2 * tn + wslot;
     wpanel = a.w0 + (size_t)(nb < a.NB ? nb : 0) * a.KB * kBlockBytes;
   }
-  wpanel += (wave & 1) * 4 * kSubBytes;
+  wpanel += (size_t)kb0 * kBlockBytes + (wave & 1) * 4 * kSubBytes;
   const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(wpanel), (short)0, a.KB * kBlockBytes, kBufferWord3);
+      const_cast<uint8_t*>(wpanel), (short)0, nkb * kBlockBytes, kBufferWord3);
   const int w_voff = lane * 16;
 
-  // The X resource starts at row m0 and ends at row M: rows >= M read zero.
+  // The X resource starts at row m0, column 64 kb0, and ends at row M:
+  // rows >= M read zero.
   const int rows_left = a.M - m0;
   const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(a.x) + (size_t)m0 * a.ldx, (short)0,
-      (int)((int64_t)rows_left * a.ldx * 2), kBufferWord3);
+      const_cast<uint16_t*>(a.x) + (size_t)m0 * a.ldx + (size_t)kb0 * 64, (short)0,
+      (int)((int64_t)rows_left * a.ldx * 2 - (int64_t)kb0 * 128), kBufferWord3);
   // Load slot p = lane of an instruction: row (lane/4) of 16, stored chunk
   // lane%4 holding logical chunk (lane%4) ^ ((row >> 2) & 3).
   const int x_rowstep = 16 * (int)a.ldx * 2;
@@ -165,7 +180,7 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   // sits between its two k quarters: after it, stage t's buffer is free for
   // stage t + kStages and stage t+1's first operands are read during the
   // MFMAs of stage t's second quarter.
-  const int T = a.KB * 2;  // stages
+  const int T = nkb * 2;  // stages
 #pragma unroll
   for (int p = 0; p < kStages; ++p)
     if (p < T) dma_issue(p, p);
@@ -229,6 +244,29 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   // 4*(lane/32) + r%4 for its 16 values r of each 32 x 32 tile.
   const int h4 = 4 * (lane >> 5);
   const int mr = lane & 31;
+  if constexpr (SPLIT) {
+    constexpr int NMAT = (MODE == 1) ? 2 : 1;
+    const size_t plane = (size_t)a.M * a.n_pad;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // SwiGLU: i < 2 gate, i >= 2 up (same n); GEMM: four n sub-tiles.
+      const int mat = (MODE == 1) ? (i >> 1) : 0;
+      float* dst = a.part + ((size_t)split * NMAT + mat) * plane;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = m0 + wm * 128 + j * 32 + mr;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = (MODE == 1) ? (tn * 128 + wn * 64 + (i & 1) * 32 + 8 * g + h4)
+                                    : (tn * 256 + wn * 128 + i * 32 + 8 * g + h4);
+          const float v[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                              acc[i][j][4 * g + 3]};
+          store4<false>(dst, a.n_pad, a.M, a.n_pad, m, n, v, true);
+        }
+      }
+    }
+    return;
+  }
   constexpr int NI = (MODE == 1) ? 2 : 4;
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
@@ -250,12 +288,38 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   }
 }
 
+// Sums the S partial planes of each output element in split order (fixed,
+// so results are reproducible) and applies the epilogue.  One thread per
+// 4 consecutive n of a row.
+template <int MODE, bool OUT_BF16, bool YVEC>
+__global__ __launch_bounds__(256) void split_reduce_kernel(TileArgs a) {
+  constexpr int NMAT = (MODE == 1) ? 2 : 1;
+  const int quads = (a.N + 3) / 4;
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= (int64_t)a.M * quads) return;
+  const int m = (int)(e / quads);
+  const int n = (int)(e - (int64_t)m * quads) * 4;
+  const size_t plane = (size_t)a.M * a.n_pad;
+  const float* src = a.part + (size_t)m * a.n_pad + n;
+  f32x4 sum[NMAT];
+#pragma unroll
+  for (int p = 0; p < NMAT; ++p) sum[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < a.S; ++sp)
+#pragma unroll
+    for (int p = 0; p < NMAT; ++p)
+      sum[p] += *reinterpret_cast<const f32x4*>(src + ((size_t)sp * NMAT + p) * plane);
+  float v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) v[q] = (MODE == 1) ? swiglu_act(sum[0][q], sum[1][q]) : sum[0][q];
+  store4<OUT_BF16>(a.y, a.ldy, a.M, a.N, m, n, v, YVEC);
+}
+
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-template <int MODE, bool OUT_BF16, bool YVEC>
-static hipError_t launch_t(const TileArgs& a, hipStream_t s) {
-  auto fn = mfma_tile_kernel<MODE, OUT_BF16, YVEC>;
+template <int MODE, bool OUT_BF16, bool YVEC, bool SPLIT>
+static hipError_t launch_tile_t(const TileArgs& a, hipStream_t s) {
+  auto fn = mfma_tile_kernel<MODE, OUT_BF16, YVEC, SPLIT>;
   static bool attr_set = false;  // per instantiation; benign race (idempotent)
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -264,8 +328,20 @@ static hipError_t launch_t(const TileArgs& a, hipStream_t s) {
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  dim3 grid(a.tiles_m * a.tiles_n), block(kThreads);
+  dim3 grid(a.tiles_m * a.tiles_n * (SPLIT ? a.S : 1)), block(kThreads);
   hipLaunchKernelGGL(fn, grid, block, kStages * kStageBytes, s, a);
+  return hipGetLastError();
+}
+
+template <int MODE, bool OUT_BF16, bool YVEC>
+static hipError_t launch_t(const TileArgs& a, hipStream_t s) {
+  if (a.S <= 1) return launch_tile_t<MODE, OUT_BF16, YVEC, false>(a, s);
+  // Partials are fp32 planes with 16-byte aligned rows: one instantiation.
+  hipError_t e = launch_tile_t<MODE, false, true, true>(a, s);
+  if (e != hipSuccess) return e;
+  const int64_t threads = (int64_t)a.M * ((a.N + 3) / 4);
+  hipLaunchKernelGGL((split_reduce_kernel<MODE, OUT_BF16, YVEC>),
+                     dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -284,11 +360,20 @@ bool llk_tile_x_fits(int M, int64_t ldx) {
   return rows * ldx * 2 < ((int64_t)1 << 31);
 }
 
+// Bytes of the partial planes of a k split over S workgroups (0 if S <= 1).
+size_t llk_tile_split_bytes(int mode, int M, int NB, int S) {
+  if (S <= 1) return 0;
+  return (size_t)S * (mode == 1 ? 2 : 1) * M * NB * 128 * sizeof(float);
+}
+
 // Internal (not part of the C ABI).  x: [M, 64*KB] bf16 with ldx % 8 == 0,
 // 16-byte aligned, columns >= K zero; llk_tile_x_fits(M, ldx) must hold.
+// S > 1 splits K over S workgroups of kbs = ceil(KB / S) blocks (every split
+// non-empty: the caller guarantees (S - 1) * kbs < KB); `part` (16-byte
+// aligned) holds llk_tile_split_bytes(mode, M, NB, S) bytes.
 hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                            const void* w1, void* y, int64_t ldy, int M, int N, int KB, int NB,
-                           bool out_bf16, bool yvec, hipStream_t s) {
+                           int S, void* part, bool out_bf16, bool yvec, hipStream_t s) {
   using namespace llk_gfx950;
   TileArgs a;
   a.x = x;
@@ -303,6 +388,11 @@ hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void*
   a.NB = NB;
   a.tiles_m = (M + kTileM - 1) / kTileM;
   a.tiles_n = mode == 1 ? NB : (NB + 1) / 2;
+  a.S = S > 1 ? S : 1;
+  a.kbs = (KB + a.S - 1) / a.S;
+  a.n_pad = NB * 128;
+  a.part = static_cast<float*>(part);
+  if (a.S > 1 && (part == nullptr || (int64_t)(a.S - 1) * a.kbs >= KB)) return hipErrorInvalidValue;
   if (mode == 1) return launch_mode<1>(a, out_bf16, yvec, s);
   return launch_mode<0>(a, out_bf16, yvec, s);
 }

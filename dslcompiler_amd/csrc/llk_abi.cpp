@@ -23,7 +23,8 @@
 // Kernel launchers (kernels/*.hip).
 hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                            const void* w1, void* y, int64_t ldy, int M, int N, int KB, int NB,
-                           bool out_bf16, bool yvec, hipStream_t s);
+                           int S, void* part, bool out_bf16, bool yvec, hipStream_t s);
+size_t llk_tile_split_bytes(int mode, int M, int NB, int S);
 bool llk_tile_x_fits(int M, int64_t ldx);
 hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                              const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
@@ -189,12 +190,43 @@ hipStream_t stream_of(const llk_kernel_context* ctx) {
 // Launch plan of one contraction (SwiGLU: nmat 2, GEMM: nmat 1).
 struct Plan {
   bool skinny = false;   // small-M bandwidth kernel
-  int S = 1;             // its k splits across workgroups
+  int S = 1;             // k splits across workgroups (either kernel)
   bool pad = false;      // tile path: copy X into a padded buffer first
   int64_t chunk = 0;     // tile path: rows per launch (32-bit X offsets)
   int64_t ld = 0;        // tile path: row stride of the X the kernel reads
+  size_t pad_bytes = 0;  // tile path: padded X at the start of the workspace
   size_t ws_bytes = 0;   // workspace the plan needs
 };
+
+// k splits of the tile kernel for `rows` rows: the S that minimises the
+// modelled time  waves(S) * (ceil(KB / S) + 2) + partial traffic  in units
+// of one 64-k step of a full wave of workgroups (about 2.06 us on MI355X:
+// a 256 x 256 tile over K = 4096 takes 132 us).  waves(S) = ceil(tiles * S /
+// tile_wgs_per_wave); the "+ 2" is the per-workgroup pipeline fill and
+// epilogue; the S partial planes (S * nmat * rows * N_pad fp32) are written
+// and read back at ~4 TB/s, plus one step for the reduce launch.
+int tile_splits(int nmat, int64_t rows, int64_t KB, int64_t NB) {
+  const int64_t forced = llk::tunable("tile_splits");
+  const int64_t min_kb = std::max<int64_t>(1, llk::tunable("tile_min_kb"));
+  int64_t smax = std::min<int64_t>(64, std::max<int64_t>(1, KB / min_kb));
+  if (forced > 0) smax = std::min(forced, KB);
+  const int64_t tiles = (rows + 255) / 256 * (nmat == 2 ? NB : (NB + 1) / 2);
+  const int64_t per_wave = std::max<int64_t>(1, llk::tunable("tile_wgs_per_wave"));
+  int64_t best_s = 1;
+  double best = 0.0;
+  for (int64_t S = forced > 0 ? smax : 1; S <= smax; ++S) {
+    const int64_t kbs = (KB + S - 1) / S;
+    const int64_t s_eff = (KB + kbs - 1) / kbs;  // no empty splits
+    const double waves = (double)((tiles * s_eff + per_wave - 1) / per_wave);
+    double cost = waves * (double)(kbs + 2);
+    if (s_eff > 1) cost += 2.0 * s_eff * nmat * rows * NB * 128 * 4 / (4e12 * 2.06e-6) + 1.0;
+    if (S == 1 || forced > 0 || cost < best) {
+      best = cost;
+      best_s = s_eff;
+    }
+  }
+  return (int)best_s;
+}
 
 // x == nullptr: plan for the worst case (X needs padding).
 Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const llk_tensor2d* x) {
@@ -219,7 +251,10 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
   p.chunk = M;
   if (!llk_tile_x_fits((int)std::min<int64_t>(M, kMaxDim), p.ld))
     p.chunk = std::max<int64_t>(256, (((int64_t)1 << 31) - 1) / (p.ld * 2) / 256 * 256 - 256);
-  if (p.pad) p.ws_bytes = (size_t)std::min(p.chunk, M) * p.ld * 2;
+  const int64_t rows = std::min(p.chunk, M);
+  if (p.pad) p.pad_bytes = ((size_t)rows * p.ld * 2 + 255) / 256 * 256;
+  p.S = tile_splits(nmat, rows, KB, NB);
+  p.ws_bytes = p.pad_bytes + llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)rows, (int)NB, p.S);
   return p;
 }
 
@@ -253,7 +288,9 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
     }
     e = llk_launch_tile(mode, xp, p.ld, w0->dev, w1 ? w1->dev : nullptr,
                         static_cast<uint8_t*>(y->data) + m0 * y->stride0 * ysz, y->stride0, rows,
-                        (int)N, (int)w0->KB, (int)w0->NB, out_bf16, yvec, s);
+                        (int)N, (int)w0->KB, (int)w0->NB, p.S,
+                        p.S > 1 ? static_cast<uint8_t*>(ws) + p.pad_bytes : nullptr, out_bf16,
+                        yvec, s);
   }
   if (e != hipSuccess) return fail_hip(e, what);
   return LLK_OK;

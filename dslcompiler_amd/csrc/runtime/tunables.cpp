@@ -16,11 +16,17 @@ struct Knob {
 // decode_splits:     force its cross-workgroup k-split count (0 = heuristic).
 // decode_target_wgs: workgroups the split heuristic aims for (1 per CU).
 // decode_min_kb:     fewest 64-k steps per split.
+// tile_splits:       force the tile kernel's k-split count (0 = cost model).
+// tile_wgs_per_wave: workgroups the tile kernel runs at once (1 per CU).
+// tile_min_kb:       fewest 64-k steps per tile-kernel split.
 Knob g_knobs[] = {
     {"decode_max_m", {64}},
     {"decode_splits", {0}},
     {"decode_target_wgs", {256}},
     {"decode_min_kb", {2}},
+    {"tile_splits", {0}},
+    {"tile_wgs_per_wave", {256}},
+    {"tile_min_kb", {4}},
 };
 
 }  // namespace

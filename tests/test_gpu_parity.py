@@ -169,6 +169,78 @@ def test_swiglu_decode_workspace_reuse(llk, gpu, orc):
             llk.set_tunable("decode_splits", old)
 
 
+class _Tunable:
+    """Sets a dispatch knob for the duration of a with-block."""
+
+    def __init__(self, llk, name, value):
+        self.llk, self.name, self.value = llk, name, value
+
+    def __enter__(self):
+        self.old = self.llk.get_tunable(self.name)
+        self.llk.set_tunable(self.name, self.value)
+
+    def __exit__(self, *exc):
+        self.llk.set_tunable(self.name, self.old)
+
+
+# (M, K, N, forced splits): aligned and padded X (K % 64 != 0), ragged M and
+# N, splits that leave a short last split (K=1000: 16 k-steps over 3 -> 6,6,4)
+# and split counts that collapse (16 steps over 5 -> 4 splits of 4).
+TILE_SPLIT_CASES = [(300, 1024, 700, 2), (300, 1000, 700, 3), (65, 4096, 384, 5),
+                    (513, 640, 130, 7), (256, 128, 256, 2)]
+
+
+@pytest.mark.parametrize("M,K,N,S", TILE_SPLIT_CASES)
+def test_swiglu_tile_splits(llk, gpu, orc, M, K, N, S):
+    """Prefill SwiGLU with K split across workgroups (gate/up partials, then
+    the reduce kernel applies the epilogue)."""
+    print(f"case swiglu tile splits M={M} K={K} N={N} S={S}", flush=True)
+    x, wg, wu = swiglu_inputs(M, K, N, seed=M + S)
+    with _Tunable(llk, "tile_splits", S):
+        _check_swiglu(llk, gpu, orc, x, wg, wu, f"tile split S={S}")
+
+
+@pytest.mark.parametrize("M,K,N,S", TILE_SPLIT_CASES)
+def test_gemm_tile_splits(llk, gpu, orc, M, K, N, S):
+    print(f"case gemm tile splits M={M} K={K} N={N} S={S}", flush=True)
+    s = 1.0 / np.sqrt(K)
+    a = normal_bf16(M + S, 0, (M, K), s)
+    b = normal_bf16(M + S, 1, (K, N), s)
+    cf_ref, _ = orc.gemm(a, b)
+    pb = llk.PackedWeights.from_host(b)
+    ad = to_dev(gpu, a)
+    with _Tunable(llk, "tile_splits", S):
+        cf = from_dev(llk.matmul(ad, pb, out_dtype=gpu.float32))
+        cb = from_dev(llk.matmul(ad, pb, out_dtype=gpu.bfloat16))
+    assert_parity(cf, cf_ref, f"gemm tile split S={S}")
+    assert_parity_bf16(cb, cf_ref, f"gemm tile split S={S} bf16")
+    assert np.array_equal(cb, to_bf16_bits(cf)), "bf16 != RNE(fp32)"
+
+
+def test_tile_splits_exact_and_reuse(llk, gpu, orc):
+    """Integer inputs make every partial sum exact, so any k split must give
+    the oracle's gate/up bit for bit: GEMM fp32 output equal, SwiGLU within
+    one bf16 ulp (expf only).  Calls alternate split counts and shapes so a
+    stale partial plane in the shared workspace would show."""
+    print("case tile splits exact + workspace reuse", flush=True)
+    rng = np.random.default_rng(7)
+    for (M, K, N, S) in [(200, 1024, 300, 4), (100, 192, 160, 3), (257, 512, 96, 2),
+                         (100, 192, 160, 1), (200, 1024, 300, 8)]:
+        a = to_bf16_bits(rng.integers(-4, 5, (M, K)).astype(np.float32))
+        b = to_bf16_bits(rng.integers(-4, 5, (K, N)).astype(np.float32))
+        wu = to_bf16_bits(rng.integers(-2, 3, (K, N)).astype(np.float32) * 0.125)
+        with _Tunable(llk, "tile_splits", S):
+            cf = from_dev(llk.matmul(to_dev(gpu, a), llk.PackedWeights.from_host(b),
+                                     out_dtype=gpu.float32))
+            wg = to_bf16_bits(bf16_bits_to_f32(b) * np.float32(0.0625))
+            yb = _run_swiglu(llk, gpu, a, wg, wu, gpu.bfloat16)
+        cf_ref, _ = orc.gemm(a, b)
+        assert np.array_equal(cf, cf_ref), f"gemm M={M} K={K} N={N} S={S}"
+        _, yb_ref = orc.swiglu(a, wg, wu)
+        d = np.abs(yb.astype(np.int32) - yb_ref.astype(np.int32))
+        assert d.max() <= 1 and np.mean(d == 0) > 0.99, f"swiglu M={M} K={K} N={N} S={S}"
+
+
 def test_swiglu_strided(llk, gpu, orc):
     print("case swiglu strided", flush=True)
     x, wg, wu = swiglu_inputs(130, 200, 136, seed=11)
