@@ -34,13 +34,23 @@ PROFILE = ROOT / "profiles" / "swiglu_prefill_2048x4096x11008.md"
 PREFILL = dict(M=2048, K=4096, N=11008)
 DECODE = dict(K=4096, N=14336)
 MLP = dict(K=5120, N=13824)
+# Secondary workloads ("extra") warm for at least this long before timing;
+# the headline honours --warmup exactly.
+EXTRA_WARM_S = 0.1
 
 
-def _time_loop(torch, fn, steps: int, warmup: int) -> float:
-    """Average ms per call, HIP events on the launch (current) stream."""
+def _time_loop(torch, fn, steps: int, warmup: int, min_warm_s: float = 0.0) -> float:
+    """Average ms per call, HIP events on the launch (current) stream.  After
+    `warmup` untimed calls, keeps warming until `min_warm_s` seconds have
+    passed (the GPU needs ~35 ms of load to reach its steady clock)."""
+    t0 = time.perf_counter()
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
+    while time.perf_counter() - t0 < min_warm_s:
+        for i in range(20):
+            fn(i)
+        torch.cuda.synchronize()
     s = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(s)
@@ -78,7 +88,8 @@ def bench_decode(torch, llk, M, steps, warmup, copies=4):
              llk.PackedWeights.from_device(_rand_w(torch, g, K, N))) for _ in range(copies)]
     x = torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-    ms = _time_loop(torch, lambda i: llk.fused_swiglu(x, *sets[i % copies], out=y), steps, warmup)
+    ms = _time_loop(torch, lambda i: llk.fused_swiglu(x, *sets[i % copies], out=y), steps, warmup,
+                    EXTRA_WARM_S)
     nbytes = 2.0 * K * N * 2 + M * K * 2 + M * N * 2
     return dict(ms=ms, gbs=nbytes / (ms * 1e-3) / 1e9)
 
@@ -90,7 +101,7 @@ def bench_gemm(torch, llk, steps, warmup):
     a = _rand_w(torch, g, n, n)
     pb = llk.PackedWeights.from_device(_rand_w(torch, g, n, n))
     c = torch.empty((n, n), dtype=torch.float32, device="cuda")
-    ms = _time_loop(torch, lambda i: llk.matmul(a, pb, out=c), steps, warmup)
+    ms = _time_loop(torch, lambda i: llk.matmul(a, pb, out=c), steps, warmup, EXTRA_WARM_S)
     return dict(ms=ms, tflops=2.0 * n ** 3 / (ms * 1e-3) / 1e12)
 
 
@@ -109,7 +120,7 @@ def bench_mlp(torch, llk, steps, warmup):
         y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
         z = torch.empty((M, K), dtype=torch.bfloat16, device="cuda")
         ms = _time_loop(torch, lambda i: llk.mlp(x, pg, pu, pd, y=y, z=z), max(5, steps // 2),
-                        warmup)
+                        warmup, EXTRA_WARM_S)
         nbytes = 3.0 * K * N * 2 + M * K * 2 * 2 + M * N * 2 * 2
         out[f"M{M}"] = {"us": round(ms * 1e3, 1),
                         "tflops": round(6.0 * M * K * N / (ms * 1e-3) / 1e12, 1),
@@ -166,8 +177,10 @@ def profiled_traffic():
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=200,
+                    help="untimed launches first (200 prefill launches = ~70 ms, past the "
+                         "~35 ms the GPU takes to reach its steady clock under load)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", choices=["prefill", "decode8", "gemm", "mlp", "copy"],
