@@ -59,14 +59,22 @@ __device__ __forceinline__ void load_x_frags(const SkinnyArgs& a, int kb, int la
     }
 }
 
-template <int NMAT, int MT, int KS, bool OUT_BF16, bool XVEC, int UNROLL>
-__global__ __launch_bounds__(KS * 64) void skinny_kernel(SkinnyArgs a) {
-  extern __shared__ __attribute__((aligned(16))) float red[];  // [KS][NMAT][MT][16][64]
+// G: 32-column groups per workgroup (1, 2 or 4 of one 128-column n-block);
+// KS: waves per group, each streaming a contiguous part of the k range.
+// Wave w serves group w % G and k part w / G, so the G waves of a k part
+// read neighbouring 1 KiB sub-blocks of the same 4 KiB (G = 4) at the same
+// time.
+template <int NMAT, int MT, int KS, int G, bool OUT_BF16, bool XVEC, int UNROLL>
+__global__ __launch_bounds__(KS * G * 64) void skinny_kernel(SkinnyArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float red[];  // [KS][G][NMAT][MT][16][64]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int ngroups = a.NB * 4;
-  const int grp = blockIdx.x % ngroups;  // 32-column group
-  const int split = blockIdx.x / ngroups;
+  const int gi = wave % G;
+  const int kpart = wave / G;
+  const int nwg = a.NB * 4 / G;  // workgroups per k split
+  const int wg = blockIdx.x % nwg;
+  const int split = blockIdx.x / nwg;
+  const int grp = wg * G + gi;  // 32-column group of this wave
   const int nb = grp >> 2, n32 = grp & 3;
 
   // k range of this workgroup, then of this wave (contiguous chunks).
@@ -74,7 +82,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_kernel(SkinnyArgs a) {
   const int kb1 = min(a.KB, kb0 + a.kb_per_split);
   const int span = kb1 > kb0 ? kb1 - kb0 : 0;
   const int per_wave = (span + KS - 1) / KS;
-  const int wb0 = kb0 + wave * per_wave;
+  const int wb0 = kb0 + kpart * per_wave;
   const int wb1 = min(kb1, wb0 + per_wave);
 
   f32x16 acc[NMAT][MT];
@@ -130,7 +138,8 @@ __global__ __launch_bounds__(KS * 64) void skinny_kernel(SkinnyArgs a) {
   }
 
   // ---- reduce the KS waves' partial sums in LDS, in wave order ----------
-  if (KS > 1) {
+  constexpr bool kLds = KS * G > 1;
+  if (kLds) {
 #pragma unroll
     for (int p = 0; p < NMAT; ++p)
 #pragma unroll
@@ -141,29 +150,32 @@ __global__ __launch_bounds__(KS * 64) void skinny_kernel(SkinnyArgs a) {
     __syncthreads();
   }
 
-  // Thread e handles (t, g, ln): rows m = t*32 + ln%32 of this group and the
-  // 4 consecutive columns n = 8g + 4*(ln/32) + 0..3 (accumulator r = 4g+q).
-  const int n_group0 = nb * kPackN + n32 * 32;
-  for (int e = threadIdx.x; e < MT * 4 * 64; e += KS * 64) {
+  // Thread e handles (group ge, t, g, ln): rows m = t*32 + ln%32 and the 4
+  // consecutive columns n = 8g + 4*(ln/32) + 0..3 (accumulator r = 4g+q) of
+  // the workgroup's group ge.  Without LDS (one wave) e = lane + 64 j, so
+  // the values are this lane's own accumulators.
+  for (int e = threadIdx.x; e < G * MT * 4 * 64; e += KS * G * 64) {
     const int ln = e & 63;
     const int g = (e >> 6) & 3;
-    const int t = e >> 8;
+    const int t = (e >> 8) % MT;
+    const int ge = e / (MT * 4 * 64);
     float sum[NMAT][4];
 #pragma unroll
     for (int p = 0; p < NMAT; ++p)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         float s = 0.0f;
-        if (KS > 1) {
+        if (kLds) {
           for (int w2 = 0; w2 < KS; ++w2)
-            s += red[(((w2 * NMAT + p) * MT + t) * 16 + 4 * g + q) * 64 + ln];
+            s += red[((((w2 * G + ge) * NMAT + p) * MT + t) * 16 + 4 * g + q) * 64 + ln];
         } else {
-          s = acc[p][t][4 * g + q];  // KS == 1: e == lane for t = g = 0 only
+          s = acc[p][t][4 * g + q];
         }
         sum[p][q] = s;
       }
+    const int eg = wg * G + ge;
     const int m = t * 32 + (ln & 31);
-    const int n = n_group0 + 8 * g + 4 * (ln >> 5);
+    const int n = (eg >> 2) * kPackN + (eg & 3) * 32 + 8 * g + 4 * (ln >> 5);
     if (a.S > 1) {
       if (n < a.n_pad) {
 #pragma unroll
@@ -204,10 +216,10 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(SkinnyArgs a, int ro
   store4<OUT_BF16>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
 }
 
-template <int NMAT, int MT, int KS, bool OUT_BF16, bool XVEC>
+template <int NMAT, int MT, int KS, int G, bool OUT_BF16, bool XVEC>
 static hipError_t launch_skinny_t(const SkinnyArgs& a, hipStream_t s) {
-  auto fn = skinny_kernel<NMAT, MT, KS, OUT_BF16, XVEC, 2>;
-  const size_t lds = KS > 1 ? (size_t)KS * NMAT * MT * 16 * 64 * sizeof(float) : 0;
+  auto fn = skinny_kernel<NMAT, MT, KS, G, OUT_BF16, XVEC, 2>;
+  const size_t lds = KS * G > 1 ? (size_t)KS * G * NMAT * MT * 16 * 64 * sizeof(float) : 0;
   static bool attr_set = false;  // per instantiation; benign race (idempotent)
   if (!attr_set && lds > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -215,7 +227,7 @@ static hipError_t launch_skinny_t(const SkinnyArgs& a, hipStream_t s) {
     if (e != hipSuccess) return e;
   }
   attr_set = true;
-  hipLaunchKernelGGL(fn, dim3(a.NB * 4 * a.S), dim3(KS * 64), lds, s, a);
+  hipLaunchKernelGGL(fn, dim3(a.NB * 4 / G * a.S), dim3(KS * G * 64), lds, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.S == 1) return e;
   const int64_t threads = (int64_t)a.M * (a.n_pad / 4);
@@ -224,15 +236,29 @@ static hipError_t launch_skinny_t(const SkinnyArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// KS (waves per workgroup) keeps the LDS reduction buffer at 64 KiB.
-template <int NMAT, int MT>
-static hipError_t launch_skinny_mt(const SkinnyArgs& a, bool out_bf16, bool xvec, hipStream_t s) {
-  constexpr int KS = (NMAT * MT <= 2) ? 8 : 4;
+// Waves per group: KS * G <= 16 (1024 threads) and the LDS reduction buffer
+// (KS * G * NMAT * MT * 4 KiB) at most 128 KiB.
+template <int NMAT, int MT, int G>
+constexpr int skinny_ks() {
+  return G == 1 ? ((NMAT * MT <= 2) ? 8 : 4) : (32 / (G * NMAT * MT) < 16 / G ? 32 / (G * NMAT * MT) : 16 / G);
+}
+
+template <int NMAT, int MT, int G>
+static hipError_t launch_skinny_g(const SkinnyArgs& a, bool out_bf16, bool xvec, hipStream_t s) {
+  constexpr int KS = skinny_ks<NMAT, MT, G>();
   if (out_bf16)
-    return xvec ? launch_skinny_t<NMAT, MT, KS, true, true>(a, s)
-                : launch_skinny_t<NMAT, MT, KS, true, false>(a, s);
-  return xvec ? launch_skinny_t<NMAT, MT, KS, false, true>(a, s)
-              : launch_skinny_t<NMAT, MT, KS, false, false>(a, s);
+    return xvec ? launch_skinny_t<NMAT, MT, KS, G, true, true>(a, s)
+                : launch_skinny_t<NMAT, MT, KS, G, true, false>(a, s);
+  return xvec ? launch_skinny_t<NMAT, MT, KS, G, false, true>(a, s)
+              : launch_skinny_t<NMAT, MT, KS, G, false, false>(a, s);
+}
+
+template <int NMAT, int MT>
+static hipError_t launch_skinny_mt(const SkinnyArgs& a, int G, bool out_bf16, bool xvec,
+                                   hipStream_t s) {
+  if (G == 4) return launch_skinny_g<NMAT, MT, 4>(a, out_bf16, xvec, s);
+  if (G == 2) return launch_skinny_g<NMAT, MT, 2>(a, out_bf16, xvec, s);
+  return launch_skinny_g<NMAT, MT, 1>(a, out_bf16, xvec, s);
 }
 
 }  // namespace llk_gfx950
@@ -246,14 +272,15 @@ size_t llk_skinny_workspace_bytes(int nmat, int M, int N_pad, int S) {
 }
 
 // Internal: called by the host dispatch layer.  mode 1 = SwiGLU (w0 = Wg,
-// w1 = Wu), mode 0 = GEMM (w0 = B).  M <= 64.  `ws` must hold
-// llk_skinny_workspace_bytes(nmat, M, 128*NB, S) bytes when S > 1.
+// w1 = Wu), mode 0 = GEMM (w0 = B).  M <= 64.  G (1, 2, 4): 32-column
+// groups per workgroup.  `ws` must hold llk_skinny_workspace_bytes(nmat, M,
+// 128*NB, S) bytes when S > 1.
 hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                              const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
-                             int NB, int S, void* ws, bool out_bf16, bool xvec, bool yvec,
+                             int NB, int S, int G, void* ws, bool out_bf16, bool xvec, bool yvec,
                              hipStream_t s) {
   using namespace llk_gfx950;
-  if (M < 1 || M > 64) return hipErrorInvalidValue;
+  if (M < 1 || M > 64 || (G != 1 && G != 2 && G != 4)) return hipErrorInvalidValue;
   SkinnyArgs a;
   a.x = x;
   a.w0 = static_cast<const uint8_t*>(w0);
@@ -274,8 +301,8 @@ hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const voi
   if (a.S > 1 && ws == nullptr) return hipErrorInvalidValue;
   const int mt = (M + 31) / 32;
   if (mode == 1)
-    return mt == 1 ? launch_skinny_mt<2, 1>(a, out_bf16, xvec, s)
-                   : launch_skinny_mt<2, 2>(a, out_bf16, xvec, s);
-  return mt == 1 ? launch_skinny_mt<1, 1>(a, out_bf16, xvec, s)
-                 : launch_skinny_mt<1, 2>(a, out_bf16, xvec, s);
+    return mt == 1 ? launch_skinny_mt<2, 1>(a, G, out_bf16, xvec, s)
+                   : launch_skinny_mt<2, 2>(a, G, out_bf16, xvec, s);
+  return mt == 1 ? launch_skinny_mt<1, 1>(a, G, out_bf16, xvec, s)
+                 : launch_skinny_mt<1, 2>(a, G, out_bf16, xvec, s);
 }

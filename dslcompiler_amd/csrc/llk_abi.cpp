@@ -28,8 +28,8 @@ size_t llk_tile_split_bytes(int mode, int M, int NB, int S);
 bool llk_tile_x_fits(int M, int64_t ldx);
 hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                              const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
-                             int NB, int S, void* ws, bool out_bf16, bool xvec, bool yvec,
-                             hipStream_t s);
+                             int NB, int S, int G, void* ws, bool out_bf16, bool xvec,
+                             bool yvec, hipStream_t s);
 size_t llk_skinny_workspace_bytes(int nmat, int M, int N_pad, int S);
 hipError_t llk_launch_pad_rows(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* out,
                                int64_t ldo, hipStream_t s);
@@ -191,6 +191,7 @@ hipStream_t stream_of(const llk_kernel_context* ctx) {
 struct Plan {
   bool skinny = false;   // small-M bandwidth kernel
   int S = 1;             // k splits across workgroups (either kernel)
+  int G = 1;             // small-M kernel: 32-column groups per workgroup
   bool pad = false;      // tile path: copy X into a padded buffer first
   int64_t chunk = 0;     // tile path: rows per launch (32-bit X offsets)
   int64_t ld = 0;        // tile path: row stride of the X the kernel reads
@@ -233,12 +234,17 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
   Plan p;
   if (M <= std::min<int64_t>(64, llk::tunable("decode_max_m"))) {
     p.skinny = true;
-    const int64_t groups = NB * 4;
+    const int64_t gw = llk::tunable("decode_group_width");
+    p.G = (gw == 2 || gw == 4) ? (int)gw : 1;
+    const int64_t groups = NB * 4 / p.G;  // workgroups per k split
     int64_t S = llk::tunable("decode_splits");
     if (S <= 0) {
+      // As many splits as fit in one round of `target` workgroups: a second
+      // round, or the partial planes and reduce launch, cost more than the
+      // idle CUs of a partly filled round (measured on MI355X).
       const int64_t target = std::max<int64_t>(1, llk::tunable("decode_target_wgs"));
       const int64_t min_kb = std::max<int64_t>(1, llk::tunable("decode_min_kb"));
-      S = std::min((target + groups - 1) / groups, std::max<int64_t>(1, KB / min_kb));
+      S = std::min(std::max<int64_t>(1, target / groups), std::max<int64_t>(1, KB / min_kb));
     }
     S = std::max<int64_t>(1, std::min(S, KB));
     const int64_t kbps = (KB + S - 1) / S;  // no empty splits
@@ -273,7 +279,8 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
   if (p.skinny) {
     e = llk_launch_skinny(mode, static_cast<const uint16_t*>(x->data), x->stride0, w0->dev,
                           w1 ? w1->dev : nullptr, y->data, y->stride0, (int)M, (int)N, (int)K,
-                          (int)w0->KB, (int)w0->NB, p.S, ws, out_bf16, x_vec_ok(x), yvec, s);
+                          (int)w0->KB, (int)w0->NB, p.S, p.G, ws, out_bf16, x_vec_ok(x), yvec,
+                          s);
     if (e != hipSuccess) return fail_hip(e, what);
     return LLK_OK;
   }

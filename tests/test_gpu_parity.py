@@ -183,6 +183,22 @@ class _Tunable:
         self.llk.set_tunable(self.name, self.old)
 
 
+@pytest.mark.parametrize("G", [1, 2, 4])
+@pytest.mark.parametrize("M,S", [(1, 1), (8, 3), (40, 1), (64, 2)])
+def test_decode_group_width(llk, gpu, orc, G, M, S):
+    """Small-M kernel with 1, 2 or 4 column groups per workgroup, with and
+    without the cross-workgroup k split; SwiGLU and GEMM, ragged N."""
+    print(f"case decode G={G} M={M} S={S}", flush=True)
+    K, N = 1280, 600
+    x, wg, wu = swiglu_inputs(M, K, N, seed=G * 100 + M)
+    with _Tunable(llk, "decode_group_width", G), _Tunable(llk, "decode_splits", S):
+        _check_swiglu(llk, gpu, orc, x, wg, wu, f"decode G={G} M={M} S={S}")
+        cf_ref, _ = orc.gemm(x, wg)
+        cf = from_dev(llk.matmul(to_dev(gpu, x), llk.PackedWeights.from_host(wg),
+                                 out_dtype=gpu.float32))
+    assert_parity(cf, cf_ref, f"decode gemm G={G} M={M} S={S}")
+
+
 # (M, K, N, forced splits): aligned and padded X (K % 64 != 0), ragged M and
 # N, splits that leave a short last split (K=1000: 16 k-steps over 3 -> 6,6,4)
 # and split counts that collapse (16 steps over 5 -> 4 splits of 4).
