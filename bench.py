@@ -190,7 +190,8 @@ def main() -> None:
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this hot path runs on one GPU; multi-GPU runs are not part of this "
-              "build (the sharding plan is in DESIGN.md)", file=sys.stderr)
+              "build (SwiGLU would shard column-parallel over N with no communication)",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch

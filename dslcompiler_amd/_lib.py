@@ -56,6 +56,35 @@ class ScheduleEntry(C.Structure):
                 ("grain_size", C.c_int64), ("parallel_axis", C.c_char * 8)]
 
 
+class KernelKeyC(C.Structure):
+    """KernelKey (KernelKey.h:45-57): same fields, types and order."""
+    _fields_ = [("operation", C.c_uint8), ("input_type", C.c_uint8), ("output_type", C.c_uint8),
+                ("M_bucket", C.c_int64), ("N", C.c_int64), ("K", C.c_int64),
+                ("weight_layout", C.c_uint8), ("isa", C.c_uint8), ("math_mode", C.c_uint8),
+                ("thread_count", C.c_uint16), ("compiler_version", C.c_uint64),
+                ("schedule_version", C.c_uint64)]
+
+
+class WeightKeyC(C.Structure):
+    """WeightKey (KernelKey.h:114-124)."""
+    _fields_ = [("weight_ptr", C.c_void_p), ("shape_hash", C.c_uint64), ("BK", C.c_int64),
+                ("BN", C.c_int64)]
+
+
+class CacheStatsC(C.Structure):
+    """CacheStats (JitCache.h:67-71)."""
+    _fields_ = [("hits", C.c_size_t * 4), ("misses", C.c_size_t * 4),
+                ("evictions", C.c_size_t * 4)]
+
+
+class LaunchPlan(C.Structure):
+    """llk_launch_plan: the dispatcher's choice for one call."""
+    _fields_ = [("kernel", C.c_int), ("splits", C.c_int), ("group_width", C.c_int),
+                ("pad_x", C.c_int), ("workgroups", C.c_int64),
+                ("threads_per_workgroup", C.c_int64), ("launches", C.c_int64),
+                ("workspace_bytes", C.c_size_t)]
+
+
 class LLKError(RuntimeError):
     """A negative llk_status, with the library's message."""
 
@@ -68,6 +97,10 @@ P = C.c_void_p
 PP = C.POINTER(C.c_void_p)
 T2 = C.POINTER(Tensor2D)
 CTX = C.POINTER(KernelContext)
+KKP = C.POINTER(KernelKeyC)
+WKP = C.POINTER(WeightKeyC)
+# llk_kernel_fn: the shape of llk_swiglu_bf16
+KERNEL_FN = C.CFUNCTYPE(C.c_int, T2, P, P, T2, C.c_int, CTX)
 
 # name -> (restype, argtypes); every function declared in include/llk/llk_abi.h.
 SIGNATURES = {
@@ -92,6 +125,10 @@ SIGNATURES = {
     "llk_pack_device_layout": (C.c_int, [T2, P]),
     "llk_swiglu_bf16": (C.c_int, [T2, P, P, T2, C.c_int, CTX]),
     "llk_swiglu_scratch_size": (C.c_size_t, [C.c_int64, C.c_int64, C.c_int64]),
+    "llk_verify_fused_swiglu": (C.c_int, [C.c_int64] * 8),
+    "llk_verify_matmul": (C.c_int, [C.c_int64, C.c_int64]),
+    "llk_describe_launch": (C.c_int, [C.c_int, C.c_int64, C.c_int64, C.c_int64, C.c_int,
+                                      C.POINTER(LaunchPlan)]),
     "llk_gemm_bf16": (C.c_int, [T2, P, T2, C.c_int, CTX]),
     "llk_mlp_bf16": (C.c_int, [T2, P, P, P, T2, T2, CTX]),
     "llk_classify_m": (C.c_int, [C.c_int64]),
@@ -101,12 +138,34 @@ SIGNATURES = {
     "llk_kernel_key_hash": (C.c_uint64, [C.c_uint8, C.c_uint8, C.c_uint8, C.c_int64, C.c_int64,
                                          C.c_int64, C.c_uint8, C.c_uint8, C.c_uint8, C.c_uint16,
                                          C.c_uint64, C.c_uint64]),
+    "llk_set_schedule_db": (C.c_int, [C.c_char_p]),
     "llk_select_schedule": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int,
                                       C.POINTER(ScheduleEntry), C.POINTER(C.c_int)]),
     "llk_fill_normal_bf16": (C.c_int, [C.c_uint64, C.c_uint64, C.c_float, P, C.c_int64,
                                        C.c_int]),
     "llk_set_tunable": (C.c_int, [C.c_char_p, C.c_int64]),
     "llk_get_tunable": (C.c_int, [C.c_char_p, C.POINTER(C.c_int64)]),
+    "llk_packed_weights_serialize": (C.c_int, [P, P, C.c_size_t, C.POINTER(C.c_size_t)]),
+    "llk_packed_weights_deserialize": (C.c_int, [P, C.c_size_t, C.c_uint, PP]),
+    "llk_packed_weights_save": (C.c_int, [P, C.c_char_p]),
+    "llk_packed_weights_load": (C.c_int, [C.c_char_p, C.c_uint, PP]),
+    "llk_cache_create": (C.c_int, [PP]),
+    "llk_cache_destroy": (None, [P]),
+    "llk_cache_lookup_or_compile": (C.c_int, [P, KKP, C.POINTER(KERNEL_FN)]),
+    "llk_cache_lookup_object_code": (C.c_int, [P, KKP, C.POINTER(KERNEL_FN)]),
+    "llk_cache_insert_object_code": (C.c_int, [P, KKP, KERNEL_FN]),
+    "llk_cache_insert_blob": (C.c_int, [P, C.c_int, C.c_char_p, C.c_size_t, C.c_char_p,
+                                        C.c_size_t]),
+    "llk_cache_lookup_blob": (C.c_int, [P, C.c_int, C.c_char_p, C.c_size_t, P, C.c_size_t,
+                                        C.POINTER(C.c_size_t)]),
+    "llk_cache_insert_packed_weights": (C.c_int, [P, WKP, P]),
+    "llk_cache_lookup_packed_weights": (C.c_int, [P, WKP, PP]),
+    "llk_cache_get_packed_weights": (C.c_int, [P, T2, C.c_int64, C.c_int, C.c_uint, PP]),
+    "llk_cache_evict_lru": (C.c_int, [P, C.c_int, C.c_size_t]),
+    "llk_cache_set_max_entries": (C.c_int, [P, C.c_int, C.c_size_t]),
+    "llk_cache_get_stats": (C.c_int, [P, C.POINTER(CacheStatsC)]),
+    "llk_cache_clear": (None, [P]),
+    "llk_cache_size": (C.c_size_t, [P]),
 }
 
 _LIB: C.CDLL | None = None

@@ -28,7 +28,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CXX = os.environ.get("CXX_HOST", "g++")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-# Packed-FP32 VALU forms are disabled for all device code.
+# Packed-FP32 VALU forms (v_pk_*_f32) are disabled for all device code: some
+# of their forms have given wrong results on MI355X machines of this pool.
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -54,6 +55,7 @@ CXX_SOURCES = [
 TOOLS = {
     "llk-bench": CSRC / "tools" / "llk_bench.cpp",
     "llk-compile": CSRC / "tools" / "llk_compile.cpp",
+    "llk-tune": CSRC / "tools" / "llk_tune.cpp",
 }
 
 

@@ -266,6 +266,21 @@ static hipError_t launch_skinny_mt(const SkinnyArgs& a, int G, bool out_bf16, bo
 // Rows of the partial buffer for M rows (whole 32-row MFMA groups).
 static int skinny_rows(int M) { return (M + 31) / 32 * 32; }
 
+// Threads per workgroup of the small-M kernel for (nmat, M, G).
+int llk_skinny_threads(int nmat, int M, int G) {
+  using namespace llk_gfx950;
+  const bool mt1 = M <= 32;
+  const int g = (G == 2 || G == 4) ? G : 1;
+  int ks;
+  if (nmat == 2)
+    ks = mt1 ? (g == 1 ? skinny_ks<2, 1, 1>() : g == 2 ? skinny_ks<2, 1, 2>() : skinny_ks<2, 1, 4>())
+             : (g == 1 ? skinny_ks<2, 2, 1>() : g == 2 ? skinny_ks<2, 2, 2>() : skinny_ks<2, 2, 4>());
+  else
+    ks = mt1 ? (g == 1 ? skinny_ks<1, 1, 1>() : g == 2 ? skinny_ks<1, 1, 2>() : skinny_ks<1, 1, 4>())
+             : (g == 1 ? skinny_ks<1, 2, 1>() : g == 2 ? skinny_ks<1, 2, 2>() : skinny_ks<1, 2, 4>());
+  return ks * g * 64;
+}
+
 size_t llk_skinny_workspace_bytes(int nmat, int M, int N_pad, int S) {
   if (S <= 1) return 0;
   return (size_t)S * nmat * skinny_rows(M) * N_pad * sizeof(float);

@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <new>
 #include <string>
@@ -31,6 +32,7 @@ hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const voi
                              int NB, int S, int G, void* ws, bool out_bf16, bool xvec,
                              bool yvec, hipStream_t s);
 size_t llk_skinny_workspace_bytes(int nmat, int M, int N_pad, int S);
+int llk_skinny_threads(int nmat, int M, int G);
 hipError_t llk_launch_pad_rows(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* out,
                                int64_t ldo, hipStream_t s);
 hipError_t llk_launch_pack(const uint16_t* w, int64_t ld, int K, int N, int KB, int NB, void* out,
@@ -206,8 +208,9 @@ struct Plan {
 // tile_wgs_per_wave); the "+ 2" is the per-workgroup pipeline fill and
 // epilogue; the S partial planes (S * nmat * rows * N_pad fp32) are written
 // and read back at ~4 TB/s, plus one step for the reduce launch.
-int tile_splits(int nmat, int64_t rows, int64_t KB, int64_t NB) {
-  const int64_t forced = llk::tunable("tile_splits");
+int tile_splits(int nmat, int64_t rows, int64_t KB, int64_t NB, int64_t db_splits) {
+  int64_t forced = llk::tunable("tile_splits");
+  if (forced <= 0) forced = db_splits;
   const int64_t min_kb = std::max<int64_t>(1, llk::tunable("tile_min_kb"));
   int64_t smax = std::min<int64_t>(64, std::max<int64_t>(1, KB / min_kb));
   if (forced > 0) smax = std::min(forced, KB);
@@ -229,15 +232,55 @@ int tile_splits(int nmat, int64_t rows, int64_t KB, int64_t NB) {
   return (int)best_s;
 }
 
-// x == nullptr: plan for the worst case (X needs padding).
+// Active schedule DB (llk_set_schedule_db, or the file named by the
+// LLK_SCHEDULE_DB environment variable at first use): the entry the
+// reference's loader + selectBest pick for (operation, M bucket), cached.
+struct ActiveDb {
+  std::mutex mu;
+  bool env_checked = false;
+  std::string path;  // empty: no DB
+  std::map<std::pair<int, int>, std::pair<bool, llk::ScheduleEntry>> sel;
+};
+ActiveDb g_db;
+
+bool db_entry(int nmat, int64_t M, llk::ScheduleEntry* out) {
+  std::lock_guard<std::mutex> lk(g_db.mu);
+  if (!g_db.env_checked) {
+    g_db.env_checked = true;
+    const char* env = std::getenv("LLK_SCHEDULE_DB");
+    if (env && *env && g_db.path.empty()) g_db.path = env;
+  }
+  if (g_db.path.empty()) return false;
+  const int bucket = llk::classifyM(M);
+  const auto key = std::make_pair(nmat, bucket);
+  auto it = g_db.sel.find(key);
+  if (it == g_db.sel.end()) {
+    bool ok = false;
+    const auto m = llk::loadScheduleDB(g_db.path, bucket, nmat == 2 ? "fused_swiglu" : "matmul", &ok);
+    it = g_db.sel.emplace(key, std::make_pair(ok && !m.empty(),
+                                              m.empty() ? llk::ScheduleEntry{} : m.front())).first;
+  }
+  if (!it->second.first) return false;
+  *out = it->second.second;
+  return true;
+}
+
+// x == nullptr: plan for the worst case (X needs padding).  Precedence for
+// each knob: a forced tunable, then the active schedule DB's entry
+// (small-M: group width = BN / 32, splits = grain_size; tile: splits =
+// grain_size; grain_size 0 = choose from the shape), then the heuristics.
 Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const llk_tensor2d* x) {
   Plan p;
+  llk::ScheduleEntry se;
+  const bool have_db = db_entry(nmat, M, &se);
   if (M <= std::min<int64_t>(64, llk::tunable("decode_max_m"))) {
     p.skinny = true;
-    const int64_t gw = llk::tunable("decode_group_width");
+    int64_t gw = llk::tunable("decode_group_width");
+    if (have_db && (se.BN == 32 || se.BN == 64 || se.BN == 128)) gw = se.BN / 32;
     p.G = (gw == 2 || gw == 4) ? (int)gw : 1;
     const int64_t groups = NB * 4 / p.G;  // workgroups per k split
     int64_t S = llk::tunable("decode_splits");
+    if (S <= 0 && have_db && se.grain_size > 0) S = se.grain_size;
     if (S <= 0) {
       // As many splits as fit in one round of `target` workgroups: a second
       // round, or the partial planes and reduce launch, cost more than the
@@ -259,7 +302,7 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
     p.chunk = std::max<int64_t>(256, (((int64_t)1 << 31) - 1) / (p.ld * 2) / 256 * 256 - 256);
   const int64_t rows = std::min(p.chunk, M);
   if (p.pad) p.pad_bytes = ((size_t)rows * p.ld * 2 + 255) / 256 * 256;
-  p.S = tile_splits(nmat, rows, KB, NB);
+  p.S = tile_splits(nmat, rows, KB, NB, have_db ? se.grain_size : 0);
   p.ws_bytes = p.pad_bytes + llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)rows, (int)NB, p.S);
   return p;
 }
@@ -507,12 +550,253 @@ int llk_pack_device_layout(const llk_tensor2d* w, void* out) {
 }
 
 // ---------------------------------------------------------------------------
+// Serialized packed weights
+// ---------------------------------------------------------------------------
+
+}  // extern "C"
+
+namespace {
+
+struct BlobHeader {
+  char magic[8];
+  uint32_t version, dtype;
+  int64_t K, N, BK, K_blocks, block_size, KB, NB;
+  uint64_t payload_bytes, checksum, reserved;
+};
+static_assert(sizeof(BlobHeader) == 96, "blob header is 96 bytes");
+constexpr char kBlobMagic[8] = {'L', 'L', 'K', 'P', 'W', '9', '5', '0'};
+
+uint64_t fnv1a64(const uint8_t* p, size_t n) {
+  uint64_t h = 0xcbf29ce484222325ULL;
+  for (size_t i = 0; i < n; ++i) h = (h ^ p[i]) * 0x100000001b3ULL;
+  return h;
+}
+
+// Device-layout payload of a handle in host memory: copied back from the
+// GPU, or computed from the host layout ([K_blocks][BK][N] holds the rows
+// of W in order, so it is W itself with row stride N).
+int payload_to_host(const llk_packed_weights* pw, uint8_t* out) {
+  const size_t bytes = llk::deviceLayoutBytes(pw->K, pw->N);
+  if (bytes == 0) return LLK_OK;
+  if (pw->dev) {
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != pw->device) e = hipSetDevice(pw->device);
+    if (e == hipSuccess) e = hipMemcpy(out, pw->dev, bytes, hipMemcpyDeviceToHost);
+    if (cur != pw->device) (void)hipSetDevice(cur);
+    return e == hipSuccess ? LLK_OK : fail_hip(e, "hipMemcpy(payload to host)");
+  }
+  if (pw->host.empty()) return fail(LLK_ERR_INVALID_ARGUMENT, "handle holds no payload");
+  llk::packDeviceLayout(pw->host.data(), pw->K, pw->N, pw->N, out);
+  return LLK_OK;
+}
+
+}  // namespace
+
+namespace llk {
+// Error hook for the runtime sources built outside this file.
+int setError(int code, const char* msg) { return fail(code, "%s", msg); }
+}  // namespace llk
+
+extern "C" {
+
+int llk_packed_weights_serialize(const llk_packed_weights* pw, void* out, size_t cap,
+                                 size_t* len) {
+  if (!pw || !len) return fail(LLK_ERR_INVALID_ARGUMENT, "NULL argument");
+  const size_t payload = llk::deviceLayoutBytes(pw->K, pw->N);
+  *len = sizeof(BlobHeader) + payload;
+  if (!out) return LLK_OK;
+  if (cap < *len) return fail(LLK_ERR_INVALID_ARGUMENT, "blob needs %zu bytes, cap %zu", *len, cap);
+  BlobHeader h{};
+  std::memcpy(h.magic, kBlobMagic, 8);
+  h.version = 1;
+  h.dtype = static_cast<uint32_t>(pw->dtype);
+  h.K = pw->K;
+  h.N = pw->N;
+  h.BK = pw->BK;
+  h.K_blocks = pw->K_blocks;
+  h.block_size = pw->block_size;
+  h.KB = pw->KB;
+  h.NB = pw->NB;
+  h.payload_bytes = payload;
+  uint8_t* body = static_cast<uint8_t*>(out) + sizeof(BlobHeader);
+  int rc = payload_to_host(pw, body);
+  if (rc) return rc;
+  h.checksum = fnv1a64(body, payload);
+  std::memcpy(out, &h, sizeof(h));
+  return LLK_OK;
+}
+
+int llk_packed_weights_deserialize(const void* blob, size_t len, unsigned flags,
+                                   llk_packed_weights** out) {
+  if (!blob || !out) return fail(LLK_ERR_INVALID_ARGUMENT, "NULL argument");
+  *out = nullptr;
+  if (len < sizeof(BlobHeader)) return fail(LLK_ERR_INVALID_ARGUMENT, "blob shorter than its header");
+  BlobHeader h;
+  std::memcpy(&h, blob, sizeof(h));
+  if (std::memcmp(h.magic, kBlobMagic, 8) != 0 || h.version != 1)
+    return fail(LLK_ERR_INVALID_ARGUMENT, "not a version-1 packed-weights blob");
+  if (h.dtype != LLK_BF16 || h.K < 0 || h.N < 0 || h.BK <= 0 || h.K > kMaxDim || h.N > kMaxDim ||
+      h.K_blocks != (h.K + h.BK - 1) / h.BK || h.block_size != h.BK * h.N * 2 ||
+      h.KB != llk::deviceBlocksK(h.K) || h.NB != llk::deviceBlocksN(h.N) ||
+      h.payload_bytes != llk::deviceLayoutBytes(h.K, h.N))
+    return fail(LLK_ERR_INVALID_ARGUMENT, "inconsistent packed-weights header");
+  if (len < sizeof(BlobHeader) + h.payload_bytes)
+    return fail(LLK_ERR_INVALID_ARGUMENT, "blob truncated: %zu < %zu bytes", len,
+                (size_t)(sizeof(BlobHeader) + h.payload_bytes));
+  const uint8_t* body = static_cast<const uint8_t*>(blob) + sizeof(BlobHeader);
+  if (fnv1a64(body, h.payload_bytes) != h.checksum)
+    return fail(LLK_ERR_INVALID_ARGUMENT, "packed-weights payload checksum mismatch");
+  const bool host_only = (flags & LLK_PACK_HOST_ONLY) != 0;
+  int dev = -1;
+  if (!host_only) {
+    int rc = current_device(&dev);
+    if (rc) return rc;
+  }
+  auto* pw = new (std::nothrow) llk_packed_weights();
+  if (!pw) return fail(LLK_ERR_OUT_OF_MEMORY, "handle allocation");
+  fill_meta(pw, h.K, h.N, h.BK);
+  try {
+    if (flags & (LLK_PACK_KEEP_HOST | LLK_PACK_HOST_ONLY)) {
+      pw->host.assign(static_cast<size_t>(pw->K_blocks * pw->BK * pw->N), 0);
+      if (h.payload_bytes) llk::unpackDeviceLayout(body, h.K, h.N, pw->host.data(), h.N);
+    }
+  } catch (const std::bad_alloc&) {
+    llk_packed_weights_free(pw);
+    return fail(LLK_ERR_OUT_OF_MEMORY, "host allocation while unpacking");
+  }
+  if (!host_only) {
+    pw->dev_bytes = h.payload_bytes;
+    const size_t alloc = h.payload_bytes ? h.payload_bytes : 256;
+    hipError_t e = hipMalloc(&pw->dev, alloc);
+    if (e != hipSuccess) {
+      pw->dev = nullptr;
+      llk_packed_weights_free(pw);
+      return fail(LLK_ERR_OUT_OF_MEMORY, "hipMalloc(%zu): %s", alloc, hipGetErrorString(e));
+    }
+    e = h.payload_bytes ? hipMemcpy(pw->dev, body, h.payload_bytes, hipMemcpyHostToDevice)
+                        : hipMemset(pw->dev, 0, alloc);
+    if (e != hipSuccess) {
+      llk_packed_weights_free(pw);
+      return fail_hip(e, "upload of packed weights");
+    }
+    pw->device = dev;
+  }
+  *out = pw;
+  return LLK_OK;
+}
+
+int llk_packed_weights_save(const llk_packed_weights* pw, const char* path) {
+  if (!pw || !path) return fail(LLK_ERR_INVALID_ARGUMENT, "NULL argument");
+  size_t len = 0;
+  int rc = llk_packed_weights_serialize(pw, nullptr, 0, &len);
+  if (rc) return rc;
+  std::vector<uint8_t> buf;
+  try {
+    buf.resize(len);
+  } catch (const std::bad_alloc&) {
+    return fail(LLK_ERR_OUT_OF_MEMORY, "host allocation of %zu bytes", len);
+  }
+  rc = llk_packed_weights_serialize(pw, buf.data(), len, &len);
+  if (rc) return rc;
+  FILE* f = std::fopen(path, "wb");
+  if (!f) return fail(LLK_ERR_NOT_FOUND, "cannot open %s for writing", path);
+  const bool ok = std::fwrite(buf.data(), 1, len, f) == len;
+  const bool closed = std::fclose(f) == 0;
+  if (!ok || !closed) return fail(LLK_ERR_NOT_FOUND, "short write to %s", path);
+  return LLK_OK;
+}
+
+int llk_packed_weights_load(const char* path, unsigned flags, llk_packed_weights** out) {
+  if (!path || !out) return fail(LLK_ERR_INVALID_ARGUMENT, "NULL argument");
+  *out = nullptr;
+  FILE* f = std::fopen(path, "rb");
+  if (!f) return fail(LLK_ERR_NOT_FOUND, "cannot open %s", path);
+  std::vector<uint8_t> buf;
+  uint8_t chunk[1 << 16];
+  size_t n;
+  try {
+    while ((n = std::fread(chunk, 1, sizeof(chunk), f)) > 0) buf.insert(buf.end(), chunk, chunk + n);
+  } catch (const std::bad_alloc&) {
+    std::fclose(f);
+    return fail(LLK_ERR_OUT_OF_MEMORY, "host allocation while reading %s", path);
+  }
+  const bool err = std::ferror(f) != 0;
+  std::fclose(f);
+  if (err) return fail(LLK_ERR_NOT_FOUND, "read error on %s", path);
+  return llk_packed_weights_deserialize(buf.data(), buf.size(), flags, out);
+}
+
+// ---------------------------------------------------------------------------
 // Kernels
 // ---------------------------------------------------------------------------
 
 size_t llk_swiglu_scratch_size(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   return plan_launch(2, M, K, llk::deviceBlocksK(K), llk::deviceBlocksN(N), nullptr).ws_bytes;
+}
+
+int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, int x_aligned,
+                        llk_launch_plan* out) {
+  if (!out) return fail(LLK_ERR_INVALID_ARGUMENT, "out is NULL");
+  *out = llk_launch_plan{};
+  if (operation != 0 && operation != 3)
+    return fail(LLK_ERR_INVALID_ARGUMENT, "operation %d has no gfx950 kernel", operation);
+  if (M < 1 || N < 1 || K < 1 || M > kMaxDim || N > kMaxDim || K > kMaxDim)
+    return fail(LLK_ERR_SHAPE, "M, N, K must be in [1, 2^30]");
+  const int nmat = operation == 0 ? 2 : 1;
+  const int64_t KB = llk::deviceBlocksK(K), NB = llk::deviceBlocksN(N);
+  // A stand-in X with the requested alignment (plan_launch reads only the
+  // pointer's alignment, the row stride and K).
+  llk_tensor2d x{reinterpret_cast<void*>(x_aligned ? 256 : 2), M, K, x_aligned ? K : K + 1, 1};
+  const Plan p = plan_launch(nmat, M, K, KB, NB, &x);
+  out->splits = p.S;
+  out->workspace_bytes = p.ws_bytes;
+  if (p.skinny) {
+    out->kernel = 0;
+    out->group_width = p.G;
+    out->workgroups = NB * 4 / p.G * p.S;
+    out->threads_per_workgroup = llk_skinny_threads(nmat, (int)M, p.G);
+    out->launches = p.S > 1 ? 2 : 1;
+    return LLK_OK;
+  }
+  out->kernel = 1;
+  out->group_width = 0;
+  out->pad_x = p.pad ? 1 : 0;
+  const int64_t rows = std::min(p.chunk, M);
+  const int64_t chunks = (M + p.chunk - 1) / p.chunk;
+  out->workgroups = (rows + 255) / 256 * (nmat == 2 ? NB : (NB + 1) / 2) * p.S;
+  out->threads_per_workgroup = 256;
+  out->launches = chunks * (1 + (p.pad ? 1 : 0) + (p.S > 1 ? 1 : 0));
+  return LLK_OK;
+}
+
+int llk_verify_fused_swiglu(int64_t x_m, int64_t x_k, int64_t wg_k, int64_t wg_n, int64_t wu_k,
+                            int64_t wu_n, int64_t init_m, int64_t init_n) {
+  auto known = [](int64_t a, int64_t b) { return a >= 0 && b >= 0; };
+  if (known(x_m, init_m) && x_m != init_m)
+    return fail(LLK_ERR_SHAPE, "M dimension mismatch: X=%lld vs init=%lld", (long long)x_m,
+                (long long)init_m);
+  if (known(wg_n, init_n) && wg_n != init_n)
+    return fail(LLK_ERR_SHAPE, "N dimension mismatch: Wg=%lld vs init=%lld", (long long)wg_n,
+                (long long)init_n);
+  if (known(x_k, wg_k) && x_k != wg_k)
+    return fail(LLK_ERR_SHAPE, "K dimension mismatch between X=%lld and Wg=%lld", (long long)x_k,
+                (long long)wg_k);
+  if (known(x_k, wu_k) && x_k != wu_k)
+    return fail(LLK_ERR_SHAPE, "K dimension mismatch between X=%lld and Wu=%lld", (long long)x_k,
+                (long long)wu_k);
+  if (known(wg_n, wu_n) && wg_n != wu_n)
+    return fail(LLK_ERR_SHAPE, "N dimension mismatch between Wg=%lld and Wu=%lld", (long long)wg_n,
+                (long long)wu_n);
+  return LLK_OK;
+}
+
+int llk_verify_matmul(int64_t a_k, int64_t b_k) {
+  if (a_k >= 0 && b_k >= 0 && a_k != b_k)
+    return fail(LLK_ERR_SHAPE, "K dimension must match: %lld vs %lld", (long long)a_k,
+                (long long)b_k);
+  return LLK_OK;
 }
 
 int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
@@ -524,12 +808,7 @@ int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
     return fail(LLK_ERR_DTYPE, "y_dtype %d unsupported (bf16 or f32)", y_dtype);
   if (!wg || !wu) return fail(LLK_ERR_INVALID_ARGUMENT, "packed weights handle is NULL");
   const int64_t M = x->dim0, K = x->dim1;
-  // FusedSwiGLUOp::verify (LLKOps.cpp:42-83) checks, same order and wording.
-  if (y->dim0 != M) return fail(LLK_ERR_SHAPE, "M dimension mismatch: X=%lld vs init=%lld", (long long)M, (long long)y->dim0);
-  if (wg->N != y->dim1) return fail(LLK_ERR_SHAPE, "N dimension mismatch: Wg=%lld vs init=%lld", (long long)wg->N, (long long)y->dim1);
-  if (K != wg->K) return fail(LLK_ERR_SHAPE, "K dimension mismatch between X=%lld and Wg=%lld", (long long)K, (long long)wg->K);
-  if (K != wu->K) return fail(LLK_ERR_SHAPE, "K dimension mismatch between X=%lld and Wu=%lld", (long long)K, (long long)wu->K);
-  if (wg->N != wu->N) return fail(LLK_ERR_SHAPE, "N dimension mismatch between Wg=%lld and Wu=%lld", (long long)wg->N, (long long)wu->N);
+  if ((rc = llk_verify_fused_swiglu(M, K, wg->K, wg->N, wu->K, wu->N, y->dim0, y->dim1))) return rc;
   if (M > kMaxDim) return fail(LLK_ERR_SHAPE, "M too large");
   if (M == 0 || wg->N == 0) return LLK_OK;
   if (K == 0) return fail(LLK_ERR_SHAPE, "K must be >= 1 (empty reduction)");
@@ -547,8 +826,8 @@ int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor
     return fail(LLK_ERR_DTYPE, "c_dtype %d unsupported (bf16 or f32)", c_dtype);
   if (!b) return fail(LLK_ERR_INVALID_ARGUMENT, "packed weights handle is NULL");
   const int64_t M = a->dim0, K = a->dim1, N = b->N;
-  // micro.mma verifier (MicroOps.cpp:246-291): lhs [M,K], rhs [K,N], acc [M,N].
-  if (K != b->K) return fail(LLK_ERR_SHAPE, "K mismatch: a=%lld vs b=%lld", (long long)K, (long long)b->K);
+  // llk.matmul / micro.mma contract: lhs [M,K], rhs [K,N], acc [M,N].
+  if ((rc = llk_verify_matmul(K, b->K))) return rc;
   if (c->dim0 != M || c->dim1 != N)
     return fail(LLK_ERR_SHAPE, "c shape (%lld, %lld) != (%lld, %lld)", (long long)c->dim0,
                 (long long)c->dim1, (long long)M, (long long)N);
@@ -625,6 +904,24 @@ uint64_t llk_kernel_key_hash(uint8_t operation, uint8_t input_type, uint8_t outp
   key.compiler_version = compiler_version;
   key.schedule_version = schedule_version;
   return key.hash();
+}
+
+int llk_set_schedule_db(const char* path) {
+  std::lock_guard<std::mutex> lk(g_db.mu);
+  g_db.env_checked = true;
+  g_db.sel.clear();
+  if (!path || !*path) {
+    g_db.path.clear();
+    return LLK_OK;
+  }
+  bool ok = false;
+  (void)llk::loadScheduleDB(path, 0, "fused_swiglu", &ok);
+  if (!ok) {
+    g_db.path.clear();
+    return fail(LLK_ERR_NOT_FOUND, "cannot read or parse schedule DB %s", path);
+  }
+  g_db.path = path;
+  return LLK_OK;
 }
 
 int llk_select_schedule(const char* db_path, const char* op_name, int m_bucket,

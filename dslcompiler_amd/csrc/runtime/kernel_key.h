@@ -31,9 +31,9 @@ enum class Isa : uint8_t {
 // micro.mma GEMM of this backend.
 enum class OperationKind : uint8_t { FusedSwiGLU = 0, RoPE = 1, Attention = 2, Matmul = 3 };
 
-// RowMajor/PackedKN as in the reference; PackedMfma16 is the device payload
-// layout of this backend (1 KiB v_mfma_f32_16x16x32_bf16 operand blocks).
-enum class Layout : uint8_t { RowMajor = 0, PackedKN = 1, PackedMfma16 = 2 };
+// RowMajor/PackedKN as in the reference; PackedMfma32 is the device payload
+// layout of this backend (1 KiB v_mfma_f32_32x32x16_bf16 operand blocks).
+enum class Layout : uint8_t { RowMajor = 0, PackedKN = 1, PackedMfma32 = 2 };
 
 enum class MathMode : uint8_t { Strict = 0, BoundedFast = 1, UnsafeFast = 2 };
 

@@ -51,3 +51,22 @@ void packDeviceLayout(const uint16_t* w, int64_t K, int64_t N, int64_t stride0, 
 }
 
 }  // namespace llk
+
+namespace llk {
+
+void unpackDeviceLayout(const uint8_t* in, int64_t K, int64_t N, uint16_t* w, int64_t stride0) {
+  const int64_t KB = deviceBlocksK(K);
+  const uint16_t* src = reinterpret_cast<const uint16_t*>(in);
+  for (int64_t k = 0; k < K; ++k) {
+    const int64_t kb = k >> 6, kk = k & 63;
+    const int64_t kq = kk >> 4, h = (kk >> 3) & 1, t = kk & 7;
+    uint16_t* row = w + k * stride0;
+    for (int64_t n = 0; n < N; ++n) {
+      const int64_t nb = n >> 7, nn = n & 127;
+      const int64_t s = kq * 4 + (nn >> 5), l = h * 32 + (nn & 31);
+      row[n] = src[(nb * KB + kb) * 8192 + (s * 64 + l) * 8 + t];
+    }
+  }
+}
+
+}  // namespace llk

@@ -18,5 +18,7 @@ int64_t deviceBlocksN(int64_t N);  // ceil(N / 128)
 int64_t deviceBlocksK(int64_t K);  // ceil(K / 64)
 size_t deviceLayoutBytes(int64_t K, int64_t N);
 void packDeviceLayout(const uint16_t* w, int64_t K, int64_t N, int64_t stride0, uint8_t* out);
+// Inverse of packDeviceLayout: writes W [K, N] (row stride stride0).
+void unpackDeviceLayout(const uint8_t* in, int64_t K, int64_t N, uint16_t* w, int64_t stride0);
 
 }  // namespace llk

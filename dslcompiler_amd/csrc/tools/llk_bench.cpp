@@ -1,0 +1,160 @@
+// llk-bench -- GPU benchmark of the gfx950 kernels, the counterpart of the
+// reference's benchmarking harness (tools/llk-bench/llk-bench.cpp:21-121):
+// same options and method (warm up for --warmup-ms, then --reps windows of
+// at least --measure-ms each, report the best), timing the real fused
+// SwiGLU / matmul launches with HIP events instead of a CPU stand-in.
+//
+//   llk-bench [--op=fused_swiglu|matmul] [--M=128] [--N=4096] [--K=4096]
+//             [--out=bf16|f32] [--warmup-ms=500] [--measure-ms=2000]
+//             [--reps=5] [--copies=1] [--seed=42]
+//
+// Inputs: X ~ N(0,1), weights ~ N(0, 1/sqrt(K)) in bf16 (llk_fill_normal_bf16),
+// resident in HBM before timing.  --copies rotates that many weight sets so
+// small-M runs stream from HBM rather than the 256 MB MALL.
+#include <hip/hip_runtime_api.h>
+
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "llk/llk_abi.h"
+
+namespace {
+
+std::string opt(int argc, char** argv, const char* name, const char* dflt) {
+  const size_t n = std::strlen(name);
+  for (int i = 1; i < argc; ++i)
+    if (std::strncmp(argv[i], name, n) == 0 && argv[i][n] == '=') return argv[i] + n + 1;
+  return dflt;
+}
+
+int64_t opt_i(int argc, char** argv, const char* name, int64_t dflt) {
+  const std::string v = opt(argc, argv, name, "");
+  return v.empty() ? dflt : std::strtoll(v.c_str(), nullptr, 10);
+}
+
+[[noreturn]] void die(const char* what, const char* msg) {
+  std::fprintf(stderr, "llk-bench: %s: %s\n", what, msg);
+  std::exit(1);
+}
+
+void check_llk(int rc, const char* what) {
+  if (rc != LLK_OK) die(what, llk_last_error());
+}
+
+void check_hip(hipError_t e, const char* what) {
+  if (e != hipSuccess) die(what, hipGetErrorString(e));
+}
+
+double now_ms() {
+  return std::chrono::duration<double, std::milli>(
+             std::chrono::steady_clock::now().time_since_epoch())
+      .count();
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  for (int i = 1; i < argc; ++i)
+    if (!std::strcmp(argv[i], "--help") || !std::strcmp(argv[i], "-h")) {
+      std::printf("llk-bench [--op=fused_swiglu|matmul] [--M=128] [--N=4096] [--K=4096] "
+                  "[--out=bf16|f32] [--warmup-ms=500] [--measure-ms=2000] [--reps=5] "
+                  "[--copies=1] [--seed=42]\n");
+      return 0;
+    }
+  const std::string op = opt(argc, argv, "--op", "fused_swiglu");
+  const int64_t M = opt_i(argc, argv, "--M", 128), N = opt_i(argc, argv, "--N", 4096),
+                K = opt_i(argc, argv, "--K", 4096);
+  const std::string out = opt(argc, argv, "--out", "bf16");
+  const int64_t warmup_ms = opt_i(argc, argv, "--warmup-ms", 500);
+  const int64_t measure_ms = opt_i(argc, argv, "--measure-ms", 2000);
+  const int reps = (int)opt_i(argc, argv, "--reps", 5);
+  const int copies = (int)std::max<int64_t>(1, opt_i(argc, argv, "--copies", 1));
+  const uint64_t seed = (uint64_t)opt_i(argc, argv, "--seed", 42);
+  const bool swiglu = op == "fused_swiglu";
+  if (!swiglu && op != "matmul") die("--op", "fused_swiglu or matmul");
+  if (out != "bf16" && out != "f32") die("--out", "bf16 or f32");
+  if (M < 1 || N < 1 || K < 1 || reps < 1) die("shape", "M, N, K and reps must be positive");
+  const int y_dtype = out == "bf16" ? LLK_BF16 : LLK_FP32;
+
+  char arch[64] = {0};
+  int cus = 0, lds = 0, clk = 0;
+  check_llk(llk_device_info(arch, sizeof arch, &cus, &lds, &clk), "device");
+  std::printf("LLK Bench — op=%s M=%lld N=%lld K=%lld out=%s device=%s CUs=%d copies=%d\n",
+              op.c_str(), (long long)M, (long long)N, (long long)K, out.c_str(), arch, cus,
+              copies);
+
+  // Host inputs (generator streams: X 0, Wg 1, Wu 2), packed once per copy.
+  std::vector<uint16_t> x((size_t)M * K), w((size_t)K * N);
+  check_llk(llk_fill_normal_bf16(seed, 0, 1.0f, x.data(), (int64_t)x.size(), 0), "fill X");
+  const int nmat = swiglu ? 2 : 1;
+  std::vector<llk_packed_weights*> packed;
+  for (int c = 0; c < copies; ++c)
+    for (int p = 0; p < nmat; ++p) {
+      check_llk(llk_fill_normal_bf16(seed + 1000 * c, 1 + p, 1.0f / std::sqrt((float)K), w.data(),
+                                     (int64_t)w.size(), 0),
+                "fill W");
+      llk_tensor2d wt{w.data(), K, N, N, 1};
+      llk_packed_weights* pw = nullptr;
+      check_llk(llk_pack_weights(&wt, 64, 0, &pw), "pack");
+      packed.push_back(pw);
+    }
+  void *dx = nullptr, *dy = nullptr;
+  check_hip(hipMalloc(&dx, x.size() * 2), "hipMalloc X");
+  check_hip(hipMalloc(&dy, (size_t)M * N * (y_dtype == LLK_BF16 ? 2 : 4)), "hipMalloc Y");
+  check_hip(hipMemcpy(dx, x.data(), x.size() * 2, hipMemcpyHostToDevice), "copy X");
+  hipStream_t stream;
+  check_hip(hipStreamCreate(&stream), "stream");
+  llk_tensor2d xt{dx, M, K, K, 1}, yt{dy, M, N, N, 1};
+  llk_kernel_context ctx{nullptr, 0, stream};
+  int64_t it = 0;
+  auto launch = [&]() {
+    const int c = (int)(it++ % copies);
+    const int rc = swiglu ? llk_swiglu_bf16(&xt, packed[2 * c], packed[2 * c + 1], &yt, y_dtype, &ctx)
+                          : llk_gemm_bf16(&xt, packed[c], &yt, y_dtype, &ctx);
+    check_llk(rc, "launch");
+  };
+
+  // Warm-up: the GPU reaches its steady clock after ~35 ms of load.
+  const double t0 = now_ms();
+  do {
+    for (int i = 0; i < 10; ++i) launch();
+    check_hip(hipStreamSynchronize(stream), "sync");
+  } while (now_ms() - t0 < (double)warmup_ms);
+
+  hipEvent_t e0, e1;
+  check_hip(hipEventCreate(&e0), "event");
+  check_hip(hipEventCreate(&e1), "event");
+  double best_ms = 0.0;
+  for (int r = 0; r < reps; ++r) {
+    int64_t iters = 0;
+    const double w0 = now_ms();
+    check_hip(hipEventRecord(e0, stream), "record");
+    do {
+      for (int i = 0; i < 10; ++i) launch();
+      iters += 10;
+      check_hip(hipEventRecord(e1, stream), "record");
+      check_hip(hipEventSynchronize(e1), "sync");
+    } while (now_ms() - w0 < (double)measure_ms);
+    float ms = 0.f;
+    check_hip(hipEventElapsedTime(&ms, e0, e1), "elapsed");
+    const double per = ms / (double)iters;
+    if (best_ms == 0.0 || per < best_ms) best_ms = per;
+  }
+  const double flops = 2.0 * nmat * (double)M * N * K;
+  const double bytes = 2.0 * nmat * (double)K * N + 2.0 * M * K +
+                       (double)M * N * (y_dtype == LLK_BF16 ? 2 : 4);
+  std::printf("Best: %.1f GFLOPS (%.6f ms/iter, %d reps)\n", flops / (best_ms * 1e-3) / 1e9,
+              best_ms, reps);
+  std::printf("      %.1f TFLOP/s, %.1f GB/s of algorithmic bytes (%.0f B/launch)\n",
+              flops / (best_ms * 1e-3) / 1e12, bytes / (best_ms * 1e-3) / 1e9, bytes);
+  for (auto* pw : packed) llk_packed_weights_free(pw);
+  (void)hipFree(dx);
+  (void)hipFree(dy);
+  (void)hipStreamDestroy(stream);
+  return 0;
+}

@@ -64,8 +64,9 @@ class PackedWeights:
     reference's packWeightMatrix exactly (PackedWeights.cpp:5-15).
     """
 
-    def __init__(self, handle: int):
+    def __init__(self, handle: int, owned: bool = True):
         self._h = C.c_void_p(handle)
+        self._owned = owned  # False: borrowed from a cache, never freed here
 
     # -- construction -------------------------------------------------------
     @classmethod
@@ -101,8 +102,41 @@ class PackedWeights:
         t = tensor2d(w.ctypes.data, w.shape[0], w.shape[1])
         check(lib().llk_repack(self._h, C.byref(t)))
 
+    # -- serialized form ----------------------------------------------------
+    def serialize(self) -> bytes:
+        """The versioned blob (96-byte header + device-layout payload)."""
+        n = C.c_size_t()
+        check(lib().llk_packed_weights_serialize(self.handle, None, 0, C.byref(n)))
+        buf = C.create_string_buffer(n.value)
+        check(lib().llk_packed_weights_serialize(self.handle, buf, n.value, C.byref(n)))
+        return buf.raw[:n.value]
+
+    @classmethod
+    def from_blob(cls, blob: bytes, keep_host: bool = False,
+                  host_only: bool = False) -> "PackedWeights":
+        flags = (LLK_PACK_KEEP_HOST if keep_host else 0) | (LLK_PACK_HOST_ONLY if host_only else 0)
+        out = C.c_void_p()
+        check(lib().llk_packed_weights_deserialize(blob, len(blob), flags, C.byref(out)))
+        return cls(out.value)
+
+    def save(self, path) -> None:
+        check(lib().llk_packed_weights_save(self.handle, str(path).encode()))
+
+    @classmethod
+    def load(cls, path, keep_host: bool = False, host_only: bool = False) -> "PackedWeights":
+        flags = (LLK_PACK_KEEP_HOST if keep_host else 0) | (LLK_PACK_HOST_ONLY if host_only else 0)
+        out = C.c_void_p()
+        check(lib().llk_packed_weights_load(str(path).encode(), flags, C.byref(out)))
+        return cls(out.value)
+
+    def release(self) -> C.c_void_p:
+        """Gives up ownership (e.g. to a cache) and returns the raw handle."""
+        h = self.handle
+        self._owned = False
+        return h
+
     def free(self) -> None:
-        if self._h is not None and self._h.value:
+        if self._h is not None and self._h.value and self._owned:
             lib().llk_packed_weights_free(self._h)
         self._h = None
 
@@ -219,6 +253,17 @@ def swiglu_scratch_size(M: int, N: int, K: int) -> int:
     return int(lib().llk_swiglu_scratch_size(M, N, K))
 
 
+def describe_launch(op: str, M: int, N: int, K: int, x_aligned: bool = True) -> dict:
+    """The dispatcher's launch for op 'fused_swiglu' or 'matmul' (host only)."""
+    code = {"fused_swiglu": 0, "matmul": 3}[op]
+    p = _lib.LaunchPlan()
+    check(lib().llk_describe_launch(code, M, N, K, int(x_aligned), C.byref(p)))
+    return {"kernel": ("small_m", "tile")[p.kernel], "splits": p.splits,
+            "group_width": p.group_width, "pad_x": bool(p.pad_x), "workgroups": p.workgroups,
+            "threads_per_workgroup": p.threads_per_workgroup, "launches": p.launches,
+            "workspace_bytes": p.workspace_bytes}
+
+
 def classify_m(M: int) -> int:
     return int(lib().llk_classify_m(M))
 
@@ -231,6 +276,11 @@ def get_tunable(name: str) -> int:
     v = C.c_int64()
     check(lib().llk_get_tunable(name.encode(), C.byref(v)))
     return v.value
+
+
+def set_schedule_db(path: str | None) -> None:
+    """Makes `path` the dispatcher's active schedule DB (None clears it)."""
+    check(lib().llk_set_schedule_db(str(path).encode() if path else None))
 
 
 def select_schedule(db_path: str, op_name: str, m_bucket: int):

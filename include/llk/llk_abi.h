@@ -163,9 +163,37 @@ int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
                     const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
                     llk_kernel_context* ctx);
 
+/* FusedSwiGLUOp::verify (LLKOps.cpp:42-83): the same checks in the same
+ * order with the same messages; a negative dimension is dynamic and skips
+ * the checks it takes part in.  LLK_OK or LLK_ERR_SHAPE.  llk_swiglu_bf16
+ * applies it to its arguments. */
+int llk_verify_fused_swiglu(int64_t x_m, int64_t x_k, int64_t wg_k, int64_t wg_n, int64_t wu_k,
+                            int64_t wu_n, int64_t init_m, int64_t init_n);
+/* MatmulOp::verify (LLKOps.cpp:336-348): K of A must equal K of B. */
+int llk_verify_matmul(int64_t a_k, int64_t b_k);
+
 /* Device workspace bytes llk_swiglu_bf16 needs for an M x N problem when the
  * caller supplies ctx->scratch (0 when none is needed). */
 size_t llk_swiglu_scratch_size(int64_t M, int64_t N, int64_t K);
+
+/* The launch the dispatcher chooses for an op (llk_kernel_key operation
+ * values: 0 fused SwiGLU, 3 matmul) on an M x N x K problem -- the role of
+ * the reference's ShapeSpecialization + ScheduleSelection passes
+ * (ShapeSpecialization.cpp:38-48, ScheduleSelection.cpp:46-67) for this
+ * backend.  x_aligned: X rows are 16-byte aligned with K % 8 == 0 (else the
+ * worst case is assumed).  Host-only, no HIP call. */
+typedef struct llk_launch_plan {
+  int kernel;                    /* 0 small-M bandwidth kernel, 1 MFMA tile kernel */
+  int splits;                    /* k splits across workgroups (1 = none) */
+  int group_width;               /* small-M kernel: 32-column groups per workgroup */
+  int pad_x;                     /* tile kernel: X copied to a padded buffer first */
+  int64_t workgroups;            /* of the main kernel, per launch */
+  int64_t threads_per_workgroup; /* of the main kernel */
+  int64_t launches;              /* kernel launches per call */
+  size_t workspace_bytes;        /* = ctx->scratch size the call needs */
+} llk_launch_plan;
+int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, int x_aligned,
+                        llk_launch_plan* out);
 
 /* micro.mma matmul  C = A B  (MicroOps.td:196-222, MicroOps.cpp:246-291;
  * llk.matmul, LLKOps.td:210-255, accumulator f32).
@@ -219,6 +247,18 @@ typedef struct llk_schedule_entry {
 int llk_select_schedule(const char* db_path, const char* op_name,
                         int m_bucket, llk_schedule_entry* out, int* n_matches);
 
+/* Makes `path` the active schedule DB of the dispatcher (NULL or "" clears
+ * it; without a call, the file named by the LLK_SCHEDULE_DB environment
+ * variable is used, if any).  For each (operation, M bucket) the entry the
+ * loader above selects sets the launch: small-M kernel -> 32-column groups
+ * per workgroup = BN / 32 (1, 2, 4) and k splits = grain_size; tile kernel
+ * -> k splits = grain_size; grain_size 0 leaves the split count to the
+ * shape heuristics.  Forced knobs (llk_set_tunable) take precedence.  This
+ * is the reference's ScheduleSelection (ScheduleSelection.cpp:46-67)
+ * driving the launch instead of the tiling pass.  LLK_ERR_NOT_FOUND when the
+ * file cannot be read or parsed (the DB is then cleared). */
+int llk_set_schedule_db(const char* path);
+
 /* ----------------------------------------------------------------------- */
 /* Synthetic inputs (no reference counterpart; used by llk-bench)          */
 /* ----------------------------------------------------------------------- */
@@ -235,11 +275,139 @@ int llk_fill_normal_bf16(uint64_t seed, uint64_t stream, float sigma,
 /* ----------------------------------------------------------------------- */
 
 /* Named integer knobs of the dispatch heuristics: "decode_max_m" (largest M
- * sent to the split-K decode kernel), "decode_splits" (force the k-split
- * count, 0 = heuristic), "decode_target_wgs", "decode_min_kb".  Returns
- * LLK_OK or LLK_ERR_INVALID_ARGUMENT for an unknown name. */
+ * sent to the small-M kernel), "decode_splits" (force its k-split count,
+ * 0 = heuristic), "decode_target_wgs", "decode_min_kb",
+ * "decode_group_width" (32-column groups per small-M workgroup: 1, 2, 4),
+ * "tile_splits" (force the tile kernel's k-split count, 0 = cost model),
+ * "tile_wgs_per_wave", "tile_min_kb".  Returns LLK_OK or
+ * LLK_ERR_INVALID_ARGUMENT for an unknown name. */
 int llk_set_tunable(const char* name, int64_t value);
 int llk_get_tunable(const char* name, int64_t* value);
+
+/* ----------------------------------------------------------------------- */
+/* Serialized packed weights (the reference's L4 stores packed weights as   */
+/* opaque blobs: JitCache.h:143-146; this is that blob's format, also used  */
+/* on disk)                                                                 */
+/* ----------------------------------------------------------------------- */
+
+/* Blob: a 96-byte little-endian header
+ *   magic "LLKPW950" | u32 version (1) | u32 dtype | i64 K | i64 N | i64 BK
+ *   | i64 K_blocks | i64 block_size | i64 KB | i64 NB | u64 payload bytes
+ *   | u64 FNV-1a 64 of the payload | u64 reserved (0)
+ * followed by the device payload (MFMA operand order, llk_pack_device_layout).
+ * llk_packed_weights_serialize writes it into `out` (capacity `cap`; with
+ * out == NULL only *len is set); a device payload is copied back from the
+ * GPU, a host-only handle's is computed on the host. */
+int llk_packed_weights_serialize(const llk_packed_weights* pw, void* out, size_t cap,
+                                 size_t* len);
+/* Rebuilds a handle from a blob (header and checksum verified):
+ * flags 0 -> device payload on the current device; LLK_PACK_KEEP_HOST ->
+ * also the reference host layout; LLK_PACK_HOST_ONLY -> host layout only. */
+int llk_packed_weights_deserialize(const void* blob, size_t len, unsigned flags,
+                                   llk_packed_weights** out);
+/* The same through a file. */
+int llk_packed_weights_save(const llk_packed_weights* pw, const char* path);
+int llk_packed_weights_load(const char* path, unsigned flags, llk_packed_weights** out);
+
+/* ----------------------------------------------------------------------- */
+/* Kernel / weight cache (JitCache: JitCache.h:67-218, JitCache.cpp:41-88,  */
+/* 247-397)                                                                 */
+/* ----------------------------------------------------------------------- */
+
+/* KernelKey (KernelKey.h:45-57): same fields, types and order.  Enum values
+ * as in the reference; this backend adds operation 3 (Matmul), layout 2
+ * (the device payload order) and isa 7 (gfx950). */
+typedef struct llk_kernel_key {
+  uint8_t operation;     /* 0 FusedSwiGLU, 1 RoPE, 2 Attention, 3 Matmul */
+  uint8_t input_type;    /* llk_dtype */
+  uint8_t output_type;   /* llk_dtype */
+  int64_t M_bucket;      /* 0-4 (llk_classify_m), -1 generic */
+  int64_t N;
+  int64_t K;
+  uint8_t weight_layout; /* 0 RowMajor, 1 PackedKN, 2 device payload */
+  uint8_t isa;           /* 0..6 CPU ISAs of the reference, 7 gfx950 */
+  uint8_t math_mode;     /* 0 Strict, 1 BoundedFast, 2 UnsafeFast */
+  uint16_t thread_count;
+  uint64_t compiler_version;
+  uint64_t schedule_version;
+} llk_kernel_key;
+
+/* WeightKey (KernelKey.h:114-124). */
+typedef struct llk_weight_key {
+  const void* weight_ptr;
+  uint64_t shape_hash;
+  int64_t BK;
+  int64_t BN;
+} llk_weight_key;
+
+/* CacheStats (JitCache.h:67-71): index 0..3 = L1..L4. */
+typedef struct llk_cache_stats {
+  size_t hits[4];
+  size_t misses[4];
+  size_t evictions[4];
+} llk_cache_stats;
+
+/* A gfx950 entry point as held by the object-code level: the shape of
+ * llk_swiglu_bf16 (w1 is ignored by GEMM entries).  Counterpart of
+ * JitCache::KernelFn (JitCache.h:79-81). */
+typedef int (*llk_kernel_fn)(const llk_tensor2d* x, const llk_packed_weights* w0,
+                             const llk_packed_weights* w1, llk_tensor2d* y, int y_dtype,
+                             llk_kernel_context* ctx);
+
+typedef struct llk_jit_cache llk_jit_cache;
+
+/* JitCache() / ~JitCache().  Destroying the cache frees the packed-weight
+ * handles it owns. */
+int llk_cache_create(llk_jit_cache** out);
+void llk_cache_destroy(llk_jit_cache* c);
+
+/* lookupOrCompile(KernelKey) (JitCache.cpp:182-250): the L3 entry for the
+ * key, or on a miss the gfx950 entry point the key selects (inserted into
+ * L3).  Nothing is compiled at run time: the kernels are built ahead of
+ * time.  Errors: LLK_ERR_UNSUPPORTED_ARCH (isa != 7), LLK_ERR_DTYPE (input
+ * not bf16, output not bf16/fp32), LLK_ERR_INVALID_ARGUMENT (RoPE,
+ * Attention or an unknown operation; N or K < 1). */
+int llk_cache_lookup_or_compile(llk_jit_cache* c, const llk_kernel_key* key,
+                                llk_kernel_fn* out);
+
+/* L3 (JitCache.cpp:256-276): lookup returns 1 on a hit (*out set), 0 on a
+ * miss; insert returns LLK_OK. */
+int llk_cache_lookup_object_code(llk_jit_cache* c, const llk_kernel_key* key, llk_kernel_fn* out);
+int llk_cache_insert_object_code(llk_jit_cache* c, const llk_kernel_key* key, llk_kernel_fn fn);
+
+/* L1 (level 1, IR) and L2 (level 2, optimized MLIR) string levels
+ * (JitCache.cpp:282-310).  Lookup returns 1 on a hit and copies up to `cap`
+ * bytes of the value into `out` (*len = full length), 0 on a miss. */
+int llk_cache_insert_blob(llk_jit_cache* c, int level, const char* key, size_t key_len,
+                          const void* value, size_t value_len);
+int llk_cache_lookup_blob(llk_jit_cache* c, int level, const char* key, size_t key_len,
+                          void* out, size_t cap, size_t* len);
+
+/* L4 (JitCache.cpp:314-328), holding packed-weight handles instead of
+ * blobs.  Insert transfers ownership of `pw` to the cache (a replaced or
+ * evicted handle is freed).  Lookup returns 1 with a borrowed handle,
+ * valid until the entry is evicted or the cache is cleared or destroyed,
+ * or 0 on a miss. */
+int llk_cache_insert_packed_weights(llk_jit_cache* c, const llk_weight_key* key,
+                                    llk_packed_weights* pw);
+int llk_cache_lookup_packed_weights(llk_jit_cache* c, const llk_weight_key* key,
+                                    llk_packed_weights** out);
+/* L4 lookup by (w->data, shape, bk), packing on a miss: from host memory
+ * (llk_pack_weights, flags as there) or, with on_device != 0, from device
+ * memory (llk_pack_weights_device on the default stream).  The WeightKey is
+ * {w->data, hash of (K, N, stride0), bk, 128}.  *out is borrowed as above. */
+int llk_cache_get_packed_weights(llk_jit_cache* c, const llk_tensor2d* w, int64_t bk,
+                                 int on_device, unsigned flags, llk_packed_weights** out);
+
+/* evictLRU / setMaxEntries (JitCache.cpp:332-363): level 1..4; trims the
+ * level to at most max_entries and makes that its capacity.  Returns
+ * LLK_ERR_INVALID_ARGUMENT for another level (the reference ignores it). */
+int llk_cache_evict_lru(llk_jit_cache* c, int level, size_t max_entries);
+int llk_cache_set_max_entries(llk_jit_cache* c, int level, size_t max_entries);
+/* getStats / clear / size (JitCache.cpp:365-397). */
+int llk_cache_get_stats(const llk_jit_cache* c, llk_cache_stats* out);
+void llk_cache_clear(llk_jit_cache* c);
+size_t llk_cache_size(const llk_jit_cache* c);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -1,0 +1,176 @@
+"""Host-side tools and dispatch on the CPU: llk-compile over MLIR text in the
+reference's syntax (shape_specialization.mlir:1-46 buckets, ops_invalid.mlir
+verifier messages), llk-tune's candidate generation and schedule-DB output,
+the exported verifiers, and schedule-DB-driven launch plans."""
+from __future__ import annotations
+
+import json
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import dslcompiler_amd as llk
+
+BIN = Path(llk.__file__).resolve().parent / "bin"
+
+
+def _swiglu_fn(name, M, K, N, outM=None, Kg=None, mode="bounded_fast"):
+    outM = M if outM is None else outM
+    Kg = K if Kg is None else Kg
+    return f"""
+func.func @{name}(%x: tensor<{M}x{K}xbf16>, %wg: tensor<{Kg}x{N}xbf16>, %wu: tensor<{K}x{N}xbf16>, %init: tensor<{outM}x{N}xbf16>) -> tensor<{outM}x{N}xbf16> {{
+  %y = llk.fused_swiglu ins(%x, %wg, %wu : tensor<{M}x{K}xbf16>, tensor<{Kg}x{N}xbf16>, tensor<{K}x{N}xbf16>)
+      outs(%init : tensor<{outM}x{N}xbf16>)
+      {{accumulator_type = f32, activation = #llk.activation<silu>, math_mode = #llk.math_mode<{mode}>}}
+      -> tensor<{outM}x{N}xbf16>
+  return %y : tensor<{outM}x{N}xbf16>
+}}
+"""
+
+
+def _compile(tmp_path, text, *args):
+    f = tmp_path / "in.mlir"
+    f.write_text(text)
+    return subprocess.run([str(BIN / "llk-compile"), str(f), *args], capture_output=True,
+                          text=True, timeout=60)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _tools_built():
+    for t in ("llk-compile", "llk-tune", "llk-bench"):
+        assert (BIN / t).exists(), f"{t} not built (run __graft_entry__.build())"
+
+
+def test_compile_buckets_follow_shape_specialization(tmp_path):
+    """shape_specialization.mlir: M = 1, 4, 16, 64, 128 -> buckets 0..4."""
+    text = "".join(_swiglu_fn(f"bucket_M{m}", m, 256, 512) for m in (1, 4, 16, 64, 128))
+    r = _compile(tmp_path, text)
+    assert r.returncode == 0, r.stderr
+    for m, b in zip((1, 4, 16, 64, 128), range(5)):
+        assert f"@bucket_M{m}: llk.fused_swiglu M={m} N=512 K=256 -> bucket {b}" in r.stdout
+    assert r.stdout.rstrip().endswith("Compilation successful")
+    assert "kernel=small_m" in r.stdout and "kernel=mfma_tile" in r.stdout
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(M=2, K=4, N=8, outM=3), "M dimension mismatch: X=2 vs init=3"),
+    (dict(M=2, K=4, N=8, Kg=5), "K dimension mismatch between X=4 and Wg=5"),
+])
+def test_compile_verifier_errors(tmp_path, kw, msg):
+    """ops_invalid.mlir cases: the reference verifier's messages, exit 1."""
+    r = _compile(tmp_path, _swiglu_fn("bad", **kw))
+    assert r.returncode == 1
+    assert msg in r.stderr
+    assert "Compilation successful" not in r.stdout
+
+
+def test_compile_dynamic_dims_and_matmul(tmp_path):
+    text = _swiglu_fn("dyn", "?", 4096, 14336) + """
+func.func @mm(%a: tensor<32x64xbf16>, %b: tensor<64x32xbf16>, %c: tensor<32x32xf32>) -> tensor<32x32xf32> {
+  %0 = llk.matmul ins(%a, %b : tensor<32x64xbf16>, tensor<64x32xbf16>)
+      outs(%c : tensor<32x32xf32>) -> tensor<32x32xf32>
+  return %0 : tensor<32x32xf32>
+}
+"""
+    r = _compile(tmp_path, text)
+    assert r.returncode == 1 and "dynamic dimension" in r.stderr
+    r = _compile(tmp_path, text, "--M=8")
+    assert r.returncode == 0, r.stderr
+    assert "@dyn: llk.fused_swiglu M=8 N=14336 K=4096 -> bucket 2" in r.stdout
+    assert "@mm: llk.matmul M=32 N=32 K=64 -> bucket 3" in r.stdout
+    r = _compile(tmp_path, text.replace("tensor<64x32xbf16>", "tensor<32x32xbf16>"), "--M", "8")
+    assert r.returncode == 1 and "K dimension must match: 64 vs 32" in r.stderr
+
+
+def test_compile_missing_input(tmp_path):
+    r = subprocess.run([str(BIN / "llk-compile"), str(tmp_path / "none.mlir")],
+                       capture_output=True, text=True, timeout=60)
+    assert r.returncode == 1 and "Failed to parse" in r.stderr
+
+
+def test_verifiers_exported():
+    L = llk.lib()
+    assert L.llk_verify_fused_swiglu(2, 4, 4, 8, 4, 8, 2, 8) == 0
+    assert L.llk_verify_fused_swiglu(-1, 4, 4, 8, 4, 8, 3, 8) == 0  # dynamic M skips
+    assert L.llk_verify_fused_swiglu(2, 4, 4, 8, 4, 9, 2, 8) == -2
+    assert b"N dimension mismatch between Wg=8 and Wu=9" in L.llk_last_error()
+    assert L.llk_verify_matmul(64, 64) == 0 and L.llk_verify_matmul(-1, 3) == 0
+    assert L.llk_verify_matmul(64, 32) == -2
+
+
+def test_tune_dry_run_writes_loadable_db(tmp_path):
+    out = tmp_path / "tune.json"
+    r = subprocess.run([str(BIN / "llk-tune"), "--op=fused_swiglu", "--M=8", "--N=14336",
+                        "--K=4096", "--dry-run", f"-o={out}", "--top=4"],
+                       capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    assert "M=8 (bucket 2) N=14336 K=4096" in r.stdout
+    db = json.loads(out.read_text())
+    assert len(db["entries"]) == 4
+    e = db["entries"][0]
+    assert e["operation"] == "fused_swiglu" and e["shape"]["M_bucket"] == 2
+    assert set(e["schedule"]) == {"BM", "BN", "BK", "VM", "VN", "vector_width", "num_threads",
+                                  "parallel_axis", "grain_size"}
+    sel, n, st = llk.select_schedule(str(out), "fused_swiglu", 2)
+    assert st == 0 and n == 4
+    assert sel.BN == e["schedule"]["BN"] and sel.grain_size == e["schedule"]["grain_size"]
+
+
+def _db(tmp_path, entries):
+    p = tmp_path / "db.json"
+    p.write_text(json.dumps({"version": 1, "entries": entries}))
+    return p
+
+
+def _entry(op, bucket, BN, grain):
+    return {"operation": op, "target": "gfx950", "shape": {"M_bucket": bucket, "N": 1, "K": 1},
+            "dtype": "bf16", "math_mode": "strict",
+            "schedule": {"BM": 32, "BN": BN, "BK": 64, "VM": 32, "VN": 32, "vector_width": 8,
+                         "num_threads": 256, "parallel_axis": "n", "grain_size": grain}}
+
+
+def test_schedule_db_drives_launch(tmp_path):
+    base_small = llk.describe_launch("fused_swiglu", 8, 14336, 4096)
+    base_tile = llk.describe_launch("matmul", 255, 5120, 13824)
+    base_m1 = llk.describe_launch("fused_swiglu", 1, 14336, 4096)
+    db = _db(tmp_path, [_entry("fused_swiglu", 2, 128, 3), _entry("fused_swiglu", 2, 32, 1),
+                        _entry("matmul", 4, 256, 5)])
+    llk.set_schedule_db(db)
+    try:
+        p = llk.describe_launch("fused_swiglu", 8, 14336, 4096)
+        assert (p["group_width"], p["splits"]) == (4, 3)  # first match wins
+        assert llk.describe_launch("matmul", 255, 5120, 13824)["splits"] == 5
+        # no entry for bucket 0: heuristics
+        assert llk.describe_launch("fused_swiglu", 1, 14336, 4096) == base_m1
+        old = llk.get_tunable("decode_splits")
+        llk.set_tunable("decode_splits", 2)  # a forced knob beats the DB
+        try:
+            assert llk.describe_launch("fused_swiglu", 8, 14336, 4096)["splits"] == 2
+        finally:
+            llk.set_tunable("decode_splits", old)
+    finally:
+        llk.set_schedule_db(None)
+    assert llk.describe_launch("fused_swiglu", 8, 14336, 4096) == base_small
+    assert llk.describe_launch("matmul", 255, 5120, 13824) == base_tile
+    with pytest.raises(llk.LLKError, match="NOT_FOUND"):
+        llk.set_schedule_db(tmp_path / "missing.json")
+
+
+def test_describe_launch_configs():
+    """Plans of the BASELINE configs (kernel choice and grid sizes)."""
+    p = llk.describe_launch("fused_swiglu", 2048, 11008, 4096)
+    assert (p["kernel"], p["workgroups"], p["splits"], p["workspace_bytes"]) == ("tile", 688, 1, 0)
+    p = llk.describe_launch("fused_swiglu", 8, 14336, 4096)
+    assert p["kernel"] == "small_m" and p["workgroups"] * p["threads_per_workgroup"] >= 256 * 256
+    p = llk.describe_launch("matmul", 4096, 4096, 4096)
+    assert (p["kernel"], p["workgroups"]) == ("tile", 256)
+    p = llk.describe_launch("fused_swiglu", 100, 1000, 1000, x_aligned=False)
+    assert p["pad_x"] and p["workspace_bytes"] >= 100 * 1024 * 2
+    assert llk.describe_launch("fused_swiglu", 100, 1000, 1000)["workspace_bytes"] == \
+        llk.swiglu_scratch_size(100, 1000, 1000)
+    from dslcompiler_amd._lib import LaunchPlan
+    import ctypes as C
+    plan = LaunchPlan()
+    assert llk.lib().llk_describe_launch(1, 8, 8, 8, 1, C.byref(plan)) == -1  # RoPE: no kernel
+    assert llk.lib().llk_describe_launch(0, 0, 8, 8, 1, C.byref(plan)) == -2
