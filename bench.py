@@ -128,6 +128,22 @@ def bench_mlp(torch, llk, steps, warmup):
     return out
 
 
+def model_vs_measured(pre: dict, extra: dict) -> dict:
+    """L0 model predictions (dslcompiler_amd.perfmodel) next to this run's
+    measurements, in microseconds."""
+    from dslcompiler_amd import perfmodel
+    P = lambda op, M, N, K: perfmodel.predict(op, M, N, K)["predicted_us"]  # noqa: E731
+    rows = {"prefill": (P("fused_swiglu", 2048, 11008, 4096), pre["ms"] * 1e3),
+            "gemm_4096": (P("matmul", 4096, 4096, 4096), extra["gemm_4096"]["us"])}
+    for M in (1, 8, 16):
+        rows[f"decode_m{M}"] = (P("fused_swiglu", M, 14336, 4096), extra[f"decode_m{M}"]["us"])
+    for M in (1, 17, 255, 1000, 4097):
+        pred = P("fused_swiglu", M, 13824, 5120) + P("matmul", M, 5120, 13824)
+        rows[f"mlp_M{M}"] = (pred, extra["mlp_k5120_n13824"][f"M{M}"]["us"])
+    return {k: {"predicted_us": round(p, 1), "measured_us": round(m, 1),
+                "ratio": round(p / m, 3)} for k, (p, m) in rows.items()}
+
+
 def cpu_baseline(x, wg, wu, budget_s: float = 12.0):
     """The oracle's AVX2 restatement of the reference fused kernel on a bounded
     sample of the headline workload: the first `rows` rows of X (full K and
@@ -227,6 +243,7 @@ def main() -> None:
         extra["gemm_4096"] = {"us": round(gem["ms"] * 1e3, 1), "tflops": round(gem["tflops"], 1),
                               "mfma_frac": round(gem["tflops"] / PEAK_BF16_TFLOPS, 4)}
         extra["mlp_k5120_n13824"] = bench_mlp(torch, llk, a.steps, a.warmup)
+        extra["model_vs_measured"] = model_vs_measured(pre, extra)
     cpu = None if a.no_cpu_baseline else cpu_baseline(x, wg, wu)
 
     achieved = pre["tflops"]
