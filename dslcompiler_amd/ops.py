@@ -218,18 +218,18 @@ def fused_swiglu(x, wg: PackedWeights, wu: PackedWeights, out=None, out_dtype=No
     return out
 
 
-def matmul(a, b: PackedWeights, out=None, out_dtype=None, stream=None):
+def matmul(a, b: PackedWeights, out=None, out_dtype=None, stream=None, scratch=None):
     """C = A B (micro.mma, fp32 accumulation) on the current device."""
     torch = _torch()
     if out is None:
         out = torch.empty((a.shape[0], b.N), dtype=out_dtype or torch.float32, device=a.device)
     check(lib().llk_gemm_bf16(C.byref(_t2d(a)), b.handle, C.byref(_t2d(out)),
-                              _out_dtype_code(out.dtype), C.byref(_ctx(stream))))
+                              _out_dtype_code(out.dtype), C.byref(_ctx(stream, scratch))))
     return out
 
 
 def mlp(x, wg: PackedWeights, wu: PackedWeights, wd: PackedWeights, y=None, z=None,
-        stream=None):
+        stream=None, scratch=None):
     """Y = SwiGLU(X) (bf16), Z = Y Wd (bf16); returns (y, z)."""
     torch = _torch()
     if y is None:
@@ -237,7 +237,7 @@ def mlp(x, wg: PackedWeights, wu: PackedWeights, wd: PackedWeights, y=None, z=No
     if z is None:
         z = torch.empty((x.shape[0], wd.N), dtype=torch.bfloat16, device=x.device)
     check(lib().llk_mlp_bf16(C.byref(_t2d(x)), wg.handle, wu.handle, wd.handle,
-                             C.byref(_t2d(y)), C.byref(_t2d(z)), C.byref(_ctx(stream))))
+                             C.byref(_t2d(y)), C.byref(_t2d(z)), C.byref(_ctx(stream, scratch))))
     return y, z
 
 

@@ -90,3 +90,26 @@ def test_config5_mlp(llk, gpu, orc, M):
     assert_parity_bf16(y[rows], yf_ref, f"config5 M={M} Y")
     zf_ref, _ = orc.gemm(y[rows], wd)
     assert_parity_bf16(z[rows], zf_ref, f"config5 M={M} Z")
+
+
+def test_x_beyond_32bit_offsets_launches_in_chunks(llk, gpu, orc):
+    """M * K * 2 bytes > 2^31: the tile kernel's 32-bit X offsets force row
+    chunks (aligned X, and padded X with K % 64 != 0)."""
+    for K in (4096, 4000):
+        M, N = 270_000, 128
+        print(f"case chunked X M={M} K={K}", flush=True)
+        assert M * K * 2 >= 1 << 31
+        x = gpu.randn((M, K), device="cuda").to(gpu.bfloat16)
+        wg = normal_bf16(7, 1, (K, N), 1.0 / np.sqrt(K))
+        wu = normal_bf16(7, 2, (K, N), 1.0 / np.sqrt(K))
+        pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
+        plan = llk.describe_launch("fused_swiglu", M, N, K)
+        assert plan["launches"] >= 2
+        y = llk.fused_swiglu(x, pg, pu, out_dtype=gpu.float32)
+        gpu.cuda.synchronize()
+        rows = [0, 131071, 131072, 262143, 262144, M - 1]
+        xs = from_dev(x[rows])
+        yf_ref, _ = orc.swiglu(xs, wg, wu)
+        assert_parity(from_dev(y[rows]), yf_ref, f"chunked K={K}")
+        del x, y
+        gpu.cuda.empty_cache()

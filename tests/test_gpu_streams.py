@@ -1,0 +1,85 @@
+"""Stream and graph behaviour: concurrent launches on two streams with their
+own scratch buffers, and HIP-graph capture + replay of SwiGLU / MLP calls
+(every replay checked against the eager result, with eager work between)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from common import assert_parity, bf16_bits_to_f32, normal_bf16, swiglu_inputs
+from gpu_util import from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def test_two_streams_own_scratch(llk, gpu):
+    print("case two streams", flush=True)
+    cases = [(300, 2048, 1000), (8, 4096, 2000)]  # tile with splits; small-M with splits
+    data = []
+    for M, K, N in cases:
+        x, wg, wu = swiglu_inputs(M, K, N, seed=M)
+        pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
+        xd = to_dev(gpu, x)
+        ref = from_dev(llk.fused_swiglu(xd, pg, pu))
+        data.append((xd, pg, pu, ref))
+    gpu.cuda.synchronize()
+    old = llk.get_tunable("tile_splits"), llk.get_tunable("decode_splits")
+    llk.set_tunable("tile_splits", 3)
+    llk.set_tunable("decode_splits", 3)
+    try:
+        streams = [gpu.cuda.Stream(), gpu.cuda.Stream()]
+        outs = []
+        for (xd, pg, pu, ref), s in zip(data, streams):
+            need = max(llk.describe_launch("fused_swiglu", xd.shape[0], pg.N, pg.K)
+                       ["workspace_bytes"], 256)
+            scratch = gpu.empty(need, dtype=gpu.uint8, device="cuda")
+            ys = []
+            with gpu.cuda.stream(s):
+                for _ in range(20):
+                    ys.append(llk.fused_swiglu(xd, pg, pu, stream=s, scratch=scratch))
+            outs.append((ys, ref, scratch))
+        gpu.cuda.synchronize()
+        for ys, ref, _ in outs:
+            for y in ys:
+                got = from_dev(y)
+                # every run bit-identical; the forced split changes the
+                # summation order, so against the unsplit result: the bar
+                assert np.array_equal(got, from_dev(ys[0]))
+                assert_parity(bf16_bits_to_f32(got), bf16_bits_to_f32(ref), "split vs unsplit")
+    finally:
+        llk.set_tunable("tile_splits", old[0])
+        llk.set_tunable("decode_splits", old[1])
+
+
+@pytest.mark.parametrize("M", [8, 300])
+def test_graph_capture_replay(llk, gpu, M):
+    """A captured SwiGLU + MLP call replays to the eager result each time."""
+    print(f"case graph M={M}", flush=True)
+    K, N = 1024, 768
+    x, wg, wu = swiglu_inputs(M, K, N, seed=11)
+    wd = normal_bf16(12, 3, (N, 512), 1.0 / np.sqrt(N))
+    pg, pu, pd = (llk.PackedWeights.from_host(w) for w in (wg, wu, wd))
+    xd = to_dev(gpu, x)
+    y = gpu.empty((M, N), dtype=gpu.bfloat16, device="cuda")
+    y2 = gpu.empty((M, N), dtype=gpu.bfloat16, device="cuda")
+    z = gpu.empty((M, pd.N), dtype=gpu.bfloat16, device="cuda")
+    s = gpu.cuda.Stream()
+    with gpu.cuda.stream(s):  # warm-up on the capture stream: allocates the workspace
+        llk.fused_swiglu(xd, pg, pu, out=y, stream=s)
+        llk.mlp(xd, pg, pu, pd, y=y2, z=z, stream=s)
+    s.synchronize()
+    eager_y, eager_z = from_dev(y), from_dev(z)
+    g = gpu.cuda.CUDAGraph()
+    with gpu.cuda.graph(g, stream=s):
+        llk.fused_swiglu(xd, pg, pu, out=y, stream=s)
+        llk.mlp(xd, pg, pu, pd, y=y2, z=z, stream=s)
+    for rep in range(4):
+        y.zero_()
+        z.zero_()
+        gpu.cuda.synchronize()
+        g.replay()
+        gpu.cuda.synchronize()
+        assert np.array_equal(from_dev(y), eager_y), rep
+        assert np.array_equal(from_dev(z), eager_z), rep
+        llk.fused_swiglu(xd, pg, pu, out=y2)  # eager work between replays
+        gpu.cuda.synchronize()
