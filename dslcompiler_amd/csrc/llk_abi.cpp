@@ -199,6 +199,7 @@ struct Plan {
   int64_t ld = 0;        // tile path: row stride of the X the kernel reads
   size_t pad_bytes = 0;  // tile path: padded X at the start of the workspace
   size_t ws_bytes = 0;   // workspace the plan needs
+  bool too_large = false;  // tile path: K beyond the kernel's 32-bit offsets
 };
 
 // k splits of the tile kernel for `rows` rows: the S that minimises the
@@ -295,7 +296,13 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
     p.ws_bytes = llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), p.S);
     return p;
   }
-  p.pad = !(x && x_vec_ok(x) && K % 64 == 0);
+  // The tile kernel's buffer offsets are 32-bit: 256 rows of X and one
+  // weight panel (KB x 16 KiB) must each span less than 2 GiB.  A wider
+  // caller stride is copied into a dense padded buffer; a longer K is an
+  // error.
+  constexpr int64_t kTileMaxLd = ((int64_t)1 << 31) / (256 * 2);
+  p.pad = !(x && x_vec_ok(x) && K % 64 == 0 && x->stride0 < kTileMaxLd);
+  p.too_large = KB * 64 >= kTileMaxLd;
   p.ld = p.pad ? KB * 64 : x->stride0;
   p.chunk = M;
   if (!llk_tile_x_fits((int)std::min<int64_t>(M, kMaxDim), p.ld))
@@ -313,6 +320,9 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
   const int64_t M = x->dim0, K = x->dim1, N = w0->N;
   const int nmat = mode == 1 ? 2 : 1;
   const Plan p = plan_launch(nmat, M, K, w0->KB, w0->NB, x);
+  if (p.too_large)
+    return fail(LLK_ERR_SHAPE, "%s: K=%lld too large for M=%lld (the tile kernel needs K <= %lld)",
+                what, (long long)K, (long long)M, (long long)(((int64_t)1 << 31) / 512 - 64));
   void* ws = nullptr;
   int rc = get_workspace(dev, p.ws_bytes, ctx, &ws);
   if (rc) return rc;
@@ -750,6 +760,9 @@ int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, int x_al
   // pointer's alignment, the row stride and K).
   llk_tensor2d x{reinterpret_cast<void*>(x_aligned ? 256 : 2), M, K, x_aligned ? K : K + 1, 1};
   const Plan p = plan_launch(nmat, M, K, KB, NB, &x);
+  if (p.too_large)
+    return fail(LLK_ERR_SHAPE, "K=%lld too large for M=%lld (the tile kernel needs K <= %lld)",
+                (long long)K, (long long)M, (long long)(((int64_t)1 << 31) / 512 - 64));
   out->splits = p.S;
   out->workspace_bytes = p.ws_bytes;
   if (p.skinny) {

@@ -174,3 +174,13 @@ def test_describe_launch_configs():
     plan = LaunchPlan()
     assert llk.lib().llk_describe_launch(1, 8, 8, 8, 1, C.byref(plan)) == -1  # RoPE: no kernel
     assert llk.lib().llk_describe_launch(0, 0, 8, 8, 1, C.byref(plan)) == -2
+
+
+def test_tile_kernel_k_limit():
+    """K beyond the tile kernel's 32-bit offsets is an error, not a launch;
+    the small-M kernel has no such limit."""
+    K = 1 << 22
+    with pytest.raises(llk.LLKError, match="too large"):
+        llk.describe_launch("fused_swiglu", 100, 256, K)
+    assert llk.describe_launch("fused_swiglu", 8, 256, K)["kernel"] == "small_m"
+    assert llk.describe_launch("fused_swiglu", 100, 256, K - 128)["kernel"] == "tile"
