@@ -83,12 +83,31 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
   return xcd * base + (xcd < extra ? xcd : extra) + local;
 }
 
-// Stores 4 consecutive n of output row m (bf16 or fp32), bounds-checked.
-template <bool OUT_BF16>
+// Output element types (values of llk_dtype).
+constexpr int kOutBF16 = 0, kOutF16 = 1, kOutF32 = 2;
+
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
+  const _Float16 h = static_cast<_Float16>(f);  // v_cvt_f16_f32: round to nearest even
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+// Stores 4 consecutive n of output row m (OUT: bf16, fp16 or fp32; both
+// 16-bit types rounded to nearest even), bounds-checked.
+template <int OUT>
 __device__ __forceinline__ void store4(void* y, int64_t ldy, int M, int N, int m, int n,
                                        const float (&v)[4], bool vec_ok) {
   if (m >= M || n >= N) return;
-  if (OUT_BF16) {
+  if (OUT == kOutF16) {
+    uint16_t* dst = reinterpret_cast<uint16_t*>(y) + (size_t)m * ldy + n;
+    if (vec_ok && n + 4 <= N) {
+      u16x4 h = {f32_to_f16_rne(v[0]), f32_to_f16_rne(v[1]), f32_to_f16_rne(v[2]),
+                 f32_to_f16_rne(v[3])};
+      *reinterpret_cast<u16x4*>(dst) = h;
+    } else {
+      for (int r = 0; r < 4; ++r)
+        if (n + r < N) dst[r] = f32_to_f16_rne(v[r]);
+    }
+  } else if (OUT == kOutBF16) {
     uint16_t* dst = reinterpret_cast<uint16_t*>(y) + (size_t)m * ldy + n;
     if (vec_ok && n + 4 <= N) {
       u16x4 h = {f32_to_bf16_rne(v[0]), f32_to_bf16_rne(v[1]), f32_to_bf16_rne(v[2]),

@@ -75,10 +75,10 @@ __device__ __forceinline__ void wait_stages(int ahead) {
 }
 
 // MODE 0: GEMM (C = X W);  MODE 1: fused SwiGLU.
-// OUT_BF16: store bf16 (RNE) instead of fp32.
+// OUT: output element type (kOutBF16, kOutF16 (GEMM only), kOutF32).
 // YVEC: Y rows allow a 4-element vector store (aligned base, ldy % 4 == 0).
 // SPLIT: store raw fp32 partial accumulators of k split s (see TileArgs).
-template <int MODE, bool OUT_BF16, bool YVEC, bool SPLIT>
+template <int MODE, int OUT, bool YVEC, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
@@ -276,7 +276,7 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
                                     : (tn * 256 + wn * 128 + i * 32 + 8 * g + h4);
           const float v[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
                               acc[i][j][4 * g + 3]};
-          store4<false>(dst, a.n_pad, a.M, a.n_pad, m, n, v, true);
+          store4<kOutF32>(dst, a.n_pad, a.M, a.n_pad, m, n, v, true);
         }
       }
     }
@@ -297,7 +297,7 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
         for (int q = 0; q < 4; ++q)
           v[q] = (MODE == 1) ? swiglu_act(acc[i][j][4 * g + q], acc[i + 2][j][4 * g + q])
                              : acc[i][j][4 * g + q];
-        store4<OUT_BF16>(a.y, a.ldy, a.M, a.N, m, n, v, YVEC);
+        store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, YVEC);
       }
     }
   }
@@ -306,7 +306,7 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
 // Sums the S partial planes of each output element in split order (fixed,
 // so results are reproducible) and applies the epilogue.  One thread per
 // 4 consecutive n of a row.
-template <int MODE, bool OUT_BF16, bool YVEC>
+template <int MODE, int OUT, bool YVEC>
 __global__ __launch_bounds__(256) void split_reduce_kernel(TileArgs a) {
   constexpr int NMAT = (MODE == 1) ? 2 : 1;
   const int quads = (a.N + 3) / 4;
@@ -326,15 +326,15 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(TileArgs a) {
   float v[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) v[q] = (MODE == 1) ? swiglu_act(sum[0][q], sum[1][q]) : sum[0][q];
-  store4<OUT_BF16>(a.y, a.ldy, a.M, a.N, m, n, v, YVEC);
+  store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, YVEC);
 }
 
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-template <int MODE, bool OUT_BF16, bool YVEC, bool SPLIT>
+template <int MODE, int OUT, bool YVEC, bool SPLIT>
 static hipError_t launch_tile_t(const TileArgs& a, hipStream_t s) {
-  auto fn = mfma_tile_kernel<MODE, OUT_BF16, YVEC, SPLIT>;
+  auto fn = mfma_tile_kernel<MODE, OUT, YVEC, SPLIT>;
   static bool attr_set = false;  // per instantiation; benign race (idempotent)
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -348,22 +348,32 @@ static hipError_t launch_tile_t(const TileArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int MODE, bool OUT_BF16, bool YVEC>
+template <int MODE, int OUT, bool YVEC>
 static hipError_t launch_t(const TileArgs& a, hipStream_t s) {
-  if (a.S <= 1) return launch_tile_t<MODE, OUT_BF16, YVEC, false>(a, s);
+  if (a.S <= 1) return launch_tile_t<MODE, OUT, YVEC, false>(a, s);
   // Partials are fp32 planes with 16-byte aligned rows: one instantiation.
-  hipError_t e = launch_tile_t<MODE, false, true, true>(a, s);
+  hipError_t e = launch_tile_t<MODE, kOutF32, true, true>(a, s);
   if (e != hipSuccess) return e;
   const int64_t threads = (int64_t)a.M * ((a.N + 3) / 4);
-  hipLaunchKernelGGL((split_reduce_kernel<MODE, OUT_BF16, YVEC>),
+  hipLaunchKernelGGL((split_reduce_kernel<MODE, OUT, YVEC>),
                      dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
+template <int MODE, int OUT>
+static hipError_t launch_out(const TileArgs& a, bool yvec, hipStream_t s) {
+  return yvec ? launch_t<MODE, OUT, true>(a, s) : launch_t<MODE, OUT, false>(a, s);
+}
+
+// fp16 output exists for the GEMM only (llk.matmul's result types).
 template <int MODE>
-static hipError_t launch_mode(const TileArgs& a, bool out_bf16, bool yvec, hipStream_t s) {
-  if (out_bf16) return yvec ? launch_t<MODE, true, true>(a, s) : launch_t<MODE, true, false>(a, s);
-  return yvec ? launch_t<MODE, false, true>(a, s) : launch_t<MODE, false, false>(a, s);
+static hipError_t launch_mode(const TileArgs& a, int out, bool yvec, hipStream_t s) {
+  if (out == kOutBF16) return launch_out<MODE, kOutBF16>(a, yvec, s);
+  if (out == kOutF32) return launch_out<MODE, kOutF32>(a, yvec, s);
+  if constexpr (MODE == 0) {
+    if (out == kOutF16) return launch_out<MODE, kOutF16>(a, yvec, s);
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace llk_gfx950
@@ -388,7 +398,7 @@ size_t llk_tile_split_bytes(int mode, int M, int NB, int S) {
 // aligned) holds llk_tile_split_bytes(mode, M, NB, S) bytes.
 hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                            const void* w1, void* y, int64_t ldy, int M, int N, int KB, int NB,
-                           int S, void* part, bool out_bf16, bool yvec, hipStream_t s) {
+                           int S, void* part, int out, bool yvec, hipStream_t s) {
   using namespace llk_gfx950;
   TileArgs a;
   a.x = x;
@@ -408,6 +418,6 @@ hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void*
   a.n_pad = NB * 128;
   a.part = static_cast<float*>(part);
   if (a.S > 1 && (part == nullptr || (int64_t)(a.S - 1) * a.kbs >= KB)) return hipErrorInvalidValue;
-  if (mode == 1) return launch_mode<1>(a, out_bf16, yvec, s);
-  return launch_mode<0>(a, out_bf16, yvec, s);
+  if (mode == 1) return launch_mode<1>(a, out, yvec, s);
+  return launch_mode<0>(a, out, yvec, s);
 }

@@ -64,7 +64,7 @@ __device__ __forceinline__ void load_x_frags(const SkinnyArgs& a, int kb, int la
 // Wave w serves group w % G and k part w / G, so the G waves of a k part
 // read neighbouring 1 KiB sub-blocks of the same 4 KiB (G = 4) at the same
 // time.
-template <int NMAT, int MT, int KS, int G, bool OUT_BF16, bool XVEC, int UNROLL>
+template <int NMAT, int MT, int KS, int G, int OUT, bool XVEC, int UNROLL>
 __global__ __launch_bounds__(KS * G * 64) void skinny_kernel(SkinnyArgs a) {
   extern __shared__ __attribute__((aligned(16))) float red[];  // [KS][G][NMAT][MT][16][64]
   const int lane = threadIdx.x & 63;
@@ -189,14 +189,14 @@ __global__ __launch_bounds__(KS * G * 64) void skinny_kernel(SkinnyArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         v[q] = (NMAT == 2) ? swiglu_act(sum[0][q], sum[1][q]) : sum[0][q];
-      store4<OUT_BF16>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
+      store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
     }
   }
 }
 
 // Adds the S partials in split order and applies the epilogue: thread
 // handles 4 consecutive n of one row.
-template <int NMAT, bool OUT_BF16>
+template <int NMAT, int OUT>
 __global__ __launch_bounds__(256) void skinny_reduce_kernel(SkinnyArgs a, int rows) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int quads = a.n_pad / 4;
@@ -213,12 +213,12 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(SkinnyArgs a, int ro
   float v[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) v[q] = (NMAT == 2) ? swiglu_act(s[0][q], s[1][q]) : s[0][q];
-  store4<OUT_BF16>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
+  store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
 }
 
-template <int NMAT, int MT, int KS, int G, bool OUT_BF16, bool XVEC>
+template <int NMAT, int MT, int KS, int G, int OUT, bool XVEC>
 static hipError_t launch_skinny_t(const SkinnyArgs& a, hipStream_t s) {
-  auto fn = skinny_kernel<NMAT, MT, KS, G, OUT_BF16, XVEC, 2>;
+  auto fn = skinny_kernel<NMAT, MT, KS, G, OUT, XVEC, 2>;
   const size_t lds = KS * G > 1 ? (size_t)KS * G * NMAT * MT * 16 * 64 * sizeof(float) : 0;
   static bool attr_set = false;  // per instantiation; benign race (idempotent)
   if (!attr_set && lds > 65536) {
@@ -231,7 +231,7 @@ static hipError_t launch_skinny_t(const SkinnyArgs& a, hipStream_t s) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.S == 1) return e;
   const int64_t threads = (int64_t)a.M * (a.n_pad / 4);
-  hipLaunchKernelGGL((skinny_reduce_kernel<NMAT, OUT_BF16>), dim3((unsigned)((threads + 255) / 256)),
+  hipLaunchKernelGGL((skinny_reduce_kernel<NMAT, OUT>), dim3((unsigned)((threads + 255) / 256)),
                      dim3(256), 0, s, a, MT * 32);
   return hipGetLastError();
 }
@@ -243,22 +243,30 @@ constexpr int skinny_ks() {
   return G == 1 ? ((NMAT * MT <= 2) ? 8 : 4) : (32 / (G * NMAT * MT) < 16 / G ? 32 / (G * NMAT * MT) : 16 / G);
 }
 
-template <int NMAT, int MT, int G>
-static hipError_t launch_skinny_g(const SkinnyArgs& a, bool out_bf16, bool xvec, hipStream_t s) {
+template <int NMAT, int MT, int G, int OUT>
+static hipError_t launch_skinny_o(const SkinnyArgs& a, bool xvec, hipStream_t s) {
   constexpr int KS = skinny_ks<NMAT, MT, G>();
-  if (out_bf16)
-    return xvec ? launch_skinny_t<NMAT, MT, KS, G, true, true>(a, s)
-                : launch_skinny_t<NMAT, MT, KS, G, true, false>(a, s);
-  return xvec ? launch_skinny_t<NMAT, MT, KS, G, false, true>(a, s)
-              : launch_skinny_t<NMAT, MT, KS, G, false, false>(a, s);
+  return xvec ? launch_skinny_t<NMAT, MT, KS, G, OUT, true>(a, s)
+              : launch_skinny_t<NMAT, MT, KS, G, OUT, false>(a, s);
+}
+
+// fp16 output exists for the GEMM (NMAT 1) only.
+template <int NMAT, int MT, int G>
+static hipError_t launch_skinny_g(const SkinnyArgs& a, int out, bool xvec, hipStream_t s) {
+  if (out == kOutBF16) return launch_skinny_o<NMAT, MT, G, kOutBF16>(a, xvec, s);
+  if (out == kOutF32) return launch_skinny_o<NMAT, MT, G, kOutF32>(a, xvec, s);
+  if constexpr (NMAT == 1) {
+    if (out == kOutF16) return launch_skinny_o<NMAT, MT, G, kOutF16>(a, xvec, s);
+  }
+  return hipErrorInvalidValue;
 }
 
 template <int NMAT, int MT>
-static hipError_t launch_skinny_mt(const SkinnyArgs& a, int G, bool out_bf16, bool xvec,
+static hipError_t launch_skinny_mt(const SkinnyArgs& a, int G, int out, bool xvec,
                                    hipStream_t s) {
-  if (G == 4) return launch_skinny_g<NMAT, MT, 4>(a, out_bf16, xvec, s);
-  if (G == 2) return launch_skinny_g<NMAT, MT, 2>(a, out_bf16, xvec, s);
-  return launch_skinny_g<NMAT, MT, 1>(a, out_bf16, xvec, s);
+  if (G == 4) return launch_skinny_g<NMAT, MT, 4>(a, out, xvec, s);
+  if (G == 2) return launch_skinny_g<NMAT, MT, 2>(a, out, xvec, s);
+  return launch_skinny_g<NMAT, MT, 1>(a, out, xvec, s);
 }
 
 }  // namespace llk_gfx950
@@ -292,7 +300,7 @@ size_t llk_skinny_workspace_bytes(int nmat, int M, int N_pad, int S) {
 // 128*NB, S) bytes when S > 1.
 hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                              const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
-                             int NB, int S, int G, void* ws, bool out_bf16, bool xvec, bool yvec,
+                             int NB, int S, int G, void* ws, int out, bool xvec, bool yvec,
                              hipStream_t s) {
   using namespace llk_gfx950;
   if (M < 1 || M > 64 || (G != 1 && G != 2 && G != 4)) return hipErrorInvalidValue;
@@ -316,8 +324,8 @@ hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const voi
   if (a.S > 1 && ws == nullptr) return hipErrorInvalidValue;
   const int mt = (M + 31) / 32;
   if (mode == 1)
-    return mt == 1 ? launch_skinny_mt<2, 1>(a, G, out_bf16, xvec, s)
-                   : launch_skinny_mt<2, 2>(a, G, out_bf16, xvec, s);
-  return mt == 1 ? launch_skinny_mt<1, 1>(a, G, out_bf16, xvec, s)
-                 : launch_skinny_mt<1, 2>(a, G, out_bf16, xvec, s);
+    return mt == 1 ? launch_skinny_mt<2, 1>(a, G, out, xvec, s)
+                   : launch_skinny_mt<2, 2>(a, G, out, xvec, s);
+  return mt == 1 ? launch_skinny_mt<1, 1>(a, G, out, xvec, s)
+                 : launch_skinny_mt<1, 2>(a, G, out, xvec, s);
 }

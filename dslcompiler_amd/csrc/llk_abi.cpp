@@ -24,12 +24,12 @@
 // Kernel launchers (kernels/*.hip).
 hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                            const void* w1, void* y, int64_t ldy, int M, int N, int KB, int NB,
-                           int S, void* part, bool out_bf16, bool yvec, hipStream_t s);
+                           int S, void* part, int out_dtype, bool yvec, hipStream_t s);
 size_t llk_tile_split_bytes(int mode, int M, int NB, int S);
 bool llk_tile_x_fits(int M, int64_t ldx);
 hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                              const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
-                             int NB, int S, int G, void* ws, bool out_bf16, bool xvec,
+                             int NB, int S, int G, void* ws, int out_dtype, bool xvec,
                              bool yvec, hipStream_t s);
 size_t llk_skinny_workspace_bytes(int nmat, int M, int N_pad, int S);
 int llk_skinny_threads(int nmat, int M, int G);
@@ -139,8 +139,10 @@ bool x_vec_ok(const llk_tensor2d* x) {
   return (reinterpret_cast<uintptr_t>(x->data) % 16 == 0) && (x->stride0 % 8 == 0) &&
          (x->dim1 % 8 == 0);
 }
-bool y_vec_ok(const llk_tensor2d* y, bool bf16) {
-  const uintptr_t align = bf16 ? 8 : 16;
+size_t dtype_size(int dtype) { return dtype == LLK_FP32 ? 4 : 2; }
+// Rows allow a 4-element vector store.
+bool y_vec_ok(const llk_tensor2d* y, int dtype) {
+  const uintptr_t align = 4 * dtype_size(dtype);
   return (reinterpret_cast<uintptr_t>(y->data) % align == 0) && (y->stride0 % 4 == 0);
 }
 
@@ -315,7 +317,7 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
 }
 
 int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w0,
-                    const llk_packed_weights* w1, llk_tensor2d* y, bool out_bf16,
+                    const llk_packed_weights* w1, llk_tensor2d* y, int out_dtype,
                     llk_kernel_context* ctx, int dev, const char* what) {
   const int64_t M = x->dim0, K = x->dim1, N = w0->N;
   const int nmat = mode == 1 ? 2 : 1;
@@ -327,17 +329,17 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
   int rc = get_workspace(dev, p.ws_bytes, ctx, &ws);
   if (rc) return rc;
   hipStream_t s = stream_of(ctx);
-  const bool yvec = y_vec_ok(y, out_bf16);
+  const bool yvec = y_vec_ok(y, out_dtype);
   hipError_t e = hipSuccess;
   if (p.skinny) {
     e = llk_launch_skinny(mode, static_cast<const uint16_t*>(x->data), x->stride0, w0->dev,
                           w1 ? w1->dev : nullptr, y->data, y->stride0, (int)M, (int)N, (int)K,
-                          (int)w0->KB, (int)w0->NB, p.S, p.G, ws, out_bf16, x_vec_ok(x), yvec,
+                          (int)w0->KB, (int)w0->NB, p.S, p.G, ws, out_dtype, x_vec_ok(x), yvec,
                           s);
     if (e != hipSuccess) return fail_hip(e, what);
     return LLK_OK;
   }
-  const size_t ysz = out_bf16 ? 2 : 4;
+  const size_t ysz = dtype_size(out_dtype);
   for (int64_t m0 = 0; m0 < M && e == hipSuccess; m0 += p.chunk) {
     const int rows = (int)std::min(p.chunk, M - m0);
     const uint16_t* xp = static_cast<const uint16_t*>(x->data) + m0 * x->stride0;
@@ -349,7 +351,7 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
     e = llk_launch_tile(mode, xp, p.ld, w0->dev, w1 ? w1->dev : nullptr,
                         static_cast<uint8_t*>(y->data) + m0 * y->stride0 * ysz, y->stride0, rows,
                         (int)N, (int)w0->KB, (int)w0->NB, p.S,
-                        p.S > 1 ? static_cast<uint8_t*>(ws) + p.pad_bytes : nullptr, out_bf16,
+                        p.S > 1 ? static_cast<uint8_t*>(ws) + p.pad_bytes : nullptr, out_dtype,
                         yvec, s);
   }
   if (e != hipSuccess) return fail_hip(e, what);
@@ -828,15 +830,15 @@ int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
   int dev;
   if ((rc = current_device(&dev))) return rc;
   if ((rc = check_packed(wg, "wg", dev)) || (rc = check_packed(wu, "wu", dev))) return rc;
-  return run_contraction(1, x, wg, wu, y, y_dtype == LLK_BF16, ctx, dev, "swiglu");
+  return run_contraction(1, x, wg, wu, y, y_dtype, ctx, dev, "swiglu");
 }
 
 int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor2d* c,
                   int c_dtype, llk_kernel_context* ctx) {
   int rc;
   if ((rc = check_tensor(a, "a")) || (rc = check_tensor(c, "c"))) return rc;
-  if (c_dtype != LLK_BF16 && c_dtype != LLK_FP32)
-    return fail(LLK_ERR_DTYPE, "c_dtype %d unsupported (bf16 or f32)", c_dtype);
+  if (c_dtype != LLK_BF16 && c_dtype != LLK_FP16 && c_dtype != LLK_FP32)
+    return fail(LLK_ERR_DTYPE, "c_dtype %d unsupported (bf16, f16 or f32)", c_dtype);
   if (!b) return fail(LLK_ERR_INVALID_ARGUMENT, "packed weights handle is NULL");
   const int64_t M = a->dim0, K = a->dim1, N = b->N;
   // llk.matmul / micro.mma contract: lhs [M,K], rhs [K,N], acc [M,N].
@@ -850,7 +852,7 @@ int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor
   int dev;
   if ((rc = current_device(&dev))) return rc;
   if ((rc = check_packed(b, "b", dev))) return rc;
-  return run_contraction(0, a, b, nullptr, c, c_dtype == LLK_BF16, ctx, dev, "gemm");
+  return run_contraction(0, a, b, nullptr, c, c_dtype, ctx, dev, "gemm");
 }
 
 int llk_mlp_bf16(const llk_tensor2d* x, const llk_packed_weights* wg, const llk_packed_weights* wu,

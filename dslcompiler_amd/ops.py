@@ -54,6 +54,8 @@ def _out_dtype_code(dtype) -> int:
         return LLK_BF16
     if dtype == torch.float32:
         return LLK_FP32
+    if dtype == torch.float16:
+        return _lib.LLK_FP16
     raise ValueError(f"unsupported output dtype {dtype}")
 
 

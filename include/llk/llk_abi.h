@@ -198,7 +198,9 @@ int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, int x_al
 /* micro.mma matmul  C = A B  (MicroOps.td:196-222, MicroOps.cpp:246-291;
  * llk.matmul, LLKOps.td:210-255, accumulator f32).
  * a: bf16 [M, K] device; b: packed [K, N] handle; c: [M, N] device of
- * c_dtype LLK_FP32 or LLK_BF16 (RNE of the fp32 sum). */
+ * c_dtype LLK_FP32, LLK_BF16 or LLK_FP16 (the result types llk.matmul
+ * allows; both 16-bit types round the fp32 sum to nearest even, fp16
+ * overflows to infinity). */
 int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b,
                   llk_tensor2d* c, int c_dtype, llk_kernel_context* ctx);
 

@@ -489,3 +489,31 @@ def test_golden_config1_samples_on_gpu(llk, gpu):
     yb = _run_swiglu(llk, gpu, x, wg, wu, gpu.bfloat16).ravel()[s["index"]]
     assert_parity(yf, s["y_fp32"], "config1 samples fp32")
     assert np.mean(yb == s["y_bf16"]) > 0.99
+
+
+@pytest.mark.parametrize("M,splits", [(300, 0), (300, 3), (8, 0), (40, 2)])
+def test_gemm_fp16_out(llk, gpu, orc, M, splits):
+    """llk.matmul's f16 result type: the fp16 output is RNE of the same
+    kernel's fp32 result (numpy's float32 -> float16 rounds to nearest even)
+    and meets the bar against the oracle; overflow gives infinity."""
+    print(f"case gemm fp16 M={M} splits={splits}", flush=True)
+    K, N = 768, 520
+    s = 1.0 / np.sqrt(K)
+    a = normal_bf16(13, 0, (M, K), s * 8)
+    b = normal_bf16(13, 1, (K, N), s)
+    pb = llk.PackedWeights.from_host(b)
+    ad = to_dev(gpu, a)
+    knob = "tile_splits" if M > 64 else "decode_splits"
+    with _Tunable(llk, knob, splits):
+        cf = from_dev(llk.matmul(ad, pb, out_dtype=gpu.float32))
+        ch = from_dev(llk.matmul(ad, pb, out_dtype=gpu.float16))
+    assert ch.dtype == np.float16
+    assert np.array_equal(ch.view(np.uint16), cf.astype(np.float16).view(np.uint16))
+    cf_ref, _ = orc.gemm(a, b)
+    assert_parity(ch.astype(np.float32), cf_ref, f"gemm fp16 M={M}")
+    # overflow: exact integer products beyond fp16's 65504
+    big = to_bf16_bits(np.full((M, 64), 64.0, np.float32))
+    ones = to_bf16_bits(np.full((64, 128), 32.0, np.float32))  # 64*64*32 = 131072
+    hb = from_dev(llk.matmul(to_dev(gpu, big), llk.PackedWeights.from_host(ones),
+                             out_dtype=gpu.float16))
+    assert np.all(np.isposinf(hb))
