@@ -16,12 +16,18 @@
 //
 // K loop: 32 k per stage, a ring of 4 LDS stages of 32 KiB (16 KiB weights
 // + 16 KiB X).  Operands go straight from memory into LDS
-// (buffer_load_dwordx4 ... lds) two to three stages ahead of the 32 MFMAs
-// per wave that consume them, and each stage's barrier sits between two
-// halves of the previous stage's MFMAs, so LDS reads never stall the MFMA
-// stream.  Weights sit in LDS as 1 KiB MFMA-ordered sub-blocks (contiguous,
-// conflict-free operand reads); X as XOR-swizzled 64-byte rows, so its loads
-// move whole rows and its operand reads are conflict-free too.
+// (buffer_load_dwordx4 ... lds) three stages ahead of the 32 MFMAs per wave
+// that consume them.  Each stage's barrier sits between its two k quarters;
+// the refill of the freed buffer is issued one load per MFMA pair across
+// the second quarter, and the next stage's first operands are read during
+// it, so neither loads nor LDS reads leave the MFMA pipe idle.  Weights sit
+// in LDS as 1 KiB MFMA-ordered sub-blocks (contiguous, conflict-free operand
+// reads); X as XOR-swizzled 64-byte rows, so its loads move whole rows and
+// its operand reads are conflict-free too.
+//
+// Optional k split across workgroups (SPLIT): raw fp32 partial planes plus
+// split_reduce_kernel, which sums them in split order and applies the
+// epilogue.
 //
 // X must be padded to whole 64-k steps with 16-byte aligned rows (the host
 // copies it into a padded buffer otherwise); rows >= M read as zero through

@@ -7,10 +7,12 @@
 // (v_mfma_f32_32x32x16_bf16 A operand); X (at most 64 rows) is tiny and
 // served from L2.
 //
-// Grid: (4 * NB column groups of 32 n) x S k-splits.  A workgroup of KS
-// waves owns one 32-column group of every matrix; its k range is divided
-// among the waves, each streaming its part with UNROLL 64-k steps of loads
-// in flight.  The waves' partial sums meet in LDS, in wave order (a fixed
+// Grid: (4 * NB / G workgroups) x S k-splits.  A workgroup owns G adjacent
+// 32-column groups (of one 128-column n-block) of every matrix with KS
+// waves per group; each group's k range is divided among its KS waves, each
+// streaming its part with UNROLL 64-k steps of loads in flight, and the G
+// waves of a k part read neighbouring 1 KiB sub-blocks of the same 4 KiB
+// together.  The waves' partial sums meet in LDS, in wave order (a fixed
 // order, so results are deterministic).  With S == 1 the workgroup then
 // applies the epilogue (FuseDoubleContraction.cpp:175-199 for SwiGLU) and
 // stores Y.  With S > 1 it writes fp32 partials to a workspace and a second
