@@ -5,7 +5,7 @@ config 3), bf16 inputs, fp32 accumulation, bf16 output, in TFLOP/s with
 4*M*K*N flops per step.  One step = one llk_swiglu_bf16 call over inputs
 already resident in HBM; the average launch time comes from HIP events on
 the launch stream.  Reported in "extra": decode SwiGLU (config 4,
-M in {1, 8, 16}, K=4096, N=14336) in HBM GB/s with weights rotated over four
+M in {1, 8, 16, 64}, K=4096, N=14336) in HBM GB/s with weights rotated over four
 copies (940 MB, beyond the 256 MB MALL); the 4096^3 GEMM (config 2); the
 MLP block (config 5) over its ragged M sweep.
 
@@ -33,6 +33,7 @@ PROFILE = ROOT / "profiles" / "swiglu_prefill_2048x4096x11008.md"
 
 PREFILL = dict(M=2048, K=4096, N=11008)
 DECODE = dict(K=4096, N=14336)
+DECODE_M = (1, 8, 16, 64)
 MLP = dict(K=5120, N=13824)
 # Secondary workloads ("extra") warm for at least this long before timing;
 # the headline honours --warmup exactly.
@@ -135,7 +136,7 @@ def model_vs_measured(pre: dict, extra: dict) -> dict:
     P = lambda op, M, N, K: perfmodel.predict(op, M, N, K)["predicted_us"]  # noqa: E731
     rows = {"prefill": (P("fused_swiglu", 2048, 11008, 4096), pre["ms"] * 1e3),
             "gemm_4096": (P("matmul", 4096, 4096, 4096), extra["gemm_4096"]["us"])}
-    for M in (1, 8, 16):
+    for M in DECODE_M:
         rows[f"decode_m{M}"] = (P("fused_swiglu", M, 14336, 4096), extra[f"decode_m{M}"]["us"])
     for M in (1, 17, 255, 1000, 4097):
         pred = P("fused_swiglu", M, 13824, 5120) + P("matmul", M, 5120, 13824)
@@ -199,7 +200,7 @@ def main() -> None:
                          "~35 ms the GPU takes to reach its steady clock under load)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode8", "gemm", "mlp", "copy"],
+    ap.add_argument("--only", choices=["prefill", "decode8", "decode64", "gemm", "mlp", "copy"],
                     help="run one workload for --steps launches and print its timing only "
                          "(for profiler runs); 'copy' is a 256 MiB device copy used to "
                          "calibrate byte counters")
@@ -217,8 +218,8 @@ def main() -> None:
     if a.only:
         if a.only == "prefill":
             r = {"ms": bench_prefill(torch, llk, a.steps, a.warmup)["ms"]}
-        elif a.only == "decode8":
-            r = bench_decode(torch, llk, 8, a.steps, a.warmup)
+        elif a.only in ("decode8", "decode64"):
+            r = bench_decode(torch, llk, int(a.only[6:]), a.steps, a.warmup)
         elif a.only == "gemm":
             r = bench_gemm(torch, llk, a.steps, a.warmup)
         elif a.only == "mlp":
@@ -235,7 +236,7 @@ def main() -> None:
     par = spot_parity(x, wg, wu, pre["y"])
     extra = {"prefill_parity_rows": {k: round(v, 6) for k, v in par.items()}}
     if not a.no_extra:
-        for M in (1, 8, 16):
+        for M in DECODE_M:
             d = bench_decode(torch, llk, M, a.steps, a.warmup)
             extra[f"decode_m{M}"] = {"us": round(d["ms"] * 1e3, 2), "gbs": round(d["gbs"], 1),
                                      "hbm_frac": round(d["gbs"] / PEAK_HBM_GBS, 4)}

@@ -7,17 +7,18 @@
 // (v_mfma_f32_32x32x16_bf16 A operand); X (at most 64 rows) is tiny and
 // served from L2.
 //
-// Grid: (4 * NB / G workgroups) x S k-splits.  A workgroup owns G adjacent
-// 32-column groups (of one 128-column n-block) of every matrix with KS
-// waves per group; each group's k range is divided among its KS waves, each
-// streaming its part with UNROLL 64-k steps of loads in flight, and the G
-// waves of a k part read neighbouring 1 KiB sub-blocks of the same 4 KiB
-// together.  The waves' partial sums meet in LDS, in wave order (a fixed
-// order, so results are deterministic).  With S == 1 the workgroup then
-// applies the epilogue (FuseDoubleContraction.cpp:175-199 for SwiGLU) and
-// stores Y.  With S > 1 it writes fp32 partials to a workspace and a second
-// kernel adds the S partials in split order and applies the epilogue -- the
-// kernel boundary orders the two, so no device-scope fences are needed.
+// Grid: (4 * NB / W workgroups) x S k-splits.  A workgroup owns W adjacent
+// 32-column groups (of one 128-column n-block) of every matrix, as G wave
+// groups of GW groups each with KS waves per wave group; each wave group's
+// k range is divided among its KS waves, each streaming its part with
+// UNROLL 64-k steps of loads in flight, and the waves of a k part read
+// neighbouring 1 KiB sub-blocks of the same 4 KiB together.  The waves'
+// partial sums meet in LDS, in wave order (a fixed order, so results are
+// deterministic).  With S == 1 the workgroup then applies the epilogue
+// (FuseDoubleContraction.cpp:175-199 for SwiGLU) and stores Y.  With S > 1
+// it writes fp32 partials to a workspace and a second kernel adds the S
+// partials in split order and applies the epilogue -- the kernel boundary
+// orders the two, so no device-scope fences are needed.
 #include "common.h"
 
 namespace llk_gfx950 {
@@ -61,23 +62,27 @@ __device__ __forceinline__ void load_x_frags(const SkinnyArgs& a, int kb, int la
     }
 }
 
-// G: 32-column groups per workgroup (1, 2 or 4 of one 128-column n-block);
-// KS: waves per group, each streaming a contiguous part of the k range.
-// Wave w serves group w % G and k part w / G, so the G waves of a k part
-// read neighbouring 1 KiB sub-blocks of the same 4 KiB (G = 4) at the same
-// time.
-template <int NMAT, int MT, int KS, int G, int OUT, bool XVEC, int UNROLL>
+// A workgroup covers G * GW adjacent 32-column groups of one 128-column
+// n-block: G wave groups of GW groups each, KS waves per wave group, each
+// streaming a contiguous part of the k range.  Wave w serves wave group
+// w % G and k part w / G; it loads each X fragment once for its GW groups
+// (X traffic per workgroup is G * M * K * 2 bytes, against the weights'
+// G * GW * 32 * K * 2 * NMAT), and the G * GW sub-blocks a k part reads at
+// one k step are neighbouring 1 KiB pieces of the same 4 KiB.
+template <int NMAT, int MT, int KS, int G, int GW, int OUT, bool XVEC, int UNROLL>
 __global__ __launch_bounds__(KS * G * 64) void skinny_kernel(SkinnyArgs a) {
-  extern __shared__ __attribute__((aligned(16))) float red[];  // [KS][G][NMAT][MT][16][64]
+  extern __shared__ __attribute__((aligned(16))) float red[];  // [KS][G][GW][MT][16][64], one matrix
+  constexpr int NT = KS * G * 64;
+  constexpr int TOT = G * GW * MT * 4 * 64;  // output quads of the workgroup
+  constexpr int EPT = (TOT + NT - 1) / NT;   // quads per thread
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int gi = wave % G;
   const int kpart = wave / G;
-  const int nwg = a.NB * 4 / G;  // workgroups per k split
+  const int nwg = a.NB * 4 / (G * GW);  // workgroups per k split
   const int wg = blockIdx.x % nwg;
   const int split = blockIdx.x / nwg;
-  const int grp = wg * G + gi;  // 32-column group of this wave
-  const int nb = grp >> 2, n32 = grp & 3;
+  const int grp0 = (wg * G + gi) * GW;  // first 32-column group of this wave
 
   // k range of this workgroup, then of this wave (contiguous chunks).
   const int kb0 = split * a.kb_per_split;
@@ -87,29 +92,35 @@ __global__ __launch_bounds__(KS * G * 64) void skinny_kernel(SkinnyArgs a) {
   const int wb0 = kb0 + kpart * per_wave;
   const int wb1 = min(kb1, wb0 + per_wave);
 
-  f32x16 acc[NMAT][MT];
+  f32x16 acc[GW][NMAT][MT];
 #pragma unroll
-  for (int p = 0; p < NMAT; ++p)
+  for (int j = 0; j < GW; ++j)
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
+    for (int p = 0; p < NMAT; ++p)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[p][t][r] = 0.0f;
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][p][t][r] = 0.0f;
 
-  // Sub-block (kq, n32) of block (nb, kb): + kb*16K + (kq*4 + n32)*1K.
+  // Sub-block (kq, n32 + j) of block (nb, kb): + kb*16K + (kq*4 + n32 + j)*1K;
+  // GW divides 4 and grp0, so the GW groups share the n-block.
+  const int nb = grp0 >> 2, n32 = grp0 & 3;
   const size_t panel = (size_t)nb * a.KB * kBlockBytes + n32 * kSubBytes + lane * 16;
   const uint8_t* wbase[2] = {a.w0 + panel, (NMAT == 2 ? a.w1 : a.w0) + panel};
 
   int kb = wb0;
   for (; kb + UNROLL <= wb1; kb += UNROLL) {
-    u32x4 w[UNROLL][NMAT][4];
+    u32x4 w[UNROLL][NMAT][4][GW];
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u)
 #pragma unroll
       for (int p = 0; p < NMAT; ++p)
 #pragma unroll
         for (int kq = 0; kq < 4; ++kq)
-          w[u][p][kq] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-              wbase[p] + (size_t)(kb + u) * kBlockBytes + kq * 4 * kSubBytes));
+#pragma unroll
+          for (int j = 0; j < GW; ++j)
+            w[u][p][kq][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+                wbase[p] + (size_t)(kb + u) * kBlockBytes + (kq * 4 + j) * kSubBytes));
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       bf16x8 xf[4][MT];
@@ -117,11 +128,13 @@ __global__ __launch_bounds__(KS * G * 64) void skinny_kernel(SkinnyArgs a) {
 #pragma unroll
       for (int kq = 0; kq < 4; ++kq)
 #pragma unroll
-        for (int p = 0; p < NMAT; ++p) {
-          const bf16x8 wop = *reinterpret_cast<const bf16x8*>(&w[u][p][kq]);
+        for (int j = 0; j < GW; ++j)
 #pragma unroll
-          for (int t = 0; t < MT; ++t) acc[p][t] = mfma32(wop, xf[kq][t], acc[p][t]);
-        }
+          for (int p = 0; p < NMAT; ++p) {
+            const bf16x8 wop = *reinterpret_cast<const bf16x8*>(&w[u][p][kq][j]);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) acc[j][p][t] = mfma32(wop, xf[kq][t], acc[j][p][t]);
+          }
     }
   }
   for (; kb < wb1; ++kb) {  // remainder steps
@@ -130,52 +143,57 @@ __global__ __launch_bounds__(KS * G * 64) void skinny_kernel(SkinnyArgs a) {
 #pragma unroll
     for (int kq = 0; kq < 4; ++kq)
 #pragma unroll
-      for (int p = 0; p < NMAT; ++p) {
-        const u32x4 wv = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-            wbase[p] + (size_t)kb * kBlockBytes + kq * 4 * kSubBytes));
-        const bf16x8 wop = *reinterpret_cast<const bf16x8*>(&wv);
+      for (int j = 0; j < GW; ++j)
 #pragma unroll
-        for (int t = 0; t < MT; ++t) acc[p][t] = mfma32(wop, xf[kq][t], acc[p][t]);
-      }
+        for (int p = 0; p < NMAT; ++p) {
+          const u32x4 wv = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+              wbase[p] + (size_t)kb * kBlockBytes + (kq * 4 + j) * kSubBytes));
+          const bf16x8 wop = *reinterpret_cast<const bf16x8*>(&wv);
+#pragma unroll
+          for (int t = 0; t < MT; ++t) acc[j][p][t] = mfma32(wop, xf[kq][t], acc[j][p][t]);
+        }
   }
 
-  // ---- reduce the KS waves' partial sums in LDS, in wave order ----------
-  constexpr bool kLds = KS * G > 1;
-  if (kLds) {
+  // ---- reduce the KS waves' partial sums in LDS, in wave order, one matrix
+  // per pass.  Quad e of the workgroup = (group ge, t, g, ln): rows m = t*32 +
+  // ln%32 and the 4 consecutive columns 8g + 4*(ln/32) + 0..3 (accumulator
+  // r = 4g + q) of group ge; thread x handles quads x, x + NT, ...
+  float sum[EPT][NMAT][4];
 #pragma unroll
-    for (int p = 0; p < NMAT; ++p)
+  for (int p = 0; p < NMAT; ++p) {
+    if (p > 0) __syncthreads();  // the previous pass's readers are done
+#pragma unroll
+    for (int j = 0; j < GW; ++j)
 #pragma unroll
       for (int t = 0; t < MT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          red[(((wave * NMAT + p) * MT + t) * 16 + r) * 64 + lane] = acc[p][t][r];
+          red[(((wave * GW + j) * MT + t) * 16 + r) * 64 + lane] = acc[j][p][t][r];
     __syncthreads();
-  }
-
-  // Thread e handles (group ge, t, g, ln): rows m = t*32 + ln%32 and the 4
-  // consecutive columns n = 8g + 4*(ln/32) + 0..3 (accumulator r = 4g+q) of
-  // the workgroup's group ge.  Without LDS (one wave) e = lane + 64 j, so
-  // the values are this lane's own accumulators.
-  for (int e = threadIdx.x; e < G * MT * 4 * 64; e += KS * G * 64) {
-    const int ln = e & 63;
-    const int g = (e >> 6) & 3;
-    const int t = (e >> 8) % MT;
-    const int ge = e / (MT * 4 * 64);
-    float sum[NMAT][4];
 #pragma unroll
-    for (int p = 0; p < NMAT; ++p)
+    for (int i = 0; i < EPT; ++i) {
+      const int e = threadIdx.x + i * NT;
+      if (TOT % NT != 0 && e >= TOT) break;
+      const int ln = e & 63, g = (e >> 6) & 3, t = (e >> 8) % MT, ge = e / (MT * 4 * 64);
+      const int gg = ge / GW, j = ge % GW;  // wave group, group within the wave
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         float s = 0.0f;
-        if (kLds) {
-          for (int w2 = 0; w2 < KS; ++w2)
-            s += red[((((w2 * G + ge) * NMAT + p) * MT + t) * 16 + 4 * g + q) * 64 + ln];
-        } else {
-          s = acc[p][t][4 * g + q];
-        }
-        sum[p][q] = s;
+        for (int w2 = 0; w2 < KS; ++w2)
+          s += red[((((w2 * G + gg) * GW + j) * MT + t) * 16 + 4 * g + q) * 64 + ln];
+        sum[i][p][q] = s;
       }
-    const int eg = wg * G + ge;
+    }
+  }
+
+  // With S == 1 apply the epilogue (FuseDoubleContraction.cpp:175-199 for
+  // SwiGLU) and store Y; with S > 1 write the fp32 partials.
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int e = threadIdx.x + i * NT;
+    if (TOT % NT != 0 && e >= TOT) break;
+    const int ln = e & 63, g = (e >> 6) & 3, t = (e >> 8) % MT, ge = e / (MT * 4 * 64);
+    const int eg = wg * G * GW + ge;
     const int m = t * 32 + (ln & 31);
     const int n = (eg >> 2) * kPackN + (eg & 3) * 32 + 8 * g + 4 * (ln >> 5);
     if (a.S > 1) {
@@ -183,14 +201,15 @@ __global__ __launch_bounds__(KS * G * 64) void skinny_kernel(SkinnyArgs a) {
 #pragma unroll
         for (int p = 0; p < NMAT; ++p) {
           float* dst = a.part + (((size_t)split * NMAT + p) * (MT * 32) + m) * a.n_pad + n;
-          *reinterpret_cast<f32x4*>(dst) = f32x4{sum[p][0], sum[p][1], sum[p][2], sum[p][3]};
+          *reinterpret_cast<f32x4*>(dst) =
+              f32x4{sum[i][p][0], sum[i][p][1], sum[i][p][2], sum[i][p][3]};
         }
       }
     } else {
       float v[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        v[q] = (NMAT == 2) ? swiglu_act(sum[0][q], sum[1][q]) : sum[0][q];
+        v[q] = (NMAT == 2) ? swiglu_act(sum[i][0][q], sum[i][1][q]) : sum[i][0][q];
       store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
     }
   }
@@ -218,18 +237,41 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(SkinnyArgs a, int ro
   store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
 }
 
-template <int NMAT, int MT, int KS, int G, int OUT, bool XVEC>
+// Launch shape for (NMAT, MT) and a workgroup width of W 32-column groups:
+// GW groups per wave, G = W / GW wave groups, KS waves per wave group,
+// UNROLL k steps of weight loads in flight.  One matrix with M <= 32 rows
+// already holds an X fragment for two groups (GW = 2, the X traffic halves);
+// SwiGLU with M <= 32 keeps GW = 1 and 16 waves (X is a small part of its
+// traffic, the deeper wave count wins); with M > 32 both use GW = 2 (at
+// M = 64 X traffic equals the weights').  Register budgets: KS * G * 64
+// threads with at most 512 / waves-per-SIMD VGPRs each; the SwiGLU M > 32
+// form holds 2 x 2 x 2 accumulators plus 2 k steps of loads (~312 VGPRs, one
+// wave per SIMD).  LDS per pass: KS * G * GW * MT * 4 KiB <= 128 KiB.
+template <int NMAT, int MT, int W>
+struct SkinnyCfg {
+  static constexpr int GW = (W == 1 || (NMAT == 2 && MT == 1)) ? 1 : 2;
+  static constexpr int G = W / GW;
+  static constexpr int KS =
+      GW == 1 ? (G == 1 ? ((NMAT * MT <= 2) ? 8 : 4)
+                        : (32 / (G * NMAT * MT) < 16 / G ? 32 / (G * NMAT * MT) : 16 / G))
+              : (NMAT == 2 ? 4 / G : (MT == 1 ? 16 / G : 4));
+  static constexpr int UNROLL = (GW == 2 && NMAT == 1 && MT == 1) ? 1 : 2;
+  static constexpr size_t lds = (size_t)KS * G * GW * MT * 16 * 64 * sizeof(float);
+  static_assert(G * GW == W && KS * G <= 16 && lds <= 131072, "small-M launch shape");
+};
+
+template <int NMAT, int MT, int W, int OUT, bool XVEC>
 static hipError_t launch_skinny_t(const SkinnyArgs& a, hipStream_t s) {
-  auto fn = skinny_kernel<NMAT, MT, KS, G, OUT, XVEC, 2>;
-  const size_t lds = KS * G > 1 ? (size_t)KS * G * NMAT * MT * 16 * 64 * sizeof(float) : 0;
+  using C = SkinnyCfg<NMAT, MT, W>;
+  auto fn = skinny_kernel<NMAT, MT, C::KS, C::G, C::GW, OUT, XVEC, C::UNROLL>;
   static bool attr_set = false;  // per instantiation; benign race (idempotent)
-  if (!attr_set && lds > 65536) {
+  if (!attr_set && C::lds > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::lds);
     if (e != hipSuccess) return e;
   }
   attr_set = true;
-  hipLaunchKernelGGL(fn, dim3(a.NB * 4 / G * a.S), dim3(KS * G * 64), lds, s, a);
+  hipLaunchKernelGGL(fn, dim3(a.NB * 4 / W * a.S), dim3(C::KS * C::G * 64), C::lds, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.S == 1) return e;
   const int64_t threads = (int64_t)a.M * (a.n_pad / 4);
@@ -238,37 +280,36 @@ static hipError_t launch_skinny_t(const SkinnyArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Waves per group: KS * G <= 16 (1024 threads) and the LDS reduction buffer
-// (KS * G * NMAT * MT * 4 KiB) at most 128 KiB.
-template <int NMAT, int MT, int G>
-constexpr int skinny_ks() {
-  return G == 1 ? ((NMAT * MT <= 2) ? 8 : 4) : (32 / (G * NMAT * MT) < 16 / G ? 32 / (G * NMAT * MT) : 16 / G);
-}
-
-template <int NMAT, int MT, int G, int OUT>
+template <int NMAT, int MT, int W, int OUT>
 static hipError_t launch_skinny_o(const SkinnyArgs& a, bool xvec, hipStream_t s) {
-  constexpr int KS = skinny_ks<NMAT, MT, G>();
-  return xvec ? launch_skinny_t<NMAT, MT, KS, G, OUT, true>(a, s)
-              : launch_skinny_t<NMAT, MT, KS, G, OUT, false>(a, s);
+  return xvec ? launch_skinny_t<NMAT, MT, W, OUT, true>(a, s)
+              : launch_skinny_t<NMAT, MT, W, OUT, false>(a, s);
 }
 
 // fp16 output exists for the GEMM (NMAT 1) only.
-template <int NMAT, int MT, int G>
+template <int NMAT, int MT, int W>
 static hipError_t launch_skinny_g(const SkinnyArgs& a, int out, bool xvec, hipStream_t s) {
-  if (out == kOutBF16) return launch_skinny_o<NMAT, MT, G, kOutBF16>(a, xvec, s);
-  if (out == kOutF32) return launch_skinny_o<NMAT, MT, G, kOutF32>(a, xvec, s);
+  if (out == kOutBF16) return launch_skinny_o<NMAT, MT, W, kOutBF16>(a, xvec, s);
+  if (out == kOutF32) return launch_skinny_o<NMAT, MT, W, kOutF32>(a, xvec, s);
   if constexpr (NMAT == 1) {
-    if (out == kOutF16) return launch_skinny_o<NMAT, MT, G, kOutF16>(a, xvec, s);
+    if (out == kOutF16) return launch_skinny_o<NMAT, MT, W, kOutF16>(a, xvec, s);
   }
   return hipErrorInvalidValue;
 }
 
 template <int NMAT, int MT>
-static hipError_t launch_skinny_mt(const SkinnyArgs& a, int G, int out, bool xvec,
+static hipError_t launch_skinny_mt(const SkinnyArgs& a, int W, int out, bool xvec,
                                    hipStream_t s) {
-  if (G == 4) return launch_skinny_g<NMAT, MT, 4>(a, out, xvec, s);
-  if (G == 2) return launch_skinny_g<NMAT, MT, 2>(a, out, xvec, s);
+  if (W == 4) return launch_skinny_g<NMAT, MT, 4>(a, out, xvec, s);
+  if (W == 2) return launch_skinny_g<NMAT, MT, 2>(a, out, xvec, s);
   return launch_skinny_g<NMAT, MT, 1>(a, out, xvec, s);
+}
+
+template <int NMAT, int MT>
+static int skinny_threads_w(int W) {
+  if (W == 4) return SkinnyCfg<NMAT, MT, 4>::KS * SkinnyCfg<NMAT, MT, 4>::G * 64;
+  if (W == 2) return SkinnyCfg<NMAT, MT, 2>::KS * SkinnyCfg<NMAT, MT, 2>::G * 64;
+  return SkinnyCfg<NMAT, MT, 1>::KS * SkinnyCfg<NMAT, MT, 1>::G * 64;
 }
 
 }  // namespace llk_gfx950
@@ -276,19 +317,13 @@ static hipError_t launch_skinny_mt(const SkinnyArgs& a, int G, int out, bool xve
 // Rows of the partial buffer for M rows (whole 32-row MFMA groups).
 static int skinny_rows(int M) { return (M + 31) / 32 * 32; }
 
-// Threads per workgroup of the small-M kernel for (nmat, M, G).
+// Threads per workgroup of the small-M kernel for (nmat, M, G), G = 32-column
+// groups per workgroup.
 int llk_skinny_threads(int nmat, int M, int G) {
   using namespace llk_gfx950;
-  const bool mt1 = M <= 32;
-  const int g = (G == 2 || G == 4) ? G : 1;
-  int ks;
-  if (nmat == 2)
-    ks = mt1 ? (g == 1 ? skinny_ks<2, 1, 1>() : g == 2 ? skinny_ks<2, 1, 2>() : skinny_ks<2, 1, 4>())
-             : (g == 1 ? skinny_ks<2, 2, 1>() : g == 2 ? skinny_ks<2, 2, 2>() : skinny_ks<2, 2, 4>());
-  else
-    ks = mt1 ? (g == 1 ? skinny_ks<1, 1, 1>() : g == 2 ? skinny_ks<1, 1, 2>() : skinny_ks<1, 1, 4>())
-             : (g == 1 ? skinny_ks<1, 2, 1>() : g == 2 ? skinny_ks<1, 2, 2>() : skinny_ks<1, 2, 4>());
-  return ks * g * 64;
+  const int w = (G == 2 || G == 4) ? G : 1;
+  if (nmat == 2) return M <= 32 ? skinny_threads_w<2, 1>(w) : skinny_threads_w<2, 2>(w);
+  return M <= 32 ? skinny_threads_w<1, 1>(w) : skinny_threads_w<1, 2>(w);
 }
 
 size_t llk_skinny_workspace_bytes(int nmat, int M, int N_pad, int S) {
@@ -298,7 +333,7 @@ size_t llk_skinny_workspace_bytes(int nmat, int M, int N_pad, int S) {
 
 // Internal: called by the host dispatch layer.  mode 1 = SwiGLU (w0 = Wg,
 // w1 = Wu), mode 0 = GEMM (w0 = B).  M <= 64.  G (1, 2, 4): 32-column
-// groups per workgroup.  `ws` must hold llk_skinny_workspace_bytes(nmat, M,
+// groups per workgroup (the W of SkinnyCfg).  `ws` must hold llk_skinny_workspace_bytes(nmat, M,
 // 128*NB, S) bytes when S > 1.
 hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                              const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
