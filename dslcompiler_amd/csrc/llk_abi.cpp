@@ -268,10 +268,68 @@ bool db_entry(int nmat, int64_t M, llk::ScheduleEntry* out) {
   return true;
 }
 
+// Small-M launch choice: workgroup width W (32-column groups) and k splits
+// S minimising the modelled time
+//   rounds x max(weight bytes / 26.5 GB/s, (weight + X bytes) / 31 GB/s)
+//   + (S > 1: reduce launch ~4 us + partial planes written and read at 4 TB/s)
+// per workgroup, rounds = ceil(workgroups / decode_target_wgs): on MI355X
+// each CU streams its loads at ~26-31 GB/s whatever the grid, so a round's
+// time is one workgroup's bytes.  X is read once per wave group (SkinnyCfg
+// in kernels/swiglu_decode.hip: GW = 2 groups per wave except SwiGLU with
+// M <= 32 or W = 1).  A forced width or split count (> 0) is kept; an
+// automatic width is 2 unless 1 is modelled 3% faster (width 2 measured
+// ahead on ties: decode M = 8 39.9 vs 41.1 us).
+struct SmallMChoice {
+  int width = 2, splits = 1;
+};
+
+SmallMChoice small_m_choice(int nmat, int64_t M, int64_t KB, int64_t NB, int64_t force_w,
+                            int64_t force_s) {
+  const int64_t target = std::max<int64_t>(1, llk::tunable("decode_target_wgs"));
+  const int64_t min_kb = std::max<int64_t>(1, llk::tunable("decode_min_kb"));
+  const int64_t rows = (M + 31) / 32 * 32;
+  auto cost = [&](int64_t W, int64_t S, int64_t* s_out) {
+    const int64_t kbs = (KB + S - 1) / S;
+    const int64_t s_eff = (KB + kbs - 1) / kbs;  // no empty splits
+    const int64_t per_wave = (W == 1 || (nmat == 2 && M <= 32)) ? 1 : 2;
+    const int64_t wave_groups = W / per_wave;
+    const int64_t wgs = NB * 4 / W * s_eff;
+    const double k_bytes = (double)kbs * 64 * 2;
+    const double wbytes = (double)W * 32 * nmat * k_bytes;
+    const double xbytes = (double)wave_groups * M * k_bytes;
+    double t = (double)((wgs + target - 1) / target) *
+               std::max(wbytes / 26.5e9, (wbytes + xbytes) / 31e9);
+    if (s_eff > 1) t += 4e-6 + 2.0 * s_eff * nmat * rows * NB * 128 * 4 / 4e12;
+    *s_out = s_eff;
+    return t;
+  };
+  SmallMChoice best;
+  double best_t = 0.0;
+  const int64_t widths[2] = {2, 1};
+  const bool auto_w = !(force_w == 1 || force_w == 2 || force_w == 4);
+  for (int wi = 0; wi < (auto_w ? 2 : 1); ++wi) {
+    const int64_t W = auto_w ? widths[wi] : force_w;
+    int64_t s_lo = 1, s_hi = std::min<int64_t>(64, std::max<int64_t>(1, KB / min_kb));
+    if (force_s > 0) s_lo = s_hi = std::min(force_s, KB);
+    for (int64_t S = s_lo; S <= s_hi; ++S) {
+      int64_t s_eff = 1;
+      double t = cost(W, S, &s_eff);
+      if (W == 1 && auto_w) t /= 0.97;  // width 1 must win by 3%
+      if (best_t == 0.0 || t < best_t) {
+        best_t = t;
+        best.width = (int)W;
+        best.splits = (int)s_eff;
+      }
+    }
+  }
+  return best;
+}
+
 // x == nullptr: plan for the worst case (X needs padding).  Precedence for
 // each knob: a forced tunable, then the active schedule DB's entry
 // (small-M: group width = BN / 32, splits = grain_size; tile: splits =
-// grain_size; grain_size 0 = choose from the shape), then the heuristics.
+// grain_size; BN 0 or grain_size 0 = choose from the shape), then the cost
+// models (small_m_choice, tile_splits).
 Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const llk_tensor2d* x) {
   Plan p;
   llk::ScheduleEntry se;
@@ -279,22 +337,12 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
   if (M <= std::min<int64_t>(64, llk::tunable("decode_max_m"))) {
     p.skinny = true;
     int64_t gw = llk::tunable("decode_group_width");
-    if (have_db && (se.BN == 32 || se.BN == 64 || se.BN == 128)) gw = se.BN / 32;
-    p.G = (gw == 2 || gw == 4) ? (int)gw : 1;
-    const int64_t groups = NB * 4 / p.G;  // workgroups per k split
+    if (gw <= 0 && have_db && (se.BN == 32 || se.BN == 64 || se.BN == 128)) gw = se.BN / 32;
     int64_t S = llk::tunable("decode_splits");
     if (S <= 0 && have_db && se.grain_size > 0) S = se.grain_size;
-    if (S <= 0) {
-      // As many splits as fit in one round of `target` workgroups: a second
-      // round, or the partial planes and reduce launch, cost more than the
-      // idle CUs of a partly filled round (measured on MI355X).
-      const int64_t target = std::max<int64_t>(1, llk::tunable("decode_target_wgs"));
-      const int64_t min_kb = std::max<int64_t>(1, llk::tunable("decode_min_kb"));
-      S = std::min(std::max<int64_t>(1, target / groups), std::max<int64_t>(1, KB / min_kb));
-    }
-    S = std::max<int64_t>(1, std::min(S, KB));
-    const int64_t kbps = (KB + S - 1) / S;  // no empty splits
-    p.S = static_cast<int>((KB + kbps - 1) / kbps);
+    const SmallMChoice c = small_m_choice(nmat, M, KB, NB, gw, S);
+    p.G = c.width;
+    p.S = c.splits;
     p.ws_bytes = llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), p.S);
     return p;
   }

@@ -13,10 +13,11 @@ struct Knob {
 };
 
 // decode_max_m:      largest M (<= 64) routed to the small-M bandwidth kernel.
-// decode_splits:     force its cross-workgroup k-split count (0 = heuristic).
-// decode_target_wgs: workgroups the split heuristic aims for (1 per CU).
+// decode_splits:     force its cross-workgroup k-split count (0 = cost model).
+// decode_target_wgs: workgroups per round in the small-M cost model (1 per CU).
 // decode_min_kb:     fewest 64-k steps per split.
-// decode_group_width: 32-column groups per small-M workgroup (1, 2 or 4).
+// decode_group_width: force the 32-column groups per small-M workgroup (1, 2
+//                    or 4; 0 = cost model, 2 or 1).
 // tile_splits:       force the tile kernel's k-split count (0 = cost model).
 // tile_wgs_per_wave: workgroups the tile kernel runs at once (1 per CU).
 // tile_min_kb:       fewest 64-k steps per tile-kernel split.
@@ -25,7 +26,7 @@ Knob g_knobs[] = {
     {"decode_splits", {0}},
     {"decode_target_wgs", {256}},
     {"decode_min_kb", {2}},
-    {"decode_group_width", {2}},
+    {"decode_group_width", {0}},
     {"tile_splits", {0}},
     {"tile_wgs_per_wave", {256}},
     {"tile_min_kb", {4}},

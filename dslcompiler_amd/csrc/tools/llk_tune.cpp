@@ -9,14 +9,15 @@
 //            [--copies=0] [--dry-run]
 //
 // Candidates are the dispatcher's launch knobs for the shape's kernel:
-// small-M kernel (M <= 64): 32-column groups per workgroup G in {1, 2, 4}
+// small-M kernel (M <= 64): the dispatcher's own choice (width and splits
+// from its cost model), then 32-column groups per workgroup G in {1, 2, 4}
 // x k splits S in {auto, 1, 2, 3, 4, 6, 8}; tile kernel: S in {auto, 1, 2,
 // 3, 4, 6, 8, 12, 16} (at least 4 k-steps of 64 per split).  Each is timed
 // with HIP events (best of 3 windows of --measure-ms after a warm-up); the
 // --top fastest are written as schedule_db.json records in the reference
 // schema with this target's field meaning (BN = 32 G for the small-M
-// kernel, grain_size = S, 0 = auto), best first, so that the loader's
-// first-match rule picks the best.  --copies rotates weight sets (default:
+// kernel, grain_size = S; 0 = the dispatcher chooses), best first, so that
+// the loader's first-match rule picks the best.  --copies rotates weight sets (default:
 // enough to exceed the 256 MB MALL for small M, 1 otherwise).
 #include <hip/hip_runtime_api.h>
 
@@ -65,7 +66,7 @@ double now_ms() {
 }
 
 struct Candidate {
-  int G = 0;  // 0: tile kernel
+  int G = 0;  // small-M workgroup width; 0: chosen by the dispatcher (or tile kernel)
   int S = 0;  // 0: auto
   llk_launch_plan plan{};
   double us = 0.0;
@@ -107,7 +108,7 @@ int main(int argc, char** argv) {
   check_llk(llk_get_tunable("decode_splits", &saved_ds), "tunable");
   check_llk(llk_get_tunable("tile_splits", &saved_ts), "tunable");
   auto apply = [&](const Candidate& c) {
-    check_llk(llk_set_tunable("decode_group_width", c.G ? c.G : saved_g), "tunable");
+    check_llk(llk_set_tunable("decode_group_width", small ? c.G : saved_g), "tunable");
     check_llk(llk_set_tunable(small ? "decode_splits" : "tile_splits", c.S), "tunable");
   };
   auto restore = [&]() {
@@ -116,6 +117,7 @@ int main(int argc, char** argv) {
     (void)llk_set_tunable("tile_splits", saved_ts);
   };
   if (small) {
+    cands.push_back({0, 0});  // the dispatcher's own choice (width and splits)
     for (int g : gs)
       for (int s : small_s)
         if (s <= KB) cands.push_back({g, s});
@@ -134,7 +136,8 @@ int main(int argc, char** argv) {
     bool dup = false;
     for (const auto& u : uniq)
       dup |= u.plan.kernel == c.plan.kernel && u.plan.splits == c.plan.splits &&
-             u.plan.group_width == c.plan.group_width && (u.S == 0) == (c.S == 0);
+             u.plan.group_width == c.plan.group_width && (u.S == 0) == (c.S == 0) &&
+             (u.G == 0) == (c.G == 0);
     if (!dup) uniq.push_back(c);
   }
   cands.swap(uniq);
@@ -220,7 +223,8 @@ int main(int argc, char** argv) {
   std::printf("\n%s candidates:\n", dry ? "Generated" : "Measured");
   for (size_t i = 0; i < cands.size(); ++i) {
     const auto& c = cands[i];
-    std::printf("  [%zu] G=%d S=%s -> splits=%d group_width=%d workgroups=%lld", i, c.G,
+    std::printf("  [%zu] G=%s S=%s -> splits=%d group_width=%d workgroups=%lld", i,
+                c.G ? std::to_string(c.G).c_str() : "auto",
                 c.S ? std::to_string(c.S).c_str() : "auto", c.plan.splits, c.plan.group_width,
                 (long long)c.plan.workgroups);
     if (!dry)
@@ -238,7 +242,8 @@ int main(int argc, char** argv) {
     const auto& c = cands[i];
     const bool sm = c.plan.kernel == 0;
     const int64_t BM = sm ? (M <= 32 ? 32 : 64) : 256;
-    const int64_t BN = sm ? 32 * c.plan.group_width : (swiglu ? 128 : 256);
+    // BN 0 / grain_size 0: the dispatcher chooses for each shape
+    const int64_t BN = sm ? (c.G ? 32 * c.plan.group_width : 0) : (swiglu ? 128 : 256);
     std::fprintf(f,
                  "    {\"operation\": \"%s\", \"target\": \"gfx950\", \"shape\": {\"M_bucket\": %d, "
                  "\"N\": %lld, \"K\": %lld}, \"dtype\": \"bf16\", \"math_mode\": \"strict\",\n"

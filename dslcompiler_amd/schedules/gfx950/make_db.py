@@ -28,6 +28,8 @@ SHAPES += [("matmul", m, 5120, 13824) for m in (1, 17, 255, 1000, 4097)]
 # the down projection, bucket 1 of SwiGLU)
 SHAPES += [("fused_swiglu", 4, 14336, 4096), ("matmul", 4, 5120, 13824),
            ("matmul", 8, 5120, 13824), ("matmul", 16, 5120, 13824)]
+# batch-64 decode: bucket 3 also spans two 32-row groups
+SHAPES += [("fused_swiglu", 64, 14336, 4096), ("matmul", 64, 5120, 13824)]
 
 
 def tune(op: str, M: int, N: int, K: int, measure_ms: int) -> list[dict]:

@@ -278,8 +278,9 @@ int llk_fill_normal_bf16(uint64_t seed, uint64_t stream, float sigma,
 
 /* Named integer knobs of the dispatch heuristics: "decode_max_m" (largest M
  * sent to the small-M kernel), "decode_splits" (force its k-split count,
- * 0 = heuristic), "decode_target_wgs", "decode_min_kb",
- * "decode_group_width" (32-column groups per small-M workgroup: 1, 2, 4),
+ * 0 = cost model), "decode_target_wgs", "decode_min_kb",
+ * "decode_group_width" (force the 32-column groups per small-M workgroup:
+ * 1, 2, 4; 0 = cost model),
  * "tile_splits" (force the tile kernel's k-split count, 0 = cost model),
  * "tile_wgs_per_wave", "tile_min_kb".  Returns LLK_OK or
  * LLK_ERR_INVALID_ARGUMENT for an unknown name. */

@@ -176,6 +176,37 @@ def test_describe_launch_configs():
     assert llk.lib().llk_describe_launch(0, 0, 8, 8, 1, C.byref(plan)) == -2
 
 
+def test_small_m_cost_model_choices():
+    """The small-M dispatcher's (width, splits) against llk-tune's measured
+    best on MI355X for the BASELINE decode shapes: config 1 (M=64, N=1376,
+    K=512: 8.27 us at width 1 unsplit; every split adds ~2.8 us), config 4
+    (width 2 unsplit, 224 workgroups), M=64 decode (width 2: 53.9 us vs 68.0
+    at width 1), the config-5 down projection (width 2, 3 splits: 240
+    workgroups in one round)."""
+    plan = lambda op, M, N, K: (lambda p: (p["group_width"], p["splits"]))(  # noqa: E731
+        llk.describe_launch(op, M, N, K))
+    assert plan("fused_swiglu", 64, 1376, 512) == (1, 1)
+    for M in (1, 8, 16, 64):
+        assert plan("fused_swiglu", M, 14336, 4096) == (2, 1)
+    assert plan("fused_swiglu", 17, 13824, 5120) == (2, 1)
+    for M in (1, 17, 64):
+        assert plan("matmul", M, 5120, 13824) == (2, 3)
+    # a narrow N spreads K over splits instead
+    w, s = plan("fused_swiglu", 8, 128, 4096)
+    assert s > 8
+    # forced knobs are kept as given
+    old_w, old_s = llk.get_tunable("decode_group_width"), llk.get_tunable("decode_splits")
+    try:
+        llk.set_tunable("decode_group_width", 4)
+        assert plan("fused_swiglu", 64, 1376, 512)[0] == 4
+        llk.set_tunable("decode_splits", 2)
+        assert plan("fused_swiglu", 8, 14336, 4096) == (4, 2)
+    finally:
+        llk.set_tunable("decode_group_width", old_w)
+        llk.set_tunable("decode_splits", old_s)
+    assert old_w == 0 and old_s == 0  # defaults: chosen by the cost model
+
+
 def test_tile_kernel_k_limit():
     """K beyond the tile kernel's 32-bit offsets is an error, not a launch;
     the small-M kernel has no such limit."""
