@@ -62,13 +62,21 @@ def _time_loop(torch, fn, steps: int, warmup: int, min_warm_s: float = 0.0) -> f
     return e0.elapsed_time(e1) / steps
 
 
-def bench_prefill(torch, llk, steps, warmup):
+def bench_prefill(torch, llk, steps, warmup, fill="normal"):
+    """fill "const" (diagnostic, --only runs): every operand the bf16 0x3C3C
+    (~0.0115), so the MFMA datapath sees no bit toggling; the time difference
+    to "normal" is the data-dependent power / clock effect."""
     from common import STREAM_WG, STREAM_WU, STREAM_X
     from gpu_util import to_dev
     M, K, N = PREFILL["M"], PREFILL["K"], PREFILL["N"]
-    x = llk.fill_normal_bf16(42, STREAM_X, (M, K))
-    wg = llk.fill_normal_bf16(42, STREAM_WG, (K, N), 1.0 / np.sqrt(K))
-    wu = llk.fill_normal_bf16(42, STREAM_WU, (K, N), 1.0 / np.sqrt(K))
+    if fill == "const":
+        x = np.full((M, K), 0x3C3C, np.uint16)
+        wg = np.full((K, N), 0x3C3C, np.uint16)
+        wu = wg.copy()
+    else:
+        x = llk.fill_normal_bf16(42, STREAM_X, (M, K))
+        wg = llk.fill_normal_bf16(42, STREAM_WG, (K, N), 1.0 / np.sqrt(K))
+        wu = llk.fill_normal_bf16(42, STREAM_WU, (K, N), 1.0 / np.sqrt(K))
     pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
     xd = to_dev(torch, x)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
@@ -204,6 +212,9 @@ def main() -> None:
                     help="run one workload for --steps launches and print its timing only "
                          "(for profiler runs); 'copy' is a 256 MiB device copy used to "
                          "calibrate byte counters")
+    ap.add_argument("--fill", choices=["normal", "const"], default="normal",
+                    help="operands of --only prefill: N(0,1) data (default) or one constant "
+                         "value (diagnostic: MFMA power depends on operand bit toggling)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this hot path runs on one GPU; multi-GPU runs are not part of this "
@@ -217,7 +228,8 @@ def main() -> None:
 
     if a.only:
         if a.only == "prefill":
-            r = {"ms": bench_prefill(torch, llk, a.steps, a.warmup)["ms"]}
+            pre = bench_prefill(torch, llk, a.steps, a.warmup, a.fill)
+            r = {"ms": pre["ms"], "tflops": pre["tflops"], "fill": a.fill}
         elif a.only in ("decode8", "decode64"):
             r = bench_decode(torch, llk, int(a.only[6:]), a.steps, a.warmup)
         elif a.only == "gemm":
