@@ -265,9 +265,14 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   // 4*(lane/32) + r%4 for its 16 values r of each 32 x 32 tile.
   const int h4 = 4 * (lane >> 5);
   const int mr = lane & 31;
+  // A tile that lies wholly inside Y (or the partial planes) stores without
+  // per-element bounds checks (a wave-uniform branch per store; ragged edge
+  // tiles take the checked path).
+  const int n_end = (MODE == 1) ? tn * 128 + 128 : tn * 256 + 256;
   if constexpr (SPLIT) {
     constexpr int NMAT = (MODE == 1) ? 2 : 1;
     const size_t plane = (size_t)a.M * a.n_pad;
+    const bool interior = m0 + kTileM <= a.M && n_end <= a.n_pad;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       // SwiGLU: i < 2 gate, i >= 2 up (same n); GEMM: four n sub-tiles.
@@ -282,13 +287,15 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
                                     : (tn * 256 + wn * 128 + i * 32 + 8 * g + h4);
           const float v[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
                               acc[i][j][4 * g + 3]};
-          store4<kOutF32>(dst, a.n_pad, a.M, a.n_pad, m, n, v, true);
+          if (interior) store4_unchecked<kOutF32>(dst, a.n_pad, m, n, v);
+          else store4<kOutF32>(dst, a.n_pad, a.M, a.n_pad, m, n, v, true);
         }
       }
     }
     return;
   }
   constexpr int NI = (MODE == 1) ? 2 : 4;
+  const bool interior = YVEC && m0 + kTileM <= a.M && n_end <= a.N;
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
 #pragma unroll
@@ -303,7 +310,8 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
         for (int q = 0; q < 4; ++q)
           v[q] = (MODE == 1) ? swiglu_act(acc[i][j][4 * g + q], acc[i + 2][j][4 * g + q])
                              : acc[i][j][4 * g + q];
-        store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, YVEC);
+        if (interior) store4_unchecked<OUT>(a.y, a.ldy, m, n, v);
+        else store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, YVEC);
       }
     }
   }

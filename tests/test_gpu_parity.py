@@ -293,6 +293,32 @@ def test_swiglu_exact_integers(llk, gpu, orc, M):
     assert np.mean(d == 0) > 0.99
 
 
+@pytest.mark.parametrize("M", [1, 65])
+def test_swiglu_epilogue_accuracy(llk, gpu, M):
+    """The SiLU(g) * u epilogue alone (K = 1, X = 1, Wg = g, Wu = 1, so gate
+    and up are exact) on every finite bf16 g with |g| <= 80, on the small-M
+    (M = 1) and tile (M = 65) kernels: within 4 ulp of the correctly rounded
+    g / (1 + exp(-g)) (fp64 closed form; expf plus an IEEE divide is within
+    3 ulp on the same set)."""
+    print(f"case swiglu epilogue accuracy M={M}", flush=True)
+    bits = np.arange(1 << 16, dtype=np.uint32)
+    gv = (bits << 16).view(np.float32)
+    gv = np.unique(gv[np.isfinite(gv) & (np.abs(gv) <= 80.0)])
+    N = gv.size
+    x = to_bf16_bits(np.ones((M, 1), np.float32))
+    wg = to_bf16_bits(gv.reshape(1, N))
+    wu = to_bf16_bits(np.ones((1, N), np.float32))
+    yf = _run_swiglu(llk, gpu, x, wg, wu, gpu.float32)
+    g = gv.astype(np.float64)
+    ref = (g / (1.0 + np.exp(-g))).astype(np.float32)
+    def ordered(a):  # float32 -> integers in value order (+0 and -0 both 0)
+        i = a.view(np.int32).astype(np.int64)
+        return np.where(i < 0, -(i & 0x7FFFFFFF), i)
+    for row in (0, M - 1):
+        ulp = np.abs(ordered(yf[row]) - ordered(ref))
+        assert ulp.max() <= 4, (ulp.max(), gv[ulp.argmax()])
+
+
 def test_swiglu_known_values(llk, gpu):
     """swiglu_reference.cpp:156-175 (X=1, Wg=2, Wu=3 -> 5.2847825) and
     edge_cases.cpp:47-60 (x=2, wg=.5, wu=.3 -> 0.43863515)."""
