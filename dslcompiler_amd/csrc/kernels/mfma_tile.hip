@@ -63,6 +63,7 @@ constexpr int kStageBytes = 32768;    // 16 KiB weights + 16 KiB X
 constexpr int kXOff = 16384;          // X rows inside a stage
 constexpr int kStages = 4;            // LDS ring of stages
 constexpr int kLoadsPerStage = 8;     // buffer_load ... lds per wave per stage
+constexpr int kStripRow = 144;        // epilogue staging: 128-byte rows + 16-byte pad
 
 // s_waitcnt with vmcnt(n) (n < 64) and the other counters left alone.
 template <int N>
@@ -265,55 +266,109 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   // 4*(lane/32) + r%4 for its 16 values r of each 32 x 32 tile.
   const int h4 = 4 * (lane >> 5);
   const int mr = lane & 31;
-  // A tile that lies wholly inside Y (or the partial planes) stores without
-  // per-element bounds checks (a wave-uniform branch per store; ragged edge
-  // tiles take the checked path).
   const int n_end = (MODE == 1) ? tn * 128 + 128 : tn * 256 + 256;
+  // Outputs go through LDS: each wave writes a 128-byte-wide column strip
+  // of its 128 rows into LDS (144-byte rows, 16-byte pad), then copies whole
+  // 128-byte row segments out, 8 rows per instruction, where the accumulator
+  // layout would store 8- or 16-byte pieces of 32 rows per instruction
+  // (measured: GEMM 4096^3 epilogue 12 -> 3.4 us).  A tile wholly inside Y
+  // (or the partial planes) with 16-byte aligned rows copies 16-byte chunks
+  // unchecked; an edge tile checks each chunk and copies the chunks that
+  // straddle a bound (or unaligned rows) element by element.  The stage ring
+  // is free once every wave is past its last operand read.
+  __syncthreads();
+  uint8_t* const strip = smem + wave * (128 * kStripRow);
+  // Copies the wave's strip to gdst (row 0, column 0 of the strip in the
+  // destination; E-byte elements; rows_ok / cols_ok in bounds).
+  auto strip_out = [&](auto E, bool fast, bool al16, uint8_t* gdst, int64_t ld_bytes,
+                       int rows_ok, int cols_ok) {
+    constexpr int kE = decltype(E)::value;
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's strip writes are done
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int row = k * 8 + (lane >> 3);
+      const uint4 d = *reinterpret_cast<const uint4*>(strip + row * kStripRow + (lane & 7) * 16);
+      uint8_t* const out = gdst + row * ld_bytes + (lane & 7) * 16;
+      const int c0 = (lane & 7) * (16 / kE);
+      if (fast || (al16 && row < rows_ok && c0 + 16 / kE <= cols_ok)) {
+        *reinterpret_cast<uint4*>(out) = d;
+      } else if (row < rows_ok) {
+        const uint32_t w[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+        for (int e = 0; e < 16 / kE; ++e) {
+          if (c0 + e >= cols_ok) break;
+          if constexpr (kE == 4) reinterpret_cast<uint32_t*>(out)[e] = w[e];
+          else reinterpret_cast<uint16_t*>(out)[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // ... and its reads, before the strip is rewritten
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+  };
+  const int rows_ok = a.M - (m0 + wm * 128);
   if constexpr (SPLIT) {
     constexpr int NMAT = (MODE == 1) ? 2 : 1;
     const size_t plane = (size_t)a.M * a.n_pad;
-    const bool interior = m0 + kTileM <= a.M && n_end <= a.n_pad;
+    const bool fast = m0 + kTileM <= a.M && n_end <= a.n_pad;  // plane rows are 16-byte aligned
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       // SwiGLU: i < 2 gate, i >= 2 up (same n); GEMM: four n sub-tiles.
       const int mat = (MODE == 1) ? (i >> 1) : 0;
-      float* dst = a.part + ((size_t)split * NMAT + mat) * plane;
+      const int col0 = (MODE == 1) ? tn * 128 + wn * 64 + (i & 1) * 32 : tn * 256 + wn * 128 + i * 32;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int m = m0 + wm * 128 + j * 32 + mr;
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int n = (MODE == 1) ? (tn * 128 + wn * 64 + (i & 1) * 32 + 8 * g + h4)
-                                    : (tn * 256 + wn * 128 + i * 32 + 8 * g + h4);
-          const float v[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                              acc[i][j][4 * g + 3]};
-          if (interior) store4_unchecked<kOutF32>(dst, a.n_pad, m, n, v);
-          else store4<kOutF32>(dst, a.n_pad, a.M, a.n_pad, m, n, v, true);
-        }
-      }
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4*>(strip + (j * 32 + mr) * kStripRow + (8 * g + h4) * 4) =
+              f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                    acc[i][j][4 * g + 3]};
+      strip_out(std::integral_constant<int, 4>{}, fast, true,
+                reinterpret_cast<uint8_t*>(a.part + ((size_t)split * NMAT + mat) * plane +
+                                           (size_t)(m0 + wm * 128) * a.n_pad + col0),
+                (int64_t)a.n_pad * 4, rows_ok, a.n_pad - col0);
     }
     return;
   }
   constexpr int NI = (MODE == 1) ? 2 : 4;
-  const bool interior = YVEC && m0 + kTileM <= a.M && n_end <= a.N;
+  constexpr int kElem = (OUT == kOutF32) ? 4 : 2;
+  constexpr int kPerStrip = 128 / (32 * kElem);  // 32-column groups per strip: 2 or 1
+  const bool al16 = ((reinterpret_cast<uintptr_t>(a.y) | (uintptr_t)(a.ldy * kElem)) & 15) == 0;
+  const bool fast = YVEC && m0 + kTileM <= a.M && n_end <= a.N && al16;
+  const int n_w = (MODE == 1) ? tn * 128 + wn * 64 : tn * 256 + wn * 128;
+  uint8_t* const ybase =
+      static_cast<uint8_t*>(a.y) + ((size_t)max(0, m0 + wm * 128) * a.ldy + n_w) * kElem;
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
+  for (int sidx = 0; sidx < NI / kPerStrip; ++sidx) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = m0 + wm * 128 + j * 32 + mr;
+    for (int ii = 0; ii < kPerStrip; ++ii) {
+      const int i = sidx * kPerStrip + ii;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = (MODE == 1) ? (tn * 128 + wn * 64 + i * 32 + 8 * g + h4)
-                                  : (tn * 256 + wn * 128 + i * 32 + 8 * g + h4);
-        float v[4];
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          v[q] = (MODE == 1) ? swiglu_act(acc[i][j][4 * g + q], acc[i + 2][j][4 * g + q])
-                             : acc[i][j][4 * g + q];
-        if (interior) store4_unchecked<OUT>(a.y, a.ldy, m, n, v);
-        else store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, YVEC);
-      }
+        for (int g = 0; g < 4; ++g) {
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            v[q] = (MODE == 1) ? swiglu_act(acc[i][j][4 * g + q], acc[i + 2][j][4 * g + q])
+                               : acc[i][j][4 * g + q];
+          uint8_t* const dst = strip + (j * 32 + mr) * kStripRow + (ii * 32 + 8 * g + h4) * kElem;
+          if constexpr (OUT == kOutF32) {
+            *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+          } else if constexpr (OUT == kOutBF16) {
+            *reinterpret_cast<uint2*>(dst) =
+                make_uint2(f32x2_to_bf16x2_rne(v[0], v[1]), f32x2_to_bf16x2_rne(v[2], v[3]));
+          } else {
+            *reinterpret_cast<uint2*>(dst) =
+                make_uint2((uint32_t)f32_to_f16_rne(v[0]) | ((uint32_t)f32_to_f16_rne(v[1]) << 16),
+                           (uint32_t)f32_to_f16_rne(v[2]) | ((uint32_t)f32_to_f16_rne(v[3]) << 16));
+          }
+        }
     }
+    strip_out(std::integral_constant<int, kElem>{}, fast, al16, ybase + sidx * 128,
+              a.ldy * kElem, rows_ok, a.N - (n_w + sidx * 128 / kElem));
   }
 }
 
