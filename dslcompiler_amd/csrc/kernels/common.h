@@ -110,25 +110,6 @@ __device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
   return __builtin_bit_cast(uint16_t, h);
 }
 
-// Stores 4 consecutive n of output row m with one vector store, no bounds
-// checks: the caller guarantees m < M, n + 4 <= N and an aligned row
-// (OUT: bf16, fp16 or fp32; both 16-bit types rounded to nearest even).
-template <int OUT>
-__device__ __forceinline__ void store4_unchecked(void* y, int64_t ldy, int m, int n,
-                                                 const float (&v)[4]) {
-  if (OUT == kOutF32) {
-    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(y) + (size_t)m * ldy + n) =
-        f32x4{v[0], v[1], v[2], v[3]};
-  } else if (OUT == kOutBF16) {
-    const uint2 h = make_uint2(f32x2_to_bf16x2_rne(v[0], v[1]), f32x2_to_bf16x2_rne(v[2], v[3]));
-    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(y) + (size_t)m * ldy + n) = h;
-  } else {
-    u16x4 h = {f32_to_f16_rne(v[0]), f32_to_f16_rne(v[1]), f32_to_f16_rne(v[2]),
-               f32_to_f16_rne(v[3])};
-    *reinterpret_cast<u16x4*>(reinterpret_cast<uint16_t*>(y) + (size_t)m * ldy + n) = h;
-  }
-}
-
 // Stores 4 consecutive n of output row m (OUT: bf16, fp16 or fp32; both
 // 16-bit types rounded to nearest even), bounds-checked.
 template <int OUT>

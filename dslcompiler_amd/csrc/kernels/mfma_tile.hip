@@ -4,7 +4,7 @@
 // Computes  D^T = W^T X^T  on v_mfma_f32_32x32x16_bf16: the packed weight
 // (n rows, k contiguous) is the MFMA A operand and the activation X (m rows,
 // k contiguous) is the B operand, so each lane's accumulators are runs of
-// four consecutive n of one output row m (8- or 16-byte stores).
+// four consecutive n of one output row m.
 //
 // Workgroup: 256 threads (4 waves, 2 x 2).  Workgroup tile 256 m x 256
 // MFMA rows:  GEMM -> 256 n;  SwiGLU -> 128 n of Wg + the same 128 n of Wu,
@@ -24,6 +24,10 @@
 // in LDS as 1 KiB MFMA-ordered sub-blocks (contiguous, conflict-free operand
 // reads); X as XOR-swizzled 64-byte rows, so its loads move whole rows and
 // its operand reads are conflict-free too.
+//
+// Epilogue: SiLU(g)*u (SwiGLU), rounding to the output type, and stores
+// staged through the freed LDS ring so that every store instruction writes
+// whole 128-byte row segments.
 //
 // Optional k split across workgroups (SPLIT): raw fp32 partial planes plus
 // split_reduce_kernel, which sums them in split order and applies the
