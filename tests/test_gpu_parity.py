@@ -273,6 +273,50 @@ def test_swiglu_outliers(llk, gpu, orc):
     _check_swiglu(llk, gpu, orc, x, wg, wu, "outliers")
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+def test_y_misaligned_base(llk, gpu, orc, dtype):
+    """Outputs written to a view that starts one element into its buffer (no
+    16-byte row alignment, 2- or 4-byte aligned) on ragged tiles: the
+    epilogue's element-wise stores, for SwiGLU (bf16, f32) and GEMM (every
+    result type); the columns either side of the view stay untouched."""
+    print(f"case y misaligned base {dtype}", flush=True)
+    M, K, N = 300, 256, 200
+    x, wg, wu = swiglu_inputs(M, K, N, seed=77)
+    tdt = {"bf16": gpu.bfloat16, "f16": gpu.float16, "f32": gpu.float32}[dtype]
+    xd = to_dev(gpu, x)
+
+    def run(fn, *w):
+        buf = gpu.full((M, N + 8), 7.0, dtype=tdt, device="cuda")
+        y = buf[:, 1:N + 1]
+        fn(xd, *w, out=y)
+        gpu.cuda.synchronize()
+        host = from_dev(buf)
+        edge = np.concatenate([host[:, :1], host[:, N + 1:]], axis=1)
+        as_f32 = edge.astype(np.float32) if dtype != "bf16" else bf16_bits_to_f32(edge)
+        assert np.all(as_f32 == 7.0), "wrote outside the view"
+        return host[:, 1:N + 1]
+
+    pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
+    yf_ref, _ = orc.swiglu(x, wg, wu)
+    if dtype == "f32":
+        assert_parity(run(llk.fused_swiglu, pg, pu), yf_ref, "swiglu misaligned f32")
+    elif dtype == "bf16":
+        assert_parity_bf16(run(llk.fused_swiglu, pg, pu), yf_ref, "swiglu misaligned bf16")
+    b = normal_bf16(9, 1, (K, N), 1.0 / np.sqrt(K))
+    cf_ref, _ = orc.gemm(x, b)
+    pb = llk.PackedWeights.from_host(b)
+    c = run(llk.matmul, pb)
+    if dtype == "f32":
+        assert_parity(c, cf_ref, "gemm misaligned f32")
+    elif dtype == "bf16":
+        assert_parity_bf16(c, cf_ref, "gemm misaligned bf16")
+    else:
+        # fp16 result = RNE of the kernel's fp32 sum (the same kernel, aligned)
+        cf = from_dev(llk.matmul(xd, pb, out_dtype=gpu.float32))
+        assert_parity(cf, cf_ref, "gemm misaligned f16 (fp32 run)")
+        assert np.array_equal(c.view(np.uint16), cf.astype(np.float16).view(np.uint16))
+
+
 @pytest.mark.parametrize("M", [3, 100])
 def test_swiglu_exact_integers(llk, gpu, orc, M):
     """Small-integer inputs: every product and partial sum is exact in fp32,
