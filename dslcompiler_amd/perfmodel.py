@@ -5,11 +5,19 @@ For one call the model takes the dispatcher's launch plan
 (llk_describe_launch) and returns
     compute = rounds x per-workgroup MFMA work / per-CU rate,
               rounds = ceil(workgroups / CUs)  (one workgroup per CU at a time)
-    memory  = (weights + X + Y + split partials written and read back) / stream rate
-    per_cu  = small-M kernel only: rounds x max(weight share / per-CU weight rate,
+    memory  = (weights + X + Y, or the partial planes written instead of Y) / stream rate
+    per_cu  = per-CU loads.  Tile kernel: rounds x (weight panel / weight rate
+              + X panel / L2 rate), the weight rate being HBM's when there is
+              one m tile (each weight byte is read once, from HBM) and L2's
+              otherwise; a single-round k split adds the partial-plane write
+              burst that every workgroup issues at the same moment.
+              Small-M kernel: rounds x max(weight share / per-CU weight rate,
               (weight share + X reads) / per-CU load rate); a workgroup reads
               X once per wave group, so at M = 64 X is as large as the weights
-    time    = max(compute, memory, per_cu, shortest launch) + (launches - 1) x launch gap.
+    reduce  = tile k split only: the reduce kernel reads the partial planes and
+              writes Y, after the main kernel
+    time    = max(compute, memory, per_cu, shortest launch) + reduce
+              + (launches - 1) x launch gap.
 The small-M kernel's MFMA work counts whole 32-row groups.
 """
 from __future__ import annotations
@@ -39,11 +47,24 @@ def predict(op: str, M: int, N: int, K: int, machine_path: str = str(MACHINE)) -
     plan = describe_launch(op, M, N, K)
     nmat = 2 if op == "fused_swiglu" else 1
     S = plan["splits"]
-    if plan["kernel"] == "tile":
-        rows = 256 if op == "fused_swiglu" else 256  # MFMA rows per workgroup tile
-        wg_flops = 2.0 * 256 * rows * math.ceil(K / 64) * 64 / S
-        compute = math.ceil(plan["workgroups"] / cus) * wg_flops / cal["tile_flops_per_cu"]
     per_cu = 0.0
+    reduce = 0.0
+    partials = 2.0 * plan["workspace_bytes"] if S > 1 else 0.0
+    if plan["kernel"] == "tile":
+        # Workgroup tile: 256 m x 256 MFMA rows (SwiGLU: 128 n of Wg + 128 n of Wu).
+        kpart = math.ceil(K / 64) * 64 / S
+        rounds = math.ceil(plan["workgroups"] / cus)
+        compute = rounds * 2.0 * 256 * 256 * kpart / cal["tile_flops_per_cu"]
+        # Per-CU loads: one m tile means every weight byte comes from HBM
+        # once; with more m tiles the panels are re-read from L2 / MALL.
+        w_rate = (cal["tile_hbm_weight_bytes_per_cu_s"] if math.ceil(M / 256) == 1
+                  else cal["tile_l2_bytes_per_cu_s"])
+        per_cu = rounds * (256 * kpart * 2.0 / w_rate
+                           + min(M, 256) * kpart * 2.0 / cal["tile_l2_bytes_per_cu_s"])
+        if S > 1:  # split_reduce_kernel: reads the partial planes, writes Y
+            reduce = (partials / 2 + 2.0 * M * N) / cal["stream_bytes_per_s"]
+            if rounds == 1:  # every workgroup writes its partials at once, after its loads
+                per_cu += partials / 2 / cal["stream_bytes_per_s"]
     if plan["kernel"] != "tile":
         groups = plan["workgroups"]
         mrows = 32 * math.ceil(M / 32)
@@ -59,12 +80,15 @@ def predict(op: str, M: int, N: int, K: int, machine_path: str = str(MACHINE)) -
         x_wg = (width // gw) * M * kpart * 2.0
         per_cu = math.ceil(groups / cus) * max(w_wg / cal["small_m_weight_bytes_per_cu_s"],
                                                (w_wg + x_wg) / cal["small_m_bytes_per_cu_s"])
-    partials = 2.0 * plan["workspace_bytes"] if S > 1 else 0.0
-    nbytes = 2.0 * nmat * K * N + 2.0 * M * K + 2.0 * M * N + partials
+    if reduce:  # the main kernel writes the partial planes, the reduce reads them and writes Y
+        nbytes = 2.0 * nmat * K * N + 2.0 * M * K + partials / 2
+    else:
+        nbytes = 2.0 * nmat * K * N + 2.0 * M * K + 2.0 * M * N + partials
     memory = nbytes / cal["stream_bytes_per_s"]
-    t = max(compute, memory, per_cu, cal["launch_min_s"]) + (plan["launches"] - 1) * cal["launch_gap_s"]
+    t = (max(compute, memory, per_cu, cal["launch_min_s"]) + reduce
+         + (plan["launches"] - 1) * cal["launch_gap_s"])
     return {"compute_us": compute * 1e6, "memory_us": memory * 1e6, "per_cu_us": per_cu * 1e6,
-            "predicted_us": t * 1e6,
+            "reduce_us": reduce * 1e6, "predicted_us": t * 1e6,
             "bound": "mfma" if compute >= max(memory, per_cu) else "hbm", "plan": plan}
 
 
