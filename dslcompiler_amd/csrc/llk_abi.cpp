@@ -76,8 +76,9 @@ struct DeviceState {
   int checked = 0;  // 0 unknown, 1 gfx950, -1 other
   char arch[64] = {0};
   int cu_count = 0, lds = 0, clock_khz = 0;
-  void* ws = nullptr;  // library-owned workspace (counters zeroed)
+  void* ws = nullptr;  // library-owned workspace, zero-filled when allocated
   size_t ws_bytes = 0;
+  std::vector<void*> retired;  // outgrown workspaces, kept until process exit
 };
 DeviceState g_dev[kMaxDevices];
 
@@ -149,7 +150,11 @@ bool y_vec_ok(const llk_tensor2d* y, int dtype) {
 // Workspace: the caller's (ctx->scratch) if given, else the library's own
 // per-device buffer, grown on demand.  Launches that use the library's
 // buffer on different streams of one device must not overlap (pass a
-// scratch buffer per stream instead).
+// scratch buffer per stream instead).  An outgrown buffer is retired, not
+// freed: launches still queued, captured in a graph or about to be issued
+// by another thread may name it, and freeing would need a device-wide
+// synchronisation.  Growth is geometric (x1.5 at least), so the retired
+// buffers add up to less than twice the current one.
 int get_workspace(int dev, size_t need, llk_kernel_context* ctx, void** out) {
   *out = nullptr;
   if (need == 0) return LLK_OK;
@@ -165,22 +170,24 @@ int get_workspace(int dev, size_t need, llk_kernel_context* ctx, void** out) {
   DeviceState& st = g_dev[dev];
   std::lock_guard<std::mutex> lk(st.mu);
   if (st.ws_bytes < need) {
-    if (st.ws) {
-      hipError_t e = hipDeviceSynchronize();
-      if (e != hipSuccess) return fail_hip(e, "hipDeviceSynchronize");
-      (void)hipFree(st.ws);
-      st.ws = nullptr;
-      st.ws_bytes = 0;
-    }
-    size_t bytes = std::max(need, (size_t)1 << 20);
-    hipError_t e = hipMalloc(&st.ws, bytes);
-    if (e != hipSuccess) {
-      st.ws = nullptr;
+    const size_t bytes = std::max({need, st.ws_bytes + st.ws_bytes / 2, (size_t)1 << 20});
+    void* fresh = nullptr;
+    hipError_t e = hipMalloc(&fresh, bytes);
+    if (e != hipSuccess)
       return fail(LLK_ERR_OUT_OF_MEMORY, "hipMalloc(%zu) for workspace: %s", bytes,
                   hipGetErrorString(e));
+    e = hipMemset(fresh, 0, bytes);
+    if (e != hipSuccess) {
+      (void)hipFree(fresh);
+      return fail_hip(e, "hipMemset(workspace)");
     }
-    e = hipMemset(st.ws, 0, bytes);
-    if (e != hipSuccess) return fail_hip(e, "hipMemset(workspace)");
+    try {
+      if (st.ws) st.retired.push_back(st.ws);
+    } catch (const std::bad_alloc&) {
+      (void)hipFree(fresh);
+      return fail(LLK_ERR_OUT_OF_MEMORY, "workspace bookkeeping");
+    }
+    st.ws = fresh;
     st.ws_bytes = bytes;
   }
   *out = st.ws;
@@ -521,7 +528,15 @@ int llk_pack_weights_device(const llk_tensor2d* w, int64_t bk, void* stream,
   if (!pw) return fail(LLK_ERR_OUT_OF_MEMORY, "handle allocation");
   fill_meta(pw, w->dim0, w->dim1, bk);
   pw->dev_bytes = llk::deviceLayoutBytes(pw->K, pw->N);
-  if (pw->dev_bytes > 0) {
+  if (pw->dev_bytes == 0) {
+    // Empty matrix: a small zeroed payload, as llk_pack_weights keeps.
+    hipError_t e = hipMalloc(&pw->dev, 256);
+    if (e == hipSuccess) e = hipMemset(pw->dev, 0, 256);
+    if (e != hipSuccess) {
+      llk_packed_weights_free(pw);
+      return fail_hip(e, "hipMalloc(empty payload)");
+    }
+  } else {
     hipError_t e = hipMalloc(&pw->dev, pw->dev_bytes);
     if (e != hipSuccess) {
       pw->dev = nullptr;
@@ -928,9 +943,7 @@ int llk_set_tunable(const char* name, int64_t value) {
 
 int llk_get_tunable(const char* name, int64_t* value) {
   if (!name || !value) return fail(LLK_ERR_INVALID_ARGUMENT, "NULL argument");
-  if (!llk::setTunable(name, llk::tunable(name)))
-    return fail(LLK_ERR_INVALID_ARGUMENT, "unknown tunable %s", name);
-  *value = llk::tunable(name);
+  if (!llk::getTunable(name, value)) return fail(LLK_ERR_INVALID_ARGUMENT, "unknown tunable %s", name);
   return LLK_OK;
 }
 

@@ -49,4 +49,13 @@ bool setTunable(const char* name, int64_t value) {
   return false;
 }
 
+bool getTunable(const char* name, int64_t* value) {
+  for (auto& k : g_knobs)
+    if (std::strcmp(k.name, name) == 0) {
+      *value = k.value.load(std::memory_order_relaxed);
+      return true;
+    }
+  return false;
+}
+
 }  // namespace llk

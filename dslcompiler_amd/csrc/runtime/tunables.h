@@ -11,5 +11,7 @@ namespace llk {
 int64_t tunable(const char* name);
 // Sets a knob; returns false for an unknown name.
 bool setTunable(const char* name, int64_t value);
+// Reads a knob into *value; returns false for an unknown name.
+bool getTunable(const char* name, int64_t* value);
 
 }  // namespace llk

@@ -416,6 +416,19 @@ def test_swiglu_m0(llk, gpu):
     assert y.shape == (0, 8)
 
 
+def test_empty_weights_both_pack_paths(llk, gpu):
+    """An empty weight matrix (N = 0) packs on the host and on the device
+    into usable handles: SwiGLU and GEMM give empty outputs."""
+    print("case empty weights", flush=True)
+    x = gpu.ones((3, 4), dtype=gpu.bfloat16, device="cuda")
+    w_host = normal_bf16(1, 1, (4, 0))
+    for pw in (llk.PackedWeights.from_host(w_host),
+               llk.PackedWeights.from_device(gpu.empty((4, 0), dtype=gpu.bfloat16, device="cuda"))):
+        assert pw.N == 0 and pw.K == 4
+        assert llk.fused_swiglu(x, pw, pw).shape == (3, 0)
+        assert llk.matmul(x, pw).shape == (3, 0)
+
+
 def test_swiglu_deterministic_and_row_permutation(llk, gpu):
     """Size-independent properties: two runs are bit-identical, and
     permuting the rows of X permutes the rows of Y bit for bit (every row is

@@ -83,3 +83,49 @@ def test_graph_capture_replay(llk, gpu, M):
         assert np.array_equal(from_dev(z), eager_z), rep
         llk.fused_swiglu(xd, pg, pu, out=y2)  # eager work between replays
         gpu.cuda.synchronize()
+
+
+def test_graph_survives_workspace_growth(llk, gpu):
+    """A graph captured while the library's own workspace was in use still
+    replays correctly after a later call outgrew that workspace (the library
+    retires an outgrown buffer instead of freeing it)."""
+    print("case graph + workspace growth", flush=True)
+    M, K, N = 300, 1024, 768
+    x, wg, wu = swiglu_inputs(M, K, N, seed=21)
+    pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
+    xd = to_dev(gpu, x)
+    y = gpu.empty((M, N), dtype=gpu.bfloat16, device="cuda")
+    old = llk.get_tunable("tile_splits")
+    llk.set_tunable("tile_splits", 3)
+    try:
+        assert llk.describe_launch("fused_swiglu", M, N, K)["workspace_bytes"] > 0
+        s = gpu.cuda.Stream()
+        with gpu.cuda.stream(s):
+            llk.fused_swiglu(xd, pg, pu, out=y, stream=s)
+        s.synchronize()
+        eager = from_dev(y)
+        g = gpu.cuda.CUDAGraph()
+        with gpu.cuda.graph(g, stream=s):
+            llk.fused_swiglu(xd, pg, pu, out=y, stream=s)
+        # a split GEMM whose partial planes (8 x 4096 x 12288 fp32 = 1.6 GB)
+        # exceed any earlier workspace by more than the 1.5x growth step
+        llk.set_tunable("tile_splits", 8)
+        Mb, Kb, Nb = 4096, 4096, 12288
+        assert llk.describe_launch("matmul", Mb, Nb, Kb)["workspace_bytes"] >= 1_500_000_000
+        a = gpu.randn((Mb, Kb), device="cuda").to(gpu.bfloat16)
+        pb = llk.PackedWeights.from_device(gpu.randn((Kb, Nb), device="cuda").to(gpu.bfloat16) * 0.02)
+        c = llk.matmul(a, pb)
+        gpu.cuda.synchronize()
+        assert bool(gpu.isfinite(c).all())
+        del a, c, pb
+        # memory freed by torch in between is handed out again: fill it
+        junk = gpu.full((1 << 28,), 3.0, device="cuda")
+        for rep in range(3):
+            y.zero_()
+            gpu.cuda.synchronize()
+            g.replay()
+            gpu.cuda.synchronize()
+            assert np.array_equal(from_dev(y), eager), rep
+        del junk
+    finally:
+        llk.set_tunable("tile_splits", old)
