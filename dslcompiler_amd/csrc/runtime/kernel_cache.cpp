@@ -144,8 +144,17 @@ int llk_cache_lookup_blob(llk_jit_cache* c, int level, const char* key, size_t k
 int llk_cache_insert_packed_weights(llk_jit_cache* c, const llk_weight_key* key,
                                     llk_packed_weights* pw) {
   if (!c || !key || !pw) return llk::setError(LLK_ERR_INVALID_ARGUMENT, "NULL argument");
-  c->weights.insert(weight_key_string(*key),
-                    std::shared_ptr<llk_packed_weights>(pw, &llk_packed_weights_free));
+  // Re-inserting the handle a key already holds only refreshes the entry
+  // (a second owner of the same handle would free it twice).
+  try {
+    c->weights.insert_with(
+        weight_key_string(*key),
+        [pw](const std::shared_ptr<llk_packed_weights>& h) { return h.get() == pw; },
+        [pw] { return std::shared_ptr<llk_packed_weights>(pw, &llk_packed_weights_free); });
+  } catch (const std::bad_alloc&) {
+    // The owning shared_ptr (made or being made) has freed pw.
+    return llk::setError(LLK_ERR_OUT_OF_MEMORY, "cache insertion");
+  }
   return LLK_OK;
 }
 
@@ -172,10 +181,10 @@ int llk_cache_get_packed_weights(llk_jit_cache* c, const llk_tensor2d* w, int64_
   key.BN = 128;
   if (llk_cache_lookup_packed_weights(c, &key, out) == 1) return LLK_OK;
   llk_packed_weights* pw = nullptr;
-  const int rc = on_device ? llk_pack_weights_device(w, bk, nullptr, &pw)
-                           : llk_pack_weights(w, bk, flags, &pw);
+  int rc = on_device ? llk_pack_weights_device(w, bk, nullptr, &pw)
+                     : llk_pack_weights(w, bk, flags, &pw);
   if (rc) return rc;
-  llk_cache_insert_packed_weights(c, &key, pw);
+  if ((rc = llk_cache_insert_packed_weights(c, &key, pw))) return rc;  // pw freed on failure
   *out = pw;
   return LLK_OK;
 }

@@ -57,6 +57,30 @@ class LruLevel {
     index_[key] = order_.begin();
   }
 
+  // insert() whose value is made only when needed: if `key` holds a value
+  // for which same(value) is true, that entry is just refreshed and make()
+  // is not called (an owning value for the same object is never made twice).
+  // If an allocation throws, the level is left as it was.
+  template <class Same, class Make>
+  void insert_with(const std::string& key, Same same, Make make) {
+    std::unique_lock<std::shared_mutex> lk(mu_);
+    auto it = index_.find(key);
+    if (it != index_.end()) {
+      if (!same(it->second->second)) it->second->second = make();
+      order_.splice(order_.begin(), order_, it->second);
+      return;
+    }
+    while (!order_.empty() && order_.size() >= max_entries_) pop_back();
+    auto slot = index_.emplace(key, order_.end()).first;
+    try {
+      order_.emplace_front(key, make());
+    } catch (...) {
+      index_.erase(slot);
+      throw;
+    }
+    slot->second = order_.begin();
+  }
+
   bool remove(const std::string& key) {
     std::unique_lock<std::shared_mutex> lk(mu_);
     auto it = index_.find(key);

@@ -387,10 +387,12 @@ int llk_cache_lookup_blob(llk_jit_cache* c, int level, const char* key, size_t k
                           void* out, size_t cap, size_t* len);
 
 /* L4 (JitCache.cpp:314-328), holding packed-weight handles instead of
- * blobs.  Insert transfers ownership of `pw` to the cache (a replaced or
- * evicted handle is freed).  Lookup returns 1 with a borrowed handle,
- * valid until the entry is evicted or the cache is cleared or destroyed,
- * or 0 on a miss. */
+ * blobs.  Insert transfers ownership of `pw` to the cache: a replaced or
+ * evicted handle is freed; inserting the handle its key already holds only
+ * refreshes the entry; a handle belongs under one key at a time; on
+ * LLK_ERR_OUT_OF_MEMORY the handle has been freed.  Lookup returns 1 with
+ * a borrowed handle, valid until the entry is evicted or the cache is
+ * cleared or destroyed, or 0 on a miss. */
 int llk_cache_insert_packed_weights(llk_jit_cache* c, const llk_weight_key* key,
                                     llk_packed_weights* pw);
 int llk_cache_lookup_packed_weights(llk_jit_cache* c, const llk_weight_key* key,

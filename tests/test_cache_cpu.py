@@ -77,6 +77,23 @@ def test_l4_packed_weight_cache():
     assert c.lookup_packed_weights(WeightKey(0xDEADBEEF, 12345, 64, 128)) is None
 
 
+def test_l4_reinsert_same_handle_refreshes():
+    """Inserting the handle a key already holds (C ABI, raw handle) only
+    refreshes the entry: the handle stays valid, and clearing the cache
+    frees it once (a second owner would free it twice)."""
+    c = JitCache()
+    _, pw = _host_pw()
+    raw = pw.release()
+    key = WeightKey(0x5150, 7, 64, 128)
+    for _ in range(3):
+        assert lib().llk_cache_insert_packed_weights(c._c, C.byref(key.c()), raw) == 0
+    got = c.lookup_packed_weights(key)
+    assert got is not None and got.handle.value == raw.value and got.N == 150
+    assert c.size() == 1
+    c.clear()
+    assert c.size() == 0 and c.lookup_packed_weights(key) is None
+
+
 def test_stats_accumulate():
     c = JitCache()
     c.lookup_ir("nonexistent")
