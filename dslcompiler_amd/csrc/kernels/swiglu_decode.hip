@@ -358,7 +358,10 @@ hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const voi
   a.n_pad = NB * kPackN;
   a.yvec = yvec;
   a.part = static_cast<float*>(ws);
-  if (a.S > 1 && ws == nullptr) return hipErrorInvalidValue;
+  // Every split must own at least one 64-k block (the dispatcher passes
+  // S = ceil(KB / ceil(KB / S_requested))).
+  if (a.S > 1 && (ws == nullptr || (int64_t)(a.S - 1) * a.kb_per_split >= KB))
+    return hipErrorInvalidValue;
   const int mt = (M + 31) / 32;
   if (mode == 1)
     return mt == 1 ? launch_skinny_mt<2, 1>(a, G, out, xvec, s)

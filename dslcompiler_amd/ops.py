@@ -42,6 +42,21 @@ def _ctx(stream=None, scratch=None) -> KernelContext:
     return ctx
 
 
+def _check_operand(t, name: str, dtypes) -> None:
+    """A kernel operand must be a 2-D tensor of an accepted dtype on the
+    current CUDA device: the C ABI takes raw pointers and cannot tell host
+    memory (a GPU memory fault when a kernel reads it) or another device's
+    memory from the current device's."""
+    torch = _torch()
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{name} must be a CUDA tensor")
+    if t.dtype not in dtypes:
+        raise ValueError(f"{name} has dtype {t.dtype}; expected one of {tuple(dtypes)}")
+    cur = torch.cuda.current_device()
+    if t.device.index != cur:
+        raise ValueError(f"{name} is on cuda:{t.device.index}, the current device is cuda:{cur}")
+
+
 def _t2d(t) -> _lib.Tensor2D:
     if t.dim() != 2:
         raise ValueError("expected a 2-D tensor")
@@ -91,8 +106,7 @@ class PackedWeights:
     def from_device(cls, w, bk: int = 64, stream=None) -> "PackedWeights":
         """Packs a torch bf16 [K, N] CUDA tensor with the device pack kernel."""
         torch = _torch()
-        if w.dtype != torch.bfloat16 or not w.is_cuda:
-            raise ValueError("w must be a CUDA bfloat16 tensor")
+        _check_operand(w, "w", (torch.bfloat16,))
         out = C.c_void_p()
         check(lib().llk_pack_weights_device(C.byref(_t2d(w)), bk, _stream_handle(stream),
                                             C.byref(out)))
@@ -213,8 +227,10 @@ def fused_swiglu(x, wg: PackedWeights, wu: PackedWeights, out=None, out_dtype=No
                  stream=None, scratch=None):
     """Y = SiLU(X Wg) * (X Wu) on the current device (asynchronous)."""
     torch = _torch()
+    _check_operand(x, "x", (torch.bfloat16,))
     if out is None:
         out = torch.empty((x.shape[0], wg.N), dtype=out_dtype or torch.bfloat16, device=x.device)
+    _check_operand(out, "out", (torch.bfloat16, torch.float32))
     check(lib().llk_swiglu_bf16(C.byref(_t2d(x)), wg.handle, wu.handle, C.byref(_t2d(out)),
                                 _out_dtype_code(out.dtype), C.byref(_ctx(stream, scratch))))
     return out
@@ -223,8 +239,10 @@ def fused_swiglu(x, wg: PackedWeights, wu: PackedWeights, out=None, out_dtype=No
 def matmul(a, b: PackedWeights, out=None, out_dtype=None, stream=None, scratch=None):
     """C = A B (micro.mma, fp32 accumulation) on the current device."""
     torch = _torch()
+    _check_operand(a, "a", (torch.bfloat16,))
     if out is None:
         out = torch.empty((a.shape[0], b.N), dtype=out_dtype or torch.float32, device=a.device)
+    _check_operand(out, "out", (torch.bfloat16, torch.float16, torch.float32))
     check(lib().llk_gemm_bf16(C.byref(_t2d(a)), b.handle, C.byref(_t2d(out)),
                               _out_dtype_code(out.dtype), C.byref(_ctx(stream, scratch))))
     return out
@@ -234,10 +252,13 @@ def mlp(x, wg: PackedWeights, wu: PackedWeights, wd: PackedWeights, y=None, z=No
         stream=None, scratch=None):
     """Y = SwiGLU(X) (bf16), Z = Y Wd (bf16); returns (y, z)."""
     torch = _torch()
+    _check_operand(x, "x", (torch.bfloat16,))
     if y is None:
         y = torch.empty((x.shape[0], wg.N), dtype=torch.bfloat16, device=x.device)
     if z is None:
         z = torch.empty((x.shape[0], wd.N), dtype=torch.bfloat16, device=x.device)
+    _check_operand(y, "y", (torch.bfloat16,))
+    _check_operand(z, "z", (torch.bfloat16,))
     check(lib().llk_mlp_bf16(C.byref(_t2d(x)), wg.handle, wu.handle, wd.handle,
                              C.byref(_t2d(y)), C.byref(_t2d(z)), C.byref(_ctx(stream, scratch))))
     return y, z

@@ -122,6 +122,23 @@ def test_host_only_handle_is_rejected_by_kernels(llk):
     assert L.llk_packed_weights_device_data(wg.handle) is None
 
 
+def test_python_wrappers_reject_host_tensors(llk):
+    """The torch wrappers refuse operands that are not CUDA tensors of the
+    accepted dtype before calling the C ABI (which takes raw pointers: a
+    host pointer would reach a kernel)."""
+    import torch
+    wg = llk.PackedWeights.from_host(normal_bf16(1, 1, (16, 32)), host_only=True)
+    x = torch.zeros((4, 16), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="x must be a CUDA tensor"):
+        llk.fused_swiglu(x, wg, wg)
+    with pytest.raises(ValueError, match="a must be a CUDA tensor"):
+        llk.matmul(x, wg)
+    with pytest.raises(ValueError, match="x must be a CUDA tensor"):
+        llk.mlp(x, wg, wg, wg)
+    with pytest.raises(ValueError, match="w must be a CUDA tensor"):
+        llk.PackedWeights.from_device(torch.zeros((16, 32), dtype=torch.bfloat16))
+
+
 def test_tunables(llk):
     assert llk.get_tunable("decode_max_m") == 64
     llk.set_tunable("decode_splits", 3)

@@ -541,6 +541,14 @@ def test_errors(llk, gpu):
     with pytest.raises(llk.LLKError, match="LLK_ERR_SCRATCH"):
         llk.fused_swiglu(gpu.zeros((4, 1024), dtype=gpu.bfloat16, device="cuda"), big, big,
                          scratch=gpu.zeros(4, dtype=gpu.uint8, device="cuda"))
+    # operand dtypes the kernels do not read or write are refused up front
+    with pytest.raises(ValueError, match="x has dtype"):
+        llk.fused_swiglu(x.float(), wg, wg)
+    with pytest.raises(ValueError, match="out has dtype"):
+        llk.fused_swiglu(x, wg, wg, out=gpu.empty((4, 32), dtype=gpu.float16, device="cuda"))
+    with pytest.raises(ValueError, match="y has dtype"):
+        llk.mlp(x, wg, wg, llk.PackedWeights.from_host(normal_bf16(1, 3, (32, 8))),
+                y=gpu.empty((4, 32), dtype=gpu.float32, device="cuda"))
 
 
 GOLDEN = __import__("pathlib").Path(__file__).resolve().parent / "golden"
