@@ -24,6 +24,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace llk_gfx950 {
 
 constexpr int kPackN = 128;           // n per packed block
@@ -144,6 +146,20 @@ __device__ __forceinline__ void store4(void* y, int64_t ldy, int M, int N, int m
         if (n + r < N) dst[r] = v[r];
     }
   }
+}
+
+// Raises the dynamic-LDS limit of kernel `fn` to `bytes`, once per device
+// (the attribute belongs to the current device); `done` is the caller's
+// per-kernel bit set of devices already configured.
+inline hipError_t ensure_dynamic_lds(const void* fn, int bytes, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = (dev >= 0 && dev < 64) ? (uint64_t)1 << dev : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_release);
+  return e;
 }
 
 }  // namespace llk_gfx950

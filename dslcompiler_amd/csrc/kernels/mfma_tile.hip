@@ -408,14 +408,9 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(TileArgs a) {
 template <int MODE, int OUT, bool YVEC, bool SPLIT>
 static hipError_t launch_tile_t(const TileArgs& a, hipStream_t s) {
   auto fn = mfma_tile_kernel<MODE, OUT, YVEC, SPLIT>;
-  static bool attr_set = false;  // per instantiation; benign race (idempotent)
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       kStages * kStageBytes);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};  // devices configured, per instantiation
+  hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(fn), kStages * kStageBytes, lds_set);
+  if (e != hipSuccess) return e;
   dim3 grid(a.tiles_m * a.tiles_n * (SPLIT ? a.S : 1)), block(kThreads);
   hipLaunchKernelGGL(fn, grid, block, kStages * kStageBytes, s, a);
   return hipGetLastError();

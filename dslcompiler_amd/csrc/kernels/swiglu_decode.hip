@@ -264,13 +264,11 @@ template <int NMAT, int MT, int W, int OUT, bool XVEC>
 static hipError_t launch_skinny_t(const SkinnyArgs& a, hipStream_t s) {
   using C = SkinnyCfg<NMAT, MT, W>;
   auto fn = skinny_kernel<NMAT, MT, C::KS, C::G, C::GW, OUT, XVEC, C::UNROLL>;
-  static bool attr_set = false;  // per instantiation; benign race (idempotent)
-  if (!attr_set && C::lds > 65536) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::lds);
+  static std::atomic<uint64_t> lds_set{0};  // devices configured, per instantiation
+  if (C::lds > 65536) {
+    hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(fn), (int)C::lds, lds_set);
     if (e != hipSuccess) return e;
   }
-  attr_set = true;
   hipLaunchKernelGGL(fn, dim3(a.NB * 4 / W * a.S), dim3(C::KS * C::G * 64), C::lds, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.S == 1) return e;
