@@ -40,6 +40,30 @@
 
 #include "common.h"
 
+// Phase timestamps (the llk-tile-phases tool builds this file with
+// LLK_TILE_PHASES defined): each workgroup records the 100 MHz real-time
+// counter at entry, when its first stage has landed, after the K loop and
+// after the epilogue.  Empty in the library build.
+#ifdef LLK_TILE_PHASES
+#define LLK_PHASE(var) const unsigned long long var = __builtin_amdgcn_s_memrealtime()
+#define LLK_PHASE_STORE()                                                        \
+  do {                                                                           \
+    const unsigned long long t_end = __builtin_amdgcn_s_memrealtime();           \
+    if (threadIdx.x == 0) {                                                      \
+      unsigned long long* r = a.phases + (size_t)blockIdx.x * 4;                 \
+      r[0] = t_entry;                                                            \
+      r[1] = t_first;                                                            \
+      r[2] = t_loop;                                                             \
+      r[3] = t_end;                                                              \
+    }                                                                            \
+  } while (0)
+#else
+#define LLK_PHASE(var)
+#define LLK_PHASE_STORE() \
+  do {                    \
+  } while (0)
+#endif
+
 namespace llk_gfx950 {
 
 struct TileArgs {
@@ -58,6 +82,9 @@ struct TileArgs {
   // in split order and applies the epilogue.
   float* part;
   int S, kbs, n_pad;
+#ifdef LLK_TILE_PHASES
+  unsigned long long* phases;  // [workgroups][4] timestamps (phase tool)
+#endif
 };
 
 constexpr int kThreads = 256;
@@ -101,6 +128,7 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   // Workgroup -> (split s, tile): tiles of one split are contiguous, so
   // after the XCD remap the tiles that share X's k slice (and, m fastest,
   // the tiles that share W columns) run on one XCD.
+  LLK_PHASE(t_entry);
   const int tiles = a.tiles_m * a.tiles_n;
   const int idx = xcd_remap(blockIdx.x, tiles * (SPLIT ? a.S : 1));
   const int split = SPLIT ? idx / tiles : 0;
@@ -202,6 +230,7 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
     if (p < T) dma_issue(p, p);
   wait_stages(min(kStages - 1, T - 1));
   __syncthreads();
+  LLK_PHASE(t_first);
 
   bf16x8 aq0[4], bq0[4], aq1[4], bq1[4];
 #pragma unroll
@@ -265,6 +294,7 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   for (; t + kStages < T; ++t) stage(t, std::true_type{}, std::true_type{});  // steady state
   for (; t + 1 < T; ++t) stage(t, std::false_type{}, std::true_type{});       // drain
   stage(t, std::false_type{}, std::false_type{});                             // last stage
+  LLK_PHASE(t_loop);
 
   // ---- epilogue: lane holds m = base + lane%32, n = base + 8*(r/4) +
   // 4*(lane/32) + r%4 for its 16 values r of each 32 x 32 tile.
@@ -334,6 +364,7 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
                                            (size_t)(m0 + wm * 128) * a.n_pad + col0),
                 (int64_t)a.n_pad * 4, rows_ok, a.n_pad - col0);
     }
+    LLK_PHASE_STORE();
     return;
   }
   constexpr int NI = (MODE == 1) ? 2 : 4;
@@ -355,9 +386,12 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
         for (int g = 0; g < 4; ++g) {
           float v[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            v[q] = (MODE == 1) ? swiglu_act(acc[i][j][4 * g + q], acc[i + 2][j][4 * g + q])
-                               : acc[i][j][4 * g + q];
+          for (int q = 0; q < 4; ++q) {
+            if constexpr (MODE == 1)
+              v[q] = swiglu_act(acc[i][j][4 * g + q], acc[i + 2][j][4 * g + q]);
+            else
+              v[q] = acc[i][j][4 * g + q];
+          }
           uint8_t* const dst = strip + (j * 32 + mr) * kStripRow + (ii * 32 + 8 * g + h4) * kElem;
           if constexpr (OUT == kOutF32) {
             *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
@@ -374,6 +408,7 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
     strip_out(std::integral_constant<int, kElem>{}, fast, al16, ybase + sidx * 128,
               a.ldy * kElem, rows_ok, a.N - (n_w + sidx * 128 / kElem));
   }
+  LLK_PHASE_STORE();
 }
 
 // Sums the S partial planes of each output element in split order (fixed,
@@ -398,7 +433,12 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(TileArgs a) {
       sum[p] += *reinterpret_cast<const f32x4*>(src + ((size_t)sp * NMAT + p) * plane);
   float v[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) v[q] = (MODE == 1) ? swiglu_act(sum[0][q], sum[1][q]) : sum[0][q];
+  for (int q = 0; q < 4; ++q) {
+    if constexpr (MODE == 1)
+      v[q] = swiglu_act(sum[0][q], sum[1][q]);
+    else
+      v[q] = sum[0][q];
+  }
   store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, YVEC);
 }
 
@@ -446,6 +486,11 @@ static hipError_t launch_mode(const TileArgs& a, int out, bool yvec, hipStream_t
 
 }  // namespace llk_gfx950
 
+#ifdef LLK_TILE_PHASES
+// Device buffer of [workgroups][4] timestamps the next launches write.
+unsigned long long* llk_tile_phases_buffer = nullptr;
+#endif
+
 // Largest X span (bytes, rows padded to whole tiles) the 32-bit buffer
 // offsets of the tile kernel can address.
 bool llk_tile_x_fits(int M, int64_t ldx) {
@@ -485,6 +530,9 @@ hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void*
   a.kbs = (KB + a.S - 1) / a.S;
   a.n_pad = NB * 128;
   a.part = static_cast<float*>(part);
+#ifdef LLK_TILE_PHASES
+  a.phases = llk_tile_phases_buffer;
+#endif
   if (a.S > 1 && (part == nullptr || (int64_t)(a.S - 1) * a.kbs >= KB)) return hipErrorInvalidValue;
   if (mode == 1) return launch_mode<1>(a, out, yvec, s);
   return launch_mode<0>(a, out, yvec, s);

@@ -208,8 +208,12 @@ __global__ __launch_bounds__(KS * G * 64) void skinny_kernel(SkinnyArgs a) {
     } else {
       float v[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        v[q] = (NMAT == 2) ? swiglu_act(sum[i][0][q], sum[i][1][q]) : sum[i][0][q];
+      for (int q = 0; q < 4; ++q) {
+        if constexpr (NMAT == 2)
+          v[q] = swiglu_act(sum[i][0][q], sum[i][1][q]);
+        else
+          v[q] = sum[i][0][q];
+      }
       store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
     }
   }
@@ -233,7 +237,12 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(SkinnyArgs a, int ro
       s[p] += *reinterpret_cast<const f32x4*>(a.part + (((size_t)sp * NMAT + p) * rows + m) * a.n_pad + n);
   float v[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) v[q] = (NMAT == 2) ? swiglu_act(s[0][q], s[1][q]) : s[0][q];
+  for (int q = 0; q < 4; ++q) {
+    if constexpr (NMAT == 2)
+      v[q] = swiglu_act(s[0][q], s[1][q]);
+    else
+      v[q] = s[0][q];
+  }
   store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
 }
 
