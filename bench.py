@@ -7,7 +7,9 @@ already resident in HBM; the average launch time comes from HIP events on
 the launch stream.  Reported in "extra": decode SwiGLU (config 4,
 M in {1, 8, 16, 64}, K=4096, N=14336) in HBM GB/s with weights rotated over four
 copies (940 MB, beyond the 256 MB MALL); the 4096^3 GEMM (config 2); the
-MLP block (config 5) over its ragged M sweep.
+MLP block (config 5) over its ragged M sweep; the reference's CPU path (the
+AVX2 restatement) on configs 1, 4 and 5 beside the headline's cpu_baseline;
+torch.matmul (hipBLASLt) on the same shapes for comparison.
 
 Prints ONE JSON line.  --gpus N with N > 1 exits: this path runs on one GPU.
 """
@@ -103,13 +105,15 @@ def bench_decode(torch, llk, M, steps, warmup, copies=4):
     return dict(ms=ms, gbs=nbytes / (ms * 1e-3) / 1e9)
 
 
-def bench_gemm(torch, llk, steps, warmup):
+def bench_gemm(torch, llk, steps, warmup, out_dtype=None):
+    """Config 2 (fp32 output); out_dtype bf16 for the comparison with the
+    vendor GEMM, whose output is bf16."""
     n = 4096
     g = torch.Generator(device="cuda")
     g.manual_seed(42)
     a = _rand_w(torch, g, n, n)
     pb = llk.PackedWeights.from_device(_rand_w(torch, g, n, n))
-    c = torch.empty((n, n), dtype=torch.float32, device="cuda")
+    c = torch.empty((n, n), dtype=out_dtype or torch.float32, device="cuda")
     ms = _time_loop(torch, lambda i: llk.matmul(a, pb, out=c), steps, warmup, EXTRA_WARM_S)
     return dict(ms=ms, tflops=2.0 * n ** 3 / (ms * 1e-3) / 1e12)
 
@@ -137,6 +141,42 @@ def bench_mlp(torch, llk, steps, warmup):
     return out
 
 
+def bench_vendor(torch, steps, warmup):
+    """The vendor library on the same box, for comparison: torch.matmul
+    (hipBLASLt) on config 3 as one GEMM against [Wg | Wu] (2048 x 4096 x
+    22016, the fused kernel's flops) followed by torch's SiLU and product
+    (the unfused path), and the 4096^3 GEMM with bf16 output (torch has no
+    bf16-input, fp32-output matmul)."""
+    import torch.nn.functional as F
+    g = torch.Generator(device="cuda")
+    g.manual_seed(42)
+    M, K, N = PREFILL["M"], PREFILL["K"], PREFILL["N"]
+    x = torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16)
+    w = _rand_w(torch, g, K, 2 * N)
+    gu = torch.empty((M, 2 * N), dtype=torch.bfloat16, device="cuda")
+    ms_gemm = _time_loop(torch, lambda i: torch.matmul(x, w, out=gu), steps, warmup,
+                         EXTRA_WARM_S)
+    ms_full = _time_loop(torch, lambda i: _unfused_swiglu(torch, F, x, w, gu, N), steps, warmup,
+                         EXTRA_WARM_S)
+    n = 4096
+    a = _rand_w(torch, g, n, n)
+    b = _rand_w(torch, g, n, n)
+    c = torch.empty((n, n), dtype=torch.bfloat16, device="cuda")
+    ms_sq = _time_loop(torch, lambda i: torch.matmul(a, b, out=c), steps, warmup, EXTRA_WARM_S)
+    f3 = 4.0 * M * K * N
+    return {"swiglu_2048x4096x11008_unfused": {"us": round(ms_full * 1e3, 1),
+                                              "tflops": round(f3 / (ms_full * 1e-3) / 1e12, 1)},
+            "gemm_2048x4096x22016_only": {"us": round(ms_gemm * 1e3, 1),
+                                          "tflops": round(f3 / (ms_gemm * 1e-3) / 1e12, 1)},
+            "gemm_4096_bf16_out": {"us": round(ms_sq * 1e3, 1),
+                                   "tflops": round(2.0 * n ** 3 / (ms_sq * 1e-3) / 1e12, 1)}}
+
+
+def _unfused_swiglu(torch, F, x, w, gu, N):
+    torch.matmul(x, w, out=gu)
+    return F.silu(gu[:, :N]) * gu[:, N:]
+
+
 def model_vs_measured(pre: dict, extra: dict) -> dict:
     """L0 model predictions (dslcompiler_amd.perfmodel) next to this run's
     measurements, in microseconds."""
@@ -158,8 +198,7 @@ def cpu_baseline(x, wg, wu, budget_s: float = 12.0):
     sample of the headline workload: the first `rows` rows of X (full K and
     N), best of up to 5 runs within about `budget_s` seconds."""
     import oracle
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    threads = max(1, min(threads, os.cpu_count() or 1))
+    threads = _cpu_threads()
     K, N = wg.shape
     t0 = time.perf_counter()
     oracle.swiglu_avx2(x[:32], wg, wu, threads)  # warm-up + estimate
@@ -177,6 +216,52 @@ def cpu_baseline(x, wg, wu, budget_s: float = 12.0):
             "sample": f"fused SwiGLU rows 0..{rows - 1} of M=2048 (K=4096, N=11008), best of "
                       f"{reps} runs; AVX2 BM32/BN64/BK64/VM4/VN8 tiles, ThreadPool-style "
                       f"dynamic tile queue"}
+
+
+def _cpu_threads() -> int:
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return max(1, min(threads, os.cpu_count() or 1))
+
+
+def cpu_port_configs(llk, budget_s: float = 3.0) -> dict:
+    """The AVX2 restatement of the reference's fused SwiGLU path (the only
+    executable CPU path the reference has for these ops) on the other
+    BASELINE SwiGLU configs, full shapes, best of up to 3 runs within about
+    `budget_s` seconds each: config 1 in GFLOP/s, decode config 4 (M = 8) in
+    GB/s over the same algorithmic bytes as the GPU figure, and config 5's
+    SwiGLU half at M = 255 in GFLOP/s.  Config 2 (plain GEMM) has no CPU
+    figure: `micro.mma` is verifier-only and `llk.matmul` has no lowering
+    in the reference (LLKToLinalg.cpp:621-646), so nothing executes it."""
+    from common import STREAM_WG, STREAM_WU, STREAM_X
+    threads = _cpu_threads()
+
+    def best_s(M, K, N):
+        x = llk.fill_normal_bf16(42, STREAM_X, (M, K))
+        wg = llk.fill_normal_bf16(42, STREAM_WG, (K, N), 1.0 / np.sqrt(K))
+        wu = llk.fill_normal_bf16(42, STREAM_WU, (K, N), 1.0 / np.sqrt(K))
+        import oracle
+        best, t_end, reps = float("inf"), time.perf_counter() + budget_s, 0
+        while reps < 1 or (time.perf_counter() < t_end and reps < 3):
+            t = time.perf_counter()
+            oracle.swiglu_avx2(x, wg, wu, threads)
+            best = min(best, time.perf_counter() - t)
+            reps += 1
+        return best
+
+    out = {"threads": threads, "kind": "port"}
+    s = best_s(64, 512, 1376)
+    out["c1_swiglu_64x512x1376"] = {"us": round(s * 1e6, 1),
+                                    "gflops": round(4.0 * 64 * 512 * 1376 / s / 1e9, 1)}
+    K, N = DECODE["K"], DECODE["N"]
+    s = best_s(8, K, N)
+    nbytes = 2.0 * K * N * 2 + 8 * K * 2 + 8 * N * 2
+    out["c4_decode_m8"] = {"us": round(s * 1e6, 1), "gbs": round(nbytes / s / 1e9, 1)}
+    K, N = MLP["K"], MLP["N"]
+    s = best_s(255, K, N)
+    out["c5_swiglu_m255"] = {"us": round(s * 1e6, 1),
+                             "gflops": round(4.0 * 255 * K * N / s / 1e9, 1)}
+    out["c2_gemm"] = None
+    return out
 
 
 def spot_parity(x, wg, wu, y_dev):
@@ -208,7 +293,8 @@ def main() -> None:
                          "~35 ms the GPU takes to reach its steady clock under load)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode8", "decode64", "gemm", "mlp", "copy"],
+    ap.add_argument("--only", choices=["prefill", "decode8", "decode64", "gemm", "mlp", "vendor",
+                                       "copy"],
                     help="run one workload for --steps launches and print its timing only "
                          "(for profiler runs); 'copy' is a 256 MiB device copy used to "
                          "calibrate byte counters")
@@ -236,6 +322,11 @@ def main() -> None:
             r = bench_gemm(torch, llk, a.steps, a.warmup)
         elif a.only == "mlp":
             r = bench_mlp(torch, llk, a.steps, a.warmup)
+        elif a.only == "vendor":
+            g16 = bench_gemm(torch, llk, a.steps, a.warmup, torch.bfloat16)
+            r = {"vendor_hipblaslt": bench_vendor(torch, a.steps, a.warmup),
+                 "llk_gemm_4096_bf16_out": {"us": round(g16["ms"] * 1e3, 1),
+                                            "tflops": round(g16["tflops"], 1)}}
         else:
             src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
             dst = torch.empty_like(src)
@@ -256,8 +347,14 @@ def main() -> None:
         extra["gemm_4096"] = {"us": round(gem["ms"] * 1e3, 1), "tflops": round(gem["tflops"], 1),
                               "mfma_frac": round(gem["tflops"] / PEAK_BF16_TFLOPS, 4)}
         extra["mlp_k5120_n13824"] = bench_mlp(torch, llk, a.steps, a.warmup)
+        extra["vendor_hipblaslt"] = bench_vendor(torch, max(10, a.steps // 2), a.warmup)
+        g16 = bench_gemm(torch, llk, max(10, a.steps // 2), a.warmup, torch.bfloat16)
+        extra["gemm_4096_bf16_out"] = {"us": round(g16["ms"] * 1e3, 1),
+                                       "tflops": round(g16["tflops"], 1)}
         extra["model_vs_measured"] = model_vs_measured(pre, extra)
     cpu = None if a.no_cpu_baseline else cpu_baseline(x, wg, wu)
+    if not a.no_cpu_baseline and not a.no_extra:
+        extra["cpu_port_other_configs"] = cpu_port_configs(llk)
 
     achieved = pre["tflops"]
     line = {
