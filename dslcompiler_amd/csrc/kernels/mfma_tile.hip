@@ -1,10 +1,14 @@
 // mfma_tile.hip -- bf16 MFMA tile kernels for gfx950: the fused SwiGLU
 // prefill kernel and the micro.mma GEMM.
 //
-// Computes  D^T = W^T X^T  on v_mfma_f32_32x32x16_bf16: the packed weight
+// Computes  D^T = W^T X^T  on v_mfma_f32_16x16x32_bf16: the packed weight
 // (n rows, k contiguous) is the MFMA A operand and the activation X (m rows,
 // k contiguous) is the B operand, so each lane's accumulators are runs of
-// four consecutive n of one output row m.
+// four consecutive n of one output row m.  The 16x16x32 form issues the same
+// flops per cycle as the 32x32x16 one but moves half the accumulator
+// register traffic per flop; on N(0,1) data, where the board's power limit
+// sets the clock, it sustains ~15% more (register-only loop: 1.96 vs 1.70
+// PFLOP/s) and this kernel 6-9% more.
 //
 // Workgroup: 256 threads (4 waves, 2 x 2).  Workgroup tile 256 m x 256
 // MFMA rows:  GEMM -> 256 n;  SwiGLU -> 128 n of Wg + the same 128 n of Wu,
@@ -12,18 +16,30 @@
 // and the SiLU(g)*u epilogue runs from registers (the reference's
 // FuseDoubleContraction.cpp:175-199 epilogue, fused after the contraction of
 // FuseDoubleContraction.cpp:155-173).  Wave tile: 128 m x 128 MFMA rows =
-// 4 x 4 MFMA tiles of 32 x 32, 256 fp32 accumulators per lane (AGPRs).
+// 8 x 8 MFMA tiles of 16 x 16, 256 fp32 accumulators per lane (AGPRs).
 //
-// K loop: 32 k per stage, a ring of 4 LDS stages of 32 KiB (16 KiB weights
-// + 16 KiB X).  Operands go straight from memory into LDS
-// (buffer_load_dwordx4 ... lds) three stages ahead of the 32 MFMAs per wave
-// that consume them.  Each stage's barrier sits between its two k quarters;
-// the refill of the freed buffer is issued one load per MFMA pair across
-// the second quarter, and the next stage's first operands are read during
-// it, so neither loads nor LDS reads leave the MFMA pipe idle.  Weights sit
-// in LDS as 1 KiB MFMA-ordered sub-blocks (contiguous, conflict-free operand
-// reads); X as XOR-swizzled 64-byte rows, so its loads move whole rows and
-// its operand reads are conflict-free too.
+// K loop: 32 k per stage (one MFMA k step), a ring of 4 LDS stages of 32 KiB
+// (16 KiB weights + 16 KiB X).  Operands go straight from memory into LDS
+// (buffer_load_dwordx4 ... lds) three stages ahead of the 64 MFMAs per wave
+// that consume them.  Each stage's barrier sits between its two halves of
+// 32 MFMAs; after it the refill of the freed buffer is issued one load per
+// 4 MFMAs, and each next-stage operand is read once its register's last MFMA
+// of this stage has issued, so neither loads nor LDS reads leave the MFMA
+// pipe idle.  Weights sit in LDS as the payload's 1 KiB sub-blocks (32 n x
+// 16 k, lane order); a 16 x 32 A operand gathers two half sub-blocks, each
+// 16-lane group reading 256 contiguous bytes (conflict-free).  X sits as
+// XOR-swizzled 64-byte rows, so its loads move whole rows and its operand
+// reads (16 rows x 64 bytes) are conflict-free too.
+//
+// The MFMAs are issued from inline assembly with the accumulator tied to
+// its AGPRs: through the builtin the register allocator routes a varying
+// set of the 64 four-register accumulators through temporaries every stage
+// (up to 4 AGPR moves and s_nops per MFMA).  What the hazard recognizer
+// would otherwise see for these instructions is covered by construction:
+// A/B operands come only from LDS loads (the compiler places their waits),
+// accumulators are written by nothing but the MFMAs inside the K loop, and
+// the epilogue reads them only after explicit padding (acc_fence).
+// tests/test_isa_cpu.py checks this on the built code object.
 //
 // Epilogue: SiLU(g)*u (SwiGLU), rounding to the output type, and stores
 // staged through the freed LDS ring so that every store instruction writes
@@ -104,12 +120,28 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-// Waits until at most `ahead` stages of this wave's loads are outstanding.
-__device__ __forceinline__ void wait_stages(int ahead) {
-  if (ahead >= 3) wait_vmcnt<3 * kLoadsPerStage>();
-  else if (ahead == 2) wait_vmcnt<2 * kLoadsPerStage>();
-  else if (ahead == 1) wait_vmcnt<kLoadsPerStage>();
-  else wait_vmcnt<0>();
+// acc += A B on v_mfma_f32_16x16x32_bf16, accumulating in place in the
+// accumulator's AGPRs (see the header comment for why this is inline
+// assembly).  Lane l supplies A row l%16 / B column l%16 with k values
+// 8*(l/16) .. +8 and receives D column l%16, rows 4*(l/16) + 0..3.
+__device__ __forceinline__ void mfma16(const bf16x8& a, const bf16x8& b, f32x4& acc) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+// 64 wait states: more than a 16x16x32 MFMA needs before a VALU instruction
+// may read its result (or before an MFMA may read an AGPR a VALU wrote).
+__device__ __forceinline__ void mfma_drain() {
+  asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15");
+}
+
+// Orders every accumulator after the preceding inline assembly: volatile
+// asm statements keep their order, and the accumulators' later readers (and
+// earlier writers) depend on these.
+__device__ __forceinline__ void acc_fence(f32x4 (&acc)[8][8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) asm volatile("" : "+a"(acc[i][j]));
 }
 
 // MODE 0: GEMM (C = X W);  MODE 1: fused SwiGLU.
@@ -147,8 +179,9 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   // sub-blocks (w&1)*4 .. +4 of slot w>>1.
   // X: 256 rows of 32 k = 64 bytes, row r at kXOff + 64 r.  Inside a row the
   // four 16-byte chunks c (8 k each) are stored at slot c ^ ((r >> 2) & 3),
-  // so the MFMA operand reads (32 rows, one chunk) hit distinct banks.  Wave
-  // w fills rows w*64 .. +64: each load instruction covers 16 full rows.
+  // so an MFMA operand read (16 rows, lane group g reading chunk g of each)
+  // hits every bank once per 16 lanes.  Wave w fills rows w*64 .. +64: each
+  // load instruction covers 16 full rows.
   const int wslot = wave >> 1;
   const uint8_t* wpanel;
   if (MODE == 1) {
@@ -196,115 +229,99 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
     for (int i = 0; i < 4; ++i) dma_x(t, buf, i);
   };
 
-  f32x16 acc[4][4];
+  // Accumulators: acc[i][j] = MFMA rows (n) 16 i .. +16 of the wave's 128
+  // (SwiGLU: i < 4 gate, i >= 4 up of the same n), m 16 j .. +16 of its 128.
+  f32x4 acc[8][8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  acc_fence(acc);  // the zeroed AGPRs are written ...
+  mfma_drain();    // ... well before the first MFMA reads them
 
-  // LDS byte offsets (within a stage, before the lane's own offset) of the
-  // A operand i and the B operand j of the stage's k quarter q (0, 1).
-  const int a_lane = lane * 16;
-  const int sw = ((lane & 31) >> 2) & 3;
-  const int b_lane[2] = {(lane & 31) * 64 + (((lane >> 5)) ^ sw) * 16,
-                         (lane & 31) * 64 + ((2 + (lane >> 5)) ^ sw) * 16};
-  auto a_off = [&](int q, int i) -> int {
-    if (MODE == 1) return (i >> 1) * 8 * kSubBytes + (q * 4 + wn * 2 + (i & 1)) * kSubBytes + a_lane;
-    return wn * 8 * kSubBytes + (q * 4 + i) * kSubBytes + a_lane;
+  // Operands of v_mfma_f32_16x16x32_bf16 (stage-local k 0..31).
+  // A operand i: 16 MFMA rows; SwiGLU i < 4 -> Wg rows wn*64 + 16 i, i >= 4
+  // -> the same rows of Wu; GEMM -> rows 16 i of n-block wn.  Lane l needs
+  // row l%16 and k 8*(l/16) .. +8: k quarter l/32 of the stage, slot
+  // (row % 32) + 32*((l/16) % 2) of that quarter's 32 n x 16 k sub-block.
+  // B operand j: X rows wm*128 + 16 j + l%16, logical chunk l/16 (8 k).
+  const int a_lane = (lane >> 5) * 4 * kSubBytes + ((lane & 15) + 32 * ((lane >> 4) & 1)) * 16;
+  const int brow = lane & 15;
+  const int b_lane = brow * 64 + (((lane >> 4) ^ ((brow >> 2) & 3)) * 16);
+  auto a_off = [&](int i) -> int {
+    const int slot = (MODE == 1) ? (i >> 2) : wn;
+    const int nn = (MODE == 1) ? wn * 64 + 16 * (i & 3) : 16 * i;
+    return slot * 8 * kSubBytes + (nn >> 5) * kSubBytes + ((nn >> 4) & 1) * 256 + a_lane;
   };
-  auto b_off = [&](int q, int j) -> int { return kXOff + (wm * 128 + j * 32) * 64 + b_lane[q]; };
+  auto b_off = [&](int j) -> int { return kXOff + (wm * 128 + j * 16) * 64 + b_lane; };
   auto rd = [&](int buf, int off) {
     return *reinterpret_cast<const bf16x8*>(smem + buf * kStageBytes + off);
   };
 
-  // Pipeline: every stage buffer starts free, so stages 0..kStages-1 are
-  // issued up front.  While stage t computes, the barrier for stage t+1
-  // sits between its two k quarters: after it, stage t's buffer is free for
-  // stage t + kStages and stage t+1's first operands are read during the
-  // MFMAs of stage t's second quarter.
+  // Pipeline: one loop body for every stage.  Stages 0..kStages-1 are
+  // issued up front; stage t refills its own buffer with stage t + kStages
+  // after its barrier, so at that barrier stage t+1 has landed once at most
+  // the loads of stages t+2 and t+3 are outstanding.  Refills past the last
+  // stage T-1 re-read stage T-1 (in bounds) into buffers no MFMA reads
+  // again, which keeps the wait counts uniform; they all land before the
+  // epilogue reuses the ring.
   const int T = nkb * 2;  // stages
 #pragma unroll
-  for (int p = 0; p < kStages; ++p)
-    if (p < T) dma_issue(p, p);
-  wait_stages(min(kStages - 1, T - 1));
+  for (int p = 0; p < kStages; ++p) dma_issue(min(p, T - 1), p);
+  wait_vmcnt<(kStages - 1) * kLoadsPerStage>();
   __syncthreads();
   LLK_PHASE(t_first);
 
-  bf16x8 aq0[4], bq0[4], aq1[4], bq1[4];
+  bf16x8 A[8], B[8];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) bq0[j] = rd(0, b_off(0, j));
+  for (int j = 0; j < 8; ++j) B[j] = rd(0, b_off(j));
 #pragma unroll
-  for (int i = 0; i < 4; ++i) aq0[i] = rd(0, a_off(0, i));
+  for (int i = 0; i < 4; ++i) A[i] = rd(0, a_off(i));
 
-  // One stage.  ISSUE: refill stage t's buffer with stage t + kStages.
-  // MORE: a stage t+1 follows (sync on it and prefetch its operands).
-  auto stage = [&](int t, auto ISSUE, auto MORE) {
-    constexpr bool kIssue = decltype(ISSUE)::value, kMore = decltype(MORE)::value;
+  for (int t = 0; t < T; ++t) {
     const int buf = t % kStages;
-    // k quarter 0 of stage t; read quarter 1's operands meanwhile.
+    // Half 0: A0..3 x B0..7, A outer; A4..7 of stage t are read meanwhile.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      A[4 + i] = rd(buf, a_off(4 + i));
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (j == 0) bq1[i] = rd(buf, b_off(1, i));
-        if (j == 2) aq1[i] = rd(buf, a_off(1, i));
-        acc[i][j] = mfma32(aq0[i], bq0[j], acc[i][j]);
-        if (j == 0 || j == 2) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
-          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMAs
-        }
-      }
+      for (int j = 0; j < 8; ++j) mfma16(A[i], B[j], acc[i][j]);
     }
-    if constexpr (kMore) {
-      wait_lgkmcnt0();  // this wave's reads of stage t are complete
-      if constexpr (kIssue) wait_vmcnt<(kStages - 2) * kLoadsPerStage>();  // stage t+1 landed
-      else wait_stages(min(kStages - 2, T - 2 - t));
-      __syncthreads();  // ... for every wave; stage t's buffer is free
-    }
+    wait_lgkmcnt0();                               // this wave's reads of stage t are done
+    wait_vmcnt<(kStages - 2) * kLoadsPerStage>();  // stage t+1 landed
+    __syncthreads();                               // ... for every wave; buffer t is free
+    // Half 1: A4..7 x B0..7, B outer.  After column j's four MFMAs: one
+    // refill load of buffer t (weights for j < 4, X for j >= 4), then B[j]
+    // (and A[j], j < 4) of stage t+1 -- their registers' last use this stage.
     const int nbuf = (t + 1) % kStages;
-    // k quarter 1 of stage t; read stage t+1's quarter-0 operands meanwhile
-    // and (ISSUE) refill stage t's buffer with stage t + kStages, one load
-    // per MFMA pair: a burst of loads after the barrier leaves the MFMA
-    // pipe idle (measured: 8% slower on config 3).
+    const int tr = min(t + kStages, T - 1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (kMore && j == 0) bq0[i] = rd(nbuf, b_off(0, i));
-        if (kMore && j == 2) aq0[i] = rd(nbuf, a_off(0, i));
-        if (kIssue && j == 1) dma_w(t + kStages, buf, i);
-        if (kIssue && j == 3) dma_x(t + kStages, buf, i);
-        acc[i][j] = mfma32(aq1[i], bq1[j], acc[i][j]);
-      }
-      if (kMore) {  // per i: [DS read, MFMA, load, MFMA] x 2
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (kIssue) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (kIssue) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      }
+    for (int j = 0; j < 8; ++j) {
+      mfma16(A[4], B[j], acc[4][j]);
+      mfma16(A[5], B[j], acc[5][j]);
+      if (j < 4) dma_w(tr, buf, j);
+      else dma_x(tr, buf, j - 4);
+      mfma16(A[6], B[j], acc[6][j]);
+      mfma16(A[7], B[j], acc[7][j]);
+      B[j] = rd(nbuf, b_off(j));
+      if (j < 4) A[j] = rd(nbuf, a_off(j));
     }
-  };
-  int t = 0;
-  for (; t + kStages < T; ++t) stage(t, std::true_type{}, std::true_type{});  // steady state
-  for (; t + 1 < T; ++t) stage(t, std::false_type{}, std::true_type{});       // drain
-  stage(t, std::false_type{}, std::false_type{});                             // last stage
+  }
+  wait_vmcnt<0>();  // the trailing refills have landed (the epilogue reuses the ring)
+  mfma_drain();
+  acc_fence(acc);   // the epilogue reads the accumulators only after the drain
   LLK_PHASE(t_loop);
 
-  // ---- epilogue: lane holds m = base + lane%32, n = base + 8*(r/4) +
-  // 4*(lane/32) + r%4 for its 16 values r of each 32 x 32 tile.
-  const int h4 = 4 * (lane >> 5);
-  const int mr = lane & 31;
+  // ---- epilogue: acc[i][j] holds, in lane l, output row m = m0 + wm*128 +
+  // 16 j + l%16 and the four consecutive n = (wave's first n) + 16 i' +
+  // 4*(l/16) + 0..3, i' = i (GEMM) or i % 4 (SwiGLU: i >= 4 is the up half).
+  const int h4 = 4 * (lane >> 4);
+  const int mr = lane & 15;
   const int n_end = (MODE == 1) ? tn * 128 + 128 : tn * 256 + 256;
   // Outputs go through LDS: each wave writes a 128-byte-wide column strip
   // of its 128 rows into LDS (144-byte rows, 16-byte pad), then copies whole
   // 128-byte row segments out, 8 rows per instruction, where the accumulator
-  // layout would store 8- or 16-byte pieces of 32 rows per instruction
+  // layout would store 8- or 16-byte pieces of 16 rows per instruction
   // (measured: GEMM 4096^3 epilogue 12 -> 3.4 us).  A tile wholly inside Y
   // (or the partial planes) with 16-byte aligned rows copies 16-byte chunks
   // unchecked; an edge tile checks each chunk and copies the chunks that
@@ -348,17 +365,17 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
     const size_t plane = (size_t)a.M * a.n_pad;
     const bool fast = m0 + kTileM <= a.M && n_end <= a.n_pad;  // plane rows are 16-byte aligned
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // SwiGLU: i < 2 gate, i >= 2 up (same n); GEMM: four n sub-tiles.
-      const int mat = (MODE == 1) ? (i >> 1) : 0;
-      const int col0 = (MODE == 1) ? tn * 128 + wn * 64 + (i & 1) * 32 : tn * 256 + wn * 128 + i * 32;
+    for (int sp = 0; sp < 4; ++sp) {
+      // Strip sp: 32 fp32 columns = accumulator rows i = 2 sp, 2 sp + 1.
+      // SwiGLU: sp < 2 gate, sp >= 2 up (same n); GEMM: four n sub-tiles.
+      const int mat = (MODE == 1) ? (sp >> 1) : 0;
+      const int col0 = (MODE == 1) ? tn * 128 + wn * 64 + (sp & 1) * 32 : tn * 256 + wn * 128 + sp * 32;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<f32x4*>(strip + (j * 32 + mr) * kStripRow + (8 * g + h4) * 4) =
-              f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                    acc[i][j][4 * g + 3]};
+        for (int j = 0; j < 8; ++j)
+          *reinterpret_cast<f32x4*>(strip + (j * 16 + mr) * kStripRow + (ii * 16 + h4) * 4) =
+              acc[2 * sp + ii][j];
       strip_out(std::integral_constant<int, 4>{}, fast, true,
                 reinterpret_cast<uint8_t*>(a.part + ((size_t)split * NMAT + mat) * plane +
                                            (size_t)(m0 + wm * 128) * a.n_pad + col0),
@@ -367,9 +384,9 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
     LLK_PHASE_STORE();
     return;
   }
-  constexpr int NI = (MODE == 1) ? 2 : 4;
+  constexpr int NI = (MODE == 1) ? 4 : 8;         // 16-column groups of the wave's output
   constexpr int kElem = (OUT == kOutF32) ? 4 : 2;
-  constexpr int kPerStrip = 128 / (32 * kElem);  // 32-column groups per strip: 2 or 1
+  constexpr int kPerStrip = 128 / (16 * kElem);  // 16-column groups per 128-byte strip: 4 or 2
   const bool al16 = ((reinterpret_cast<uintptr_t>(a.y) | (uintptr_t)(a.ldy * kElem)) & 15) == 0;
   const bool fast = YVEC && m0 + kTileM <= a.M && n_end <= a.N && al16;
   const int n_w = (MODE == 1) ? tn * 128 + wn * 64 : tn * 256 + wn * 128;
@@ -381,29 +398,27 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
     for (int ii = 0; ii < kPerStrip; ++ii) {
       const int i = sidx * kPerStrip + ii;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 8; ++j) {
+        float v[4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float v[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            if constexpr (MODE == 1)
-              v[q] = swiglu_act(acc[i][j][4 * g + q], acc[i + 2][j][4 * g + q]);
-            else
-              v[q] = acc[i][j][4 * g + q];
-          }
-          uint8_t* const dst = strip + (j * 32 + mr) * kStripRow + (ii * 32 + 8 * g + h4) * kElem;
-          if constexpr (OUT == kOutF32) {
-            *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
-          } else if constexpr (OUT == kOutBF16) {
-            *reinterpret_cast<uint2*>(dst) =
-                make_uint2(f32x2_to_bf16x2_rne(v[0], v[1]), f32x2_to_bf16x2_rne(v[2], v[3]));
-          } else {
-            *reinterpret_cast<uint2*>(dst) =
-                make_uint2((uint32_t)f32_to_f16_rne(v[0]) | ((uint32_t)f32_to_f16_rne(v[1]) << 16),
-                           (uint32_t)f32_to_f16_rne(v[2]) | ((uint32_t)f32_to_f16_rne(v[3]) << 16));
-          }
+        for (int q = 0; q < 4; ++q) {
+          if constexpr (MODE == 1)
+            v[q] = swiglu_act(acc[i][j][q], acc[i + 4][j][q]);
+          else
+            v[q] = acc[i][j][q];
         }
+        uint8_t* const dst = strip + (j * 16 + mr) * kStripRow + (ii * 16 + h4) * kElem;
+        if constexpr (OUT == kOutF32) {
+          *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+        } else if constexpr (OUT == kOutBF16) {
+          *reinterpret_cast<uint2*>(dst) =
+              make_uint2(f32x2_to_bf16x2_rne(v[0], v[1]), f32x2_to_bf16x2_rne(v[2], v[3]));
+        } else {
+          *reinterpret_cast<uint2*>(dst) =
+              make_uint2((uint32_t)f32_to_f16_rne(v[0]) | ((uint32_t)f32_to_f16_rne(v[1]) << 16),
+                         (uint32_t)f32_to_f16_rne(v[2]) | ((uint32_t)f32_to_f16_rne(v[3]) << 16));
+        }
+      }
     }
     strip_out(std::integral_constant<int, kElem>{}, fast, al16, ybase + sidx * 128,
               a.ldy * kElem, rows_ok, a.N - (n_w + sidx * 128 / kElem));
