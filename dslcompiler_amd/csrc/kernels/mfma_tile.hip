@@ -229,16 +229,6 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
     for (int i = 0; i < 4; ++i) dma_x(t, buf, i);
   };
 
-  // Accumulators: acc[i][j] = MFMA rows (n) 16 i .. +16 of the wave's 128
-  // (SwiGLU: i < 4 gate, i >= 4 up of the same n), m 16 j .. +16 of its 128.
-  f32x4 acc[8][8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  acc_fence(acc);  // the zeroed AGPRs are written ...
-  mfma_drain();    // ... well before the first MFMA reads them
-
   // Operands of v_mfma_f32_16x16x32_bf16 (stage-local k 0..31).
   // A operand i: 16 MFMA rows; SwiGLU i < 4 -> Wg rows wn*64 + 16 i, i >= 4
   // -> the same rows of Wu; GEMM -> rows 16 i of n-block wn.  Lane l needs
@@ -268,6 +258,17 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   const int T = nkb * 2;  // stages
 #pragma unroll
   for (int p = 0; p < kStages; ++p) dma_issue(min(p, T - 1), p);
+
+  // Accumulators: acc[i][j] = MFMA rows (n) 16 i .. +16 of the wave's 128
+  // (SwiGLU: i < 4 gate, i >= 4 up of the same n), m 16 j .. +16 of its 128.
+  // Zeroed while the first stages are in flight.
+  f32x4 acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  acc_fence(acc);  // the zeroed AGPRs are written ...
+  mfma_drain();    // ... well before the first MFMA reads them
   wait_vmcnt<(kStages - 1) * kLoadsPerStage>();
   __syncthreads();
   LLK_PHASE(t_first);

@@ -213,8 +213,8 @@ struct Plan {
 
 // k splits of the tile kernel for `rows` rows: the S that minimises the
 // modelled time  waves(S) * (ceil(KB / S) + 2) + partial traffic  in units
-// of one 64-k step of a full wave of workgroups (about 2.06 us on MI355X:
-// a 256 x 256 tile over K = 4096 takes 132 us).  waves(S) = ceil(tiles * S /
+// of one 64-k step of a full wave of workgroups (about 1.6 us on MI355X:
+// a 256 x 256 tile over K = 4096 takes ~102 us).  waves(S) = ceil(tiles * S /
 // tile_wgs_per_wave); the "+ 2" is the per-workgroup pipeline fill and
 // epilogue; the S partial planes (S * nmat * rows * N_pad fp32) are written
 // and read back at ~4 TB/s, plus one step for the reduce launch.
@@ -233,7 +233,7 @@ int tile_splits(int nmat, int64_t rows, int64_t KB, int64_t NB, int64_t db_split
     const int64_t s_eff = (KB + kbs - 1) / kbs;  // no empty splits
     const double waves = (double)((tiles * s_eff + per_wave - 1) / per_wave);
     double cost = waves * (double)(kbs + 2);
-    if (s_eff > 1) cost += 2.0 * s_eff * nmat * rows * NB * 128 * 4 / (4e12 * 2.06e-6) + 1.0;
+    if (s_eff > 1) cost += 2.0 * s_eff * nmat * rows * NB * 128 * 4 / (4e12 * 1.6e-6) + 1.0;
     if (S == 1 || forced > 0 || cost < best) {
       best = cost;
       best_s = s_eff;

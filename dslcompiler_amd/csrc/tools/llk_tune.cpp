@@ -242,16 +242,17 @@ int main(int argc, char** argv) {
     const auto& c = cands[i];
     const bool sm = c.plan.kernel == 0;
     const int64_t BM = sm ? (M <= 32 ? 32 : 64) : 256;
-    // BN 0 / grain_size 0: the dispatcher chooses for each shape
+    // BN 0 / grain_size 0: the dispatcher chooses for each shape; VM x VN is
+    // the MFMA tile (small-M kernel 32x32x16, tile kernel 16x16x32)
     const int64_t BN = sm ? (c.G ? 32 * c.plan.group_width : 0) : (swiglu ? 128 : 256);
     std::fprintf(f,
                  "    {\"operation\": \"%s\", \"target\": \"gfx950\", \"shape\": {\"M_bucket\": %d, "
                  "\"N\": %lld, \"K\": %lld}, \"dtype\": \"bf16\", \"math_mode\": \"strict\",\n"
-                 "     \"schedule\": {\"BM\": %lld, \"BN\": %lld, \"BK\": %d, \"VM\": 32, \"VN\": 32, "
+                 "     \"schedule\": {\"BM\": %lld, \"BN\": %lld, \"BK\": %d, \"VM\": %d, \"VN\": %d, "
                  "\"vector_width\": 8, \"num_threads\": %lld, \"parallel_axis\": \"%s\", "
                  "\"grain_size\": %d},\n     \"source\": \"llk-tune\", \"measured_us\": %.3f}%s\n",
                  op.c_str(), bucket, (long long)N, (long long)K, (long long)BM, (long long)BN,
-                 sm ? 64 : 32, (long long)c.plan.threads_per_workgroup, sm ? "n" : "mn", c.S, c.us,
+                 sm ? 64 : 32, sm ? 32 : 16, sm ? 32 : 16, (long long)c.plan.threads_per_workgroup, sm ? "n" : "mn", c.S, c.us,
                  i + 1 < count ? "," : "");
   }
   std::fprintf(f, "  ]\n}\n");

@@ -81,7 +81,8 @@ def main() -> None:
             "bucket; relative_time = mean of time / best time over the bucket's shapes). Field "
             "meaning on this target: BM/BN = workgroup tile rows / columns per weight matrix "
             "(small-M kernel: BN / 32 = column groups per workgroup); BK = k per step; VM/VN = "
-            "MFMA tile (v_mfma_f32_32x32x16_bf16); vector_width = bf16 per lane operand; "
+            "MFMA tile (small-M kernel v_mfma_f32_32x32x16_bf16, tile kernel "
+            "v_mfma_f32_16x16x32_bf16); vector_width = bf16 per lane operand; "
             "num_threads = threads per workgroup; parallel_axis = grid decomposition; "
             "grain_size = k splits across workgroups (0 = chosen from the shape)."),
         "measured": measured,
