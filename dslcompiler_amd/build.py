@@ -60,6 +60,7 @@ TOOLS = {
 # Self-contained HIP tools (their own build of the kernels they measure).
 HIP_TOOLS = {
     "llk-tile-phases": CSRC / "tools" / "tile_phases.hip",
+    "llk-mfma-rate": CSRC / "tools" / "mfma_rate.hip",
 }
 
 

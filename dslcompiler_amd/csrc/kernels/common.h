@@ -17,8 +17,10 @@
 // A 1 KiB sub-block is exactly the A operand of one v_mfma_f32_32x32x16_bf16
 // (32 rows n x 16 k) in lane order, so one contiguous 1 KiB wave load (global
 // or LDS) yields a ready operand with no bank conflicts, and a 16 KiB block
-// streams contiguously from HBM.  (On gfx950 the 32x32x16 bf16 MFMA issues
-// twice the flops per cycle of the 16x16x32 one.)
+// streams contiguously from HBM.  A v_mfma_f32_16x16x32_bf16 A operand (16
+// rows x 32 k) is two 256-byte halves of two such sub-blocks (k quarters q,
+// q+1), so the same layout serves both MFMA forms (the small-M kernel uses
+// the 32x32x16 form, the tile kernel the 16x16x32 one).
 #pragma once
 
 #include <hip/hip_runtime.h>
