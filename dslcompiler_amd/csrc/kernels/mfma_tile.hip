@@ -18,21 +18,26 @@
 // FuseDoubleContraction.cpp:155-173).  Wave tile: 128 m x 128 MFMA rows =
 // 8 x 8 MFMA tiles of 16 x 16, 256 fp32 accumulators per lane (AGPRs).
 //
-// K loop: 32 k per stage (one MFMA k step), a ring of 4 LDS stages of 32 KiB
-// (16 KiB weights + 16 KiB X).  Operands go straight from memory into LDS
-// (buffer_load_dwordx4 ... lds) three stages ahead of the 64 MFMAs per wave
-// that consume them.  Each stage's barrier sits between its two halves of
-// 32 MFMAs; after it the refill of the freed buffer is issued one load per
-// 4 MFMAs, and each next-stage operand is read once its register's last MFMA
-// of this stage has issued, so neither loads nor LDS reads leave the MFMA
-// pipe idle.  Weights sit in LDS as the payload's 1 KiB sub-blocks (32 n x
-// 16 k, lane order); a 16 x 32 A operand gathers two half sub-blocks, each
-// 16-lane group reading 256 contiguous bytes (conflict-free).  X sits as
-// XOR-swizzled 64-byte rows, so its loads move whole rows and its operand
-// reads (16 rows x 64 bytes) are conflict-free too.
+// K loop: 32 k per stage (one MFMA k step).  LDS holds a ring of 4 weight
+// stages (16 KiB each) and a ring of 3 X blocks of 64 k (256 rows x 128
+// bytes, 32 KiB each): 160 KiB.  Operands go straight from memory into LDS
+// (buffer_load_dwordx4 ... lds) three or more stages ahead of the 64 MFMAs
+// per wave that consume them; X loads move whole 128-byte lines.  Each
+// stage's barrier sits between its two halves of 32 MFMAs; after it the
+// refills of the freed slots are issued one or two loads per 4 MFMAs, and
+// each next-stage operand is read once its register's last MFMA of this
+// stage has issued, so neither loads nor LDS reads leave the MFMA pipe
+// idle.  Weights sit in LDS as the payload's 1 KiB sub-blocks (32 n x 16 k,
+// lane order); a 16 x 32 A operand gathers two half sub-blocks, each 16-lane
+// group reading 256 contiguous bytes (conflict-free).  X sits as
+// XOR-swizzled 128-byte rows, conflict-free for the operand reads (16 rows x
+// 16 bytes per 16 lanes) as well.
 //
-// The MFMAs are issued from inline assembly with the accumulator tied to
-// its AGPRs: through the builtin the register allocator routes a varying
+// The MFMAs and the LDS-DMA loads are issued from inline assembly.  The
+// compiler's LDS-DMA alias tracking cannot tell ring slots indexed at run
+// time apart and would wait for every load before the next LDS read
+// (vmcnt(0) at most barriers); the kernel's explicit vmcnt waits encode the
+// pipeline instead.  The MFMAs have the accumulator tied to its AGPRs: through the builtin the register allocator routes a varying
 // set of the 64 four-register accumulators through temporaries every stage
 // (up to 4 AGPR moves and s_nops per MFMA).  What the hazard recognizer
 // would otherwise see for these instructions is covered by construction:
@@ -106,10 +111,14 @@ struct TileArgs {
 constexpr int kThreads = 256;
 constexpr int kTileM = 256;
 constexpr int kStageK = 32;           // k per pipeline stage
-constexpr int kStageBytes = 32768;    // 16 KiB weights + 16 KiB X
-constexpr int kXOff = 16384;          // X rows inside a stage
-constexpr int kStages = 4;            // LDS ring of stages
-constexpr int kLoadsPerStage = 8;     // buffer_load ... lds per wave per stage
+constexpr int kWStageBytes = 16384;   // weights of one 32-k stage (256 MFMA rows)
+constexpr int kWStages = 4;           // LDS ring of weight stages
+constexpr int kXBlockBytes = 32768;   // X of one 64-k block: 256 rows x 128 bytes
+constexpr int kXBlocks = 3;           // LDS ring of X blocks
+constexpr int kXRingOff = kWStages * kWStageBytes;
+constexpr int kLdsBytes = kXRingOff + kXBlocks * kXBlockBytes;  // 160 KiB
+constexpr int kWLoads = 4;            // buffer_load ... lds per wave per weight stage
+constexpr int kXLoads = 8;            // ... per wave per X block
 constexpr int kStripRow = 144;        // epilogue staging: 128-byte rows + 16-byte pad
 
 // s_waitcnt with vmcnt(n) (n < 64) and the other counters left alone.
@@ -119,6 +128,39 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Raw buffer resource (stride 0) over [base, base + bytes), wave-uniform.
+__device__ __forceinline__ u32x4 buffer_rsrc(const void* base, int bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  u32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane((uint32_t)b);
+  r.y = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32) & 0xffffu);  // stride 0
+  r.z = __builtin_amdgcn_readfirstlane((uint32_t)bytes);
+  r.w = kBufferWord3;
+  return r;
+}
+
+// One buffer_load_dwordx4 ... lds: 16 bytes per lane from the resource at
+// voff (per lane, range-checked: out of range reads zero) + soff (uniform)
+// into LDS at lds + 16 * lane.  Issued from inline assembly so that the
+// compiler's LDS-DMA alias tracking, which cannot tell ring slots indexed
+// at run time apart, adds no waits of its own: the kernel's explicit vmcnt
+// waits order every DMA against the LDS reads of its stage.
+// M0 is clobbered explicitly; the compiler uses M0 for nothing else in these
+// kernels (checked on the code object by tests/test_isa_cpu.py), so its
+// warning about clobbering a reserved register is silenced here.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const u32x4& rsrc, int voff, int soff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// LDS byte address of a pointer into the kernel's dynamic shared memory.
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+  return (uint32_t)(uintptr_t)(lds_ptr_t)(const_cast<uint8_t*>(p));
+}
 
 // acc += A B on v_mfma_f32_16x16x32_bf16, accumulating in place in the
 // accumulator's AGPRs (see the header comment for why this is inline
@@ -172,16 +214,20 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   const int nkb = SPLIT ? min(a.KB - kb0, a.kbs) : a.KB;
 
   // ---- operand streams ----------------------------------------------------
-  // Stage t holds k range [32 t, 32 t + 32).
-  // Weights: LDS slot b (0, 1) holds the 8 sub-blocks (k quarters 2(t%2),
-  // 2(t%2)+1 of block (nb, t/2)) of one packed n-block, 8 KiB contiguous in
+  // Stage t holds k range [32 t, 32 t + 32); X block u = k [64 u, 64 u + 64)
+  // (stages 2u, 2u+1).
+  // Weights: ring slot t % 4 holds stage t: 8 KiB of each of two packed
+  // n-blocks (k quarters 2(t%2), 2(t%2)+1 of block (nb, t/2)), contiguous in
   // the payload at t * 8 KiB of the n-block's panel.  Wave w fills
-  // sub-blocks (w&1)*4 .. +4 of slot w>>1.
-  // X: 256 rows of 32 k = 64 bytes, row r at kXOff + 64 r.  Inside a row the
-  // four 16-byte chunks c (8 k each) are stored at slot c ^ ((r >> 2) & 3),
-  // so an MFMA operand read (16 rows, lane group g reading chunk g of each)
-  // hits every bank once per 16 lanes.  Wave w fills rows w*64 .. +64: each
-  // load instruction covers 16 full rows.
+  // sub-blocks (w&1)*4 .. +4 of half w>>1.
+  // X: ring slot u % 3 holds block u: 256 rows of 64 k = 128 bytes, row r at
+  // 128 r.  Each load instruction moves 8 whole rows -- full 128-byte lines,
+  // where 64-byte rows of a single stage took half lines (measured: the
+  // half-line loads cost 2.6% of config 3 on N(0,1) data, in power).  Inside
+  // a row the eight 16-byte chunks c (8 k each) sit at slot c ^ ((r >> 1) & 7):
+  // rows r and r + 2 share banks (128-byte rows), so the 16 rows of an MFMA
+  // operand read (lane group g reading chunk 4h + g of each) land on 16
+  // distinct 16-byte bank groups.  Wave w fills rows w*64 .. +64.
   const int wslot = wave >> 1;
   const uint8_t* wpanel;
   if (MODE == 1) {
@@ -193,40 +239,40 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
     wpanel = a.w0 + (size_t)(nb < a.NB ? nb : 0) * a.KB * kBlockBytes;
   }
   wpanel += (size_t)kb0 * kBlockBytes + (wave & 1) * 4 * kSubBytes;
-  const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(wpanel), (short)0, nkb * kBlockBytes, kBufferWord3);
+  const u32x4 wrsrc = buffer_rsrc(wpanel, nkb * kBlockBytes);
   const int w_voff = lane * 16;
 
   // The X resource starts at row m0, column 64 kb0, and ends at row M:
   // rows >= M read zero.
   const int rows_left = a.M - m0;
-  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(a.x) + (size_t)m0 * a.ldx + (size_t)kb0 * 64, (short)0,
-      (int)((int64_t)rows_left * a.ldx * 2 - (int64_t)kb0 * 128), kBufferWord3);
-  // Load slot p = lane of an instruction: row (lane/4) of 16, stored chunk
-  // lane%4 holding logical chunk (lane%4) ^ ((row >> 2) & 3).
-  const int x_rowstep = 16 * (int)a.ldx * 2;
-  const int x_voff =
-      (((lane >> 2) + wave * 64) * (int)a.ldx + (((lane & 3) ^ ((lane >> 4) & 3)) * 8)) * 2;
+  const u32x4 xrsrc = buffer_rsrc(a.x + (size_t)m0 * a.ldx + (size_t)kb0 * 64,
+                                 (int)((int64_t)rows_left * a.ldx * 2 - (int64_t)kb0 * 128));
+  // Load slot p = lane of load i: row w*64 + 8 i + p/8, stored chunk p%8
+  // holding logical chunk (p%8) ^ ((row >> 1) & 7) = (p%8) ^ (p/16) ^ 4(i%2).
+  const int x_rowstep = 8 * (int)a.ldx * 2;
+  const int x_voff[2] = {
+      (((lane >> 3) + wave * 64) * (int)a.ldx + (((lane & 7) ^ (lane >> 4)) * 8)) * 2,
+      (((lane >> 3) + wave * 64) * (int)a.ldx + (((lane & 7) ^ (lane >> 4) ^ 4) * 8)) * 2};
 
-  // Load i (0..3) of this wave's share of stage t into LDS buffer buf.
-  auto dma_w = [&](int t, int buf, int i) {
-    uint8_t* st = smem + buf * kStageBytes + (wave * 4) * kSubBytes;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(wrsrc, (lds_ptr_t)(st + i * kSubBytes), 16, w_voff,
-                                             t * 8 * kSubBytes + i * kSubBytes, 0, 0);
+  // Load i (0..3) of this wave's share of weight stage t into ring slot wb.
+  auto dma_w = [&](int t, int wb, int i) {
+    const uint8_t* st = smem + wb * kWStageBytes + (wave * 4) * kSubBytes;
+    dma16(wrsrc, w_voff, t * 8 * kSubBytes + i * kSubBytes, lds_addr(st + i * kSubBytes));
   };
-  auto dma_x = [&](int t, int buf, int i) {
-    uint8_t* st = smem + buf * kStageBytes + (wave * 4) * kSubBytes;
+  // Load i (0..7) of this wave's share of X block u into ring slot xb.
+  auto dma_x = [&](int u, int xb, int i) {
+    const uint8_t* st = smem + kXRingOff + xb * kXBlockBytes + (wave * 8) * kSubBytes;
     // whole offset in the VGPR operand so the range check covers it
-    const int voff = x_voff + i * x_rowstep + t * (kStageK * 2);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(xrsrc, (lds_ptr_t)(st + kXOff + i * kSubBytes), 16,
-                                             voff, 0, 0, 0);
+    const int voff = x_voff[i & 1] + i * x_rowstep + u * (kPackK * 2);
+    dma16(xrsrc, voff, 0, lds_addr(st + i * kSubBytes));
   };
-  auto dma_issue = [&](int t, int buf) {
+  auto dma_w_stage = [&](int t, int wb) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma_w(t, buf, i);
+    for (int i = 0; i < kWLoads; ++i) dma_w(t, wb, i);
+  };
+  auto dma_x_block = [&](int u, int xb) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma_x(t, buf, i);
+    for (int i = 0; i < kXLoads; ++i) dma_x(u, xb, i);
   };
 
   // Operands of v_mfma_f32_16x16x32_bf16 (stage-local k 0..31).
@@ -234,30 +280,43 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   // -> the same rows of Wu; GEMM -> rows 16 i of n-block wn.  Lane l needs
   // row l%16 and k 8*(l/16) .. +8: k quarter l/32 of the stage, slot
   // (row % 32) + 32*((l/16) % 2) of that quarter's 32 n x 16 k sub-block.
-  // B operand j: X rows wm*128 + 16 j + l%16, logical chunk l/16 (8 k).
+  // B operand j of a stage with block half h (t % 2): X rows wm*128 + 16 j +
+  // l%16, logical chunk 4h + l/16 (8 k).
   const int a_lane = (lane >> 5) * 4 * kSubBytes + ((lane & 15) + 32 * ((lane >> 4) & 1)) * 16;
   const int brow = lane & 15;
-  const int b_lane = brow * 64 + (((lane >> 4) ^ ((brow >> 2) & 3)) * 16);
+  const int b_lane[2] = {brow * 128 + (((lane >> 4) ^ (brow >> 1)) * 16),
+                         brow * 128 + (((4 + (lane >> 4)) ^ (brow >> 1)) * 16)};
   auto a_off = [&](int i) -> int {
     const int slot = (MODE == 1) ? (i >> 2) : wn;
     const int nn = (MODE == 1) ? wn * 64 + 16 * (i & 3) : 16 * i;
     return slot * 8 * kSubBytes + (nn >> 5) * kSubBytes + ((nn >> 4) & 1) * 256 + a_lane;
   };
-  auto b_off = [&](int j) -> int { return kXOff + (wm * 128 + j * 16) * 64 + b_lane; };
-  auto rd = [&](int buf, int off) {
-    return *reinterpret_cast<const bf16x8*>(smem + buf * kStageBytes + off);
+  auto rd_a = [&](int wb, int i) {
+    return *reinterpret_cast<const bf16x8*>(smem + wb * kWStageBytes + a_off(i));
+  };
+  auto rd_b = [&](int xb, int h, int j) {
+    return *reinterpret_cast<const bf16x8*>(smem + kXRingOff + xb * kXBlockBytes +
+                                            (wm * 128 + j * 16) * 128 + b_lane[h]);
   };
 
-  // Pipeline: one loop body for every stage.  Stages 0..kStages-1 are
-  // issued up front; stage t refills its own buffer with stage t + kStages
-  // after its barrier, so at that barrier stage t+1 has landed once at most
-  // the loads of stages t+2 and t+3 are outstanding.  Refills past the last
-  // stage T-1 re-read stage T-1 (in bounds) into buffers no MFMA reads
-  // again, which keeps the wait counts uniform; they all land before the
+  // Pipeline: stage t refills weight slot t % 4 with stage t + 4 after its
+  // barrier, and an odd stage 2u+1 also refills X slot u % 3 with block
+  // u + 3 (block u's last operand reads were for stage 2u+1, in stage 2u).
+  // The prologue issues X0 W0 W1 X1 W2 W3 X2, the order the steady state
+  // would have issued them in, so at every barrier "stage t+1 has landed"
+  // is one wait count: at most 24 loads outstanding at an even stage (X of
+  // stage t-3, the refills of t-2 and t-1), 16 at an odd one.  Refills past
+  // the end re-read the last stage / block (in bounds) into slots no MFMA
+  // reads again, which keeps the counts uniform; they all land before the
   // epilogue reuses the ring.
   const int T = nkb * 2;  // stages
-#pragma unroll
-  for (int p = 0; p < kStages; ++p) dma_issue(min(p, T - 1), p);
+  dma_x_block(0, 0);
+  dma_w_stage(0, 0);
+  dma_w_stage(min(1, T - 1), 1);
+  dma_x_block(min(1, nkb - 1), 1);
+  dma_w_stage(min(2, T - 1), 2);
+  dma_w_stage(min(3, T - 1), 3);
+  dma_x_block(min(2, nkb - 1), 2);
 
   // Accumulators: acc[i][j] = MFMA rows (n) 16 i .. +16 of the wave's 128
   // (SwiGLU: i < 4 gate, i >= 4 up of the same n), m 16 j .. +16 of its 128.
@@ -269,44 +328,57 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
     for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   acc_fence(acc);  // the zeroed AGPRs are written ...
   mfma_drain();    // ... well before the first MFMA reads them
-  wait_vmcnt<(kStages - 1) * kLoadsPerStage>();
+  wait_vmcnt<2 * kXLoads + 3 * kWLoads>();  // X0 and W0 landed
   __syncthreads();
   LLK_PHASE(t_first);
 
   bf16x8 A[8], B[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) B[j] = rd(0, b_off(j));
+  for (int j = 0; j < 8; ++j) B[j] = rd_b(0, 0, j);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) A[i] = rd(0, a_off(i));
+  for (int i = 0; i < 4; ++i) A[i] = rd_a(0, i);
 
-  for (int t = 0; t < T; ++t) {
-    const int buf = t % kStages;
-    // Half 0: A0..3 x B0..7, A outer; A4..7 of stage t are read meanwhile.
+  // Stage t = 2u + H (H = 0, 1).  Half 0: A0..3 x B0..7, A outer; A4..7 of
+  // stage t are read meanwhile.  Half 1: A4..7 x B0..7, B outer; after
+  // column j's four MFMAs the refill loads (weights for j < 4, for odd
+  // stages X two per column for j >= 4), then B[j] (and A[j], j < 4) of
+  // stage t+1 -- their registers' last use this stage.
+  auto stage = [&](int u, auto H) {
+    constexpr int kH = decltype(H)::value;
+    const int t = 2 * u + kH;
+    const int wb = t % kWStages;
+    const int xb = u % kXBlocks;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      A[4 + i] = rd(buf, a_off(4 + i));
+      A[4 + i] = rd_a(wb, 4 + i);
 #pragma unroll
       for (int j = 0; j < 8; ++j) mfma16(A[i], B[j], acc[i][j]);
     }
-    wait_lgkmcnt0();                               // this wave's reads of stage t are done
-    wait_vmcnt<(kStages - 2) * kLoadsPerStage>();  // stage t+1 landed
-    __syncthreads();                               // ... for every wave; buffer t is free
-    // Half 1: A4..7 x B0..7, B outer.  After column j's four MFMAs: one
-    // refill load of buffer t (weights for j < 4, X for j >= 4), then B[j]
-    // (and A[j], j < 4) of stage t+1 -- their registers' last use this stage.
-    const int nbuf = (t + 1) % kStages;
-    const int tr = min(t + kStages, T - 1);
+    wait_lgkmcnt0();  // this wave's reads of stage t are done
+    if constexpr (kH == 0) wait_vmcnt<2 * kXLoads + 2 * kWLoads>();  // stage t+1 landed
+    else wait_vmcnt<kXLoads + 2 * kWLoads>();
+    __syncthreads();  // ... for every wave; weight slot t (and X slot u at odd t) free
+    const int nwb = (t + 1) % kWStages;
+    const int nxb = kH == 0 ? xb : (u + 1) % kXBlocks;
+    constexpr int nh = 1 - kH;
+    const int tw = min(t + kWStages, T - 1);
+    const int ux = min(u + kXBlocks, nkb - 1);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       mfma16(A[4], B[j], acc[4][j]);
       mfma16(A[5], B[j], acc[5][j]);
-      if (j < 4) dma_w(tr, buf, j);
-      else dma_x(tr, buf, j - 4);
+      if (j < 4) dma_w(tw, wb, j);
+      else if (kH == 1) dma_x(ux, xb, 2 * (j - 4));
       mfma16(A[6], B[j], acc[6][j]);
+      if (kH == 1 && j >= 4) dma_x(ux, xb, 2 * (j - 4) + 1);
       mfma16(A[7], B[j], acc[7][j]);
-      B[j] = rd(nbuf, b_off(j));
-      if (j < 4) A[j] = rd(nbuf, a_off(j));
+      B[j] = rd_b(nxb, nh, j);
+      if (j < 4) A[j] = rd_a(nwb, j);
     }
+  };
+  for (int u = 0; u < nkb; ++u) {
+    stage(u, std::integral_constant<int, 0>{});
+    stage(u, std::integral_constant<int, 1>{});
   }
   wait_vmcnt<0>();  // the trailing refills have landed (the epilogue reuses the ring)
   mfma_drain();
@@ -465,10 +537,10 @@ template <int MODE, int OUT, bool YVEC, bool SPLIT>
 static hipError_t launch_tile_t(const TileArgs& a, hipStream_t s) {
   auto fn = mfma_tile_kernel<MODE, OUT, YVEC, SPLIT>;
   static std::atomic<uint64_t> lds_set{0};  // devices configured, per instantiation
-  hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(fn), kStages * kStageBytes, lds_set);
+  hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(fn), kLdsBytes, lds_set);
   if (e != hipSuccess) return e;
   dim3 grid(a.tiles_m * a.tiles_n * (SPLIT ? a.S : 1)), block(kThreads);
-  hipLaunchKernelGGL(fn, grid, block, kStages * kStageBytes, s, a);
+  hipLaunchKernelGGL(fn, grid, block, kLdsBytes, s, a);
   return hipGetLastError();
 }
 

@@ -7,8 +7,11 @@ recognizer does not see them.  The kernel keeps the hazards away by
 construction; these tests hold that construction on the instructions the
 compiler actually emitted, for every instantiation:
 
-* the K loop body is exactly 64 MFMAs with no AGPR copies (the reason for the
-  inline assembly) and every MFMA accumulates in place;
+* the K loop body (two 32-k stages) is exactly 128 MFMAs with no AGPR copies
+  (the reason for the inline assembly) and every MFMA accumulates in place;
+* its only vector-memory waits are the two barriers' (the LDS-DMA loads are
+  inline assembly too, so that the compiler adds no waits of its own), and M0
+  is written only by those loads' own s_mov;
 * no VALU instruction writes an MFMA's A/B operand registers shortly before
   it (operands must come from LDS loads, whose waits the compiler places);
 * nothing writes an AGPR between the MFMAs except the MFMAs themselves;
@@ -110,15 +113,30 @@ def test_every_tile_instantiation_found(asm):
     assert len(ks) >= 10, sorted(ks)
 
 
-def test_k_loop_is_64_in_place_mfmas_without_agpr_copies(asm):
+def test_k_loop_is_128_in_place_mfmas_without_agpr_copies(asm):
     for name, lines in kernels(asm).items():
         body = [b for b in k_loop(lines) if is_insn(b)]
         mf = [b for b in body if b.startswith(MFMA)]
-        assert len(mf) == 64, (name, len(mf))
+        assert len(mf) == 128, (name, len(mf))
         assert not [b for b in body if b.startswith("v_accvgpr")], name
         for b in mf:
             ops = operands(b)
             assert ops[0] == ops[3] and ops[0].startswith("a["), (name, b)
+
+
+def test_k_loop_waits_and_m0(asm):
+    for name, lines in kernels(asm).items():
+        body = [b for b in k_loop(lines) if is_insn(b)]
+        vm = [b for b in body if "vmcnt" in b]
+        assert [re.search(r"vmcnt\((\d+)\)", b).group(1) for b in vm] == ["24", "16"], (name, vm)
+        assert sum(b == "s_barrier" for b in body) == 2, name
+        insns = [b for b in lines if is_insn(b)]
+        for k, b in enumerate(insns):
+            if "m0" in b:
+                assert b.startswith("s_mov_b32 m0,"), (name, b)
+                assert insns[k + 1] == "s_nop 0" and insns[k + 2].startswith("buffer_load_dwordx4"), \
+                    (name, insns[k:k + 3])
+                assert insns[k + 2].endswith(" lds"), (name, insns[k + 2])
 
 
 def test_no_valu_writes_mfma_operands_just_before(asm):
