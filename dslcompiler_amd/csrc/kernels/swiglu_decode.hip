@@ -289,9 +289,9 @@ struct SkinnyCfg {
                         : (32 / (G * NMAT * MT) < 16 / G ? 32 / (G * NMAT * MT) : 16 / G))
               : (NMAT == 2 ? 4 / G : (MT == 1 ? 16 / G : 4));
   static constexpr int UNROLL = (GW == 2 && NMAT == 1 && MT == 1) ? 1 : 2;
-  // SwiGLU with M <= 32 and one group per wave: two steps of weights in
-  // flight fit the 128 registers of 16 waves per CU.
-  static constexpr bool PIPE = NMAT == 2 && MT == 1 && GW == 1;
+  // M <= 32 with one group per wave or one wave group (all but the GEMM's
+  // 4-group form): two steps of weights in flight fit the registers.
+  static constexpr bool PIPE = MT == 1 && (GW == 1 || G == 1);
   static constexpr size_t lds = (size_t)KS * G * GW * MT * 16 * 64 * sizeof(float);
   static_assert(G * GW == W && KS * G <= 16 && lds <= 131072, "small-M launch shape");
 };
