@@ -69,13 +69,20 @@ __device__ __forceinline__ void load_x_frags(const SkinnyArgs& a, int kb, int la
 // (X traffic per workgroup is G * M * K * 2 bytes, against the weights'
 // G * GW * 32 * K * 2 * NMAT), and the G * GW sub-blocks a k part reads at
 // one k step are neighbouring 1 KiB pieces of the same 4 KiB.
+// Floats of one matrix's partial sums in the reduction buffer, and whether
+// both matrices' fit (128 KiB) so that they reduce in one pass.
+constexpr int skinny_red_floats(int KS, int G, int GW, int MT) { return KS * G * GW * MT * 16 * 64; }
+constexpr bool skinny_one_pass(int NMAT, int red_floats) {
+  return NMAT == 2 && 2 * red_floats * (int)sizeof(float) <= 131072;
+}
+
 // PIPE: the weight loads of the next 64-k step are issued before this
 // step's MFMAs (one step of weights in flight per wave beyond the one being
 // used; UNROLL is then unused) -- the form for the shapes whose register
 // budget holds two steps, measured 1.5% faster at decode M = 8.
 template <int NMAT, int MT, int KS, int G, int GW, int OUT, bool XVEC, int UNROLL, bool PIPE>
 __global__ __launch_bounds__(KS * G * 64) void skinny_kernel(SkinnyArgs a) {
-  extern __shared__ __attribute__((aligned(16))) float red[];  // [KS][G][GW][MT][16][64], one matrix
+  extern __shared__ __attribute__((aligned(16))) float red[];  // [1 or NMAT][KS][G][GW][MT][16][64]
   constexpr int NT = KS * G * 64;
   constexpr int TOT = G * GW * MT * 4 * 64;  // output quads of the workgroup
   constexpr int EPT = (TOT + NT - 1) / NT;   // quads per thread
@@ -178,22 +185,24 @@ __global__ __launch_bounds__(KS * G * 64) void skinny_kernel(SkinnyArgs a) {
     }
   }
 
-  // ---- reduce the KS waves' partial sums in LDS, in wave order, one matrix
+  // ---- reduce the KS waves' partial sums in LDS, in wave order: both
+  // matrices in one pass when their partials fit 128 KiB, else one matrix
   // per pass.  Quad e of the workgroup = (group ge, t, g, ln): rows m = t*32 +
   // ln%32 and the 4 consecutive columns 8g + 4*(ln/32) + 0..3 (accumulator
   // r = 4g + q) of group ge; thread x handles quads x, x + NT, ...
+  constexpr int kRed = skinny_red_floats(KS, G, GW, MT);  // per matrix
+  constexpr bool kOnePass = skinny_one_pass(NMAT, kRed);
   float sum[EPT][NMAT][4];
-#pragma unroll
-  for (int p = 0; p < NMAT; ++p) {
-    if (p > 0) __syncthreads();  // the previous pass's readers are done
+  auto write_red = [&](int p, float* base) {
 #pragma unroll
     for (int j = 0; j < GW; ++j)
 #pragma unroll
       for (int t = 0; t < MT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          red[(((wave * GW + j) * MT + t) * 16 + r) * 64 + lane] = acc[j][p][t][r];
-    __syncthreads();
+          base[(((wave * GW + j) * MT + t) * 16 + r) * 64 + lane] = acc[j][p][t][r];
+  };
+  auto read_red = [&](int p, const float* base) {
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
       const int e = threadIdx.x + i * NT;
@@ -204,9 +213,24 @@ __global__ __launch_bounds__(KS * G * 64) void skinny_kernel(SkinnyArgs a) {
       for (int q = 0; q < 4; ++q) {
         float s = 0.0f;
         for (int w2 = 0; w2 < KS; ++w2)
-          s += red[((((w2 * G + gg) * GW + j) * MT + t) * 16 + 4 * g + q) * 64 + ln];
+          s += base[((((w2 * G + gg) * GW + j) * MT + t) * 16 + 4 * g + q) * 64 + ln];
         sum[i][p][q] = s;
       }
+    }
+  };
+  if constexpr (kOnePass) {
+#pragma unroll
+    for (int p = 0; p < NMAT; ++p) write_red(p, red + p * kRed);
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < NMAT; ++p) read_red(p, red + p * kRed);
+  } else {
+#pragma unroll
+    for (int p = 0; p < NMAT; ++p) {
+      if (p > 0) __syncthreads();  // the previous pass's readers are done
+      write_red(p, red);
+      __syncthreads();
+      read_red(p, red);
     }
   }
 
@@ -279,7 +303,8 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(SkinnyArgs a, int ro
 // M = 64 X traffic equals the weights').  Register budgets: KS * G * 64
 // threads with at most 512 / waves-per-SIMD VGPRs each; the SwiGLU M > 32
 // form holds 2 x 2 x 2 accumulators plus 2 k steps of loads (~312 VGPRs, one
-// wave per SIMD).  LDS per pass: KS * G * GW * MT * 4 KiB <= 128 KiB.
+// wave per SIMD).  LDS: KS * G * GW * MT * 4 KiB per matrix, both matrices
+// at once when that fits 128 KiB.
 template <int NMAT, int MT, int W>
 struct SkinnyCfg {
   static constexpr int GW = (W == 1 || (NMAT == 2 && MT == 1)) ? 1 : 2;
@@ -289,10 +314,12 @@ struct SkinnyCfg {
                         : (32 / (G * NMAT * MT) < 16 / G ? 32 / (G * NMAT * MT) : 16 / G))
               : (NMAT == 2 ? 4 / G : (MT == 1 ? 16 / G : 4));
   static constexpr int UNROLL = (GW == 2 && NMAT == 1 && MT == 1) ? 1 : 2;
-  // M <= 32 with one group per wave or one wave group (all but the GEMM's
-  // 4-group form): two steps of weights in flight fit the registers.
-  static constexpr bool PIPE = MT == 1 && (GW == 1 || G == 1);
-  static constexpr size_t lds = (size_t)KS * G * GW * MT * 16 * 64 * sizeof(float);
+  // M <= 32 with one group per wave or one wave group, up to 8 waves per
+  // wave group: two steps of weights in flight fit the registers (the
+  // 4-group forms with 4 waves per group spill).
+  static constexpr bool PIPE = MT == 1 && (GW == 1 || G == 1) && G * GW <= 2;
+  static constexpr size_t lds = (size_t)skinny_red_floats(KS, G, GW, MT) * sizeof(float) *
+                                (skinny_one_pass(NMAT, skinny_red_floats(KS, G, GW, MT)) ? 2 : 1);
   static_assert(G * GW == W && KS * G <= 16 && lds <= 131072, "small-M launch shape");
 };
 
