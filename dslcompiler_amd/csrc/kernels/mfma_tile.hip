@@ -7,8 +7,8 @@
 // four consecutive n of one output row m.  The 16x16x32 form issues the same
 // flops per cycle as the 32x32x16 one but moves half the accumulator
 // register traffic per flop; on N(0,1) data, where the board's power limit
-// sets the clock, it sustains ~15% more (register-only loop: 1.96 vs 1.70
-// PFLOP/s) and this kernel 6-9% more.
+// sets the clock, it sustains ~14% more (register-only loop: 2.07 vs 1.82
+// PFLOP/s) and this kernel 5-9% more.
 //
 // Workgroup: 256 threads (4 waves, 2 x 2).  Workgroup tile 256 m x 256
 // MFMA rows:  GEMM -> 256 n;  SwiGLU -> 128 n of Wg + the same 128 n of Wu,
@@ -37,9 +37,10 @@
 // compiler's LDS-DMA alias tracking cannot tell ring slots indexed at run
 // time apart and would wait for every load before the next LDS read
 // (vmcnt(0) at most barriers); the kernel's explicit vmcnt waits encode the
-// pipeline instead.  The MFMAs have the accumulator tied to its AGPRs: through the builtin the register allocator routes a varying
-// set of the 64 four-register accumulators through temporaries every stage
-// (up to 4 AGPR moves and s_nops per MFMA).  What the hazard recognizer
+// pipeline instead.  The MFMAs have the accumulator tied to its AGPRs:
+// through the builtin the register allocator routes a varying set of the 64
+// four-register accumulators through temporaries every stage (up to 4 AGPR
+// moves and s_nops per MFMA).  What the hazard recognizer
 // would otherwise see for these instructions is covered by construction:
 // A/B operands come only from LDS loads (the compiler places their waits),
 // accumulators are written by nothing but the MFMAs inside the K loop, and

@@ -233,6 +233,27 @@ def test_gemm_tile_splits(llk, gpu, orc, M, K, N, S):
     assert np.array_equal(cb, to_bf16_bits(cf)), "bf16 != RNE(fp32)"
 
 
+@pytest.mark.parametrize("K", [1, 32, 64, 96, 192, 320])
+def test_tile_short_k_pipeline(llk, gpu, orc, K):
+    """The tile kernel's prologue fills three 64-k X slots and four 32-k
+    weight stages before the loop; with one to five k-blocks most of those
+    loads fall past the end and are clamped.  K below one block (1, 32),
+    exactly one (64), one and a half (96, padded), and odd block counts
+    (3, 5), each with and without a k split, on two M tiles and a ragged N."""
+    print(f"case tile short k K={K}", flush=True)
+    M, N = 260, 200
+    x, wg, wu = swiglu_inputs(M, K, N, seed=K)
+    s = 1.0 / np.sqrt(K)
+    b = normal_bf16(K, 1, (K, N), s)
+    cf_ref, _ = orc.gemm(x, b)
+    pb = llk.PackedWeights.from_host(b)
+    for S in (1, 3):
+        with _Tunable(llk, "decode_max_m", 0), _Tunable(llk, "tile_splits", S):
+            _check_swiglu(llk, gpu, orc, x, wg, wu, f"tile short k K={K} S={S}")
+            cf = from_dev(llk.matmul(to_dev(gpu, x), pb, out_dtype=gpu.float32))
+        assert_parity(cf, cf_ref, f"gemm short k K={K} S={S}")
+
+
 def test_tile_splits_exact_and_reuse(llk, gpu, orc):
     """Integer inputs make every partial sum exact, so any k split must give
     the oracle's gate/up bit for bit: GEMM fp32 output equal, SwiGLU within
