@@ -209,6 +209,7 @@ struct Plan {
   size_t pad_bytes = 0;  // tile path: padded X at the start of the workspace
   size_t ws_bytes = 0;   // workspace the plan needs
   bool too_large = false;  // tile path: K beyond the kernel's 32-bit offsets
+  int64_t head_nb = 0;   // tile path: leading n-blocks launched unsplit (S applies to the rest)
 };
 
 // k splits of the tile kernel for `rows` rows: the S that minimises the
@@ -218,28 +219,57 @@ struct Plan {
 // tile_wgs_per_wave); the "+ 2" is the per-workgroup pipeline fill and
 // epilogue; the S partial planes (S * nmat * rows * N_pad fp32) are written
 // and read back at ~4 TB/s, plus one step for the reduce launch.
-int tile_splits(int nmat, int64_t rows, int64_t KB, int64_t NB, int64_t db_splits) {
-  int64_t forced = llk::tunable("tile_splits");
-  if (forced <= 0) forced = db_splits;
+struct SplitCost {
+  int S;
+  double cost;
+};
+
+SplitCost best_split(int nmat, int64_t rows, int64_t KB, int64_t NB, int64_t forced) {
   const int64_t min_kb = std::max<int64_t>(1, llk::tunable("tile_min_kb"));
   int64_t smax = std::min<int64_t>(64, std::max<int64_t>(1, KB / min_kb));
   if (forced > 0) smax = std::min(forced, KB);
   const int64_t tiles = (rows + 255) / 256 * (nmat == 2 ? NB : (NB + 1) / 2);
   const int64_t per_wave = std::max<int64_t>(1, llk::tunable("tile_wgs_per_wave"));
-  int64_t best_s = 1;
-  double best = 0.0;
+  SplitCost best{1, 0.0};
   for (int64_t S = forced > 0 ? smax : 1; S <= smax; ++S) {
     const int64_t kbs = (KB + S - 1) / S;
     const int64_t s_eff = (KB + kbs - 1) / kbs;  // no empty splits
     const double waves = (double)((tiles * s_eff + per_wave - 1) / per_wave);
     double cost = waves * (double)(kbs + 2);
     if (s_eff > 1) cost += 2.0 * s_eff * nmat * rows * NB * 128 * 4 / (4e12 * 1.6e-6) + 1.0;
-    if (S == 1 || forced > 0 || cost < best) {
-      best = cost;
-      best_s = s_eff;
-    }
+    if (S == 1 || forced > 0 || cost < best.cost) best = SplitCost{(int)s_eff, cost};
   }
-  return (int)best_s;
+  return best;
+}
+
+// The tile kernel's launch over `rows` rows: k splits S for the columns from
+// n-block head_nb on, and head_nb leading n-blocks run unsplit first (0: one
+// launch over all columns).  Tail split: when the tiles fill q >= 1 whole
+// waves and leave a partial one (config 5 at M = 4097: 340 GEMM tiles on 256
+// CUs), the whole n-tile columns that fit q waves run unsplit and only the
+// remaining columns take a k split -- one short balanced wave instead of a
+// nearly empty long one, with partial planes for the tail columns only.
+// Used when the model puts it 3% or more below the best single launch.
+struct TilePlan {
+  int S;
+  int64_t head_nb;
+};
+
+TilePlan tile_plan(int nmat, int64_t rows, int64_t KB, int64_t NB, int64_t db_splits) {
+  int64_t forced = llk::tunable("tile_splits");
+  if (forced <= 0) forced = db_splits;
+  const SplitCost all = best_split(nmat, rows, KB, NB, forced);
+  if (forced > 0 || llk::tunable("tile_tail_split") == 0) return {all.S, 0};
+  const int64_t nb_per_tile = nmat == 2 ? 1 : 2;
+  const int64_t tm = (rows + 255) / 256, tn = (NB + nb_per_tile - 1) / nb_per_tile;
+  const int64_t per_wave = std::max<int64_t>(1, llk::tunable("tile_wgs_per_wave"));
+  const int64_t head_tn = tm * tn / per_wave * per_wave / tm;  // columns of q whole waves
+  if (head_tn <= 0 || head_tn >= tn) return {all.S, 0};
+  const int64_t head_nb = head_tn * nb_per_tile;
+  const double head = (double)((tm * head_tn + per_wave - 1) / per_wave) * (double)(KB + 2);
+  const SplitCost tail = best_split(nmat, rows, KB, NB - head_nb, 0);
+  if (head + tail.cost <= 0.97 * all.cost) return {tail.S, head_nb};
+  return {all.S, 0};
 }
 
 // Active schedule DB (llk_set_schedule_db, or the file named by the
@@ -366,8 +396,11 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
     p.chunk = std::max<int64_t>(256, (((int64_t)1 << 31) - 1) / (p.ld * 2) / 256 * 256 - 256);
   const int64_t rows = std::min(p.chunk, M);
   if (p.pad) p.pad_bytes = ((size_t)rows * p.ld * 2 + 255) / 256 * 256;
-  p.S = tile_splits(nmat, rows, KB, NB, have_db ? se.grain_size : 0);
-  p.ws_bytes = p.pad_bytes + llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)rows, (int)NB, p.S);
+  const TilePlan tp = tile_plan(nmat, rows, KB, NB, have_db ? se.grain_size : 0);
+  p.S = tp.S;
+  p.head_nb = tp.head_nb;
+  p.ws_bytes = p.pad_bytes +
+               llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)rows, (int)(NB - p.head_nb), p.S);
   return p;
 }
 
@@ -403,9 +436,22 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
       if (e != hipSuccess) break;
       xp = static_cast<const uint16_t*>(ws);
     }
-    e = llk_launch_tile(mode, xp, p.ld, w0->dev, w1 ? w1->dev : nullptr,
-                        static_cast<uint8_t*>(y->data) + m0 * y->stride0 * ysz, y->stride0, rows,
-                        (int)N, (int)w0->KB, (int)w0->NB, p.S,
+    uint8_t* yp = static_cast<uint8_t*>(y->data) + m0 * y->stride0 * ysz;
+    if (p.head_nb > 0) {
+      e = llk_launch_tile(mode, xp, p.ld, w0->dev, w1 ? w1->dev : nullptr, yp, y->stride0, rows,
+                          (int)(p.head_nb * 128), (int)w0->KB, (int)p.head_nb, 1, nullptr,
+                          out_dtype, yvec, s);
+      if (e != hipSuccess) break;
+    }
+    // Columns from n-block head_nb on: the packed payload of a matrix is
+    // n-block major (KB blocks of 16 KiB per n-block), so they start
+    // head_nb * KB blocks in.
+    const size_t w_off = (size_t)p.head_nb * w0->KB * 16384;
+    const int64_t n0 = p.head_nb * 128;
+    e = llk_launch_tile(mode, xp, p.ld, static_cast<const uint8_t*>(w0->dev) + w_off,
+                        w1 ? static_cast<const uint8_t*>(w1->dev) + w_off : nullptr,
+                        yp + n0 * ysz, y->stride0, rows, (int)(N - n0), (int)w0->KB,
+                        (int)(w0->NB - p.head_nb), p.S,
                         p.S > 1 ? static_cast<uint8_t*>(ws) + p.pad_bytes : nullptr, out_dtype,
                         yvec, s);
   }
@@ -843,9 +889,13 @@ int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, int x_al
   out->pad_x = p.pad ? 1 : 0;
   const int64_t rows = std::min(p.chunk, M);
   const int64_t chunks = (M + p.chunk - 1) / p.chunk;
-  out->workgroups = (rows + 255) / 256 * (nmat == 2 ? NB : (NB + 1) / 2) * p.S;
+  const int64_t nb_per_tile = nmat == 2 ? 1 : 2, tail_nb = NB - p.head_nb;
+  out->workgroups = (rows + 255) / 256 *
+                    (p.head_nb / nb_per_tile + (tail_nb + nb_per_tile - 1) / nb_per_tile * p.S);
   out->threads_per_workgroup = 256;
-  out->launches = chunks * (1 + (p.pad ? 1 : 0) + (p.S > 1 ? 1 : 0));
+  out->launches =
+      chunks * (1 + (p.head_nb > 0 ? 1 : 0) + (p.pad ? 1 : 0) + (p.S > 1 ? 1 : 0));
+  out->head_blocks_n = p.head_nb;
   return LLK_OK;
 }
 

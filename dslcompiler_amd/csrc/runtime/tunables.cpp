@@ -21,6 +21,8 @@ struct Knob {
 // tile_splits:       force the tile kernel's k-split count (0 = cost model).
 // tile_wgs_per_wave: workgroups the tile kernel runs at once (1 per CU).
 // tile_min_kb:       fewest 64-k steps per tile-kernel split.
+// tile_tail_split:   1 = the tile kernel may run the columns of its last,
+//                    partial wave as a separate k-split launch; 0 = never.
 Knob g_knobs[] = {
     {"decode_max_m", {64}},
     {"decode_splits", {0}},
@@ -30,6 +32,7 @@ Knob g_knobs[] = {
     {"tile_splits", {0}},
     {"tile_wgs_per_wave", {256}},
     {"tile_min_kb", {4}},
+    {"tile_tail_split", {1}},
 };
 
 }  // namespace

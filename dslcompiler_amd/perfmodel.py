@@ -18,6 +18,8 @@ For one call the model takes the dispatcher's launch plan
               writes Y, after the main kernel
     time    = max(compute, memory, per_cu, shortest launch) + reduce
               + (launches - 1) x launch gap.
+A tile-kernel tail split (head_blocks_n > 0) is two such launches in a row:
+the leading columns unsplit, the remaining columns with the k split.
 The small-M kernel's MFMA work counts whole 32-row groups.
 """
 from __future__ import annotations
@@ -39,6 +41,32 @@ def machine(path: str = str(MACHINE)) -> dict:
         return yaml.safe_load(f)
 
 
+def _tile_launch(cal: dict, cus: int, nmat: int, M: int, N: int, K: int, S: int,
+                 workgroups: int) -> tuple[float, float, float, float]:
+    """(compute, memory, per_cu, reduce) seconds of one tile-kernel launch
+    over N columns with S k splits (and its reduce kernel when S > 1)."""
+    # Workgroup tile: 256 m x 256 MFMA rows (SwiGLU: 128 n of Wg + 128 n of Wu).
+    kpart = math.ceil(K / 64) * 64 / S
+    rounds = math.ceil(workgroups / cus)
+    compute = rounds * 2.0 * 256 * 256 * kpart / cal["tile_flops_per_cu"]
+    # Per-CU loads: one m tile means every weight byte comes from HBM
+    # once; with more m tiles the panels are re-read from L2 / MALL.
+    w_rate = (cal["tile_hbm_weight_bytes_per_cu_s"] if math.ceil(M / 256) == 1
+              else cal["tile_l2_bytes_per_cu_s"])
+    per_cu = rounds * (256 * kpart * 2.0 / w_rate
+                       + min(M, 256) * kpart * 2.0 / cal["tile_l2_bytes_per_cu_s"])
+    reduce = 0.0
+    if S > 1:  # split_reduce_kernel: reads the partial planes, writes Y
+        part = S * nmat * M * math.ceil(N / 128) * 128 * 4.0
+        reduce = (part + 2.0 * M * N) / cal["stream_bytes_per_s"]
+        if rounds == 1:  # every workgroup writes its partials at once, after its loads
+            per_cu += part / cal["stream_bytes_per_s"]
+        nbytes = 2.0 * nmat * K * N + 2.0 * M * K + part
+    else:
+        nbytes = 2.0 * nmat * K * N + 2.0 * M * K + 2.0 * M * N
+    return compute, nbytes / cal["stream_bytes_per_s"], per_cu, reduce
+
+
 def predict(op: str, M: int, N: int, K: int, machine_path: str = str(MACHINE)) -> dict:
     m = machine(machine_path)
     # YAML 1.1 reads 1.0e12 as a string: convert explicitly
@@ -47,25 +75,18 @@ def predict(op: str, M: int, N: int, K: int, machine_path: str = str(MACHINE)) -
     plan = describe_launch(op, M, N, K)
     nmat = 2 if op == "fused_swiglu" else 1
     S = plan["splits"]
-    per_cu = 0.0
-    reduce = 0.0
-    partials = 2.0 * plan["workspace_bytes"] if S > 1 else 0.0
+    gap = (plan["launches"] - 1) * cal["launch_gap_s"]
     if plan["kernel"] == "tile":
-        # Workgroup tile: 256 m x 256 MFMA rows (SwiGLU: 128 n of Wg + 128 n of Wu).
-        kpart = math.ceil(K / 64) * 64 / S
-        rounds = math.ceil(plan["workgroups"] / cus)
-        compute = rounds * 2.0 * 256 * 256 * kpart / cal["tile_flops_per_cu"]
-        # Per-CU loads: one m tile means every weight byte comes from HBM
-        # once; with more m tiles the panels are re-read from L2 / MALL.
-        w_rate = (cal["tile_hbm_weight_bytes_per_cu_s"] if math.ceil(M / 256) == 1
-                  else cal["tile_l2_bytes_per_cu_s"])
-        per_cu = rounds * (256 * kpart * 2.0 / w_rate
-                           + min(M, 256) * kpart * 2.0 / cal["tile_l2_bytes_per_cu_s"])
-        if S > 1:  # split_reduce_kernel: reads the partial planes, writes Y
-            reduce = (partials / 2 + 2.0 * M * N) / cal["stream_bytes_per_s"]
-            if rounds == 1:  # every workgroup writes its partials at once, after its loads
-                per_cu += partials / 2 / cal["stream_bytes_per_s"]
-    if plan["kernel"] != "tile":
+        head_nb = plan["head_blocks_n"]
+        segs = [(N, S, plan["workgroups"])]
+        if head_nb:
+            head_wgs = math.ceil(M / 256) * (head_nb if nmat == 2 else head_nb // 2)
+            segs = [(head_nb * 128, 1, head_wgs),
+                    (N - head_nb * 128, S, plan["workgroups"] - head_wgs)]
+        parts = [_tile_launch(cal, cus, nmat, M, n, K, s, wgs) for n, s, wgs in segs]
+        compute, memory, per_cu, reduce = (sum(p[i] for p in parts) for i in range(4))
+        t = sum(max(c, mem, pc, cal["launch_min_s"]) + r for c, mem, pc, r in parts) + gap
+    else:
         groups = plan["workgroups"]
         mrows = 32 * math.ceil(M / 32)
         flops = 2.0 * nmat * mrows * N * K
@@ -80,13 +101,11 @@ def predict(op: str, M: int, N: int, K: int, machine_path: str = str(MACHINE)) -
         x_wg = (width // gw) * M * kpart * 2.0
         per_cu = math.ceil(groups / cus) * max(w_wg / cal["small_m_weight_bytes_per_cu_s"],
                                                (w_wg + x_wg) / cal["small_m_bytes_per_cu_s"])
-    if reduce:  # the main kernel writes the partial planes, the reduce reads them and writes Y
-        nbytes = 2.0 * nmat * K * N + 2.0 * M * K + partials / 2
-    else:
+        partials = 2.0 * plan["workspace_bytes"] if S > 1 else 0.0
         nbytes = 2.0 * nmat * K * N + 2.0 * M * K + 2.0 * M * N + partials
-    memory = nbytes / cal["stream_bytes_per_s"]
-    t = (max(compute, memory, per_cu, cal["launch_min_s"]) + reduce
-         + (plan["launches"] - 1) * cal["launch_gap_s"])
+        memory = nbytes / cal["stream_bytes_per_s"]
+        reduce = 0.0
+        t = max(compute, memory, per_cu, cal["launch_min_s"]) + gap
     return {"compute_us": compute * 1e6, "memory_us": memory * 1e6, "per_cu_us": per_cu * 1e6,
             "reduce_us": reduce * 1e6, "predicted_us": t * 1e6,
             "bound": "mfma" if compute >= max(memory, per_cu) else "hbm", "plan": plan}

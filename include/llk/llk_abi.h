@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define LLK_ABI_VERSION 1
+#define LLK_ABI_VERSION 2
 
 /* Status codes.  The reference returns errors as llvm::Expected /
  * StringError (JitCache.cpp:200-224); this ABI uses negative integers. */
@@ -187,10 +187,13 @@ typedef struct llk_launch_plan {
   int splits;                    /* k splits across workgroups (1 = none) */
   int group_width;               /* small-M kernel: 32-column groups per workgroup */
   int pad_x;                     /* tile kernel: X copied to a padded buffer first */
-  int64_t workgroups;            /* of the main kernel, per launch */
+  int64_t workgroups;            /* of the main kernel, per row chunk (all its launches) */
   int64_t threads_per_workgroup; /* of the main kernel */
   int64_t launches;              /* kernel launches per call */
   size_t workspace_bytes;        /* = ctx->scratch size the call needs */
+  int64_t head_blocks_n;         /* tile kernel: leading 128-column blocks launched
+                                    without k split before the rest takes `splits`
+                                    (0 = one launch over all columns) */
 } llk_launch_plan;
 int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, int x_aligned,
                         llk_launch_plan* out);

@@ -254,6 +254,29 @@ def test_tile_short_k_pipeline(llk, gpu, orc, K):
         assert_parity(cf, cf_ref, f"gemm short k K={K} S={S}")
 
 
+@pytest.mark.parametrize("M,K,N", [(300, 1024, 600), (300, 1000, 600), (300, 640, 1100)])
+def test_tile_tail_split(llk, gpu, orc, M, K, N):
+    """Tail split: with 4 workgroups per wave the leading n-tile columns run
+    as one unsplit launch and the remaining (ragged) columns as a k-split
+    launch into the same Y -- aligned and padded X, SwiGLU and GEMM."""
+    print(f"case tile tail split M={M} K={K} N={N}", flush=True)
+    x, wg, wu = swiglu_inputs(M, K, N, seed=M + N)
+    s = 1.0 / np.sqrt(K)
+    b = normal_bf16(N, 1, (K, N), s)
+    cf_ref, _ = orc.gemm(x, b)
+    pb = llk.PackedWeights.from_host(b)
+    with _Tunable(llk, "tile_wgs_per_wave", 4):
+        for op in ("fused_swiglu", "matmul"):
+            plan = llk.describe_launch(op, M, N, K, x_aligned=K % 64 == 0)
+            assert plan["head_blocks_n"] > 0 and plan["splits"] > 1, plan
+        _check_swiglu(llk, gpu, orc, x, wg, wu, f"tail split M={M} K={K} N={N}")
+        xd = to_dev(gpu, x)
+        cf = from_dev(llk.matmul(xd, pb, out_dtype=gpu.float32))
+        cb = from_dev(llk.matmul(xd, pb, out_dtype=gpu.bfloat16))
+    assert_parity(cf, cf_ref, f"gemm tail split M={M} K={K} N={N}")
+    assert np.array_equal(cb, to_bf16_bits(cf)), "bf16 != RNE(fp32)"
+
+
 def test_tile_splits_exact_and_reuse(llk, gpu, orc):
     """Integer inputs make every partial sum exact, so any k split must give
     the oracle's gate/up bit for bit: GEMM fp32 output equal, SwiGLU within

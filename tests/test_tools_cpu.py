@@ -176,6 +176,32 @@ def test_describe_launch_configs():
     assert llk.lib().llk_describe_launch(0, 0, 8, 8, 1, C.byref(plan)) == -2
 
 
+def test_tile_tail_split_plans():
+    """Config 5 at M = 4097: 17 m-tiles leave a nearly empty last wave, so the
+    whole n-tile columns of the first waves run unsplit and only the rest
+    take a k split (GEMM: 15 columns x 17 = 255 tiles, then 5 x 17 x 3;
+    SwiGLU: 105 x 17 = 1785 tiles, then 3 x 17 x 5).  Shapes whose tiles fill
+    their waves, or fill too little of one, keep one launch; the knob turns it
+    off; a forced split count wins."""
+    p = llk.describe_launch("matmul", 4097, 5120, 13824)
+    assert (p["head_blocks_n"], p["splits"], p["workgroups"], p["launches"]) == (30, 3, 510, 3)
+    assert p["workspace_bytes"] == 3 * 4097 * 10 * 128 * 4
+    p = llk.describe_launch("fused_swiglu", 4097, 13824, 5120)
+    assert (p["head_blocks_n"], p["splits"], p["workgroups"], p["launches"]) == (105, 5, 2040, 3)
+    for op, M, N, K in [("fused_swiglu", 2048, 11008, 4096), ("matmul", 4096, 4096, 4096),
+                        ("fused_swiglu", 1000, 13824, 5120), ("matmul", 1000, 5120, 13824),
+                        ("matmul", 255, 5120, 13824)]:
+        assert llk.describe_launch(op, M, N, K)["head_blocks_n"] == 0, (op, M)
+    for name, value in [("tile_tail_split", 0), ("tile_splits", 2)]:
+        old = llk.get_tunable(name)
+        llk.set_tunable(name, value)
+        try:
+            p = llk.describe_launch("matmul", 4097, 5120, 13824)
+            assert p["head_blocks_n"] == 0 and p["workgroups"] == 340 * p["splits"]
+        finally:
+            llk.set_tunable(name, old)
+
+
 def test_small_m_cost_model_choices():
     """The small-M dispatcher's (width, splits) against llk-tune's measured
     best on MI355X for the BASELINE decode shapes: config 1 (M=64, N=1376,
