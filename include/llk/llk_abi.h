@@ -285,7 +285,9 @@ int llk_fill_normal_bf16(uint64_t seed, uint64_t stream, float sigma,
  * "decode_group_width" (force the 32-column groups per small-M workgroup:
  * 1, 2, 4; 0 = cost model),
  * "tile_splits" (force the tile kernel's k-split count, 0 = cost model),
- * "tile_wgs_per_wave", "tile_min_kb".  Returns LLK_OK or
+ * "tile_wgs_per_wave", "tile_min_kb", "tile_tail_split" (1: the columns
+ * of a partial last wave of tiles may run as a separate k-split launch;
+ * 0: never; a forced "tile_splits" also turns it off).  Returns LLK_OK or
  * LLK_ERR_INVALID_ARGUMENT for an unknown name. */
 int llk_set_tunable(const char* name, int64_t value);
 int llk_get_tunable(const char* name, int64_t* value);
