@@ -98,6 +98,12 @@ struct TileArgs {
   int KB;              // K_pad / 64
   int NB;              // N_pad / 128 (packed n-blocks)
   int tiles_m, tiles_n;
+  // Tile order: groups of group_m m-tiles, m fastest inside a group, then n,
+  // then the next group (0: m fastest over all m-tiles).  The 32 workgroups
+  // an XCD runs at once then share fewer X and weight panels when there are
+  // more than 8 m-tiles (GEMM 4096^3: 4 weight + 8 X panels per XCD instead
+  // of 2 + 16).
+  int group_m;
   // k split across workgroups (S > 1): workgroup (tile, s) covers the 64-k
   // blocks [s * kbs, min(KB, (s + 1) * kbs)) and writes its raw fp32
   // accumulators to part[s][mat][M][n_pad]; split_reduce_kernel adds them
@@ -208,8 +214,17 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   const int idx = xcd_remap(blockIdx.x, tiles * (SPLIT ? a.S : 1));
   const int split = SPLIT ? idx / tiles : 0;
   const int tile = SPLIT ? idx - split * tiles : idx;
-  const int tm = tile % a.tiles_m;
-  const int tn = tile / a.tiles_m;
+  int tm, tn;
+  if (a.group_m > 0 && a.tiles_m > a.group_m) {
+    const int span = a.group_m * a.tiles_n;  // tiles of one full group
+    const int g = tile / span, r = tile - g * span;
+    const int gm = min(a.group_m, a.tiles_m - g * a.group_m);  // last group may be short
+    tm = g * a.group_m + r % gm;
+    tn = r / gm;
+  } else {
+    tm = tile % a.tiles_m;
+    tn = tile / a.tiles_m;
+  }
   const int m0 = tm * kTileM;
   const int kb0 = SPLIT ? split * a.kbs : 0;
   const int nkb = SPLIT ? min(a.KB - kb0, a.kbs) : a.KB;
@@ -615,6 +630,7 @@ hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void*
   a.NB = NB;
   a.tiles_m = (M + kTileM - 1) / kTileM;
   a.tiles_n = mode == 1 ? NB : (NB + 1) / 2;
+  a.group_m = 8;
   a.S = S > 1 ? S : 1;
   a.kbs = (KB + a.S - 1) / a.S;
   a.n_pad = NB * 128;
