@@ -37,23 +37,34 @@ PREFILL = dict(M=2048, K=4096, N=11008)
 DECODE = dict(K=4096, N=14336)
 DECODE_M = (1, 8, 16, 64)
 MLP = dict(K=5120, N=13824)
-# Secondary workloads ("extra") warm for at least this long before timing;
-# the headline honours --warmup exactly.
+# Every timed workload first runs its --warmup launches, then keeps launching
+# until this much time has passed since the first one: the GPU needs ~35 ms of
+# load to reach its steady clock (the first 50 prefill launches average
+# 386 us, the steady state ~266 us), so a short --warmup alone would time
+# the clock ramp.  The headline's warm-up time and launch count are reported.
+PREFILL_WARM_S = 0.25
 EXTRA_WARM_S = 0.1
 
 
-def _time_loop(torch, fn, steps: int, warmup: int, min_warm_s: float = 0.0) -> float:
+def _time_loop(torch, fn, steps: int, warmup: int, min_warm_s: float = 0.0,
+               warm_info: dict | None = None) -> float:
     """Average ms per call, HIP events on the launch (current) stream.  After
     `warmup` untimed calls, keeps warming until `min_warm_s` seconds have
-    passed (the GPU needs ~35 ms of load to reach its steady clock)."""
+    passed (the GPU needs ~35 ms of load to reach its steady clock).
+    `warm_info`, if given, receives the untimed launch count and seconds."""
     t0 = time.perf_counter()
+    n = 0
     for i in range(warmup):
         fn(i)
+        n += 1
     torch.cuda.synchronize()
     while time.perf_counter() - t0 < min_warm_s:
         for i in range(20):
-            fn(i)
+            fn(n)
+            n += 1
         torch.cuda.synchronize()
+    if warm_info is not None:
+        warm_info.update(launches=n, seconds=round(time.perf_counter() - t0, 3))
     s = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(s)
@@ -82,9 +93,11 @@ def bench_prefill(torch, llk, steps, warmup, fill="normal"):
     pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
     xd = to_dev(torch, x)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-    ms = _time_loop(torch, lambda i: llk.fused_swiglu(xd, pg, pu, out=y), steps, warmup)
+    warm = {}
+    ms = _time_loop(torch, lambda i: llk.fused_swiglu(xd, pg, pu, out=y), steps, warmup,
+                    PREFILL_WARM_S, warm)
     flops = 4.0 * M * K * N
-    return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, inputs=(x, wg, wu), y=y)
+    return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, inputs=(x, wg, wu), y=y, warm=warm)
 
 
 def _rand_w(torch, g, K, N):
@@ -193,29 +206,52 @@ def model_vs_measured(pre: dict, extra: dict) -> dict:
                 "ratio": round(p / m, 3)} for k, (p, m) in rows.items()}
 
 
-def cpu_baseline(x, wg, wu, budget_s: float = 12.0):
+def cpu_baseline(x, wg, wu, budget_s: float = 12.0, budget1_s: float = 4.0):
     """The oracle's AVX2 restatement of the reference fused kernel on a bounded
     sample of the headline workload: the first `rows` rows of X (full K and
-    N), best of up to 5 runs within about `budget_s` seconds."""
+    N), best of up to 5 runs within about `budget_s` seconds on every host
+    thread, and the same on one thread (llk-bench's --threads 1) within about
+    `budget1_s` seconds, with the host CPU's model string."""
     import oracle
     threads = _cpu_threads()
     K, N = wg.shape
-    t0 = time.perf_counter()
-    oracle.swiglu_avx2(x[:32], wg, wu, threads)  # warm-up + estimate
-    est = time.perf_counter() - t0
-    rows = int(min(x.shape[0], max(32, 32 * round(budget_s / 3 / max(est, 1e-3)))))
-    rows -= rows % 32
-    best, reps = 0.0, 0
-    t_end = time.perf_counter() + budget_s
-    while reps < 1 or (time.perf_counter() < t_end and reps < 5):
-        t = time.perf_counter()
-        oracle.swiglu_avx2(x[:rows], wg, wu, threads)
-        best = max(best, 4.0 * rows * K * N / (time.perf_counter() - t) / 1e12)
-        reps += 1
+
+    def best_rate(nthreads, budget):
+        t0 = time.perf_counter()
+        oracle.swiglu_avx2(x[:32], wg, wu, nthreads)  # warm-up + estimate
+        est = time.perf_counter() - t0
+        rows = int(min(x.shape[0], max(32, 32 * round(budget / 3 / max(est, 1e-3)))))
+        rows -= rows % 32
+        best, reps = 0.0, 0
+        t_end = time.perf_counter() + budget
+        while reps < 1 or (time.perf_counter() < t_end and reps < 5):
+            t = time.perf_counter()
+            oracle.swiglu_avx2(x[:rows], wg, wu, nthreads)
+            best = max(best, 4.0 * rows * K * N / (time.perf_counter() - t) / 1e12)
+            reps += 1
+        return best, rows, reps
+
+    best, rows, reps = best_rate(threads, budget_s)
+    best1, rows1, reps1 = best_rate(1, budget1_s)
     return {"value": round(best, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"fused SwiGLU rows 0..{rows - 1} of M=2048 (K=4096, N=11008), best of "
                       f"{reps} runs; AVX2 BM32/BN64/BK64/VM4/VN8 tiles, ThreadPool-style "
-                      f"dynamic tile queue"}
+                      f"dynamic tile queue",
+            "threads1": {"value": round(best1, 5), "unit": "TFLOP/s", "cores": 1,
+                         "sample": f"rows 0..{rows1 - 1}, best of {reps1} runs"},
+            "cpu_model": _cpu_model(), "host_threads": os.cpu_count()}
+
+
+def _cpu_model() -> str:
+    """The host CPU's model string (/proc/cpuinfo)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
 
 
 def _cpu_threads() -> int:
@@ -364,6 +400,8 @@ def main() -> None:
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
+        "warm_untimed": {**pre["warm"], "rule": f"--warmup launches, then more until "
+                                                f"{PREFILL_WARM_S} s have passed"},
         "ms_per_step": round(pre["ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",

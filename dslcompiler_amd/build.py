@@ -57,11 +57,6 @@ TOOLS = {
     "llk-compile": CSRC / "tools" / "llk_compile.cpp",
     "llk-tune": CSRC / "tools" / "llk_tune.cpp",
 }
-# Self-contained HIP tools (their own build of the kernels they measure).
-HIP_TOOLS = {
-    "llk-tile-phases": CSRC / "tools" / "tile_phases.hip",
-    "llk-mfma-rate": CSRC / "tools" / "mfma_rate.hip",
-}
 
 
 def _run(cmd: list[str]) -> None:
@@ -110,8 +105,6 @@ def build(lib_only: bool = False, jobs: int | None = None) -> Path:
                   f"-L{PKG}", "-lllk_gfx950", f"-Wl,-rpath,{PKG}", f"-Wl,-rpath,$ORIGIN/..",
                   f"-I{ROCM}/include", "-D__HIP_PLATFORM_AMD__", f"-L{ROCM}/lib", "-lamdhip64",
                   "-pthread"])
-        for name, src in HIP_TOOLS.items():
-            _run([HIPCC, *HIP_FLAGS, *INCLUDES, str(src), "-o", str(BIN / name)])
     return LIB
 
 

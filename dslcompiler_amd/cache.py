@@ -11,7 +11,7 @@ import numpy as np
 from . import _lib
 from ._lib import (KERNEL_FN, CacheStatsC, KernelContext, KernelKeyC, WeightKeyC, check, lib,
                    tensor2d)
-from .ops import PackedWeights, _ctx, _out_dtype_code, _t2d
+from .ops import PackedWeights, _check_operand, _ctx, _out_dtype_code, _t2d, _torch
 
 # Enum values (KernelKey.h:22-38, plus this backend's additions).
 OP_FUSED_SWIGLU, OP_ROPE, OP_ATTENTION, OP_MATMUL = 0, 1, 2, 3
@@ -67,6 +67,9 @@ class KernelFn:
 
     def __call__(self, x, w0: PackedWeights, w1: PackedWeights | None, y, stream=None,
                  scratch=None) -> None:
+        torch = _torch()
+        _check_operand(x, "x", (torch.bfloat16,))
+        _check_operand(y, "y", (torch.bfloat16, torch.float16, torch.float32))
         ctx = _ctx(stream, scratch)
         check(self._fn(C.byref(_t2d(x)), w0.handle, w1.handle if w1 is not None else None,
                        C.byref(_t2d(y)), _out_dtype_code(y.dtype), C.byref(ctx)))
@@ -166,6 +169,7 @@ class JitCache:
             check(lib().llk_cache_get_packed_weights(self._c, C.byref(t), bk, 0, flags,
                                                       C.byref(out)))
         else:
+            _check_operand(w, "w", (_torch().bfloat16,))
             check(lib().llk_cache_get_packed_weights(self._c, C.byref(_t2d(w)), bk, 1, 0,
                                                       C.byref(out)))
         return PackedWeights(out.value, owned=False)

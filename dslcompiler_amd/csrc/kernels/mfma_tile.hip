@@ -62,30 +62,6 @@
 
 #include "common.h"
 
-// Phase timestamps (the llk-tile-phases tool builds this file with
-// LLK_TILE_PHASES defined): each workgroup records the 100 MHz real-time
-// counter at entry, when its first stage has landed, after the K loop and
-// after the epilogue.  Empty in the library build.
-#ifdef LLK_TILE_PHASES
-#define LLK_PHASE(var) const unsigned long long var = __builtin_amdgcn_s_memrealtime()
-#define LLK_PHASE_STORE()                                                        \
-  do {                                                                           \
-    const unsigned long long t_end = __builtin_amdgcn_s_memrealtime();           \
-    if (threadIdx.x == 0) {                                                      \
-      unsigned long long* r = a.phases + (size_t)blockIdx.x * 4;                 \
-      r[0] = t_entry;                                                            \
-      r[1] = t_first;                                                            \
-      r[2] = t_loop;                                                             \
-      r[3] = t_end;                                                              \
-    }                                                                            \
-  } while (0)
-#else
-#define LLK_PHASE(var)
-#define LLK_PHASE_STORE() \
-  do {                    \
-  } while (0)
-#endif
-
 namespace llk_gfx950 {
 
 struct TileArgs {
@@ -110,9 +86,6 @@ struct TileArgs {
   // in split order and applies the epilogue.
   float* part;
   int S, kbs, n_pad;
-#ifdef LLK_TILE_PHASES
-  unsigned long long* phases;  // [workgroups][4] timestamps (phase tool)
-#endif
 };
 
 constexpr int kThreads = 256;
@@ -209,7 +182,6 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   // Workgroup -> (split s, tile): tiles of one split are contiguous, so
   // after the XCD remap the tiles that share X's k slice (and, m fastest,
   // the tiles that share W columns) run on one XCD.
-  LLK_PHASE(t_entry);
   const int tiles = a.tiles_m * a.tiles_n;
   const int idx = xcd_remap(blockIdx.x, tiles * (SPLIT ? a.S : 1));
   const int split = SPLIT ? idx / tiles : 0;
@@ -346,7 +318,6 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   mfma_drain();    // ... well before the first MFMA reads them
   wait_vmcnt<2 * kXLoads + 3 * kWLoads>();  // X0 and W0 landed
   __syncthreads();
-  LLK_PHASE(t_first);
 
   bf16x8 A[8], B[8];
 #pragma unroll
@@ -399,7 +370,6 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   wait_vmcnt<0>();  // the trailing refills have landed (the epilogue reuses the ring)
   mfma_drain();
   acc_fence(acc);   // the epilogue reads the accumulators only after the drain
-  LLK_PHASE(t_loop);
 
   // ---- epilogue: acc[i][j] holds, in lane l, output row m = m0 + wm*128 +
   // 16 j + l%16 and the four consecutive n = (wave's first n) + 16 i' +
@@ -470,7 +440,6 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
                                            (size_t)(m0 + wm * 128) * a.n_pad + col0),
                 (int64_t)a.n_pad * 4, rows_ok, a.n_pad - col0);
     }
-    LLK_PHASE_STORE();
     return;
   }
   constexpr int NI = (MODE == 1) ? 4 : 8;         // 16-column groups of the wave's output
@@ -512,7 +481,6 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
     strip_out(std::integral_constant<int, kElem>{}, fast, al16, ybase + sidx * 128,
               a.ldy * kElem, rows_ok, a.N - (n_w + sidx * 128 / kElem));
   }
-  LLK_PHASE_STORE();
 }
 
 // Sums the S partial planes of each output element in split order (fixed,
@@ -590,11 +558,6 @@ static hipError_t launch_mode(const TileArgs& a, int out, bool yvec, hipStream_t
 
 }  // namespace llk_gfx950
 
-#ifdef LLK_TILE_PHASES
-// Device buffer of [workgroups][4] timestamps the next launches write.
-unsigned long long* llk_tile_phases_buffer = nullptr;
-#endif
-
 // Largest X span (bytes, rows padded to whole tiles) the 32-bit buffer
 // offsets of the tile kernel can address.
 bool llk_tile_x_fits(int M, int64_t ldx) {
@@ -635,9 +598,6 @@ hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void*
   a.kbs = (KB + a.S - 1) / a.S;
   a.n_pad = NB * 128;
   a.part = static_cast<float*>(part);
-#ifdef LLK_TILE_PHASES
-  a.phases = llk_tile_phases_buffer;
-#endif
   if (a.S > 1 && (part == nullptr || (int64_t)(a.S - 1) * a.kbs >= KB)) return hipErrorInvalidValue;
   if (mode == 1) return launch_mode<1>(a, out, yvec, s);
   return launch_mode<0>(a, out, yvec, s);

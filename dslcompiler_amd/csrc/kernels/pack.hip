@@ -77,18 +77,27 @@ hipError_t llk_launch_pad_rows(const uint16_t* x, int64_t ldx, int M, int K, uin
   return hipGetLastError();
 }
 
-// Fills `n` 32-bit words with zero (used instead of hipMemsetAsync so the
-// call is safe inside captured HIP graphs).
-__global__ void llk_zero_words_kernel(unsigned* p, int64_t n) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0u;
+// Writes zero to every element of a strided [M, N] matrix of 2- or 4-byte
+// elements (an empty reduction, K == 0: SiLU(0) * 0 = +0 and C = 0), as a
+// kernel rather than hipMemset2DAsync so that the call is safe inside
+// captured HIP graphs.  One thread per element.
+__global__ __launch_bounds__(256) void zero_rows_kernel(uint8_t* __restrict__ y, int64_t ld_bytes,
+                                                        int64_t N, int elem_bytes, int64_t total) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= total) return;
+  const int64_t m = idx / N, n = idx - m * N;
+  uint8_t* p = y + m * ld_bytes + n * elem_bytes;
+  if (elem_bytes == 4)
+    *reinterpret_cast<uint32_t*>(p) = 0u;
+  else
+    *reinterpret_cast<uint16_t*>(p) = 0;
 }
 
-hipError_t llk_launch_zero(void* p, size_t bytes, hipStream_t s) {
-  int64_t n = (int64_t)(bytes / 4);
-  if (n == 0) return hipSuccess;
-  int64_t blocks = (n + 255) / 256;
-  hipLaunchKernelGGL(llk_zero_words_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
-                     static_cast<unsigned*>(p), n);
+hipError_t llk_launch_zero_rows(void* y, int64_t ld_elems, int64_t M, int64_t N, int elem_bytes,
+                                hipStream_t s) {
+  const int64_t total = M * N;
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                     static_cast<uint8_t*>(y), ld_elems * elem_bytes, N, elem_bytes, total);
   return hipGetLastError();
 }

@@ -37,6 +37,8 @@ hipError_t llk_launch_pad_rows(const uint16_t* x, int64_t ldx, int M, int K, uin
                                int64_t ldo, hipStream_t s);
 hipError_t llk_launch_pack(const uint16_t* w, int64_t ld, int K, int N, int KB, int NB, void* out,
                            hipStream_t s);
+hipError_t llk_launch_zero_rows(void* y, int64_t ld_elems, int64_t M, int64_t N, int elem_bytes,
+                                hipStream_t s);
 
 struct llk_packed_weights {
   // Reference metadata (PackedWeights.h:13-19).
@@ -402,6 +404,16 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
   p.ws_bytes = p.pad_bytes +
                llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)rows, (int)(NB - p.head_nb), p.S);
   return p;
+}
+
+// K == 0: the reference's verifiers accept an empty reduction
+// (LLKOps.cpp:42-83, 336-348) and its zero-filled fp32 accumulators
+// (FuseDoubleContraction.cpp:119-135) give SiLU(0) * 0 = +0 for SwiGLU and
+// C = 0 for the matmul: the output is filled with zeros.
+int empty_reduction(llk_tensor2d* y, int out_dtype, llk_kernel_context* ctx, const char* what) {
+  hipError_t e = llk_launch_zero_rows(y->data, y->stride0, y->dim0, y->dim1,
+                                      (int)dtype_size(out_dtype), stream_of(ctx));
+  return e == hipSuccess ? LLK_OK : fail_hip(e, what);
 }
 
 int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w0,
@@ -939,10 +951,10 @@ int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
   if ((rc = llk_verify_fused_swiglu(M, K, wg->K, wg->N, wu->K, wu->N, y->dim0, y->dim1))) return rc;
   if (M > kMaxDim) return fail(LLK_ERR_SHAPE, "M too large");
   if (M == 0 || wg->N == 0) return LLK_OK;
-  if (K == 0) return fail(LLK_ERR_SHAPE, "K must be >= 1 (empty reduction)");
   int dev;
   if ((rc = current_device(&dev))) return rc;
   if ((rc = check_packed(wg, "wg", dev)) || (rc = check_packed(wu, "wu", dev))) return rc;
+  if (K == 0) return empty_reduction(y, y_dtype, ctx, "swiglu");
   return run_contraction(1, x, wg, wu, y, y_dtype, ctx, dev, "swiglu");
 }
 
@@ -961,10 +973,10 @@ int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor
                 (long long)c->dim1, (long long)M, (long long)N);
   if (M > kMaxDim) return fail(LLK_ERR_SHAPE, "M too large");
   if (M == 0 || N == 0) return LLK_OK;
-  if (K == 0) return fail(LLK_ERR_SHAPE, "K must be >= 1 (empty reduction)");
   int dev;
   if ((rc = current_device(&dev))) return rc;
   if ((rc = check_packed(b, "b", dev))) return rc;
+  if (K == 0) return empty_reduction(c, c_dtype, ctx, "gemm");
   return run_contraction(0, a, b, nullptr, c, c_dtype, ctx, dev, "gemm");
 }
 

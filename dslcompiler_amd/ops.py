@@ -35,11 +35,26 @@ def _stream_handle(stream=None) -> int:
 
 
 def _ctx(stream=None, scratch=None) -> KernelContext:
+    if scratch is not None:
+        _check_scratch(scratch)
     ctx = KernelContext(None, 0, _stream_handle(stream))
     if scratch is not None:
         ctx.scratch = scratch.data_ptr()
         ctx.scratch_size = scratch.numel() * scratch.element_size()
     return ctx
+
+
+def _check_scratch(t) -> None:
+    """A caller workspace must be contiguous device memory of the current
+    device: the kernels write partial sums into it through a raw pointer."""
+    torch = _torch()
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError("scratch must be a CUDA tensor")
+    cur = torch.cuda.current_device()
+    if t.device.index != cur:
+        raise ValueError(f"scratch is on cuda:{t.device.index}, the current device is cuda:{cur}")
+    if not t.is_contiguous():
+        raise ValueError("scratch must be contiguous")
 
 
 def _check_operand(t, name: str, dtypes) -> None:

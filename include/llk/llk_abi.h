@@ -158,7 +158,10 @@ int llk_pack_device_layout(const llk_tensor2d* w_host, void* out);
  * x: bf16 [M, K] device; wg, wu: packed [K, N] handles; y: [M, N] device of
  * y_dtype LLK_BF16 (truncf RNE of the fp32 result, the reference op's result
  * type) or LLK_FP32 (the pre-truncf value).  fp32 accumulation, exact exp.
- * M == 0 is valid and launches nothing (edge_cases.cpp:84-97). */
+ * M == 0 is valid and launches nothing (edge_cases.cpp:84-97).  K == 0 is
+ * valid (the verifier accepts an empty reduction, LLKOps.cpp:42-83) and
+ * fills Y with +0: SiLU(0) * 0 of the zero-filled fp32 accumulators
+ * (FuseDoubleContraction.cpp:119-135). */
 int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
                     const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
                     llk_kernel_context* ctx);
@@ -203,7 +206,8 @@ int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, int x_al
  * a: bf16 [M, K] device; b: packed [K, N] handle; c: [M, N] device of
  * c_dtype LLK_FP32, LLK_BF16 or LLK_FP16 (the result types llk.matmul
  * allows; both 16-bit types round the fp32 sum to nearest even, fp16
- * overflows to infinity). */
+ * overflows to infinity).  K == 0 (MatmulOp::verify accepts it,
+ * LLKOps.cpp:336-348) fills C with +0. */
 int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b,
                   llk_tensor2d* c, int c_dtype, llk_kernel_context* ctx);
 

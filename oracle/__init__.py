@@ -59,6 +59,10 @@ def orc() -> C.CDLL:
         l.orc_swiglu_fp64.argtypes = [_f64p, _f64p, _f64p, _f64p, _i64, _i64, _i64]
         l.orc_gemm.argtypes = [C.c_void_p, _i64, C.c_void_p, _i64, _i64, _i64, _i64, C.c_void_p,
                                C.c_void_p, _i64]
+        l.orc_gemm_init.argtypes = [C.c_void_p, _i64, C.c_void_p, _i64, _i64, _i64, _i64,
+                                    C.c_void_p, _i64, C.c_void_p, C.c_void_p, _i64]
+        l.orc_gemm_avx2_mt.argtypes = [C.c_void_p, _i64, C.c_void_p, _i64, _i64, _i64, _i64,
+                                       C.c_void_p, _i64, C.c_void_p, C.c_void_p, _i64, C.c_int]
         l.orc_gemm_fp64.argtypes = [_u16p, _u16p, _f64p, _i64, _i64, _i64]
         l.orc_mlp.argtypes = [_u16p, _u16p, _u16p, _u16p, _i64, _i64, _i64, _u16p, _u16p]
         l.orc_classify_m.restype = C.c_int
@@ -180,6 +184,35 @@ def gemm(a: np.ndarray, b: np.ndarray, want_f32: bool = True, want_bf16: bool = 
     cf = np.empty((M, N), np.float32) if want_f32 else None
     cb = np.empty((M, N), np.uint16) if want_bf16 else None
     orc().orc_gemm(_p(a), K, _p(b), N, M, N, K, _p(cf), _p(cb), N)
+    return cf, cb
+
+
+def gemm_init(a: np.ndarray, b: np.ndarray, c_init: np.ndarray | None, want_f32: bool = True,
+              want_bf16: bool = True):
+    """C = C0 + A B with the fp32 accumulator starting at c_init (fp32
+    [M, N], or None for 0) and the products added in k order."""
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    M, K = a.shape
+    N = b.shape[1]
+    ci = None if c_init is None else np.ascontiguousarray(c_init, dtype=np.float32)
+    cf = np.empty((M, N), np.float32) if want_f32 else None
+    cb = np.empty((M, N), np.uint16) if want_bf16 else None
+    orc().orc_gemm_init(_p(a), K, _p(b), N, M, N, K, _p(ci), N, _p(cf), _p(cb), N)
+    return cf, cb
+
+
+def gemm_avx2(a: np.ndarray, b: np.ndarray, threads: int, c_init: np.ndarray | None = None,
+              want_f32: bool = True, want_bf16: bool = True):
+    """gemm_init on `threads` host threads (bit-equal to it): for full-size checks."""
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    M, K = a.shape
+    N = b.shape[1]
+    ci = None if c_init is None else np.ascontiguousarray(c_init, dtype=np.float32)
+    cf = np.empty((M, N), np.float32) if want_f32 else None
+    cb = np.empty((M, N), np.uint16) if want_bf16 else None
+    orc().orc_gemm_avx2_mt(_p(a), K, _p(b), N, M, N, K, _p(ci), N, _p(cf), _p(cb), N, threads)
     return cf, cb
 
 

@@ -16,8 +16,10 @@
 //       source (oracle/_ref), fp64 closed form.
 //   orc_swiglu_fp64                 pinned: reference fp64 routine (oracle/_ref)
 //       and known-answer values.
-//   orc_gemm                        pinned: exact small-integer cases, brute
-//       force fp64, identity / permutation matrices.
+//   orc_gemm / orc_gemm_init        pinned: exact small-integer cases, brute
+//       force fp64, identity / permutation matrices; with an initial
+//       accumulator, the integer closed form C0 + A B.
+//   orc_gemm_avx2_mt                pinned against orc_gemm_init (bit-equal).
 //   orc_mlp                         pinned through its two parts above.
 //   orc_classify_m, tiling helpers  pinned: reference test tables.
 //   orc_kernel_key_hash             pinned: reference header compiled from
@@ -184,12 +186,31 @@ void orc_swiglu_fp64(const double* x, const double* wg, const double* wu,
 // truncf RNE).  Sequential-k order.
 // a: [M,K] stride lda; b: [K,N] stride ldb.
 // ---------------------------------------------------------------------------
+void orc_gemm_init(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                   int64_t M, int64_t N, int64_t K, const float* c_init,
+                   int64_t ldi, float* c_f32, uint16_t* c_bf16, int64_t ldc);
+
 void orc_gemm(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
               int64_t M, int64_t N, int64_t K, float* c_f32, uint16_t* c_bf16,
               int64_t ldc) {
+  orc_gemm_init(a, lda, b, ldb, M, N, K, nullptr, 0, c_f32, c_bf16, ldc);
+}
+
+// micro.mma with a non-zero accumulator: acc[M,N] += lhs * rhs
+// (MicroOps.td:196-222; linalg.matmul accumulates into its `outs` operand,
+// the init of llk.matmul's outs(init), LLKOps.td:210-255).  The fp32
+// accumulator starts at c_init (row stride ldi; NULL = 0, as the fused
+// path's zero-filled accumulators, FuseDoubleContraction.cpp:119-135) and
+// takes the products in k order; the result is cast once to the output type.
+void orc_gemm_init(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                   int64_t M, int64_t N, int64_t K, const float* c_init,
+                   int64_t ldi, float* c_f32, uint16_t* c_bf16, int64_t ldc) {
   std::vector<float> acc(static_cast<size_t>(N));
   for (int64_t m = 0; m < M; ++m) {
-    std::fill(acc.begin(), acc.end(), 0.0f);
+    if (c_init)
+      std::copy(c_init + m * ldi, c_init + m * ldi + N, acc.begin());
+    else
+      std::fill(acc.begin(), acc.end(), 0.0f);
     for (int64_t k = 0; k < K; ++k) {
       const float av = orc_bf16_to_f32(a[m * lda + k]);
       const uint16_t* br = b + k * ldb;
@@ -468,6 +489,64 @@ void orc_swiglu_avx2_mt(const uint16_t* x, int64_t ldx, const uint16_t* wg,
   pool.parallel_for(mt * nt, grain, [&](int64_t t) {
     avx2_tile(x, ldx, wg, wu, ldw, M, N, K, y, yf, ldy, (t / nt) * kBM,
               (t % nt) * kBN);
+  });
+}
+
+// The same GEMM as orc_gemm_init, multithreaded and vectorised for
+// full-size parity checks: 32 x 64 output tiles on the pool above, each
+// element's fp32 accumulator taking the products in k order from its
+// initial value.  A bf16 x bf16 product is exact in fp32, so the AVX2 fma
+// rounds exactly as the scalar multiply-then-add: bit-equal to orc_gemm_init.
+namespace {
+
+__attribute__((target("avx2,fma"))) void avx2_gemm_tile(
+    const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t M, int64_t N,
+    int64_t K, const float* c_init, int64_t ldi, float* cf, uint16_t* cb, int64_t ldc,
+    int64_t m0, int64_t n0) {
+  alignas(32) float acc[kBM][kBN];
+  const int64_t bm = std::min(kBM, M - m0), bn = std::min(kBN, N - n0);
+  for (int64_t mi = 0; mi < bm; ++mi)
+    for (int64_t ni = 0; ni < bn; ++ni)
+      acc[mi][ni] = c_init ? c_init[(m0 + mi) * ldi + n0 + ni] : 0.0f;
+  for (int64_t mi = 0; mi < bm; mi += kVM) {
+    const int64_t vm = std::min(kVM, bm - mi);
+    int64_t ni = 0;
+    for (; ni + kVN <= bn; ni += kVN) {
+      __m256 c[kVM];
+      for (int r = 0; r < kVM; ++r) c[r] = _mm256_load_ps(&acc[mi + r][ni]);
+      for (int64_t k = 0; k < K; ++k) {
+        const __m256 bv = load8_bf16(b + k * ldb + n0 + ni);
+        for (int r = 0; r < kVM; ++r) {
+          if (r >= vm) break;
+          const __m256 av = _mm256_set1_ps(orc_bf16_to_f32(a[(m0 + mi + r) * lda + k]));
+          c[r] = _mm256_fmadd_ps(av, bv, c[r]);
+        }
+      }
+      for (int r = 0; r < kVM; ++r) _mm256_store_ps(&acc[mi + r][ni], c[r]);
+    }
+    for (; ni < bn; ++ni)  // N tail: scalar, same order
+      for (int64_t r = 0; r < vm; ++r)
+        for (int64_t k = 0; k < K; ++k)
+          acc[mi + r][ni] += orc_bf16_to_f32(a[(m0 + mi + r) * lda + k]) *
+                             orc_bf16_to_f32(b[k * ldb + n0 + ni]);
+  }
+  for (int64_t mi = 0; mi < bm; ++mi)
+    for (int64_t ni = 0; ni < bn; ++ni) {
+      if (cf) cf[(m0 + mi) * ldc + n0 + ni] = acc[mi][ni];
+      if (cb) cb[(m0 + mi) * ldc + n0 + ni] = orc_f32_to_bf16_rne(acc[mi][ni]);
+    }
+}
+
+}  // namespace
+
+void orc_gemm_avx2_mt(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                      int64_t M, int64_t N, int64_t K, const float* c_init, int64_t ldi,
+                      float* cf, uint16_t* cb, int64_t ldc, int threads) {
+  const int64_t mt = (M + kBM - 1) / kBM, nt = (N + kBN - 1) / kBN;
+  TilePool pool(std::max(1, threads));
+  pool.parallel_for(mt * nt, 1, [&](int64_t t) {
+    avx2_gemm_tile(a, lda, b, ldb, M, N, K, c_init, ldi, cf, cb, ldc, (t / nt) * kBM,
+                   (t % nt) * kBN);
   });
 }
 

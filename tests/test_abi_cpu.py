@@ -139,6 +139,31 @@ def test_python_wrappers_reject_host_tensors(llk):
         llk.PackedWeights.from_device(torch.zeros((16, 32), dtype=torch.bfloat16))
 
 
+def test_cache_and_scratch_paths_reject_host_tensors(llk):
+    """The entry point handed out by the cache's object-code level, the L4
+    device-pack path and a caller workspace are checked like the wrappers'
+    operands, before any C call (a host or fp32 tensor would otherwise reach
+    a kernel as a raw pointer)."""
+    import torch
+    from dslcompiler_amd import cache, ops
+    jc = cache.JitCache()
+    fn = jc.lookup_or_compile(cache.KernelKey(operation=cache.OP_FUSED_SWIGLU, N=32, K=16,
+                                              isa=cache.ISA_GFX950))
+    wg = llk.PackedWeights.from_host(normal_bf16(1, 1, (16, 32)), host_only=True)
+    x = torch.zeros((4, 16), dtype=torch.bfloat16)
+    y = torch.zeros((4, 32), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="x must be a CUDA tensor"):
+        fn(x, wg, wg, y)
+    with pytest.raises(ValueError, match="w must be a CUDA tensor"):
+        jc.get_packed_weights(torch.zeros((16, 32), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="w must be a CUDA tensor"):
+        jc.get_packed_weights(torch.zeros((16, 32), dtype=torch.float32))
+    with pytest.raises(ValueError, match="scratch must be a CUDA tensor"):
+        ops._ctx(None, torch.zeros(1024, dtype=torch.uint8))
+    assert jc.stats()["misses"][3] == 0  # nothing reached the L4 level
+    jc.close()
+
+
 def test_tunables(llk):
     assert llk.get_tunable("decode_max_m") == 64
     llk.set_tunable("decode_splits", 3)

@@ -1,8 +1,12 @@
-"""GPU tests at the BASELINE.json sizes.  The CPU oracle is too slow for whole
-outputs, so each test checks sampled rows against the oracle (to the
-north-star bar) plus size-independent properties: bit-identical reruns,
-and bf16 output = RNE of the same kernel's fp32 output."""
+"""GPU tests at the BASELINE.json sizes.  Every output row is compared with
+the oracle (to the north-star bar) through its multithreaded AVX2 legs,
+which are bit-equal to the scalar sequential-k oracle (test_oracle.py), so a
+misplaced or swapped tile anywhere in the output fails; plus size-independent
+properties: bit-identical reruns, and bf16 output = RNE of the same kernel's
+fp32 output."""
 from __future__ import annotations
+
+import os
 
 import numpy as np
 import pytest
@@ -12,6 +16,11 @@ from common import (STREAM_WD, assert_parity, assert_parity_bf16, bf16_bits_to_f
 from gpu_util import from_dev, to_dev
 
 pytestmark = pytest.mark.gpu
+
+
+def _threads() -> int:
+    """Host threads for the oracle legs (at most 16: the GPU box's CPU share)."""
+    return max(1, min(16, os.cpu_count() or 1))
 
 
 def _swiglu_dev(llk, torch, xd, pg, pu, dtype):
@@ -32,10 +41,15 @@ def test_config3_prefill_2048x4096x11008(llk, gpu, orc):
     assert np.array_equal(yb, yb2), "reruns differ"
     yf = _swiglu_dev(llk, gpu, xd, pg, pu, gpu.float32)
     assert np.array_equal(yb, to_bf16_bits(yf))
-    rows = [0, 255, 256, 1023, 2047]
-    yf_ref, _ = orc.swiglu_rows(x, wg, wu, rows)
-    assert_parity(yf[rows], yf_ref, "config3 fp32 rows")
-    assert_parity_bf16(yb[rows], yf_ref, "config3 bf16 rows")
+    _, yf_ref = orc.swiglu_avx2(x, wg, wu, _threads(), want_f32=True)
+    assert_parity(yf, yf_ref, "config3 fp32 (all rows)")
+    assert_parity_bf16(yb, yf_ref, "config3 bf16 (all rows)")
+    # every 256 x 128 output tile on its own (a swapped tile would pass a
+    # global norm only if the two tiles were alike)
+    for m0 in range(0, M, 256):
+        for n0 in range(0, N, 128):
+            t = (slice(m0, m0 + 256), slice(n0, n0 + 128))
+            assert_parity(yf[t], yf_ref[t], f"config3 tile m0={m0} n0={n0}")
 
 
 @pytest.mark.parametrize("M", [1, 8, 16])
@@ -56,7 +70,7 @@ def test_config4_decode(llk, gpu, orc, M):
 
 
 def test_config2_gemm_4096(llk, gpu, orc):
-    """Config 2: C = A B, 4096^3, fp32 out (sampled rows + fp64 brute force)."""
+    """Config 2: C = A B, 4096^3, fp32 out (all rows + fp64 brute force)."""
     print("case config2 gemm 4096^3", flush=True)
     n = 4096
     s = 1.0 / np.sqrt(n)
@@ -64,18 +78,21 @@ def test_config2_gemm_4096(llk, gpu, orc):
     b = normal_bf16(42, 1, (n, n), s)
     pb = llk.PackedWeights.from_host(b)
     c = from_dev(llk.matmul(to_dev(gpu, a), pb, out_dtype=gpu.float32))
-    rows = [0, 1, 2048, 4095]
-    cf_ref, _ = orc.gemm(a[rows], b)
-    assert_parity(c[rows], cf_ref, "config2 rows")
-    c64 = orc.gemm_fp64(a[rows[:1]], b)
-    assert np.max(np.abs(c[rows[:1]] - c64)) < 1e-4
+    cf_ref, _ = orc.gemm_avx2(a, b, _threads(), want_bf16=False)
+    assert_parity(c, cf_ref, "config2 (all rows)")
+    for m0 in range(0, n, 256):
+        for n0 in range(0, n, 256):
+            t = (slice(m0, m0 + 256), slice(n0, n0 + 256))
+            assert_parity(c[t], cf_ref[t], f"config2 tile m0={m0} n0={n0}")
+    c64 = orc.gemm_fp64(a[:1], b)
+    assert np.max(np.abs(c[:1] - c64)) < 1e-4
 
 
 @pytest.mark.parametrize("M", [1, 17, 255, 1000, 4097])
 def test_config5_mlp(llk, gpu, orc, M):
     """Config 5: SwiGLU (K=5120, N=13824) then Z = Y Wd, Wd [13824, 5120];
     ragged M; 1% of X scaled x20; bf16 out.  Each stage against the oracle on
-    sampled rows; Z against the oracle applied to the GPU's own Y."""
+    every row; Z against the oracle applied to the GPU's own Y."""
     print(f"case config5 M={M}", flush=True)
     K, N = 5120, 13824
     x, wg, wu = swiglu_inputs(M, K, N, seed=42)
@@ -85,11 +102,14 @@ def test_config5_mlp(llk, gpu, orc, M):
     yd, zd = llk.mlp(to_dev(gpu, x), pg, pu, pd)
     gpu.cuda.synchronize()
     y, z = from_dev(yd), from_dev(zd)
-    rows = sorted({0, M // 2, M - 1})
-    yf_ref, _ = orc.swiglu_rows(x, wg, wu, rows)
-    assert_parity_bf16(y[rows], yf_ref, f"config5 M={M} Y")
-    zf_ref, _ = orc.gemm(y[rows], wd)
-    assert_parity_bf16(z[rows], zf_ref, f"config5 M={M} Z")
+    _, yf_ref = orc.swiglu_avx2(x, wg, wu, _threads(), want_f32=True)
+    assert_parity_bf16(y, yf_ref, f"config5 M={M} Y (all rows)")
+    zf_ref, _ = orc.gemm_avx2(y, wd, _threads(), want_bf16=False)
+    assert_parity_bf16(z, zf_ref, f"config5 M={M} Z (all rows)")
+    for m0 in range(0, M, 256):
+        rs = slice(m0, m0 + 256)
+        assert_parity_bf16(y[rs], yf_ref[rs], f"config5 M={M} Y rows {m0}..")
+        assert_parity_bf16(z[rs], zf_ref[rs], f"config5 M={M} Z rows {m0}..")
 
 
 def test_x_beyond_32bit_offsets_launches_in_chunks(llk, gpu, orc):

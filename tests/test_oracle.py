@@ -272,6 +272,43 @@ def test_gemm_vs_fp64_and_identity(orc):
     assert np.array_equal(ci, bf16_bits_to_f32(a))
 
 
+def test_gemm_init_closed_form(orc):
+    """micro.mma's acc += lhs * rhs: with integer-valued operands and an
+    integer initial accumulator every partial sum is exact in fp32, so the
+    result equals C0 + A B computed in integers; a dropped or doubled C0 (or
+    a transposed operand) fails it."""
+    rng = np.random.default_rng(15)
+    ai = rng.integers(-8, 9, (21, 75))
+    bi = rng.integers(-8, 9, (75, 37))
+    ci = rng.integers(-1000, 1001, (21, 37))
+    a, b = to_bf16_bits(ai.astype(np.float32)), to_bf16_bits(bi.astype(np.float32))
+    cf, cb = orc.gemm_init(a, b, ci.astype(np.float32))
+    want = (ci + ai @ bi).astype(np.float32)
+    assert np.array_equal(cf, want)
+    assert np.array_equal(cb, to_bf16_bits(want))
+    assert not np.array_equal(cf, (ai @ bi).astype(np.float32))
+    f0, _ = orc.gemm_init(a, b, None)
+    assert np.array_equal(f0, (ai @ bi).astype(np.float32))
+
+
+@pytest.mark.parametrize("threads", [1, 4])
+def test_gemm_avx2_equals_oracle(orc, threads):
+    """The multithreaded AVX2 GEMM leg used for full-size checks: bit-equal
+    to the scalar sequential-k oracle on ragged shapes, with and without an
+    initial accumulator."""
+    if not orc.orc().orc_cpu_has_avx2_fma():
+        pytest.skip("host CPU lacks AVX2/FMA")
+    for M, N, K in ((37, 67, 131), (64, 128, 64), (3, 5, 7), (70, 9, 200)):
+        a = normal_bf16(16, 0, (M, K))
+        b = normal_bf16(16, 1, (K, N), 1.0 / np.sqrt(K))
+        c0 = bf16_bits_to_f32(normal_bf16(16, 2, (M, N)))
+        for ci in (None, c0):
+            f1, b1 = orc.gemm_init(a, b, ci)
+            f2, b2 = orc.gemm_avx2(a, b, threads, ci)
+            assert np.array_equal(f1.view(np.uint32), f2.view(np.uint32)), (M, N, K)
+            assert np.array_equal(b1, b2)
+
+
 def test_mlp_composition(orc):
     x, wg, wu = swiglu_inputs(5, 64, 96, seed=9)
     wd = normal_bf16(9, 3, (96, 64), 0.1)

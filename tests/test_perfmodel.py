@@ -33,3 +33,54 @@ def test_model_split_phases():
     assert abs(p["predicted_us"] - (p["per_cu_us"] + p["reduce_us"] + 3.0)) < 1e-6
     # no split: no reduce phase
     assert perfmodel.predict("fused_swiglu", 2048, 11008, 4096)["reduce_us"] == 0
+
+
+def _engines():
+    import yaml
+    from pathlib import Path
+    path = Path(perfmodel.__file__).resolve().parent / "machines" / "mi355x.yaml"
+    doc = yaml.safe_load(path.read_text())
+    return doc, {e["name"]: e for e in doc["compute"]["matrix_engines"]}
+
+
+def _profile_mfma_rates():
+    """Register-only MFMA rates (TFLOP/s) from the committed profile table
+    `| v_mfma_... | N(0,1) | constant |`."""
+    import re
+    from pathlib import Path
+    text = (Path(__file__).resolve().parents[1] / "profiles" /
+            "swiglu_prefill_clock_vs_operand_data.md").read_text()
+    rates = {}
+    for form, rnd, const in re.findall(
+            r"\|\s*`v_mfma_f32_(\d+x\d+x\d+)_bf16`\s*\|\s*([0-9.]+) TFLOP/s\s*\|\s*([0-9.]+) TFLOP/s",
+            text):
+        rates[form] = (float(rnd), float(const))
+    return rates
+
+
+def test_matrix_engines_match_spec_and_measurements():
+    """Both bf16 MFMA forms issue at the full 1024 flops per SIMD-cycle (the
+    spec peak), back-to-back issue = flops per instruction / 1024, and the
+    sustained rates equal the committed register-only measurements."""
+    doc, eng = _engines()
+    rates = _profile_mfma_rates()
+    assert set(rates) == {"32x32x16", "16x16x32"}, rates
+    simds = doc["compute"]["owners"]["vector_engine"]["count"]
+    for form, (rnd, const) in rates.items():
+        e = eng[f"mfma-bf16-{form}"]
+        m, n, k = e["tile_shapes"][0]
+        assert e["flops_per_cycle"] == 1024, e
+        assert e["issue_cycles"] * e["flops_per_cycle"] == 2 * m * n * k, e
+        peak = e["flops_per_cycle"] * e["count"] * doc["clock_hz"]
+        assert abs(peak - 2.5e15) / 2.5e15 < 0.02 and e["count"] == simds
+        assert abs(e["sustained_flops_random_operands"] - rnd * 1e12) / (rnd * 1e12) < 0.01, form
+        assert abs(e["sustained_flops_constant_operands"] - const * 1e12) / (const * 1e12) < 0.01
+        assert e["sustained_flops_random_operands"] < e["sustained_flops_constant_operands"] <= peak
+    # the 16x16x32 form keeps more of its rate on random data (the tile kernel's choice)
+    assert (eng["mfma-bf16-16x16x32"]["sustained_flops_random_operands"] >
+            eng["mfma-bf16-32x32x16"]["sustained_flops_random_operands"])
+    # the fitted tile-kernel rate cannot exceed the register-only rate of its MFMA form
+    cal = doc["calibration"]
+    workers = doc["compute"]["owners"]["worker"]["count"]
+    assert float(cal["tile_flops_per_cu"]) * workers < eng["mfma-bf16-16x16x32"][
+        "sustained_flops_random_operands"]
