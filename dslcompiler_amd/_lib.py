@@ -85,6 +85,13 @@ class LaunchPlan(C.Structure):
                 ("workspace_bytes", C.c_size_t), ("head_blocks_n", C.c_int64)]
 
 
+class MemRef2D(C.Structure):
+    """MemRef2D (JitCache.h:43-51): 56 bytes."""
+    _fields_ = [("allocated", C.c_void_p), ("aligned", C.c_void_p), ("offset", C.c_int64),
+                ("size0", C.c_int64), ("size1", C.c_int64), ("stride0", C.c_int64),
+                ("stride1", C.c_int64)]
+
+
 class LLKError(RuntimeError):
     """A negative llk_status, with the library's message."""
 
@@ -101,6 +108,8 @@ KKP = C.POINTER(KernelKeyC)
 WKP = C.POINTER(WeightKeyC)
 # llk_kernel_fn: the shape of llk_swiglu_bf16
 KERNEL_FN = C.CFUNCTYPE(C.c_int, T2, P, P, T2, C.c_int, CTX)
+
+MR = C.POINTER(MemRef2D)
 
 # name -> (restype, argtypes); every function declared in include/llk/llk_abi.h.
 SIGNATURES = {
@@ -149,6 +158,9 @@ SIGNATURES = {
     "llk_packed_weights_deserialize": (C.c_int, [P, C.c_size_t, C.c_uint, PP]),
     "llk_packed_weights_save": (C.c_int, [P, C.c_char_p]),
     "llk_packed_weights_load": (C.c_int, [C.c_char_p, C.c_uint, PP]),
+    "llk_swiglu_kernel_fn": (None, [MR, MR, MR, MR, MR]),
+    "llk_kernel_fn_status": (C.c_int, []),
+    "llk_kernel_fn_cache": (C.c_void_p, []),
     "llk_cache_create": (C.c_int, [PP]),
     "llk_cache_destroy": (None, [P]),
     "llk_cache_lookup_or_compile": (C.c_int, [P, KKP, C.POINTER(KERNEL_FN)]),

@@ -43,7 +43,10 @@ HIP_SOURCES = [
     CSRC / "kernels" / "swiglu_decode.hip",
     CSRC / "kernels" / "pack.hip",
     CSRC / "llk_abi.cpp",  # host code that calls the HIP runtime
+    CSRC / "kernel_fn.cpp",
 ]
+# Host sources built by hipcc (they call the HIP runtime or hold device data).
+HIP_HOST_SOURCES = {"llk_abi.cpp", "kernel_fn.cpp"}
 CXX_SOURCES = [
     CSRC / "runtime" / "json.cpp",
     CSRC / "runtime" / "schedule.cpp",
@@ -75,7 +78,7 @@ def _obj(src: Path) -> Path:
 
 def _compile(src: Path) -> Path:
     obj = _obj(src)
-    if src.suffix == ".hip" or src.name == "llk_abi.cpp":
+    if src.suffix == ".hip" or src.name in HIP_HOST_SOURCES:
         cmd = [HIPCC, *HIP_FLAGS, *INCLUDES]
         if src.suffix == ".cpp":
             cmd += ["-x", "hip"]

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -73,13 +74,20 @@ int fail_hip(hipError_t e, const char* what) {
 
 constexpr int kMaxDevices = 64;
 
+// A library-owned workspace: device memory, zero-filled when allocated.
+struct Workspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+
 struct DeviceState {
   std::mutex mu;
   int checked = 0;  // 0 unknown, 1 gfx950, -1 other
   char arch[64] = {0};
   int cu_count = 0, lds = 0, clock_khz = 0;
-  void* ws = nullptr;  // library-owned workspace, zero-filled when allocated
-  size_t ws_bytes = 0;
+  // Library-owned workspaces, one per stream (the per-thread default stream:
+  // one per thread), so launches on different streams never share one.
+  std::map<std::pair<uintptr_t, uint64_t>, Workspace> ws;
   std::vector<void*> retired;  // outgrown workspaces, kept until process exit
 };
 DeviceState g_dev[kMaxDevices];
@@ -149,14 +157,25 @@ bool y_vec_ok(const llk_tensor2d* y, int dtype) {
   return (reinterpret_cast<uintptr_t>(y->data) % align == 0) && (y->stride0 % 4 == 0);
 }
 
+// Key of the library workspace of a stream: the stream handle, and for the
+// per-thread default stream (a different stream on every thread) the thread.
+std::pair<uintptr_t, uint64_t> workspace_key(hipStream_t s) {
+  static std::atomic<uint64_t> next_thread{1};
+  thread_local const uint64_t thread_id = next_thread.fetch_add(1);
+  return {reinterpret_cast<uintptr_t>(s), s == hipStreamPerThread ? thread_id : 0};
+}
+
 // Workspace: the caller's (ctx->scratch) if given, else the library's own
-// per-device buffer, grown on demand.  Launches that use the library's
-// buffer on different streams of one device must not overlap (pass a
-// scratch buffer per stream instead).  An outgrown buffer is retired, not
-// freed: launches still queued, captured in a graph or about to be issued
-// by another thread may name it, and freeing would need a device-wide
-// synchronisation.  Growth is geometric (x1.5 at least), so the retired
-// buffers add up to less than twice the current one.
+// buffer for the launch stream, grown on demand.  Launches are ordered on
+// their stream, so work on one stream never overlaps in its workspace, and
+// two streams never share one.  (A HIP graph captured on a stream keeps
+// that stream's workspace: replaying it concurrently with direct launches
+// on the capture stream is the caller's race, as with any captured buffer.)
+// An outgrown buffer is retired, not freed: launches still queued, captured
+// in a graph or about to be issued by another thread may name it, and
+// freeing would need a device-wide synchronisation.  Growth is geometric
+// (x1.5 at least), so the retired buffers of a stream add up to less than
+// twice its current one.
 int get_workspace(int dev, size_t need, llk_kernel_context* ctx, void** out) {
   *out = nullptr;
   if (need == 0) return LLK_OK;
@@ -170,9 +189,16 @@ int get_workspace(int dev, size_t need, llk_kernel_context* ctx, void** out) {
     return LLK_OK;
   }
   DeviceState& st = g_dev[dev];
+  const auto key = workspace_key(ctx ? static_cast<hipStream_t>(ctx->stream) : nullptr);
   std::lock_guard<std::mutex> lk(st.mu);
-  if (st.ws_bytes < need) {
-    const size_t bytes = std::max({need, st.ws_bytes + st.ws_bytes / 2, (size_t)1 << 20});
+  Workspace* w = nullptr;
+  try {
+    w = &st.ws[key];
+  } catch (const std::bad_alloc&) {
+    return fail(LLK_ERR_OUT_OF_MEMORY, "workspace bookkeeping");
+  }
+  if (w->bytes < need) {
+    const size_t bytes = std::max({need, w->bytes + w->bytes / 2, (size_t)1 << 20});
     void* fresh = nullptr;
     hipError_t e = hipMalloc(&fresh, bytes);
     if (e != hipSuccess)
@@ -184,15 +210,15 @@ int get_workspace(int dev, size_t need, llk_kernel_context* ctx, void** out) {
       return fail_hip(e, "hipMemset(workspace)");
     }
     try {
-      if (st.ws) st.retired.push_back(st.ws);
+      if (w->ptr) st.retired.push_back(w->ptr);
     } catch (const std::bad_alloc&) {
       (void)hipFree(fresh);
       return fail(LLK_ERR_OUT_OF_MEMORY, "workspace bookkeeping");
     }
-    st.ws = fresh;
-    st.ws_bytes = bytes;
+    w->ptr = fresh;
+    w->bytes = bytes;
   }
-  *out = st.ws;
+  *out = w->ptr;
   return LLK_OK;
 }
 
@@ -369,7 +395,11 @@ SmallMChoice small_m_choice(int nmat, int64_t M, int64_t KB, int64_t NB, int64_t
 // (small-M: group width = BN / 32, splits = grain_size; tile: splits =
 // grain_size; BN 0 or grain_size 0 = choose from the shape), then the cost
 // models (small_m_choice, tile_splits).
-Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const llk_tensor2d* x) {
+// max_ws: the largest workspace the caller can provide (the no-allocation
+// entry point's fixed buffer); a plan that needs more takes fewer k splits
+// and, for a padded X, shorter row chunks.
+Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const llk_tensor2d* x,
+                 size_t max_ws = SIZE_MAX) {
   Plan p;
   llk::ScheduleEntry se;
   const bool have_db = db_entry(nmat, M, &se);
@@ -383,6 +413,10 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
     p.G = c.width;
     p.S = c.splits;
     p.ws_bytes = llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), p.S);
+    while (p.ws_bytes > max_ws && p.S > 1) {
+      --p.S;
+      p.ws_bytes = llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), p.S);
+    }
     return p;
   }
   // The tile kernel's buffer offsets are 32-bit: 256 rows of X and one
@@ -403,6 +437,24 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
   p.head_nb = tp.head_nb;
   p.ws_bytes = p.pad_bytes +
                llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)rows, (int)(NB - p.head_nb), p.S);
+  if (p.ws_bytes <= max_ws) return p;
+  // Over the caller's limit: a padded X in row chunks that fit (whole
+  // 256-row tiles; fewer than 256 rows do not fit: ws_bytes stays above
+  // max_ws and the call is rejected), then the most k splits whose partial
+  // planes fit beside it.
+  if (p.pad && p.pad_bytes > max_ws) {
+    const int64_t fit = (int64_t)(max_ws / ((size_t)p.ld * 2)) / 256 * 256;
+    if (fit < 256) return p;
+    p.chunk = std::min(p.chunk, fit);
+    p.pad_bytes = ((size_t)std::min(p.chunk, M) * p.ld * 2 + 255) / 256 * 256;
+  }
+  const int64_t crows = std::min(p.chunk, M);
+  for (; p.S >= 1; --p.S) {
+    if (p.S == 1) p.head_nb = 0;
+    p.ws_bytes = p.pad_bytes + llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)crows,
+                                                    (int)(NB - p.head_nb), p.S);
+    if (p.ws_bytes <= max_ws || p.S == 1) break;
+  }
   return p;
 }
 
@@ -418,13 +470,18 @@ int empty_reduction(llk_tensor2d* y, int out_dtype, llk_kernel_context* ctx, con
 
 int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w0,
                     const llk_packed_weights* w1, llk_tensor2d* y, int out_dtype,
-                    llk_kernel_context* ctx, int dev, const char* what) {
+                    llk_kernel_context* ctx, int dev, const char* what,
+                    size_t max_ws = SIZE_MAX) {
   const int64_t M = x->dim0, K = x->dim1, N = w0->N;
   const int nmat = mode == 1 ? 2 : 1;
-  const Plan p = plan_launch(nmat, M, K, w0->KB, w0->NB, x);
+  const Plan p = plan_launch(nmat, M, K, w0->KB, w0->NB, x, max_ws);
   if (p.too_large)
     return fail(LLK_ERR_SHAPE, "%s: K=%lld too large for M=%lld (the tile kernel needs K <= %lld)",
                 what, (long long)K, (long long)M, (long long)(((int64_t)1 << 31) / 512 - 64));
+  if (p.ws_bytes > max_ws)
+    return fail(LLK_ERR_SCRATCH,
+                "%s: M=%lld K=%lld needs %zu workspace bytes, more than the %zu available",
+                what, (long long)M, (long long)K, p.ws_bytes, max_ws);
   void* ws = nullptr;
   int rc = get_workspace(dev, p.ws_bytes, ctx, &ws);
   if (rc) return rc;

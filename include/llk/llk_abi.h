@@ -423,6 +423,49 @@ int llk_cache_get_stats(const llk_jit_cache* c, llk_cache_stats* out);
 void llk_cache_clear(llk_jit_cache* c);
 size_t llk_cache_size(const llk_jit_cache* c);
 
+/* ----------------------------------------------------------------------- */
+/* The reference's KernelFn calling convention (JitCache.h:43-51, 79-81)    */
+/* ----------------------------------------------------------------------- */
+
+/* MemRef2D (JitCache.h:43-51): the same seven fields in the same order (56
+ * bytes).  Element strides; the data address is aligned + offset elements. */
+typedef struct llk_memref2d {
+  void* allocated;
+  void* aligned;
+  int64_t offset;
+  int64_t size0;
+  int64_t size1;
+  int64_t stride0;
+  int64_t stride1;
+} llk_memref2d;
+
+/* JitCache::KernelFn (JitCache.h:79-81): x, wg, wu, init, result. */
+typedef void (*llk_memref_kernel_fn)(llk_memref2d* x, llk_memref2d* wg, llk_memref2d* wu,
+                                     llk_memref2d* init, llk_memref2d* result);
+
+/* The fused SwiGLU with exactly the KernelFn shape, a drop-in for the
+ * function JitCache::lookupOrCompile returns for an llk.fused_swiglu module
+ * (JitCache.h:79-109): bf16 x [M, K], raw row-major bf16 wg, wu [K, N],
+ * init and result [M, N] (callers pass init == result; init is only
+ * shape-checked), result = bf16(SiLU(x wg) * (x wu)).  wg and wu are
+ * resolved through the L4 weight level of the current device's cache
+ * (llk_kernel_fn_cache; WeightKey = address, shape, BK 64: JitCache.h:143-146,
+ * KernelKey.h:114-124), packed on a miss, so repeated calls with the same
+ * weight buffers reuse the packed handles (a caller that rewrites a weight
+ * buffer in place clears the cache, as with the reference's L4).  Operands
+ * may be device memory (used in place) or host memory (staged through
+ * device buffers).  Runs on the null stream with the library's workspace
+ * for that stream and returns when the result is written, like the
+ * reference's JIT'd function.  No return value: the status of the calling
+ * thread's last call is llk_kernel_fn_status(), its message llk_last_error(). */
+void llk_swiglu_kernel_fn(llk_memref2d* x, llk_memref2d* wg, llk_memref2d* wu,
+                          llk_memref2d* init, llk_memref2d* result);
+int llk_kernel_fn_status(void);
+/* The cache llk_swiglu_kernel_fn uses on the current device (created on first
+ * use, owned by the library; llk_cache_get_stats / llk_cache_clear apply),
+ * or NULL without a device. */
+llk_jit_cache* llk_kernel_fn_cache(void);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

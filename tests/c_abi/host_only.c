@@ -24,10 +24,16 @@ static int fake_entry(const llk_tensor2d* x, const llk_packed_weights* w0,
   return LLK_OK;
 }
 
+/* The KernelFn-shaped entry point has exactly the reference's type
+ * (JitCache.h:79-81) and MemRef2D is 56 bytes (JitCache.h:43-51). */
+static const llk_memref_kernel_fn kernel_fn_shape = &llk_swiglu_kernel_fn;
+typedef char memref_is_56_bytes[sizeof(llk_memref2d) == 56 ? 1 : -1];
+
 int main(void) {
   const int64_t K = 100, N = 150, BK = 64;
   uint16_t* w = malloc((size_t)(K * N) * sizeof(uint16_t));
   int64_t i;
+  memref_is_56_bytes* unused_size_check = NULL;
   llk_tensor2d wt;
   llk_packed_weights* pw = NULL;
   llk_packed_weights* back = NULL;
@@ -38,6 +44,8 @@ int main(void) {
   llk_kernel_key key;
   llk_kernel_fn fn = NULL;
   llk_weight_key wk;
+  (void)unused_size_check;
+  CHECK(kernel_fn_shape != NULL);
   llk_packed_weights* hit = NULL;
   llk_cache_stats st;
   llk_schedule_entry se;

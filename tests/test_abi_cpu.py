@@ -181,3 +181,25 @@ def test_scratch_size_query(llk):
     assert llk.swiglu_scratch_size(0, 10, 10) == 0
     assert llk.swiglu_scratch_size(8, 5120, 13824 * 4) >= 0
     assert llk.swiglu_scratch_size(2048, 11008, 4096) > 0  # worst case: X needs padding
+
+
+def test_kernel_fn_shape_errors_before_any_device_call(llk):
+    """llk_swiglu_kernel_fn (JitCache::KernelFn shape) verifies the memrefs
+    with the op's verifier before touching a device; its status and message
+    are the calling thread's."""
+    import ctypes as C
+    from dslcompiler_amd._lib import MemRef2D
+    L = llk.lib()
+    buf = (C.c_uint16 * 64)()
+    x = MemRef2D(C.addressof(buf), C.addressof(buf), 0, 4, 8, 8, 1)
+    w = MemRef2D(C.addressof(buf), C.addressof(buf), 0, 4, 8, 8, 1)  # K = 4 != 8
+    L.llk_swiglu_kernel_fn(C.byref(x), C.byref(w), C.byref(w), C.byref(x), C.byref(x))
+    assert L.llk_kernel_fn_status() == llk._lib.LLK_ERR_SHAPE
+    assert b"K dimension mismatch between X=8 and Wg=4" in L.llk_last_error()
+    y = MemRef2D(C.addressof(buf), C.addressof(buf), 0, 4, 5, 5, 1)
+    w8 = MemRef2D(C.addressof(buf), C.addressof(buf), 0, 8, 4, 4, 1)
+    init = MemRef2D(C.addressof(buf), C.addressof(buf), 0, 4, 4, 4, 1)
+    L.llk_swiglu_kernel_fn(C.byref(x), C.byref(w8), C.byref(w8), C.byref(init), C.byref(y))
+    assert L.llk_kernel_fn_status() == llk._lib.LLK_ERR_SHAPE
+    assert b"result shape differs from init" in L.llk_last_error()
+    assert C.sizeof(MemRef2D) == 56

@@ -1,6 +1,7 @@
 """Stream and graph behaviour: concurrent launches on two streams with their
-own scratch buffers, and HIP-graph capture + replay of SwiGLU / MLP calls
-(every replay checked against the eager result, with eager work between)."""
+own scratch buffers and with the library's workspace (one per stream), and
+HIP-graph capture + replay of SwiGLU / MLP calls (every replay checked
+against the eager result, with eager work between)."""
 from __future__ import annotations
 
 import numpy as np
@@ -46,6 +47,44 @@ def test_two_streams_own_scratch(llk, gpu):
                 # summation order, so against the unsplit result: the bar
                 assert np.array_equal(got, from_dev(ys[0]))
                 assert_parity(bf16_bits_to_f32(got), bf16_bits_to_f32(ref), "split vs unsplit")
+    finally:
+        llk.set_tunable("tile_splits", old[0])
+        llk.set_tunable("decode_splits", old[1])
+
+
+def test_two_streams_library_workspace(llk, gpu, orc):
+    """No caller scratch: both streams' k-split launches take their workspace
+    from the library, which keeps one per stream, so interleaved launches on
+    two streams with different shapes never share partial planes."""
+    print("case two streams, library workspace", flush=True)
+    cases = [(300, 2048, 1000), (8, 4096, 2000), (255, 5120, 1536)]
+    data = []
+    for M, K, N in cases:
+        x, wg, wu = swiglu_inputs(M, K, N, seed=M + 1)
+        pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
+        yf_ref, _ = orc.swiglu(x, wg, wu)
+        data.append((to_dev(gpu, x), pg, pu, yf_ref))
+    gpu.cuda.synchronize()
+    old = llk.get_tunable("tile_splits"), llk.get_tunable("decode_splits")
+    llk.set_tunable("tile_splits", 3)
+    llk.set_tunable("decode_splits", 3)
+    try:
+        for xd, pg, pu, _ in data:
+            assert llk.describe_launch("fused_swiglu", xd.shape[0], pg.N, pg.K)[
+                "workspace_bytes"] > 0
+        streams = [gpu.cuda.Stream() for _ in data]
+        outs = [[] for _ in data]
+        for _ in range(20):
+            for i, ((xd, pg, pu, _), s) in enumerate(zip(data, streams)):
+                with gpu.cuda.stream(s):
+                    outs[i].append(llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.float32,
+                                                    stream=s))
+        gpu.cuda.synchronize()
+        for ys, (_, _, _, yf_ref) in zip(outs, data):
+            first = from_dev(ys[0])
+            assert_parity(first, yf_ref, "library workspace vs oracle")
+            for y in ys[1:]:
+                assert np.array_equal(from_dev(y).view(np.uint32), first.view(np.uint32))
     finally:
         llk.set_tunable("tile_splits", old[0])
         llk.set_tunable("decode_splits", old[1])
