@@ -133,6 +133,7 @@ SIGNATURES = {
     "llk_pack_device_bytes": (C.c_size_t, [C.c_int64, C.c_int64]),
     "llk_pack_device_layout": (C.c_int, [T2, P]),
     "llk_swiglu_bf16": (C.c_int, [T2, P, P, T2, C.c_int, CTX]),
+    "llk_swiglu_bf16_noalloc": (C.c_int, [T2, P, P, T2, C.c_int, P]),
     "llk_swiglu_scratch_size": (C.c_size_t, [C.c_int64, C.c_int64, C.c_int64]),
     "llk_verify_fused_swiglu": (C.c_int, [C.c_int64] * 8),
     "llk_verify_matmul": (C.c_int, [C.c_int64, C.c_int64]),

@@ -89,6 +89,7 @@ struct DeviceState {
   // one per thread), so launches on different streams never share one.
   std::map<std::pair<uintptr_t, uint64_t>, Workspace> ws;
   std::vector<void*> retired;  // outgrown workspaces, kept until process exit
+  void* noalloc_scratch = nullptr;  // device address of `scratch` (below)
 };
 DeviceState g_dev[kMaxDevices];
 
@@ -219,6 +220,34 @@ int get_workspace(int dev, size_t need, llk_kernel_context* ctx, void** out) {
     w->bytes = bytes;
   }
   *out = w->ptr;
+  return LLK_OK;
+}
+
+// Workspace of llk_swiglu_bf16_noalloc: a fixed device array, one copy per
+// GPU (allocated when the library's code object is loaded on the device, so
+// the entry point itself allocates nothing).  Its contents persist between
+// calls; no kernel relies on them (every byte a launch reads from it -- k-split
+// partial planes, the padded X -- was written earlier in the same call), so
+// nothing is cleared.  Calls that overlap on one GPU race on it.  In host code
+// `scratch` names a host-side stand-in: its device address comes from
+// hipGetSymbolAddress, once per device, and only that address is used.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+// Device address of `scratch` on device `dev` (the current device), looked
+// up on the first no-allocation call on that device.
+int noalloc_scratch(int dev, void** out) {
+  DeviceState& st = g_dev[dev];
+  std::lock_guard<std::mutex> lk(st.mu);
+  if (!st.noalloc_scratch) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return fail_hip(e, "hipGetSymbolAddress(scratch)");
+    if (!p || reinterpret_cast<uintptr_t>(p) % 256 != 0)
+      return fail(LLK_ERR_HIP, "hipGetSymbolAddress(scratch) returned an unaligned address");
+    st.noalloc_scratch = p;
+  }
+  *out = st.noalloc_scratch;
   return LLK_OK;
 }
 
@@ -996,9 +1025,15 @@ int llk_verify_matmul(int64_t a_k, int64_t b_k) {
   return LLK_OK;
 }
 
-int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
-                    const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
-                    llk_kernel_context* ctx) {
+}  // extern "C"
+
+namespace {
+
+// llk_swiglu_bf16 and its no-allocation variant (noalloc: the workspace is
+// the device's `scratch` array, whatever ctx->scratch says).
+int swiglu_entry(const llk_tensor2d* x, const llk_packed_weights* wg,
+                 const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
+                 llk_kernel_context* ctx, bool noalloc) {
   int rc;
   if ((rc = check_tensor(x, "x")) || (rc = check_tensor(y, "y"))) return rc;
   if (y_dtype != LLK_BF16 && y_dtype != LLK_FP32)
@@ -1012,7 +1047,28 @@ int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
   if ((rc = current_device(&dev))) return rc;
   if ((rc = check_packed(wg, "wg", dev)) || (rc = check_packed(wu, "wu", dev))) return rc;
   if (K == 0) return empty_reduction(y, y_dtype, ctx, "swiglu");
-  return run_contraction(1, x, wg, wu, y, y_dtype, ctx, dev, "swiglu");
+  if (!noalloc) return run_contraction(1, x, wg, wu, y, y_dtype, ctx, dev, "swiglu");
+  llk_kernel_context fixed{nullptr, kNoAllocScratchBytes, ctx ? ctx->stream : nullptr};
+  if ((rc = noalloc_scratch(dev, &fixed.scratch))) return rc;
+  return run_contraction(1, x, wg, wu, y, y_dtype, &fixed, dev, "swiglu (no allocation)",
+                         kNoAllocScratchBytes);
+}
+
+}  // namespace
+
+extern "C" {
+
+int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
+                    const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
+                    llk_kernel_context* ctx) {
+  return swiglu_entry(x, wg, wu, y, y_dtype, ctx, false);
+}
+
+int llk_swiglu_bf16_noalloc(const llk_tensor2d* x, const llk_packed_weights* wg,
+                            const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
+                            void* stream) {
+  llk_kernel_context ctx{nullptr, 0, stream};
+  return swiglu_entry(x, wg, wu, y, y_dtype, &ctx, true);
 }
 
 int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor2d* c,

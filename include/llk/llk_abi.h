@@ -166,6 +166,22 @@ int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
                     const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
                     llk_kernel_context* ctx);
 
+/* llk_swiglu_bf16 for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  Same arguments, checks and results as
+ * llk_swiglu_bf16 (launched on `stream`, NULL = the default stream), but the
+ * workspace is a fixed 64 MiB device array built into the library (one per
+ * GPU, held until the process ends) instead of ctx->scratch or the library's
+ * growable buffers: the call makes no hipMalloc/hipFree.  Plans that would
+ * need more workspace use fewer k splits or shorter row chunks; a shape whose
+ * smallest plan still needs more (a padded X with K > ~65000) returns
+ * LLK_ERR_SCRATCH.  Every call on a GPU shares that array: calls that overlap
+ * on one GPU (two streams, two threads) race and must be serialised by the
+ * caller. */
+int llk_swiglu_bf16_noalloc(const llk_tensor2d* x, const llk_packed_weights* wg,
+                            const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
+                            void* stream);
+
 /* FusedSwiGLUOp::verify (LLKOps.cpp:42-83): the same checks in the same
  * order with the same messages; a negative dimension is dynamic and skips
  * the checks it takes part in.  LLK_OK or LLK_ERR_SHAPE.  llk_swiglu_bf16
