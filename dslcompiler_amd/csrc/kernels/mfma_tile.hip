@@ -21,13 +21,17 @@
 // K loop: 32 k per stage (one MFMA k step).  LDS holds a ring of 4 weight
 // stages (16 KiB each) and a ring of 3 X blocks of 64 k (256 rows x 128
 // bytes, 32 KiB each): 160 KiB.  Operands go straight from memory into LDS
-// (buffer_load_dwordx4 ... lds) three or more stages ahead of the 64 MFMAs
+// (buffer_load_dwordx4 ... lds) two or more stages ahead of the 64 MFMAs
 // per wave that consume them; X loads move whole 128-byte lines.  Each
-// stage's barrier sits between its two halves of 32 MFMAs; after it the
-// refills of the freed slots are issued one or two loads per 4 MFMAs, and
-// each next-stage operand is read once its register's last MFMA of this
-// stage has issued, so neither loads nor LDS reads leave the MFMA pipe
-// idle.  Weights sit in LDS as the payload's 1 KiB sub-blocks (32 n x 16 k,
+// stage's barrier sits between its two halves of 32 MFMAs; every half-stage
+// issues four refill loads, one per eight MFMAs, and each next-stage
+// operand is read once its register's last MFMA of this stage has issued.
+// The loop body is twelve stages, the period of the two rings, so every
+// ring slot, LDS address and M0 value is a compile-time constant: with one
+// wave per SIMD every instruction besides the MFMAs takes an issue slot of
+// the wave, and the run-time slot arithmetic of a two-stage body (ring
+// indices, clamps: ~46 scalar instructions per stage) cost 4.5% of config 3
+// and 3% of the 4096^3 GEMM.  Weights sit in LDS as the payload's 1 KiB sub-blocks (32 n x 16 k,
 // lane order); a 16 x 32 A operand gathers two half sub-blocks, each 16-lane
 // group reading 256 contiguous bytes (conflict-free).  X sits as
 // XOR-swizzled 128-byte rows, conflict-free for the operand reads (16 rows x
@@ -97,8 +101,7 @@ constexpr int kXBlockBytes = 32768;   // X of one 64-k block: 256 rows x 128 byt
 constexpr int kXBlocks = 3;           // LDS ring of X blocks
 constexpr int kXRingOff = kWStages * kWStageBytes;
 constexpr int kLdsBytes = kXRingOff + kXBlocks * kXBlockBytes;  // 160 KiB
-constexpr int kWLoads = 4;            // buffer_load ... lds per wave per weight stage
-constexpr int kXLoads = 8;            // ... per wave per X block
+// Per wave: 4 buffer_load ... lds per weight stage, 8 per X block.
 constexpr int kStripRow = 144;        // epilogue staging: 128-byte rows + 16-byte pad
 
 // s_waitcnt with vmcnt(n) (n < 64) and the other counters left alone.
@@ -254,13 +257,27 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
     const int voff = x_voff[i & 1] + i * x_rowstep + u * (kPackK * 2);
     dma16(xrsrc, voff, 0, lds_addr(st + i * kSubBytes));
   };
-  auto dma_w_stage = [&](int t, int wb) {
+  // K-loop refills go through resources whose base follows the data being
+  // refilled, so that inside the loop every ring slot and load offset is a
+  // compile-time constant and the buffer range check (offset < num_records)
+  // turns each refill past the end into zeros with no clamp.  rw starts at
+  // the weight stage a refill targets (advanced 8 KiB per stage: its
+  // num_records stays a multiple of a stage, so a load is either wholly in
+  // the panel or reads zeros); rx at the X block a refill targets (advanced
+  // 128 bytes per block).  Per-load X offsets are fixed per load index.
+  int x_off[8];
 #pragma unroll
-    for (int i = 0; i < kWLoads; ++i) dma_w(t, wb, i);
+  for (int i = 0; i < 8; ++i) x_off[i] = x_voff[i & 1] + i * x_rowstep;
+  // Refill load i (0..3) of weight stage s into ring slot wb: the stage
+  // offset in the VGPR operand, so the range check covers it.
+  auto dma_rw = [&](int s, int wb, int i) {
+    const uint8_t* st = smem + wb * kWStageBytes + (wave * 4) * kSubBytes;
+    dma16(wrsrc, w_voff + s * 8 * kSubBytes, i * kSubBytes, lds_addr(st + i * kSubBytes));
   };
-  auto dma_x_block = [&](int u, int xb) {
-#pragma unroll
-    for (int i = 0; i < kXLoads; ++i) dma_x(u, xb, i);
+  // Refill load i (0..7) of X block u into ring slot xb.
+  auto dma_rx = [&](int u, int xb, int i) {
+    const uint8_t* st = smem + kXRingOff + xb * kXBlockBytes + (wave * 8) * kSubBytes;
+    dma16(xrsrc, x_off[i] + u * (kPackK * 2), 0, lds_addr(st + i * kSubBytes));
   };
 
   // Operands of v_mfma_f32_16x16x32_bf16 (stage-local k 0..31).
@@ -287,24 +304,37 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
                                             (wm * 128 + j * 16) * 128 + b_lane[h]);
   };
 
-  // Pipeline: stage t refills weight slot t % 4 with stage t + 4 after its
-  // barrier, and an odd stage 2u+1 also refills X slot u % 3 with block
-  // u + 3 (block u's last operand reads were for stage 2u+1, in stage 2u).
-  // The prologue issues X0 W0 W1 X1 W2 W3 X2, the order the steady state
-  // would have issued them in, so at every barrier "stage t+1 has landed"
-  // is one wait count: at most 24 loads outstanding at an even stage (X of
-  // stage t-3, the refills of t-2 and t-1), 16 at an odd one.  Refills past
-  // the end re-read the last stage / block (in bounds) into slots no MFMA
-  // reads again, which keeps the counts uniform; they all land before the
-  // epilogue reuses the ring.
+  // Pipeline: every half-stage issues exactly four loads per wave -- two of
+  // a weight refill and two of an X refill -- one per eight MFMAs, so the
+  // load path sees an even stream (a half-stage with twelve loads per wave
+  // outran it).  Weight slot t % 4 is free after stage t's barrier and takes
+  // stage t + 4: loads 0-1 in half 1 of stage t, loads 2-3 in half 0 of
+  // stage t + 1.  X slot u % 3 is free after the barrier of stage 2u + 1
+  // (block u's last operand reads were for stage 2u + 1, in stage 2u) and
+  // takes block u + 3: loads 0-1 in half 1 of stage 2u + 1, 2-3 in half 0
+  // and 4-5 in half 1 of stage 2u + 2, 6-7 in half 0 of stage 2u + 3.  The
+  // data stage t + 1 needs (its weights; at odd t its X block) was complete
+  // by half 0 of stage t - 2, so at every barrier "stage t+1 has landed" is
+  // one wait count: 16 loads outstanding (four half-stages of four).  The
+  // prologue issues the first stages in the order the steady state would
+  // have.  Refills past the end are issued all the same (the counts stay
+  // uniform): in the K loop they read zeros through the range check, in the
+  // prologue they re-read the last stage / block; either way into slots no
+  // MFMA reads again, and all land before the epilogue reuses the ring.
   const int T = nkb * 2;  // stages
-  dma_x_block(0, 0);
-  dma_w_stage(0, 0);
-  dma_w_stage(min(1, T - 1), 1);
-  dma_x_block(min(1, nkb - 1), 1);
-  dma_w_stage(min(2, T - 1), 2);
-  dma_w_stage(min(3, T - 1), 3);
-  dma_x_block(min(2, nkb - 1), 2);
+  {
+    const int w1 = min(1, T - 1), w2 = min(2, T - 1), w3 = min(3, T - 1);
+    const int x1 = min(1, nkb - 1), x2 = min(2, nkb - 1);
+    dma_x(0, 0, 0), dma_x(0, 0, 1);                                      // half 1 of stage -5
+    dma_x(0, 0, 2), dma_x(0, 0, 3);                                      // half 0 of -4
+    dma_w(0, 0, 0), dma_w(0, 0, 1), dma_x(0, 0, 4), dma_x(0, 0, 5);      // half 1 of -4
+    dma_w(0, 0, 2), dma_w(0, 0, 3), dma_x(0, 0, 6), dma_x(0, 0, 7);      // half 0 of -3
+    dma_w(w1, 1, 0), dma_w(w1, 1, 1), dma_x(x1, 1, 0), dma_x(x1, 1, 1);  // half 1 of -3
+    dma_w(w1, 1, 2), dma_w(w1, 1, 3), dma_x(x1, 1, 2), dma_x(x1, 1, 3);  // half 0 of -2
+    dma_w(w2, 2, 0), dma_w(w2, 2, 1), dma_x(x1, 1, 4), dma_x(x1, 1, 5);  // half 1 of -2
+    dma_w(w2, 2, 2), dma_w(w2, 2, 3), dma_x(x1, 1, 6), dma_x(x1, 1, 7);  // half 0 of -1
+    dma_w(w3, 3, 0), dma_w(w3, 3, 1), dma_x(x2, 2, 0), dma_x(x2, 2, 1);  // half 1 of -1
+  }
 
   // Accumulators: acc[i][j] = MFMA rows (n) 16 i .. +16 of the wave's 128
   // (SwiGLU: i < 4 gate, i >= 4 up of the same n), m 16 j .. +16 of its 128.
@@ -316,7 +346,7 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
     for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   acc_fence(acc);  // the zeroed AGPRs are written ...
   mfma_drain();    // ... well before the first MFMA reads them
-  wait_vmcnt<2 * kXLoads + 3 * kWLoads>();  // X0 and W0 landed
+  wait_vmcnt<20>();  // X0 and W0 landed (five half-stages of loads since)
   __syncthreads();
 
   bf16x8 A[8], B[8];
@@ -325,47 +355,75 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) A[i] = rd_a(0, i);
 
-  // Stage t = 2u + H (H = 0, 1).  Half 0: A0..3 x B0..7, A outer; A4..7 of
-  // stage t are read meanwhile.  Half 1: A4..7 x B0..7, B outer; after
-  // column j's four MFMAs the refill loads (weights for j < 4, for odd
-  // stages X two per column for j >= 4), then B[j] (and A[j], j < 4) of
-  // stage t+1 -- their registers' last use this stage.
-  auto stage = [&](int u, auto H) {
-    constexpr int kH = decltype(H)::value;
-    const int t = 2 * u + kH;
-    const int wb = t % kWStages;
-    const int xb = u % kXBlocks;
+  // Stage t (= g + KS, KS = t % 12 a compile-time constant, H = t % 2, X
+  // block u = t / 2).  Half 0: A0..3 x B0..7, A outer; A4..7 of stage t are
+  // read meanwhile, and one refill load follows the first MFMA of each A.
+  // Half 1: A4..7 x B0..7, B outer; a refill load follows the second MFMA of
+  // every other column, and after column j's four MFMAs B[j] (and A[j],
+  // j < 4) of stage t+1 are read -- their registers' last use this stage.
+  // The weight ring (4 slots) and the X ring (3 slots of two stages) repeat
+  // every 12 stages, so with KS constant every slot index is too.
+  // Before stage 0: rw at weight stage 3, rx at X block 2 (the prologue
+  // issued their first loads).
+  int g = 0;  // first stage of the current group of 12
+  auto stage = [&](auto KSc) {
+    constexpr int KS = decltype(KSc)::value;
+    constexpr int kH = KS % 2;
+    constexpr int wb = KS % kWStages;         // slot of stage t
+    constexpr int xb = (KS / 2) % kXBlocks;   // slot of block u
+    constexpr int wb0 = (KS + 3) % kWStages;  // half 0: loads 2-3 of stage t + 3
+    constexpr int xb0 = (KS / 2 + 2) % kXBlocks;  // block u + 2
+    constexpr int nwb = (KS + 1) % kWStages;
+    constexpr int nxb = kH == 0 ? xb : (KS / 2 + 1) % kXBlocks;
+    constexpr int nh = 1 - kH;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       A[4 + i] = rd_a(wb, 4 + i);
+      mfma16(A[i], B[0], acc[i][0]);
+      if (i < 2) dma_rw(g + KS + 3, wb0, 2 + i);
+      else dma_rx(g / 2 + KS / 2 + 2, xb0, (kH == 0 ? 2 : 6) + (i - 2));
 #pragma unroll
-      for (int j = 0; j < 8; ++j) mfma16(A[i], B[j], acc[i][j]);
+      for (int j = 1; j < 8; ++j) mfma16(A[i], B[j], acc[i][j]);
     }
-    wait_lgkmcnt0();  // this wave's reads of stage t are done
-    if constexpr (kH == 0) wait_vmcnt<2 * kXLoads + 2 * kWLoads>();  // stage t+1 landed
-    else wait_vmcnt<kXLoads + 2 * kWLoads>();
-    __syncthreads();  // ... for every wave; weight slot t (and X slot u at odd t) free
-    const int nwb = (t + 1) % kWStages;
-    const int nxb = kH == 0 ? xb : (u + 1) % kXBlocks;
-    constexpr int nh = 1 - kH;
-    const int tw = min(t + kWStages, T - 1);
-    const int ux = min(u + kXBlocks, nkb - 1);
+    wait_lgkmcnt0();   // this wave's reads of stage t are done
+    wait_vmcnt<16>();  // stage t+1 landed
+    __syncthreads();   // ... for every wave; weight slot t (and X slot u at odd t) free
+    // half 1: loads 0-1 of stage t + 4 into slot t % 4; X loads 4-5 of block
+    // u + 2 (H = 0) or loads 0-1 of block u + 3 into slot u % 3 (H = 1)
+    constexpr int xb1 = kH == 0 ? xb0 : xb;
+    constexpr int du1 = kH == 0 ? 2 : 3;  // block u + 2 or u + 3
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       mfma16(A[4], B[j], acc[4][j]);
       mfma16(A[5], B[j], acc[5][j]);
-      if (j < 4) dma_w(tw, wb, j);
-      else if (kH == 1) dma_x(ux, xb, 2 * (j - 4));
+      if (j == 0 || j == 2) dma_rw(g + KS + 4, wb, j / 2);
+      else if (j == 4 || j == 6) dma_rx(g / 2 + KS / 2 + du1, xb1, (kH == 0 ? 4 : 0) + (j - 4) / 2);
       mfma16(A[6], B[j], acc[6][j]);
-      if (kH == 1 && j >= 4) dma_x(ux, xb, 2 * (j - 4) + 1);
       mfma16(A[7], B[j], acc[7][j]);
       B[j] = rd_b(nxb, nh, j);
       if (j < 4) A[j] = rd_a(nwb, j);
     }
   };
-  for (int u = 0; u < nkb; ++u) {
-    stage(u, std::integral_constant<int, 0>{});
-    stage(u, std::integral_constant<int, 1>{});
+  using std::integral_constant;
+  for (; g < T; g += 12) {
+    // T is even: stages come in pairs
+    stage(integral_constant<int, 0>{});
+    stage(integral_constant<int, 1>{});
+    if (g + 2 >= T) break;
+    stage(integral_constant<int, 2>{});
+    stage(integral_constant<int, 3>{});
+    if (g + 4 >= T) break;
+    stage(integral_constant<int, 4>{});
+    stage(integral_constant<int, 5>{});
+    if (g + 6 >= T) break;
+    stage(integral_constant<int, 6>{});
+    stage(integral_constant<int, 7>{});
+    if (g + 8 >= T) break;
+    stage(integral_constant<int, 8>{});
+    stage(integral_constant<int, 9>{});
+    if (g + 10 >= T) break;
+    stage(integral_constant<int, 10>{});
+    stage(integral_constant<int, 11>{});
   }
   wait_vmcnt<0>();  // the trailing refills have landed (the epilogue reuses the ring)
   mfma_drain();

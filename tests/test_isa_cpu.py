@@ -7,9 +7,12 @@ recognizer does not see them.  The kernel keeps the hazards away by
 construction; these tests hold that construction on the instructions the
 compiler actually emitted, for every instantiation:
 
-* the K loop body (two 32-k stages) is exactly 128 MFMAs with no AGPR copies
-  (the reason for the inline assembly) and every MFMA accumulates in place;
-* its only vector-memory waits are the two barriers' (the LDS-DMA loads are
+* the K loop body (twelve 32-k stages: the period of the two LDS rings, so
+  every ring slot is a compile-time constant) is exactly 768 MFMAs with no
+  AGPR copies (the reason for the inline assembly) and every MFMA
+  accumulates in place;
+* its only vector-memory waits are the twelve barriers' (16 loads
+  outstanding each: the refills are spread evenly; the LDS-DMA loads are
   inline assembly too, so that the compiler adds no waits of its own), and M0
   is written only by those loads' own s_mov;
 * no VALU instruction writes an MFMA's A/B operand registers shortly before
@@ -113,11 +116,11 @@ def test_every_tile_instantiation_found(asm):
     assert len(ks) >= 10, sorted(ks)
 
 
-def test_k_loop_is_128_in_place_mfmas_without_agpr_copies(asm):
+def test_k_loop_is_768_in_place_mfmas_without_agpr_copies(asm):
     for name, lines in kernels(asm).items():
         body = [b for b in k_loop(lines) if is_insn(b)]
         mf = [b for b in body if b.startswith(MFMA)]
-        assert len(mf) == 128, (name, len(mf))
+        assert len(mf) == 12 * 64, (name, len(mf))
         assert not [b for b in body if b.startswith("v_accvgpr")], name
         for b in mf:
             ops = operands(b)
@@ -128,8 +131,8 @@ def test_k_loop_waits_and_m0(asm):
     for name, lines in kernels(asm).items():
         body = [b for b in k_loop(lines) if is_insn(b)]
         vm = [b for b in body if "vmcnt" in b]
-        assert [re.search(r"vmcnt\((\d+)\)", b).group(1) for b in vm] == ["24", "16"], (name, vm)
-        assert sum(b == "s_barrier" for b in body) == 2, name
+        assert [re.search(r"vmcnt\((\d+)\)", b).group(1) for b in vm] == ["16"] * 12, (name, vm)
+        assert sum(b == "s_barrier" for b in body) == 12, name
         insns = [b for b in lines if is_insn(b)]
         for k, b in enumerate(insns):
             if "m0" in b:
