@@ -37,6 +37,7 @@ PREFILL = dict(M=2048, K=4096, N=11008)
 DECODE = dict(K=4096, N=14336)
 DECODE_M = (1, 8, 16, 64)
 MLP = dict(K=5120, N=13824)
+MLP_M = (1, 17, 255, 1000, 4097)
 # Every timed workload first runs its --warmup launches, then keeps launching
 # until this much time has passed since the first one: the GPU needs ~35 ms of
 # load to reach its steady clock (the first 50 prefill launches average
@@ -131,9 +132,10 @@ def bench_gemm(torch, llk, steps, warmup, out_dtype=None):
     return dict(ms=ms, tflops=2.0 * n ** 3 / (ms * 1e-3) / 1e12)
 
 
-def bench_mlp(torch, llk, steps, warmup):
-    """Config 5: Y = SwiGLU(X; K=5120, N=13824), Z = Y Wd; per M: us, TFLOP/s
-    (6*M*K*N) and GB/s over the compulsory bytes (weights + X + Y twice + Z)."""
+def bench_mlp(torch, llk, steps, warmup, rows=MLP_M):
+    """Config 5: Y = SwiGLU(X; K=5120, N=13824), Z = Y Wd; per M in `rows`:
+    us, TFLOP/s (6*M*K*N) and GB/s over the compulsory bytes (weights + X +
+    Y twice + Z)."""
     K, N = MLP["K"], MLP["N"]
     g = torch.Generator(device="cuda")
     g.manual_seed(42)
@@ -141,7 +143,7 @@ def bench_mlp(torch, llk, steps, warmup):
     pu = llk.PackedWeights.from_device(_rand_w(torch, g, K, N))
     pd = llk.PackedWeights.from_device(_rand_w(torch, g, N, K))
     out = {}
-    for M in (1, 17, 255, 1000, 4097):
+    for M in rows:
         x = torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16)
         y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
         z = torch.empty((M, K), dtype=torch.bfloat16, device="cuda")
@@ -337,6 +339,8 @@ def main() -> None:
     ap.add_argument("--fill", choices=["normal", "const"], default="normal",
                     help="operands of --only prefill: N(0,1) data (default) or one constant "
                          "value (diagnostic: MFMA power depends on operand bit toggling)")
+    ap.add_argument("--mlp-m", help="comma-separated M values of --only mlp (default: all of "
+                                    "config 5's)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this hot path runs on one GPU; multi-GPU runs are not part of this "
@@ -357,7 +361,8 @@ def main() -> None:
         elif a.only == "gemm":
             r = bench_gemm(torch, llk, a.steps, a.warmup)
         elif a.only == "mlp":
-            r = bench_mlp(torch, llk, a.steps, a.warmup)
+            r = bench_mlp(torch, llk, a.steps, a.warmup,
+                          tuple(int(v) for v in a.mlp_m.split(",")) if a.mlp_m else MLP_M)
         elif a.only == "vendor":
             g16 = bench_gemm(torch, llk, a.steps, a.warmup, torch.bfloat16)
             r = {"vendor_hipblaslt": bench_vendor(torch, a.steps, a.warmup),
