@@ -165,6 +165,10 @@ SIGNATURES = {
     "llk_cache_create": (C.c_int, [PP]),
     "llk_cache_destroy": (None, [P]),
     "llk_cache_lookup_or_compile": (C.c_int, [P, KKP, C.POINTER(KERNEL_FN)]),
+    "llk_cache_set_object_dir": (C.c_int, [P, C.c_char_p]),
+    "llk_code_object_path": (C.c_int, [C.c_int, C.c_char_p, C.c_char_p, C.c_size_t]),
+    "llk_code_object_info": (C.c_int, [C.c_char_p, C.POINTER(C.c_int), C.c_char_p, C.c_size_t,
+                                       C.POINTER(C.c_size_t)]),
     "llk_cache_lookup_object_code": (C.c_int, [P, KKP, C.POINTER(KERNEL_FN)]),
     "llk_cache_insert_object_code": (C.c_int, [P, KKP, KERNEL_FN]),
     "llk_cache_insert_blob": (C.c_int, [P, C.c_int, C.c_char_p, C.c_size_t, C.c_char_p,

@@ -3,8 +3,10 @@
     python -m dslcompiler_amd.build            # library + tools
     python -m dslcompiler_amd.build --lib-only
 
-Objects go to dslcompiler_amd/_build/ and the library to
-dslcompiler_amd/libllk_gfx950.so.  HIP sources are compiled with
+Objects go to dslcompiler_amd/_build/, the library to
+dslcompiler_amd/libllk_gfx950.so, and the per-operation gfx950 code objects
+the kernel cache loads at run time (hipModuleLoadData) to
+dslcompiler_amd/objects/.  HIP sources are compiled with
 ``hipcc --offload-arch=gfx950``; pure C++ runtime sources with g++.
 """
 from __future__ import annotations
@@ -23,6 +25,7 @@ CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libllk_gfx950.so"
 BIN = PKG / "bin"
+OBJECTS = PKG / "objects"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CXX = os.environ.get("CXX_HOST", "g++")
@@ -44,9 +47,13 @@ HIP_SOURCES = [
     CSRC / "kernels" / "pack.hip",
     CSRC / "llk_abi.cpp",  # host code that calls the HIP runtime
     CSRC / "kernel_fn.cpp",
+    CSRC / "code_object.cpp",
 ]
 # Host sources built by hipcc (they call the HIP runtime or hold device data).
-HIP_HOST_SOURCES = {"llk_abi.cpp", "kernel_fn.cpp"}
+HIP_HOST_SOURCES = {"llk_abi.cpp", "kernel_fn.cpp", "code_object.cpp"}
+# One code object per operation (kernels/code_object.hip with LLK_CO_OP),
+# named as code_object.cpp looks them up.
+CODE_OBJECTS = {"llk_fused_swiglu_gfx950.hsaco": 1, "llk_matmul_gfx950.hsaco": 0}
 CXX_SOURCES = [
     CSRC / "runtime" / "json.cpp",
     CSRC / "runtime" / "schedule.cpp",
@@ -89,13 +96,28 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+def _code_object(name: str) -> Path:
+    out = OBJECTS / name
+    tmp = out.with_suffix(".hsaco.tmp")
+    _run([HIPCC, *HIP_FLAGS, *INCLUDES, "--genco", "--no-gpu-bundle-output",
+          f"-DLLK_CO_OP={CODE_OBJECTS[name]}", str(CSRC / "kernels" / "code_object.hip"),
+          "-o", str(tmp)])
+    os.replace(tmp, out)
+    return out
+
+
 def build(lib_only: bool = False, jobs: int | None = None) -> Path:
-    """Compiles every source and links the library (always a full rebuild)."""
+    """Compiles every source, links the library and builds the code objects
+    (always a full rebuild)."""
     BUILD.mkdir(exist_ok=True)
+    OBJECTS.mkdir(exist_ok=True)
     sources = HIP_SOURCES + [s for s in CXX_SOURCES if s.exists()]
     jobs = jobs or min(8, os.cpu_count() or 4)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        cos = [ex.submit(_code_object, n) for n in CODE_OBJECTS]
         objs = list(ex.map(_compile, sources))
+        for f in cos:
+            f.result()
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, LIB)

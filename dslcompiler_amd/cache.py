@@ -75,6 +75,28 @@ class KernelFn:
                        C.byref(_t2d(y)), _out_dtype_code(y.dtype), C.byref(ctx)))
 
 
+def code_object_path(operation: int, directory: str | None = None) -> str:
+    """Path of the gfx950 code object of `operation` (OP_FUSED_SWIGLU or
+    OP_MATMUL) in `directory` (None: the default directory)."""
+    n = lib().llk_code_object_path(operation, directory.encode() if directory else None, None, 0)
+    if n < 0:
+        check(n)
+    buf = C.create_string_buffer(n + 1)
+    lib().llk_code_object_path(operation, directory.encode() if directory else None, buf, n + 1)
+    return buf.value.decode()
+
+
+def code_object_info(path: str) -> list[str]:
+    """Reads and checks a code object without loading it: its kernel symbols."""
+    count, n = C.c_int(), C.c_size_t()
+    check(lib().llk_code_object_info(path.encode(), C.byref(count), None, 0, C.byref(n)))
+    buf = C.create_string_buffer(n.value + 1)
+    check(lib().llk_code_object_info(path.encode(), C.byref(count), buf, n.value + 1, C.byref(n)))
+    names = buf.value.decode().split()
+    assert len(names) == count.value
+    return names
+
+
 class JitCache:
     """Four LRU levels: L1 IR text, L2 optimized text, L3 KernelKey -> entry
     point, L4 WeightKey -> packed weights (owned by the cache)."""
@@ -95,6 +117,10 @@ class JitCache:
             pass
 
     # -- L3 -------------------------------------------------------------------
+    def set_object_dir(self, path: str | None) -> None:
+        """Directory the code objects are read from (None: the default)."""
+        check(lib().llk_cache_set_object_dir(self._c, path.encode() if path else None))
+
     def lookup_or_compile(self, key: KernelKey) -> KernelFn:
         fn = KERNEL_FN()
         check(lib().llk_cache_lookup_or_compile(self._c, C.byref(key.c()), C.byref(fn)))

@@ -65,6 +65,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "launch.h"
 
 namespace llk_gfx950 {
 
@@ -573,43 +574,64 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(TileArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Host launchers
+// Host launchers (mod: a loaded per-operation code object, or null for the
+// library's own kernels).  A build of one operation's code object
+// (LLK_CO_OP: 1 SwiGLU, 0 GEMM) instantiates that operation's kernels only.
 // ---------------------------------------------------------------------------
 template <int MODE, int OUT, bool YVEC, bool SPLIT>
-static hipError_t launch_tile_t(const TileArgs& a, hipStream_t s) {
-  auto fn = mfma_tile_kernel<MODE, OUT, YVEC, SPLIT>;
-  static std::atomic<uint64_t> lds_set{0};  // devices configured, per instantiation
-  hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(fn), kLdsBytes, lds_set);
-  if (e != hipSuccess) return e;
-  dim3 grid(a.tiles_m * a.tiles_n * (SPLIT ? a.S : 1)), block(kThreads);
-  hipLaunchKernelGGL(fn, grid, block, kLdsBytes, s, a);
-  return hipGetLastError();
+const char* tile_symbol() {
+  static const std::string name = "_ZN10llk_gfx95016mfma_tile_kernelI" + mangle_int(MODE) +
+                                  mangle_int(OUT) + mangle_bool(YVEC) + mangle_bool(SPLIT) +
+                                  "EEvNS_8TileArgsE";
+  return name.c_str();
 }
 
 template <int MODE, int OUT, bool YVEC>
-static hipError_t launch_t(const TileArgs& a, hipStream_t s) {
-  if (a.S <= 1) return launch_tile_t<MODE, OUT, YVEC, false>(a, s);
+const char* split_reduce_symbol() {
+  static const std::string name = "_ZN10llk_gfx95019split_reduce_kernelI" + mangle_int(MODE) +
+                                  mangle_int(OUT) + mangle_bool(YVEC) + "EEvNS_8TileArgsE";
+  return name.c_str();
+}
+
+template <int MODE, int OUT, bool YVEC, bool SPLIT>
+static hipError_t launch_tile_t(const TileArgs& a, const llk::ModuleFns* mod, hipStream_t s) {
+  auto fn = mfma_tile_kernel<MODE, OUT, YVEC, SPLIT>;
+  if (!mod) {
+    static std::atomic<uint64_t> lds_set{0};  // devices configured, per instantiation
+    hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(fn), kLdsBytes, lds_set);
+    if (e != hipSuccess) return e;
+  }
+  dim3 grid(a.tiles_m * a.tiles_n * (SPLIT ? a.S : 1)), block(kThreads);
+  return launch_kernel(mod, reinterpret_cast<const void*>(fn),
+                       &tile_symbol<MODE, OUT, YVEC, SPLIT>, grid, block, kLdsBytes, s, a);
+}
+
+template <int MODE, int OUT, bool YVEC>
+static hipError_t launch_t(const TileArgs& a, const llk::ModuleFns* mod, hipStream_t s) {
+  if (a.S <= 1) return launch_tile_t<MODE, OUT, YVEC, false>(a, mod, s);
   // Partials are fp32 planes with 16-byte aligned rows: one instantiation.
-  hipError_t e = launch_tile_t<MODE, kOutF32, true, true>(a, s);
+  hipError_t e = launch_tile_t<MODE, kOutF32, true, true>(a, mod, s);
   if (e != hipSuccess) return e;
   const int64_t threads = (int64_t)a.M * ((a.N + 3) / 4);
-  hipLaunchKernelGGL((split_reduce_kernel<MODE, OUT, YVEC>),
-                     dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a);
-  return hipGetLastError();
+  return launch_kernel(mod, reinterpret_cast<const void*>(split_reduce_kernel<MODE, OUT, YVEC>),
+                       &split_reduce_symbol<MODE, OUT, YVEC>,
+                       dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a);
 }
 
 template <int MODE, int OUT>
-static hipError_t launch_out(const TileArgs& a, bool yvec, hipStream_t s) {
-  return yvec ? launch_t<MODE, OUT, true>(a, s) : launch_t<MODE, OUT, false>(a, s);
+static hipError_t launch_out(const TileArgs& a, bool yvec, const llk::ModuleFns* mod,
+                             hipStream_t s) {
+  return yvec ? launch_t<MODE, OUT, true>(a, mod, s) : launch_t<MODE, OUT, false>(a, mod, s);
 }
 
 // fp16 output exists for the GEMM only (llk.matmul's result types).
 template <int MODE>
-static hipError_t launch_mode(const TileArgs& a, int out, bool yvec, hipStream_t s) {
-  if (out == kOutBF16) return launch_out<MODE, kOutBF16>(a, yvec, s);
-  if (out == kOutF32) return launch_out<MODE, kOutF32>(a, yvec, s);
+static hipError_t launch_mode(const TileArgs& a, int out, bool yvec, const llk::ModuleFns* mod,
+                              hipStream_t s) {
+  if (out == kOutBF16) return launch_out<MODE, kOutBF16>(a, yvec, mod, s);
+  if (out == kOutF32) return launch_out<MODE, kOutF32>(a, yvec, mod, s);
   if constexpr (MODE == 0) {
-    if (out == kOutF16) return launch_out<MODE, kOutF16>(a, yvec, s);
+    if (out == kOutF16) return launch_out<MODE, kOutF16>(a, yvec, mod, s);
   }
   return hipErrorInvalidValue;
 }
@@ -636,7 +658,8 @@ size_t llk_tile_split_bytes(int mode, int M, int NB, int S) {
 // aligned) holds llk_tile_split_bytes(mode, M, NB, S) bytes.
 hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                            const void* w1, void* y, int64_t ldy, int M, int N, int KB, int NB,
-                           int S, void* part, int out, bool yvec, hipStream_t s) {
+                           int S, void* part, int out, bool yvec, const llk::ModuleFns* mod,
+                           hipStream_t s) {
   using namespace llk_gfx950;
   TileArgs a;
   a.x = x;
@@ -657,6 +680,11 @@ hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void*
   a.n_pad = NB * 128;
   a.part = static_cast<float*>(part);
   if (a.S > 1 && (part == nullptr || (int64_t)(a.S - 1) * a.kbs >= KB)) return hipErrorInvalidValue;
-  if (mode == 1) return launch_mode<1>(a, out, yvec, s);
-  return launch_mode<0>(a, out, yvec, s);
+#if !defined(LLK_CO_OP) || LLK_CO_OP == 1
+  if (mode == 1) return launch_mode<1>(a, out, yvec, mod, s);
+#endif
+#if !defined(LLK_CO_OP) || LLK_CO_OP == 0
+  if (mode == 0) return launch_mode<0>(a, out, yvec, mod, s);
+#endif
+  return hipErrorInvalidValue;
 }

@@ -3,6 +3,7 @@
 // one 16-byte lane slot (8 consecutive k of one n); entries outside [K, N]
 // are written as zero, so the whole payload is defined.
 #include "common.h"
+#include "launch.h"
 
 namespace llk_gfx950 {
 
@@ -68,13 +69,17 @@ __global__ __launch_bounds__(256) void pad_rows_kernel(const uint16_t* __restric
   *reinterpret_cast<uint4*>(out + m * ldo + c0) = v;
 }
 
+static const char* pad_rows_symbol() { return "_Z15pad_rows_kernelPKtliiPtl"; }
+
+// mod: a loaded per-operation code object, or null for the library's own
+// kernels (likewise llk_launch_zero_rows).
 hipError_t llk_launch_pad_rows(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* out,
-                               int64_t ldo, hipStream_t s) {
+                               int64_t ldo, const llk::ModuleFns* mod, hipStream_t s) {
   const int64_t threads = (int64_t)M * (ldo / 8);
   if (threads == 0) return hipSuccess;
-  hipLaunchKernelGGL(pad_rows_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, x,
-                     ldx, M, K, out, ldo);
-  return hipGetLastError();
+  return llk_gfx950::launch_kernel(mod, reinterpret_cast<const void*>(pad_rows_kernel),
+                                   &pad_rows_symbol, dim3((unsigned)((threads + 255) / 256)),
+                                   dim3(256), 0, s, x, ldx, M, K, out, ldo);
 }
 
 // Writes zero to every element of a strided [M, N] matrix of 2- or 4-byte
@@ -93,11 +98,14 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(uint8_t* __restrict__ y,
     *reinterpret_cast<uint16_t*>(p) = 0;
 }
 
+static const char* zero_rows_symbol() { return "_Z16zero_rows_kernelPhllil"; }
+
 hipError_t llk_launch_zero_rows(void* y, int64_t ld_elems, int64_t M, int64_t N, int elem_bytes,
-                                hipStream_t s) {
+                                const llk::ModuleFns* mod, hipStream_t s) {
   const int64_t total = M * N;
   if (total <= 0) return hipSuccess;
-  hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
-                     static_cast<uint8_t*>(y), ld_elems * elem_bytes, N, elem_bytes, total);
-  return hipGetLastError();
+  return llk_gfx950::launch_kernel(mod, reinterpret_cast<const void*>(zero_rows_kernel),
+                                   &zero_rows_symbol, dim3((unsigned)((total + 255) / 256)),
+                                   dim3(256), 0, s, static_cast<uint8_t*>(y),
+                                   (int64_t)(ld_elems * elem_bytes), N, elem_bytes, total);
 }

@@ -20,6 +20,7 @@
 // partials in split order and applies the epilogue -- the kernel boundary
 // orders the two, so no device-scope fences are needed.
 #include "common.h"
+#include "launch.h"
 
 namespace llk_gfx950 {
 
@@ -323,49 +324,74 @@ struct SkinnyCfg {
   static_assert(G * GW == W && KS * G <= 16 && lds <= 131072, "small-M launch shape");
 };
 
+template <int NMAT, int MT, int KS, int G, int GW, int OUT, bool XVEC, int UNROLL, bool PIPE>
+const char* skinny_symbol() {
+  static const std::string name = "_ZN10llk_gfx95013skinny_kernelI" + mangle_int(NMAT) +
+                                  mangle_int(MT) + mangle_int(KS) + mangle_int(G) +
+                                  mangle_int(GW) + mangle_int(OUT) + mangle_bool(XVEC) +
+                                  mangle_int(UNROLL) + mangle_bool(PIPE) +
+                                  "EEvNS_10SkinnyArgsE";
+  return name.c_str();
+}
+
+template <int NMAT, int OUT>
+const char* skinny_reduce_symbol() {
+  static const std::string name = "_ZN10llk_gfx95020skinny_reduce_kernelI" + mangle_int(NMAT) +
+                                  mangle_int(OUT) + "EEvNS_10SkinnyArgsEi";
+  return name.c_str();
+}
+
+// mod: a loaded per-operation code object, or null for the library's own
+// kernels.
 template <int NMAT, int MT, int W, int OUT, bool XVEC>
-static hipError_t launch_skinny_t(const SkinnyArgs& a, hipStream_t s) {
+static hipError_t launch_skinny_t(const SkinnyArgs& a, const llk::ModuleFns* mod,
+                                  hipStream_t s) {
   using C = SkinnyCfg<NMAT, MT, W>;
   // (the element-wise X path of unaligned rows needs the registers the
   // second step of weights would take)
-  auto fn = skinny_kernel<NMAT, MT, C::KS, C::G, C::GW, OUT, XVEC, C::UNROLL, C::PIPE && XVEC>;
-  static std::atomic<uint64_t> lds_set{0};  // devices configured, per instantiation
-  if (C::lds > 65536) {
+  constexpr bool kPipe = C::PIPE && XVEC;
+  auto fn = skinny_kernel<NMAT, MT, C::KS, C::G, C::GW, OUT, XVEC, C::UNROLL, kPipe>;
+  if (C::lds > 65536 && !mod) {
+    static std::atomic<uint64_t> lds_set{0};  // devices configured, per instantiation
     hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(fn), (int)C::lds, lds_set);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(fn, dim3(a.NB * 4 / W * a.S), dim3(C::KS * C::G * 64), C::lds, s, a);
-  hipError_t e = hipGetLastError();
+  hipError_t e = launch_kernel(
+      mod, reinterpret_cast<const void*>(fn),
+      &skinny_symbol<NMAT, MT, C::KS, C::G, C::GW, OUT, XVEC, C::UNROLL, kPipe>,
+      dim3(a.NB * 4 / W * a.S), dim3(C::KS * C::G * 64), (unsigned)C::lds, s, a);
   if (e != hipSuccess || a.S == 1) return e;
   const int64_t threads = (int64_t)a.M * (a.n_pad / 4);
-  hipLaunchKernelGGL((skinny_reduce_kernel<NMAT, OUT>), dim3((unsigned)((threads + 255) / 256)),
-                     dim3(256), 0, s, a, MT * 32);
-  return hipGetLastError();
+  return launch_kernel(mod, reinterpret_cast<const void*>(skinny_reduce_kernel<NMAT, OUT>),
+                       &skinny_reduce_symbol<NMAT, OUT>,
+                       dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a, MT * 32);
 }
 
 template <int NMAT, int MT, int W, int OUT>
-static hipError_t launch_skinny_o(const SkinnyArgs& a, bool xvec, hipStream_t s) {
-  return xvec ? launch_skinny_t<NMAT, MT, W, OUT, true>(a, s)
-              : launch_skinny_t<NMAT, MT, W, OUT, false>(a, s);
+static hipError_t launch_skinny_o(const SkinnyArgs& a, bool xvec, const llk::ModuleFns* mod,
+                                  hipStream_t s) {
+  return xvec ? launch_skinny_t<NMAT, MT, W, OUT, true>(a, mod, s)
+              : launch_skinny_t<NMAT, MT, W, OUT, false>(a, mod, s);
 }
 
 // fp16 output exists for the GEMM (NMAT 1) only.
 template <int NMAT, int MT, int W>
-static hipError_t launch_skinny_g(const SkinnyArgs& a, int out, bool xvec, hipStream_t s) {
-  if (out == kOutBF16) return launch_skinny_o<NMAT, MT, W, kOutBF16>(a, xvec, s);
-  if (out == kOutF32) return launch_skinny_o<NMAT, MT, W, kOutF32>(a, xvec, s);
+static hipError_t launch_skinny_g(const SkinnyArgs& a, int out, bool xvec,
+                                  const llk::ModuleFns* mod, hipStream_t s) {
+  if (out == kOutBF16) return launch_skinny_o<NMAT, MT, W, kOutBF16>(a, xvec, mod, s);
+  if (out == kOutF32) return launch_skinny_o<NMAT, MT, W, kOutF32>(a, xvec, mod, s);
   if constexpr (NMAT == 1) {
-    if (out == kOutF16) return launch_skinny_o<NMAT, MT, W, kOutF16>(a, xvec, s);
+    if (out == kOutF16) return launch_skinny_o<NMAT, MT, W, kOutF16>(a, xvec, mod, s);
   }
   return hipErrorInvalidValue;
 }
 
 template <int NMAT, int MT>
 static hipError_t launch_skinny_mt(const SkinnyArgs& a, int W, int out, bool xvec,
-                                   hipStream_t s) {
-  if (W == 4) return launch_skinny_g<NMAT, MT, 4>(a, out, xvec, s);
-  if (W == 2) return launch_skinny_g<NMAT, MT, 2>(a, out, xvec, s);
-  return launch_skinny_g<NMAT, MT, 1>(a, out, xvec, s);
+                                   const llk::ModuleFns* mod, hipStream_t s) {
+  if (W == 4) return launch_skinny_g<NMAT, MT, 4>(a, out, xvec, mod, s);
+  if (W == 2) return launch_skinny_g<NMAT, MT, 2>(a, out, xvec, mod, s);
+  return launch_skinny_g<NMAT, MT, 1>(a, out, xvec, mod, s);
 }
 
 template <int NMAT, int MT>
@@ -401,7 +427,7 @@ size_t llk_skinny_workspace_bytes(int nmat, int M, int N_pad, int S) {
 hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                              const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
                              int NB, int S, int G, void* ws, int out, bool xvec, bool yvec,
-                             hipStream_t s) {
+                             const llk::ModuleFns* mod, hipStream_t s) {
   using namespace llk_gfx950;
   if (M < 1 || M > 64 || (G != 1 && G != 2 && G != 4)) return hipErrorInvalidValue;
   SkinnyArgs a;
@@ -426,9 +452,15 @@ hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const voi
   if (a.S > 1 && (ws == nullptr || (int64_t)(a.S - 1) * a.kb_per_split >= KB))
     return hipErrorInvalidValue;
   const int mt = (M + 31) / 32;
+#if !defined(LLK_CO_OP) || LLK_CO_OP == 1
   if (mode == 1)
-    return mt == 1 ? launch_skinny_mt<2, 1>(a, G, out, xvec, s)
-                   : launch_skinny_mt<2, 2>(a, G, out, xvec, s);
-  return mt == 1 ? launch_skinny_mt<1, 1>(a, G, out, xvec, s)
-                 : launch_skinny_mt<1, 2>(a, G, out, xvec, s);
+    return mt == 1 ? launch_skinny_mt<2, 1>(a, G, out, xvec, mod, s)
+                   : launch_skinny_mt<2, 2>(a, G, out, xvec, mod, s);
+#endif
+#if !defined(LLK_CO_OP) || LLK_CO_OP == 0
+  if (mode == 0)
+    return mt == 1 ? launch_skinny_mt<1, 1>(a, G, out, xvec, mod, s)
+                   : launch_skinny_mt<1, 2>(a, G, out, xvec, mod, s);
+#endif
+  return hipErrorInvalidValue;
 }

@@ -22,24 +22,30 @@
 #include "runtime/schedule.h"
 #include "runtime/tunables.h"
 
-// Kernel launchers (kernels/*.hip).
+namespace llk {
+struct ModuleFns;  // functions of a loaded code object (code_object.cpp)
+}
+
+// Kernel launchers (kernels/*.hip).  mod: the loaded per-operation code
+// object whose kernels to launch, or null for the library's own.
 hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                            const void* w1, void* y, int64_t ldy, int M, int N, int KB, int NB,
-                           int S, void* part, int out_dtype, bool yvec, hipStream_t s);
+                           int S, void* part, int out_dtype, bool yvec,
+                           const llk::ModuleFns* mod, hipStream_t s);
 size_t llk_tile_split_bytes(int mode, int M, int NB, int S);
 bool llk_tile_x_fits(int M, int64_t ldx);
 hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                              const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
                              int NB, int S, int G, void* ws, int out_dtype, bool xvec,
-                             bool yvec, hipStream_t s);
+                             bool yvec, const llk::ModuleFns* mod, hipStream_t s);
 size_t llk_skinny_workspace_bytes(int nmat, int M, int N_pad, int S);
 int llk_skinny_threads(int nmat, int M, int G);
 hipError_t llk_launch_pad_rows(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* out,
-                               int64_t ldo, hipStream_t s);
+                               int64_t ldo, const llk::ModuleFns* mod, hipStream_t s);
 hipError_t llk_launch_pack(const uint16_t* w, int64_t ld, int K, int N, int KB, int NB, void* out,
                            hipStream_t s);
 hipError_t llk_launch_zero_rows(void* y, int64_t ld_elems, int64_t M, int64_t N, int elem_bytes,
-                                hipStream_t s);
+                                const llk::ModuleFns* mod, hipStream_t s);
 
 struct llk_packed_weights {
   // Reference metadata (PackedWeights.h:13-19).
@@ -491,16 +497,17 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
 // (LLKOps.cpp:42-83, 336-348) and its zero-filled fp32 accumulators
 // (FuseDoubleContraction.cpp:119-135) give SiLU(0) * 0 = +0 for SwiGLU and
 // C = 0 for the matmul: the output is filled with zeros.
-int empty_reduction(llk_tensor2d* y, int out_dtype, llk_kernel_context* ctx, const char* what) {
+int empty_reduction(llk_tensor2d* y, int out_dtype, llk_kernel_context* ctx, const char* what,
+                    const llk::ModuleFns* mod) {
   hipError_t e = llk_launch_zero_rows(y->data, y->stride0, y->dim0, y->dim1,
-                                      (int)dtype_size(out_dtype), stream_of(ctx));
+                                      (int)dtype_size(out_dtype), mod, stream_of(ctx));
   return e == hipSuccess ? LLK_OK : fail_hip(e, what);
 }
 
 int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w0,
                     const llk_packed_weights* w1, llk_tensor2d* y, int out_dtype,
                     llk_kernel_context* ctx, int dev, const char* what,
-                    size_t max_ws = SIZE_MAX) {
+                    const llk::ModuleFns* mod, size_t max_ws = SIZE_MAX) {
   const int64_t M = x->dim0, K = x->dim1, N = w0->N;
   const int nmat = mode == 1 ? 2 : 1;
   const Plan p = plan_launch(nmat, M, K, w0->KB, w0->NB, x, max_ws);
@@ -521,7 +528,7 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
     e = llk_launch_skinny(mode, static_cast<const uint16_t*>(x->data), x->stride0, w0->dev,
                           w1 ? w1->dev : nullptr, y->data, y->stride0, (int)M, (int)N, (int)K,
                           (int)w0->KB, (int)w0->NB, p.S, p.G, ws, out_dtype, x_vec_ok(x), yvec,
-                          s);
+                          mod, s);
     if (e != hipSuccess) return fail_hip(e, what);
     return LLK_OK;
   }
@@ -530,7 +537,8 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
     const int rows = (int)std::min(p.chunk, M - m0);
     const uint16_t* xp = static_cast<const uint16_t*>(x->data) + m0 * x->stride0;
     if (p.pad) {
-      e = llk_launch_pad_rows(xp, x->stride0, rows, (int)K, static_cast<uint16_t*>(ws), p.ld, s);
+      e = llk_launch_pad_rows(xp, x->stride0, rows, (int)K, static_cast<uint16_t*>(ws), p.ld, mod,
+                              s);
       if (e != hipSuccess) break;
       xp = static_cast<const uint16_t*>(ws);
     }
@@ -538,7 +546,7 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
     if (p.head_nb > 0) {
       e = llk_launch_tile(mode, xp, p.ld, w0->dev, w1 ? w1->dev : nullptr, yp, y->stride0, rows,
                           (int)(p.head_nb * 128), (int)w0->KB, (int)p.head_nb, 1, nullptr,
-                          out_dtype, yvec, s);
+                          out_dtype, yvec, mod, s);
       if (e != hipSuccess) break;
     }
     // Columns from n-block head_nb on: the packed payload of a matrix is
@@ -551,7 +559,7 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
                         yp + n0 * ysz, y->stride0, rows, (int)(N - n0), (int)w0->KB,
                         (int)(w0->NB - p.head_nb), p.S,
                         p.S > 1 ? static_cast<uint8_t*>(ws) + p.pad_bytes : nullptr, out_dtype,
-                        yvec, s);
+                        yvec, mod, s);
   }
   if (e != hipSuccess) return fail_hip(e, what);
   return LLK_OK;
@@ -1030,10 +1038,11 @@ int llk_verify_matmul(int64_t a_k, int64_t b_k) {
 namespace {
 
 // llk_swiglu_bf16 and its no-allocation variant (noalloc: the workspace is
-// the device's `scratch` array, whatever ctx->scratch says).
+// the device's `scratch` array, whatever ctx->scratch says); mod: the
+// loaded code object whose kernels run (null: the library's own).
 int swiglu_entry(const llk_tensor2d* x, const llk_packed_weights* wg,
                  const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
-                 llk_kernel_context* ctx, bool noalloc) {
+                 llk_kernel_context* ctx, bool noalloc, const llk::ModuleFns* mod) {
   int rc;
   if ((rc = check_tensor(x, "x")) || (rc = check_tensor(y, "y"))) return rc;
   if (y_dtype != LLK_BF16 && y_dtype != LLK_FP32)
@@ -1046,33 +1055,16 @@ int swiglu_entry(const llk_tensor2d* x, const llk_packed_weights* wg,
   int dev;
   if ((rc = current_device(&dev))) return rc;
   if ((rc = check_packed(wg, "wg", dev)) || (rc = check_packed(wu, "wu", dev))) return rc;
-  if (K == 0) return empty_reduction(y, y_dtype, ctx, "swiglu");
-  if (!noalloc) return run_contraction(1, x, wg, wu, y, y_dtype, ctx, dev, "swiglu");
+  if (K == 0) return empty_reduction(y, y_dtype, ctx, "swiglu", mod);
+  if (!noalloc) return run_contraction(1, x, wg, wu, y, y_dtype, ctx, dev, "swiglu", mod);
   llk_kernel_context fixed{nullptr, kNoAllocScratchBytes, ctx ? ctx->stream : nullptr};
   if ((rc = noalloc_scratch(dev, &fixed.scratch))) return rc;
-  return run_contraction(1, x, wg, wu, y, y_dtype, &fixed, dev, "swiglu (no allocation)",
+  return run_contraction(1, x, wg, wu, y, y_dtype, &fixed, dev, "swiglu (no allocation)", mod,
                          kNoAllocScratchBytes);
 }
 
-}  // namespace
-
-extern "C" {
-
-int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
-                    const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
-                    llk_kernel_context* ctx) {
-  return swiglu_entry(x, wg, wu, y, y_dtype, ctx, false);
-}
-
-int llk_swiglu_bf16_noalloc(const llk_tensor2d* x, const llk_packed_weights* wg,
-                            const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
-                            void* stream) {
-  llk_kernel_context ctx{nullptr, 0, stream};
-  return swiglu_entry(x, wg, wu, y, y_dtype, &ctx, true);
-}
-
-int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor2d* c,
-                  int c_dtype, llk_kernel_context* ctx) {
+int gemm_entry(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor2d* c, int c_dtype,
+               llk_kernel_context* ctx, const llk::ModuleFns* mod) {
   int rc;
   if ((rc = check_tensor(a, "a")) || (rc = check_tensor(c, "c"))) return rc;
   if (c_dtype != LLK_BF16 && c_dtype != LLK_FP16 && c_dtype != LLK_FP32)
@@ -1089,8 +1081,30 @@ int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor
   int dev;
   if ((rc = current_device(&dev))) return rc;
   if ((rc = check_packed(b, "b", dev))) return rc;
-  if (K == 0) return empty_reduction(c, c_dtype, ctx, "gemm");
-  return run_contraction(0, a, b, nullptr, c, c_dtype, ctx, dev, "gemm");
+  if (K == 0) return empty_reduction(c, c_dtype, ctx, "gemm", mod);
+  return run_contraction(0, a, b, nullptr, c, c_dtype, ctx, dev, "gemm", mod);
+}
+
+}  // namespace
+
+extern "C" {
+
+int llk_swiglu_bf16(const llk_tensor2d* x, const llk_packed_weights* wg,
+                    const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
+                    llk_kernel_context* ctx) {
+  return swiglu_entry(x, wg, wu, y, y_dtype, ctx, false, nullptr);
+}
+
+int llk_swiglu_bf16_noalloc(const llk_tensor2d* x, const llk_packed_weights* wg,
+                            const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
+                            void* stream) {
+  llk_kernel_context ctx{nullptr, 0, stream};
+  return swiglu_entry(x, wg, wu, y, y_dtype, &ctx, true, nullptr);
+}
+
+int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor2d* c,
+                  int c_dtype, llk_kernel_context* ctx) {
+  return gemm_entry(a, b, c, c_dtype, ctx, nullptr);
 }
 
 int llk_mlp_bf16(const llk_tensor2d* x, const llk_packed_weights* wg, const llk_packed_weights* wu,
@@ -1103,6 +1117,24 @@ int llk_mlp_bf16(const llk_tensor2d* x, const llk_packed_weights* wg, const llk_
   if (rc) return rc;
   return llk_gemm_bf16(y, wd, z, LLK_BF16, ctx);
 }
+
+}  // extern "C"
+
+namespace llk {
+// The SwiGLU and GEMM entry points with the kernels of a loaded code object
+// (code_object.cpp).
+int swiglu_with_module(const llk_tensor2d* x, const llk_packed_weights* wg,
+                       const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
+                       llk_kernel_context* ctx, const ModuleFns* mod) {
+  return swiglu_entry(x, wg, wu, y, y_dtype, ctx, false, mod);
+}
+int gemm_with_module(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor2d* c,
+                     int c_dtype, llk_kernel_context* ctx, const ModuleFns* mod) {
+  return gemm_entry(a, b, c, c_dtype, ctx, mod);
+}
+}  // namespace llk
+
+extern "C" {
 
 // ---------------------------------------------------------------------------
 // Shape specialisation, tiling, keys, schedules

@@ -12,6 +12,8 @@
 
 namespace llk {
 int setError(int code, const char* msg);  // llk_abi.cpp
+// The entry point of an operation's gfx950 code object (code_object.cpp).
+int code_object_entry(int operation, int out_dtype, const std::string& dir, llk_kernel_fn* out);
 }
 
 struct llk_jit_cache {
@@ -19,6 +21,7 @@ struct llk_jit_cache {
   llk::LruLevel<std::string> optimized;  // L2
   llk::LruLevel<llk_kernel_fn> object;   // L3
   llk::LruLevel<std::shared_ptr<llk_packed_weights>> weights;  // L4
+  std::string object_dir;  // where the code objects are read (empty: the default)
 };
 
 namespace {
@@ -49,15 +52,11 @@ std::string weight_key_string(const llk_weight_key& k) {
   return w.serialize();
 }
 
-// GEMM entry with the common kernel-entry shape (w1 unused).
-int gemm_entry(const llk_tensor2d* x, const llk_packed_weights* w0, const llk_packed_weights*,
-               llk_tensor2d* y, int y_dtype, llk_kernel_context* ctx) {
-  return llk_gemm_bf16(x, w0, y, y_dtype, ctx);
-}
-
-// The entry point a key selects.  Keys of other targets, dtypes or
-// operations are errors: this backend builds no code at run time.
-int select_entry(const llk_kernel_key& k, llk_kernel_fn* out) {
+// The entry point a key selects: the operation's gfx950 code object (read,
+// checked and loaded by code_object_entry) with the key's output type bound
+// in.  Keys of other targets, dtypes or operations are errors: this backend
+// builds no code at run time.
+int select_entry(const llk_jit_cache* c, const llk_kernel_key& k, llk_kernel_fn* out) {
   if (k.isa != static_cast<uint8_t>(llk::Isa::GFX950))
     return llk::setError(LLK_ERR_UNSUPPORTED_ARCH, "kernel key isa is not gfx950 (7)");
   if (k.input_type != LLK_BF16)
@@ -67,11 +66,8 @@ int select_entry(const llk_kernel_key& k, llk_kernel_fn* out) {
   if (k.N < 1 || k.K < 1) return llk::setError(LLK_ERR_INVALID_ARGUMENT, "kernel key N, K < 1");
   switch (static_cast<llk::OperationKind>(k.operation)) {
     case llk::OperationKind::FusedSwiGLU:
-      *out = &llk_swiglu_bf16;
-      return LLK_OK;
     case llk::OperationKind::Matmul:
-      *out = &gemm_entry;
-      return LLK_OK;
+      return llk::code_object_entry(k.operation, k.output_type, c->object_dir, out);
     default:
       return llk::setError(LLK_ERR_INVALID_ARGUMENT,
                            "kernel key operation has no gfx950 kernel (RoPE and attention are "
@@ -96,10 +92,16 @@ int llk_cache_lookup_or_compile(llk_jit_cache* c, const llk_kernel_key* key, llk
   const std::string skey = to_key(*key).serialize();
   if (c->object.lookup(skey, out)) return LLK_OK;
   llk_kernel_fn fn = nullptr;
-  int rc = select_entry(*key, &fn);
+  int rc = select_entry(c, *key, &fn);
   if (rc) return rc;
   c->object.insert(skey, fn);
   *out = fn;
+  return LLK_OK;
+}
+
+int llk_cache_set_object_dir(llk_jit_cache* c, const char* dir) {
+  if (!c) return llk::setError(LLK_ERR_INVALID_ARGUMENT, "NULL argument");
+  c->object_dir = dir ? dir : "";
   return LLK_OK;
 }
 

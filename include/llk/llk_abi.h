@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define LLK_ABI_VERSION 2
+#define LLK_ABI_VERSION 3
 
 /* Status codes.  The reference returns errors as llvm::Expected /
  * StringError (JitCache.cpp:200-224); this ABI uses negative integers. */
@@ -47,7 +47,7 @@ typedef enum llk_status {
   LLK_ERR_OUT_OF_MEMORY = -8,    /* host or device allocation failed       */
   LLK_ERR_SCRATCH = -9,          /* caller scratch too small / misaligned  */
   LLK_ERR_DEVICE_MISMATCH = -10, /* handle packed for another device       */
-  LLK_ERR_NOT_FOUND = -11        /* schedule DB file missing or invalid    */
+  LLK_ERR_NOT_FOUND = -11        /* schedule DB / code object missing      */
 } llk_status;
 
 /* Element types: values of llk::DType (KernelKey.h:22). */
@@ -390,13 +390,43 @@ int llk_cache_create(llk_jit_cache** out);
 void llk_cache_destroy(llk_jit_cache* c);
 
 /* lookupOrCompile(KernelKey) (JitCache.cpp:182-250): the L3 entry for the
- * key, or on a miss the gfx950 entry point the key selects (inserted into
- * L3).  Nothing is compiled at run time: the kernels are built ahead of
- * time.  Errors: LLK_ERR_UNSUPPORTED_ARCH (isa != 7), LLK_ERR_DTYPE (input
- * not bf16, output not bf16/fp32), LLK_ERR_INVALID_ARGUMENT (RoPE,
- * Attention or an unknown operation; N or K < 1). */
+ * key, or on a miss the entry point of the key's gfx950 code object
+ * (inserted into L3).  Code objects are compiled ahead of time, one per
+ * operation (llk_fused_swiglu_gfx950.hsaco, llk_matmul_gfx950.hsaco; see
+ * llk_code_object_path): on a miss the key's object is read and checked
+ * (64-bit AMDGPU ELF, gfx950, defines kernels) and, when a HIP device is
+ * present, loaded on the current device with hipModuleLoadData and its
+ * kernels resolved with hipModuleGetFunction (else at the entry's first
+ * call on a device; each device loads it once, and it stays loaded until
+ * the process ends).  The entry runs the operation with that object's
+ * kernels, for the key's output type only (another y_dtype:
+ * LLK_ERR_DTYPE).  Errors: LLK_ERR_UNSUPPORTED_ARCH (isa != 7, or the
+ * object is not for gfx950), LLK_ERR_DTYPE (input not bf16, output not
+ * bf16/fp32), LLK_ERR_INVALID_ARGUMENT (RoPE, Attention or an unknown
+ * operation; N or K < 1; a file that is no code object), LLK_ERR_NOT_FOUND
+ * (the key's code object is missing), LLK_ERR_HIP (the load failed).  On an
+ * error nothing is inserted. */
 int llk_cache_lookup_or_compile(llk_jit_cache* c, const llk_kernel_key* key,
                                 llk_kernel_fn* out);
+
+/* Directory this cache reads code objects from (NULL or "": the default,
+ * $LLK_CODE_OBJECT_DIR or else objects/ beside the library).  No
+ * reference counterpart (the reference compiles in process). */
+int llk_cache_set_object_dir(llk_jit_cache* c, const char* dir);
+
+/* Path of the code object of `operation` (0 fused_swiglu, 3 matmul) in
+ * `dir` (NULL or "": the default directory), written to buf (up to cap
+ * bytes, NUL-terminated).  Returns its length, or LLK_ERR_INVALID_ARGUMENT
+ * for an operation without one. */
+int llk_code_object_path(int operation, const char* dir, char* buf, size_t cap);
+
+/* Reads and checks the code object at `path` without loading it: LLK_OK
+ * with its kernel count and newline-separated kernel symbols (up to cap
+ * bytes, NUL-terminated; *len = full length), or LLK_ERR_NOT_FOUND,
+ * LLK_ERR_INVALID_ARGUMENT (not an ELF code object, no kernels) or
+ * LLK_ERR_UNSUPPORTED_ARCH (not AMDGPU gfx950). */
+int llk_code_object_info(const char* path, int* kernel_count, char* names, size_t cap,
+                         size_t* len);
 
 /* L3 (JitCache.cpp:256-276): lookup returns 1 on a hit (*out set), 0 on a
  * miss; insert returns LLK_OK. */

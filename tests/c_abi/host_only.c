@@ -90,7 +90,17 @@ int main(void) {
   memset(&key, 0, sizeof key);
   key.operation = 0; key.N = N; key.K = K; key.isa = 7; key.weight_layout = 2;
   key.thread_count = 1;
-  CHECK(llk_cache_lookup_or_compile(cache, &key, &fn) == LLK_OK && fn == llk_swiglu_bf16);
+  /* the key's code object is missing from this directory: a status, and
+     nothing is cached */
+  CHECK(llk_cache_set_object_dir(cache, "/nonexistent-llk-objects") == LLK_OK);
+  CHECK(llk_cache_lookup_or_compile(cache, &key, &fn) == LLK_ERR_NOT_FOUND);
+  CHECK(strstr(llk_last_error(), "/nonexistent-llk-objects/llk_fused_swiglu_gfx950.hsaco") != NULL);
+  CHECK(llk_cache_lookup_object_code(cache, &key, &fn) == 0);
+  /* the default directory (objects/ beside the library): read and checked
+     on this host, loaded on a device at the entry's first call */
+  CHECK(llk_cache_set_object_dir(cache, NULL) == LLK_OK);
+  CHECK(llk_cache_lookup_or_compile(cache, &key, &fn) == LLK_OK && fn != NULL &&
+        fn != llk_swiglu_bf16);
   CHECK(llk_cache_lookup_object_code(cache, &key, &fn) == 1);
   key.M_bucket = 3;
   CHECK(llk_cache_insert_object_code(cache, &key, fake_entry) == LLK_OK);
@@ -100,7 +110,7 @@ int main(void) {
   CHECK(llk_cache_insert_packed_weights(cache, &wk, pw) == LLK_OK); /* cache owns pw */
   CHECK(llk_cache_lookup_packed_weights(cache, &wk, &hit) == 1 && hit == pw);
   CHECK(llk_cache_get_stats(cache, &st) == LLK_OK);
-  CHECK(st.hits[2] == 2 && st.misses[2] == 1 && st.hits[3] == 1);
+  CHECK(st.hits[2] == 2 && st.misses[2] == 3 && st.hits[3] == 1);
   CHECK(llk_cache_size(cache) == 3);
   llk_cache_destroy(cache); /* frees pw */
   free(w);

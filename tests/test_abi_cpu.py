@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(llk):
 
 
 def test_abi_version(llk):
-    assert llk.lib().llk_abi_version() == 2
+    assert llk.lib().llk_abi_version() == 3
 
 
 def _t(arr, rows=None, cols=None, stride0=None, stride1=1):
