@@ -140,6 +140,7 @@ SIGNATURES = {
     "llk_describe_launch": (C.c_int, [C.c_int, C.c_int64, C.c_int64, C.c_int64, C.c_int,
                                       C.POINTER(LaunchPlan)]),
     "llk_gemm_bf16": (C.c_int, [T2, P, T2, C.c_int, CTX]),
+    "llk_gemm_bf16_accumulate": (C.c_int, [T2, P, T2, C.c_int, CTX]),
     "llk_mlp_bf16": (C.c_int, [T2, P, P, P, T2, T2, CTX]),
     "llk_classify_m": (C.c_int, [C.c_int64]),
     "llk_num_tiles": (C.c_int64, [C.c_int64, C.c_int64]),

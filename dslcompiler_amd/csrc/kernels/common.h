@@ -150,6 +150,43 @@ __device__ __forceinline__ void store4(void* y, int64_t ldy, int M, int N, int m
   }
 }
 
+// Accumulate mode of the GEMM (C += A B, the micro.mma / linalg.matmul
+// contract): adds the output's existing values at the 4 consecutive n of row
+// m, read in the output type, to v (fp32), before the store rounds it.
+// Bounds and the vector condition as store4.
+template <int OUT>
+__device__ __forceinline__ void add_existing4(const void* y, int64_t ldy, int M, int N, int m,
+                                              int n, float (&v)[4], bool vec_ok) {
+  if (m >= M || n >= N) return;
+  if (OUT == kOutF32) {
+    const float* src = reinterpret_cast<const float*>(y) + (size_t)m * ldy + n;
+    if (vec_ok && n + 4 <= N) {
+      const f32x4 c = *reinterpret_cast<const f32x4*>(src);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] += c[r];
+    } else {
+      for (int r = 0; r < 4; ++r)
+        if (n + r < N) v[r] += src[r];
+    }
+  } else {
+    auto widen = [](uint16_t h) {
+      if constexpr (OUT == kOutF16) return static_cast<float>(__builtin_bit_cast(_Float16, h));
+      else return bf16_bits_to_f32(h);
+    };
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(y) + (size_t)m * ldy + n;
+    if (vec_ok && n + 4 <= N) {
+      const uint2 c = *reinterpret_cast<const uint2*>(src);
+      v[0] += widen((uint16_t)(c.x & 0xffffu));
+      v[1] += widen((uint16_t)(c.x >> 16));
+      v[2] += widen((uint16_t)(c.y & 0xffffu));
+      v[3] += widen((uint16_t)(c.y >> 16));
+    } else {
+      for (int r = 0; r < 4; ++r)
+        if (n + r < N) v[r] += widen(src[r]);
+    }
+  }
+}
+
 // Raises the dynamic-LDS limit of kernel `fn` to `bytes`, once per device
 // (the attribute belongs to the current device); `done` is the caller's
 // per-kernel bit set of devices already configured.

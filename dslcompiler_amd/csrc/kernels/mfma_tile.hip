@@ -91,6 +91,12 @@ struct TileArgs {
   // in split order and applies the epilogue.
   float* part;
   int S, kbs, n_pad;
+  // GEMM only: C += A B (the existing output is read, in its own type, and
+  // added in fp32 before rounding); 0: C = A B.  Taken by
+  // split_reduce_kernel: an accumulating launch always goes through the
+  // partial planes (S >= 1), which keeps the tile kernel's epilogue, and its
+  // registers, those of C = A B.
+  int accumulate;
 };
 
 constexpr int kThreads = 256;
@@ -570,6 +576,9 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(TileArgs a) {
     else
       v[q] = sum[0][q];
   }
+  if constexpr (MODE == 0) {
+    if (a.accumulate) add_existing4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, YVEC);
+  }
   store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, YVEC);
 }
 
@@ -608,7 +617,7 @@ static hipError_t launch_tile_t(const TileArgs& a, const llk::ModuleFns* mod, hi
 
 template <int MODE, int OUT, bool YVEC>
 static hipError_t launch_t(const TileArgs& a, const llk::ModuleFns* mod, hipStream_t s) {
-  if (a.S <= 1) return launch_tile_t<MODE, OUT, YVEC, false>(a, mod, s);
+  if (a.S <= 1 && !a.accumulate) return launch_tile_t<MODE, OUT, YVEC, false>(a, mod, s);
   // Partials are fp32 planes with 16-byte aligned rows: one instantiation.
   hipError_t e = launch_tile_t<MODE, kOutF32, true, true>(a, mod, s);
   if (e != hipSuccess) return e;
@@ -645,21 +654,24 @@ bool llk_tile_x_fits(int M, int64_t ldx) {
   return rows * ldx * 2 < ((int64_t)1 << 31);
 }
 
-// Bytes of the partial planes of a k split over S workgroups (0 if S <= 1).
-size_t llk_tile_split_bytes(int mode, int M, int NB, int S) {
-  if (S <= 1) return 0;
-  return (size_t)S * (mode == 1 ? 2 : 1) * M * NB * 128 * sizeof(float);
+// Bytes of the partial planes of a k split over S workgroups (0 if S <= 1
+// and the launch does not accumulate: an accumulating GEMM launch always
+// takes the planes, one at S = 1).
+size_t llk_tile_split_bytes(int mode, int M, int NB, int S, bool accumulate) {
+  if (S <= 1 && !accumulate) return 0;
+  return (size_t)(S > 1 ? S : 1) * (mode == 1 ? 2 : 1) * M * NB * 128 * sizeof(float);
 }
 
 // Internal (not part of the C ABI).  x: [M, 64*KB] bf16 with ldx % 8 == 0,
 // 16-byte aligned, columns >= K zero; llk_tile_x_fits(M, ldx) must hold.
 // S > 1 splits K over S workgroups of kbs = ceil(KB / S) blocks (every split
 // non-empty: the caller guarantees (S - 1) * kbs < KB); `part` (16-byte
-// aligned) holds llk_tile_split_bytes(mode, M, NB, S) bytes.
+// aligned) holds llk_tile_split_bytes(mode, M, NB, S, accumulate) bytes.
+// accumulate (GEMM only): y += x w instead of y = x w.
 hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                            const void* w1, void* y, int64_t ldy, int M, int N, int KB, int NB,
-                           int S, void* part, int out, bool yvec, const llk::ModuleFns* mod,
-                           hipStream_t s) {
+                           int S, void* part, int out, bool yvec, bool accumulate,
+                           const llk::ModuleFns* mod, hipStream_t s) {
   using namespace llk_gfx950;
   TileArgs a;
   a.x = x;
@@ -679,7 +691,9 @@ hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void*
   a.kbs = (KB + a.S - 1) / a.S;
   a.n_pad = NB * 128;
   a.part = static_cast<float*>(part);
+  a.accumulate = accumulate ? 1 : 0;
   if (a.S > 1 && (part == nullptr || (int64_t)(a.S - 1) * a.kbs >= KB)) return hipErrorInvalidValue;
+  if (accumulate && (mode != 0 || part == nullptr)) return hipErrorInvalidValue;
 #if !defined(LLK_CO_OP) || LLK_CO_OP == 1
   if (mode == 1) return launch_mode<1>(a, out, yvec, mod, s);
 #endif

@@ -33,6 +33,7 @@ struct SkinnyArgs {
   int64_t ldx, ldy;
   int M, N, K, KB, NB, S, kb_per_split, n_pad;
   bool yvec;
+  bool accumulate;  // GEMM only: y += x w (the existing y read in its type)
 };
 
 template <int MT, bool XVEC>
@@ -263,6 +264,9 @@ __global__ __launch_bounds__(KS * G * 64) void skinny_kernel(SkinnyArgs a) {
         else
           v[q] = sum[i][0][q];
       }
+      if constexpr (NMAT == 1) {
+        if (a.accumulate) add_existing4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
+      }
       store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
     }
   }
@@ -291,6 +295,9 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(SkinnyArgs a, int ro
       v[q] = swiglu_act(s[0][q], s[1][q]);
     else
       v[q] = s[0][q];
+  }
+  if constexpr (NMAT == 1) {
+    if (a.accumulate) add_existing4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
   }
   store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
 }
@@ -427,7 +434,7 @@ size_t llk_skinny_workspace_bytes(int nmat, int M, int N_pad, int S) {
 hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                              const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
                              int NB, int S, int G, void* ws, int out, bool xvec, bool yvec,
-                             const llk::ModuleFns* mod, hipStream_t s) {
+                             bool accumulate, const llk::ModuleFns* mod, hipStream_t s) {
   using namespace llk_gfx950;
   if (M < 1 || M > 64 || (G != 1 && G != 2 && G != 4)) return hipErrorInvalidValue;
   SkinnyArgs a;
@@ -446,7 +453,9 @@ hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const voi
   a.kb_per_split = (KB + a.S - 1) / a.S;
   a.n_pad = NB * kPackN;
   a.yvec = yvec;
+  a.accumulate = accumulate;
   a.part = static_cast<float*>(ws);
+  if (accumulate && mode != 0) return hipErrorInvalidValue;
   // Every split must own at least one 64-k block (the dispatcher passes
   // S = ceil(KB / ceil(KB / S_requested))).
   if (a.S > 1 && (ws == nullptr || (int64_t)(a.S - 1) * a.kb_per_split >= KB))

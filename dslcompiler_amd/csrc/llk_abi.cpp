@@ -30,14 +30,15 @@ struct ModuleFns;  // functions of a loaded code object (code_object.cpp)
 // object whose kernels to launch, or null for the library's own.
 hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                            const void* w1, void* y, int64_t ldy, int M, int N, int KB, int NB,
-                           int S, void* part, int out_dtype, bool yvec,
+                           int S, void* part, int out_dtype, bool yvec, bool accumulate,
                            const llk::ModuleFns* mod, hipStream_t s);
-size_t llk_tile_split_bytes(int mode, int M, int NB, int S);
+size_t llk_tile_split_bytes(int mode, int M, int NB, int S, bool accumulate);
 bool llk_tile_x_fits(int M, int64_t ldx);
 hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                              const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
                              int NB, int S, int G, void* ws, int out_dtype, bool xvec,
-                             bool yvec, const llk::ModuleFns* mod, hipStream_t s);
+                             bool yvec, bool accumulate, const llk::ModuleFns* mod,
+                             hipStream_t s);
 size_t llk_skinny_workspace_bytes(int nmat, int M, int N_pad, int S);
 int llk_skinny_threads(int nmat, int M, int G);
 hipError_t llk_launch_pad_rows(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* out,
@@ -433,8 +434,10 @@ SmallMChoice small_m_choice(int nmat, int64_t M, int64_t KB, int64_t NB, int64_t
 // max_ws: the largest workspace the caller can provide (the no-allocation
 // entry point's fixed buffer); a plan that needs more takes fewer k splits
 // and, for a padded X, shorter row chunks.
+// accumulate (GEMM, C += A B): the tile path takes the partial planes at any
+// S (the reduce adds C) and no tail split.
 Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const llk_tensor2d* x,
-                 size_t max_ws = SIZE_MAX) {
+                 size_t max_ws = SIZE_MAX, bool accumulate = false) {
   Plan p;
   llk::ScheduleEntry se;
   const bool have_db = db_entry(nmat, M, &se);
@@ -469,9 +472,10 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
   if (p.pad) p.pad_bytes = ((size_t)rows * p.ld * 2 + 255) / 256 * 256;
   const TilePlan tp = tile_plan(nmat, rows, KB, NB, have_db ? se.grain_size : 0);
   p.S = tp.S;
-  p.head_nb = tp.head_nb;
-  p.ws_bytes = p.pad_bytes +
-               llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)rows, (int)(NB - p.head_nb), p.S);
+  p.head_nb = accumulate ? 0 : tp.head_nb;
+  if (accumulate && tp.head_nb > 0) p.S = best_split(nmat, rows, KB, NB, 0).S;
+  p.ws_bytes = p.pad_bytes + llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)rows,
+                                                  (int)(NB - p.head_nb), p.S, accumulate);
   if (p.ws_bytes <= max_ws) return p;
   // Over the caller's limit: a padded X in row chunks that fit (whole
   // 256-row tiles; fewer than 256 rows do not fit: ws_bytes stays above
@@ -487,7 +491,7 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
   for (; p.S >= 1; --p.S) {
     if (p.S == 1) p.head_nb = 0;
     p.ws_bytes = p.pad_bytes + llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)crows,
-                                                    (int)(NB - p.head_nb), p.S);
+                                                    (int)(NB - p.head_nb), p.S, accumulate);
     if (p.ws_bytes <= max_ws || p.S == 1) break;
   }
   return p;
@@ -507,10 +511,11 @@ int empty_reduction(llk_tensor2d* y, int out_dtype, llk_kernel_context* ctx, con
 int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w0,
                     const llk_packed_weights* w1, llk_tensor2d* y, int out_dtype,
                     llk_kernel_context* ctx, int dev, const char* what,
-                    const llk::ModuleFns* mod, size_t max_ws = SIZE_MAX) {
+                    const llk::ModuleFns* mod, size_t max_ws = SIZE_MAX,
+                    bool accumulate = false) {
   const int64_t M = x->dim0, K = x->dim1, N = w0->N;
   const int nmat = mode == 1 ? 2 : 1;
-  const Plan p = plan_launch(nmat, M, K, w0->KB, w0->NB, x, max_ws);
+  const Plan p = plan_launch(nmat, M, K, w0->KB, w0->NB, x, max_ws, accumulate);
   if (p.too_large)
     return fail(LLK_ERR_SHAPE, "%s: K=%lld too large for M=%lld (the tile kernel needs K <= %lld)",
                 what, (long long)K, (long long)M, (long long)(((int64_t)1 << 31) / 512 - 64));
@@ -528,7 +533,7 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
     e = llk_launch_skinny(mode, static_cast<const uint16_t*>(x->data), x->stride0, w0->dev,
                           w1 ? w1->dev : nullptr, y->data, y->stride0, (int)M, (int)N, (int)K,
                           (int)w0->KB, (int)w0->NB, p.S, p.G, ws, out_dtype, x_vec_ok(x), yvec,
-                          mod, s);
+                          accumulate, mod, s);
     if (e != hipSuccess) return fail_hip(e, what);
     return LLK_OK;
   }
@@ -546,7 +551,7 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
     if (p.head_nb > 0) {
       e = llk_launch_tile(mode, xp, p.ld, w0->dev, w1 ? w1->dev : nullptr, yp, y->stride0, rows,
                           (int)(p.head_nb * 128), (int)w0->KB, (int)p.head_nb, 1, nullptr,
-                          out_dtype, yvec, mod, s);
+                          out_dtype, yvec, accumulate, mod, s);
       if (e != hipSuccess) break;
     }
     // Columns from n-block head_nb on: the packed payload of a matrix is
@@ -558,8 +563,8 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
                         w1 ? static_cast<const uint8_t*>(w1->dev) + w_off : nullptr,
                         yp + n0 * ysz, y->stride0, rows, (int)(N - n0), (int)w0->KB,
                         (int)(w0->NB - p.head_nb), p.S,
-                        p.S > 1 ? static_cast<uint8_t*>(ws) + p.pad_bytes : nullptr, out_dtype,
-                        yvec, mod, s);
+                        p.S > 1 || accumulate ? static_cast<uint8_t*>(ws) + p.pad_bytes : nullptr,
+                        out_dtype, yvec, accumulate, mod, s);
   }
   if (e != hipSuccess) return fail_hip(e, what);
   return LLK_OK;
@@ -1063,8 +1068,9 @@ int swiglu_entry(const llk_tensor2d* x, const llk_packed_weights* wg,
                          kNoAllocScratchBytes);
 }
 
+// llk_gemm_bf16 (accumulate: llk_gemm_bf16_accumulate, C += A B).
 int gemm_entry(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor2d* c, int c_dtype,
-               llk_kernel_context* ctx, const llk::ModuleFns* mod) {
+               llk_kernel_context* ctx, const llk::ModuleFns* mod, bool accumulate = false) {
   int rc;
   if ((rc = check_tensor(a, "a")) || (rc = check_tensor(c, "c"))) return rc;
   if (c_dtype != LLK_BF16 && c_dtype != LLK_FP16 && c_dtype != LLK_FP32)
@@ -1081,8 +1087,10 @@ int gemm_entry(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor2d*
   int dev;
   if ((rc = current_device(&dev))) return rc;
   if ((rc = check_packed(b, "b", dev))) return rc;
-  if (K == 0) return empty_reduction(c, c_dtype, ctx, "gemm", mod);
-  return run_contraction(0, a, b, nullptr, c, c_dtype, ctx, dev, "gemm", mod);
+  // An empty reduction adds nothing: C stays as it is (-0 included).
+  if (K == 0) return accumulate ? LLK_OK : empty_reduction(c, c_dtype, ctx, "gemm", mod);
+  return run_contraction(0, a, b, nullptr, c, c_dtype, ctx, dev,
+                         accumulate ? "gemm (accumulate)" : "gemm", mod, SIZE_MAX, accumulate);
 }
 
 }  // namespace
@@ -1105,6 +1113,11 @@ int llk_swiglu_bf16_noalloc(const llk_tensor2d* x, const llk_packed_weights* wg,
 int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor2d* c,
                   int c_dtype, llk_kernel_context* ctx) {
   return gemm_entry(a, b, c, c_dtype, ctx, nullptr);
+}
+
+int llk_gemm_bf16_accumulate(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor2d* c,
+                             int c_dtype, llk_kernel_context* ctx) {
+  return gemm_entry(a, b, c, c_dtype, ctx, nullptr, true);
 }
 
 int llk_mlp_bf16(const llk_tensor2d* x, const llk_packed_weights* wg, const llk_packed_weights* wu,

@@ -251,15 +251,21 @@ def fused_swiglu(x, wg: PackedWeights, wu: PackedWeights, out=None, out_dtype=No
     return out
 
 
-def matmul(a, b: PackedWeights, out=None, out_dtype=None, stream=None, scratch=None):
-    """C = A B (micro.mma, fp32 accumulation) on the current device."""
+def matmul(a, b: PackedWeights, out=None, out_dtype=None, stream=None, scratch=None,
+           accumulate: bool = False):
+    """C = A B (micro.mma, fp32 accumulation) on the current device; with
+    accumulate=True, out += A B (micro.mma's acc += lhs * rhs: `out` is
+    required and read in place)."""
     torch = _torch()
     _check_operand(a, "a", (torch.bfloat16,))
     if out is None:
+        if accumulate:
+            raise ValueError("accumulate=True needs `out`, the accumulator")
         out = torch.empty((a.shape[0], b.N), dtype=out_dtype or torch.float32, device=a.device)
     _check_operand(out, "out", (torch.bfloat16, torch.float16, torch.float32))
-    check(lib().llk_gemm_bf16(C.byref(_t2d(a)), b.handle, C.byref(_t2d(out)),
-                              _out_dtype_code(out.dtype), C.byref(_ctx(stream, scratch))))
+    fn = lib().llk_gemm_bf16_accumulate if accumulate else lib().llk_gemm_bf16
+    check(fn(C.byref(_t2d(a)), b.handle, C.byref(_t2d(out)), _out_dtype_code(out.dtype),
+             C.byref(_ctx(stream, scratch))))
     return out
 
 

@@ -218,7 +218,8 @@ int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, int x_al
                         llk_launch_plan* out);
 
 /* micro.mma matmul  C = A B  (MicroOps.td:196-222, MicroOps.cpp:246-291;
- * llk.matmul, LLKOps.td:210-255, accumulator f32).
+ * llk.matmul, LLKOps.td:210-255, accumulator f32), i.e. with a zero initial
+ * accumulator; llk_gemm_bf16_accumulate below is the C += A B form.
  * a: bf16 [M, K] device; b: packed [K, N] handle; c: [M, N] device of
  * c_dtype LLK_FP32, LLK_BF16 or LLK_FP16 (the result types llk.matmul
  * allows; both 16-bit types round the fp32 sum to nearest even, fp16
@@ -226,6 +227,16 @@ int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, int x_al
  * LLKOps.cpp:336-348) fills C with +0. */
 int llk_gemm_bf16(const llk_tensor2d* a, const llk_packed_weights* b,
                   llk_tensor2d* c, int c_dtype, llk_kernel_context* ctx);
+
+/* The accumulating form  C += A B: micro.mma's  acc += lhs * rhs
+ * (MicroOps.td:196-222) and llk.matmul / linalg.matmul with a non-zero
+ * outs(init) (LLKOps.td:210-255).  C's existing values are read in c_dtype,
+ * widened to fp32 and added to the fp32 sum of products before the result
+ * is rounded to c_dtype (one rounding per call; the products are summed
+ * first, then C is added).  K == 0 leaves C untouched.  Same arguments and
+ * errors as llk_gemm_bf16; c is read and written in place. */
+int llk_gemm_bf16_accumulate(const llk_tensor2d* a, const llk_packed_weights* b,
+                             llk_tensor2d* c, int c_dtype, llk_kernel_context* ctx);
 
 /* MLP block: Y = SwiGLU(X; Wg, Wu) in bf16, then Z = Y Wd (fp32 accumulate,
  * bf16 result).  wd is a packed [N, K_out] handle.  y is a caller-owned

@@ -94,6 +94,12 @@ def test_gemm_validation_errors(llk):
     assert L.llk_gemm_bf16(C.byref(_t(a)), b.handle, C.byref(_t(np.zeros((4, 33), np.float32))),
                            2, None) == -2
     assert L.llk_gemm_bf16(C.byref(_t(a)), b.handle, C.byref(_t(c)), 7, None) == -3
+    # the accumulating form checks the same contract before touching a device
+    for fn in (L.llk_gemm_bf16, L.llk_gemm_bf16_accumulate):
+        assert fn(C.byref(_t(np.zeros((4, 17), np.uint16))), b.handle, C.byref(_t(c)), 2,
+                  None) == -2
+        assert fn(C.byref(_t(a)), b.handle, C.byref(_t(c)), 7, None) == -3
+        assert fn(C.byref(_t(a)), None, C.byref(_t(c)), 2, None) == -1
 
 
 def test_pack_validation(llk):
