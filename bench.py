@@ -341,6 +341,9 @@ def main() -> None:
                          "value (diagnostic: MFMA power depends on operand bit toggling)")
     ap.add_argument("--mlp-m", help="comma-separated M values of --only mlp (default: all of "
                                     "config 5's)")
+    ap.add_argument("--set", action="append", default=[], metavar="NAME=VALUE",
+                    help="set a dispatcher knob (llk_set_tunable) before a --only run, e.g. "
+                         "tile_two_piece=1; repeatable")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this hot path runs on one GPU; multi-GPU runs are not part of this "
@@ -353,6 +356,9 @@ def main() -> None:
     torch.cuda.set_device(0)
 
     if a.only:
+        for kv in a.set:
+            name, value = kv.split("=", 1)
+            llk.set_tunable(name, int(value))
         if a.only == "prefill":
             pre = bench_prefill(torch, llk, a.steps, a.warmup, a.fill)
             r = {"ms": pre["ms"], "tflops": pre["tflops"], "fill": a.fill}
@@ -372,7 +378,7 @@ def main() -> None:
             src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
             dst = torch.empty_like(src)
             r = {"ms": _time_loop(torch, lambda i: dst.copy_(src), a.steps, a.warmup)}
-        print(json.dumps({"only": a.only, **r}), flush=True)
+        print(json.dumps({"only": a.only, **({"set": a.set} if a.set else {}), **r}), flush=True)
         return
 
     pre = bench_prefill(torch, llk, a.steps, a.warmup)

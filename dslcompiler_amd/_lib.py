@@ -82,7 +82,8 @@ class LaunchPlan(C.Structure):
     _fields_ = [("kernel", C.c_int), ("splits", C.c_int), ("group_width", C.c_int),
                 ("pad_x", C.c_int), ("workgroups", C.c_int64),
                 ("threads_per_workgroup", C.c_int64), ("launches", C.c_int64),
-                ("workspace_bytes", C.c_size_t), ("head_blocks_n", C.c_int64)]
+                ("workspace_bytes", C.c_size_t), ("head_blocks_n", C.c_int64),
+                ("two_piece_kb", C.c_int64)]
 
 
 class MemRef2D(C.Structure):

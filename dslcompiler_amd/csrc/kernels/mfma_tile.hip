@@ -57,7 +57,10 @@
 //
 // Optional k split across workgroups (SPLIT): raw fp32 partial planes plus
 // split_reduce_kernel, which sums them in split order and applies the
-// epilogue.
+// epilogue.  Or (FIX) two pieces of unequal k length per tile, finished by
+// the second piece to arrive: the long pieces of a partial last wave of
+// tiles run on as many CUs while the remaining CUs work through the short
+// ones, so the wave takes max(long, rounds x short) instead of a whole tile.
 //
 // X must be padded to whole 64-k steps with 16-byte aligned rows (the host
 // copies it into a padded buffer otherwise); rows >= M read as zero through
@@ -97,6 +100,15 @@ struct TileArgs {
   // partial planes (S >= 1), which keeps the tile kernel's epilogue, and its
   // registers, those of C = A B.
   int accumulate;
+  // Two-piece k split finished in the kernel (FIX, SwiGLU): workgroup b <
+  // tiles runs the 64-k blocks [0, kb_cut) of a tile, b >= tiles the blocks
+  // [kb_cut, KB) of one; each writes its raw fp32 accumulators to its slot
+  // part + (2 tile + piece) * 64 Ki floats (planes [gate, up][256 rows][128
+  // columns] of the tile) and counts itself in cnt[tile]; the second to
+  // arrive resets cnt[tile] to 0 and writes the tile's outputs from
+  // 0 + slot 0 + slot 1.  cnt must be zero at launch.
+  unsigned* cnt;
+  int kb_cut;
 };
 
 constexpr int kThreads = 256;
@@ -110,6 +122,7 @@ constexpr int kXRingOff = kWStages * kWStageBytes;
 constexpr int kLdsBytes = kXRingOff + kXBlocks * kXBlockBytes;  // 160 KiB
 // Per wave: 4 buffer_load ... lds per weight stage, 8 per X block.
 constexpr int kStripRow = 144;        // epilogue staging: 128-byte rows + 16-byte pad
+constexpr int kFixMaxTiles = 16384;   // two-piece k split: counters (4 bytes each) per launch
 
 // s_waitcnt with vmcnt(n) (n < 64) and the other counters left alone.
 template <int N>
@@ -180,7 +193,8 @@ __device__ __forceinline__ void acc_fence(f32x4 (&acc)[8][8]) {
 // OUT: output element type (kOutBF16, kOutF16 (GEMM only), kOutF32).
 // YVEC: Y rows allow a 4-element vector store (aligned base, ldy % 4 == 0).
 // SPLIT: store raw fp32 partial accumulators of k split s (see TileArgs).
-template <int MODE, int OUT, bool YVEC, bool SPLIT>
+// FIX: two-piece k split finished in the kernel (see TileArgs).
+template <int MODE, int OUT, bool YVEC, bool SPLIT, bool FIX = false>
 __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
@@ -192,10 +206,18 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   // Workgroup -> (split s, tile): tiles of one split are contiguous, so
   // after the XCD remap the tiles that share X's k slice (and, m fastest,
   // the tiles that share W columns) run on one XCD.
+  // FIX: the long pieces first, in launch order, so that they all start in
+  // the first wave; the remap keeps each piece class within itself.
   const int tiles = a.tiles_m * a.tiles_n;
-  const int idx = xcd_remap(blockIdx.x, tiles * (SPLIT ? a.S : 1));
-  const int split = SPLIT ? idx / tiles : 0;
-  const int tile = SPLIT ? idx - split * tiles : idx;
+  int split, tile;
+  if constexpr (FIX) {
+    split = (int)blockIdx.x >= tiles ? 1 : 0;
+    tile = xcd_remap((int)blockIdx.x - split * tiles, tiles);
+  } else {
+    const int idx = xcd_remap(blockIdx.x, tiles * (SPLIT ? a.S : 1));
+    split = SPLIT ? idx / tiles : 0;
+    tile = SPLIT ? idx - split * tiles : idx;
+  }
   int tm, tn;
   if (a.group_m > 0 && a.tiles_m > a.group_m) {
     const int span = a.group_m * a.tiles_n;  // tiles of one full group
@@ -208,8 +230,8 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
     tn = tile / a.tiles_m;
   }
   const int m0 = tm * kTileM;
-  const int kb0 = SPLIT ? split * a.kbs : 0;
-  const int nkb = SPLIT ? min(a.KB - kb0, a.kbs) : a.KB;
+  const int kb0 = FIX ? (split ? a.kb_cut : 0) : SPLIT ? split * a.kbs : 0;
+  const int nkb = FIX ? (split ? a.KB - a.kb_cut : a.kb_cut) : SPLIT ? min(a.KB - kb0, a.kbs) : a.KB;
 
   // ---- operand streams ----------------------------------------------------
   // Stage t holds k range [32 t, 32 t + 32); X block u = k [64 u, 64 u + 64)
@@ -436,6 +458,112 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   mfma_drain();
   acc_fence(acc);   // the epilogue reads the accumulators only after the drain
 
+  // ---- FIX: publish this piece, and finish the tile if it is the second.
+  // Each piece writes its raw accumulators to its slot as tile-local fp32
+  // planes [mat][256 rows][128 columns] (SwiGLU: gate, up), staged through
+  // the LDS strips like the k-split planes (whole 128-byte row segments per
+  // store; the accumulators only ever go to registers and LDS, so the K
+  // loop's register allocation is that of the other forms).  Slots are
+  // written and read with agent-scope coherent accesses (sc1: through every
+  // XCD's L2), and each thread's writes have completed (vmcnt 0) before the
+  // workgroup barrier that precedes the count, so the second piece, which
+  // reads only after seeing the first's count, reads the first's data.  It
+  // then finishes the tile from the two slots, adding piece 0 then piece 1
+  // to zero as split_reduce_kernel does (the same bits whichever piece
+  // arrives second).
+  if constexpr (FIX) {
+    constexpr int kSlotBytes = kThreads * 64 * 16;
+    constexpr int kSc1 = 16;  // cache policy bits: sc1
+    float* const slots = a.part + (size_t)tile * 2 * (kSlotBytes / 4);
+    const int h4f = 4 * (lane >> 4), mrf = lane & 15;
+    __syncthreads();  // every wave is past its last operand read: the ring is free
+    {
+      uint8_t* const strip = smem + wave * (128 * kStripRow);
+      const __amdgpu_buffer_rsrc_t mine = __builtin_amdgcn_make_buffer_rsrc(
+          slots + (size_t)split * (kSlotBytes / 4), 0, kSlotBytes, kBufferWord3);
+#pragma unroll
+      for (int sp = 0; sp < 4; ++sp) {
+        // strip sp: accumulator rows i = 2 sp, 2 sp + 1 -> matrix sp / 2,
+        // tile-local columns wn * 64 + (sp % 2) * 32 .. + 32
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            *reinterpret_cast<f32x4*>(strip + (j * 16 + mrf) * kStripRow + (ii * 16 + h4f) * 4) =
+                acc[2 * sp + ii][j];
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+        const int col0 = wn * 64 + (sp & 1) * 32;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const int row = k * 8 + (lane >> 3);
+          const u32x4 d =
+              *reinterpret_cast<const u32x4*>(strip + row * kStripRow + (lane & 7) * 16);
+          __builtin_amdgcn_raw_buffer_store_b128(
+              d, mine, (((sp >> 1) * 256 + wm * 128 + row) * 128 + col0) * 4 + (lane & 7) * 16, 0,
+              kSc1);
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+      }
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    uint32_t* const flag = reinterpret_cast<uint32_t*>(smem);
+    if (threadIdx.x == 0) {
+      const unsigned prev =
+          __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (prev == 1u) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *reinterpret_cast<volatile uint32_t*>(flag) = prev;
+    }
+    __syncthreads();
+    if (*reinterpret_cast<volatile uint32_t*>(flag) != 1u) return;  // the other piece finishes
+    const __amdgpu_buffer_rsrc_t p0 =
+        __builtin_amdgcn_make_buffer_rsrc(slots, 0, kSlotBytes, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t p1 =
+        __builtin_amdgcn_make_buffer_rsrc(slots + kSlotBytes / 4, 0, kSlotBytes, kBufferWord3);
+    const int n_t = tn * 128;  // the tile's first column (MODE 1: one 128-column block)
+    // Thread t handles quads q = t + 256 s, s = 0..31 (row q / 32, columns
+    // 4 (q % 32) ..): four batches of eight, the next batch's 32 loads in
+    // flight while one is finished (the accumulators are dead here).
+    constexpr int kQ = 8;
+    f32x4 ld[2][kQ][4];
+    auto load_batch = [&](int b, f32x4 (&dst)[kQ][4]) {
+#pragma unroll
+      for (int k = 0; k < kQ; ++k) {
+        const int qd = (int)threadIdx.x + (b * kQ + k) * kThreads;
+        const int r = qd >> 5, c4 = (qd & 31) * 4;
+        const int og = (r * 128 + c4) * 4, ou = ((256 + r) * 128 + c4) * 4;
+        dst[k][0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(p0, og, 0, kSc1));
+        dst[k][1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(p1, og, 0, kSc1));
+        dst[k][2] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(p0, ou, 0, kSc1));
+        dst[k][3] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(p1, ou, 0, kSc1));
+      }
+    };
+    load_batch(0, ld[0]);
+#pragma unroll
+    for (int b = 0; b < 32 / kQ; ++b) {
+      if (b + 1 < 32 / kQ) load_batch(b + 1, ld[(b + 1) & 1]);
+      asm volatile("" ::: "memory");  // the next batch's loads stay below this point
+#pragma unroll
+      for (int k = 0; k < kQ; ++k) {
+        const int qd = (int)threadIdx.x + (b * kQ + k) * kThreads;
+        const int m = m0 + (qd >> 5), n = n_t + (qd & 31) * 4;
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        const f32x4 g = zero + ld[b & 1][k][0] + ld[b & 1][k][1];
+        const f32x4 u = zero + ld[b & 1][k][2] + ld[b & 1][k][3];
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = swiglu_act(g[q], u[q]);
+        store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, YVEC);  // bounds-checked (m < M, n < N)
+      }
+      asm volatile("" ::: "memory");
+    }
+    return;
+  }
+
   // ---- epilogue: acc[i][j] holds, in lane l, output row m = m0 + wm*128 +
   // 16 j + l%16 and the four consecutive n = (wave's first n) + 16 i' +
   // 4*(l/16) + 0..3, i' = i (GEMM) or i % 4 (SwiGLU: i >= 4 is the up half).
@@ -587,11 +715,11 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(TileArgs a) {
 // library's own kernels).  A build of one operation's code object
 // (LLK_CO_OP: 1 SwiGLU, 0 GEMM) instantiates that operation's kernels only.
 // ---------------------------------------------------------------------------
-template <int MODE, int OUT, bool YVEC, bool SPLIT>
+template <int MODE, int OUT, bool YVEC, bool SPLIT, bool FIX>
 const char* tile_symbol() {
   static const std::string name = "_ZN10llk_gfx95016mfma_tile_kernelI" + mangle_int(MODE) +
                                   mangle_int(OUT) + mangle_bool(YVEC) + mangle_bool(SPLIT) +
-                                  "EEvNS_8TileArgsE";
+                                  mangle_bool(FIX) + "EEvNS_8TileArgsE";
   return name.c_str();
 }
 
@@ -602,21 +730,25 @@ const char* split_reduce_symbol() {
   return name.c_str();
 }
 
-template <int MODE, int OUT, bool YVEC, bool SPLIT>
+template <int MODE, int OUT, bool YVEC, bool SPLIT, bool FIX = false>
 static hipError_t launch_tile_t(const TileArgs& a, const llk::ModuleFns* mod, hipStream_t s) {
-  auto fn = mfma_tile_kernel<MODE, OUT, YVEC, SPLIT>;
+  auto fn = mfma_tile_kernel<MODE, OUT, YVEC, SPLIT, FIX>;
   if (!mod) {
     static std::atomic<uint64_t> lds_set{0};  // devices configured, per instantiation
     hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(fn), kLdsBytes, lds_set);
     if (e != hipSuccess) return e;
   }
-  dim3 grid(a.tiles_m * a.tiles_n * (SPLIT ? a.S : 1)), block(kThreads);
+  dim3 grid(a.tiles_m * a.tiles_n * (FIX ? 2 : SPLIT ? a.S : 1)), block(kThreads);
   return launch_kernel(mod, reinterpret_cast<const void*>(fn),
-                       &tile_symbol<MODE, OUT, YVEC, SPLIT>, grid, block, kLdsBytes, s, a);
+                       &tile_symbol<MODE, OUT, YVEC, SPLIT, FIX>, grid, block, kLdsBytes, s, a);
 }
 
 template <int MODE, int OUT, bool YVEC>
 static hipError_t launch_t(const TileArgs& a, const llk::ModuleFns* mod, hipStream_t s) {
+  if constexpr (MODE == 1 && YVEC) {
+    if (a.kb_cut > 0) return launch_tile_t<MODE, OUT, YVEC, false, true>(a, mod, s);
+  }
+  if (a.kb_cut > 0) return hipErrorInvalidValue;  // the two-piece form is SwiGLU's, vector Y
   if (a.S <= 1 && !a.accumulate) return launch_tile_t<MODE, OUT, YVEC, false>(a, mod, s);
   // Partials are fp32 planes with 16-byte aligned rows: one instantiation.
   hipError_t e = launch_tile_t<MODE, kOutF32, true, true>(a, mod, s);
@@ -654,6 +786,11 @@ bool llk_tile_x_fits(int M, int64_t ldx) {
   return rows * ldx * 2 < ((int64_t)1 << 31);
 }
 
+// Two-piece k split (TileArgs::kb_cut): its largest tile count (the counters
+// it needs: 4 bytes per tile) and the slot bytes of `tiles` tiles.
+int llk_tile_fix_max_tiles() { return llk_gfx950::kFixMaxTiles; }
+size_t llk_tile_fix_bytes(int tiles) { return (size_t)tiles * 2 * llk_gfx950::kThreads * 64 * 16; }
+
 // Bytes of the partial planes of a k split over S workgroups (0 if S <= 1
 // and the launch does not accumulate: an accumulating GEMM launch always
 // takes the planes, one at S = 1).
@@ -667,11 +804,14 @@ size_t llk_tile_split_bytes(int mode, int M, int NB, int S, bool accumulate) {
 // S > 1 splits K over S workgroups of kbs = ceil(KB / S) blocks (every split
 // non-empty: the caller guarantees (S - 1) * kbs < KB); `part` (16-byte
 // aligned) holds llk_tile_split_bytes(mode, M, NB, S, accumulate) bytes.
-// accumulate (GEMM only): y += x w instead of y = x w.
+// accumulate (GEMM only): y += x w instead of y = x w.  kb_cut > 0 (SwiGLU,
+// vector Y, S = 1): the two-piece k split finished in the kernel, with
+// `part` (256-byte aligned) holding llk_tile_fix_bytes(tiles) bytes and
+// `cnt` one zeroed counter per tile (tiles <= llk_tile_fix_max_tiles()).
 hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                            const void* w1, void* y, int64_t ldy, int M, int N, int KB, int NB,
-                           int S, void* part, int out, bool yvec, bool accumulate,
-                           const llk::ModuleFns* mod, hipStream_t s) {
+                           int S, void* part, int out, bool yvec, bool accumulate, int kb_cut,
+                           unsigned* cnt, const llk::ModuleFns* mod, hipStream_t s) {
   using namespace llk_gfx950;
   TileArgs a;
   a.x = x;
@@ -692,8 +832,14 @@ hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void*
   a.n_pad = NB * 128;
   a.part = static_cast<float*>(part);
   a.accumulate = accumulate ? 1 : 0;
+  a.cnt = cnt;
+  a.kb_cut = kb_cut;
   if (a.S > 1 && (part == nullptr || (int64_t)(a.S - 1) * a.kbs >= KB)) return hipErrorInvalidValue;
   if (accumulate && (mode != 0 || part == nullptr)) return hipErrorInvalidValue;
+  if (kb_cut != 0 && (mode != 1 || kb_cut < 0 || kb_cut >= KB || part == nullptr ||
+                      cnt == nullptr || accumulate || a.S > 1 ||
+                      (int64_t)a.tiles_m * a.tiles_n > kFixMaxTiles))
+    return hipErrorInvalidValue;
 #if !defined(LLK_CO_OP) || LLK_CO_OP == 1
   if (mode == 1) return launch_mode<1>(a, out, yvec, mod, s);
 #endif

@@ -109,3 +109,21 @@ hipError_t llk_launch_zero_rows(void* y, int64_t ld_elems, int64_t M, int64_t N,
                                    dim3(256), 0, s, static_cast<uint8_t*>(y),
                                    (int64_t)(ld_elems * elem_bytes), N, elem_bytes, total);
 }
+
+// Zeroes `words` 32-bit words (the two-piece k split's arrival counters in
+// a caller's scratch), as a kernel so that the call can be captured in a
+// HIP graph.
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* __restrict__ p, int64_t words) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < words) p[i] = 0u;
+}
+
+static const char* zero_words_symbol() { return "_Z17zero_words_kernelPjl"; }
+
+hipError_t llk_launch_zero(void* p, size_t bytes, const llk::ModuleFns* mod, hipStream_t s) {
+  const int64_t words = (int64_t)(bytes / 4);
+  if (words <= 0) return hipSuccess;
+  return llk_gfx950::launch_kernel(mod, reinterpret_cast<const void*>(zero_words_kernel),
+                                   &zero_words_symbol, dim3((unsigned)((words + 255) / 256)),
+                                   dim3(256), 0, s, static_cast<uint32_t*>(p), words);
+}

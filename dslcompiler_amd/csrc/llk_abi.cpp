@@ -31,7 +31,9 @@ struct ModuleFns;  // functions of a loaded code object (code_object.cpp)
 hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                            const void* w1, void* y, int64_t ldy, int M, int N, int KB, int NB,
                            int S, void* part, int out_dtype, bool yvec, bool accumulate,
-                           const llk::ModuleFns* mod, hipStream_t s);
+                           int kb_cut, unsigned* cnt, const llk::ModuleFns* mod, hipStream_t s);
+int llk_tile_fix_max_tiles();
+size_t llk_tile_fix_bytes(int tiles);
 size_t llk_tile_split_bytes(int mode, int M, int NB, int S, bool accumulate);
 bool llk_tile_x_fits(int M, int64_t ldx);
 hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const void* w0,
@@ -47,6 +49,7 @@ hipError_t llk_launch_pack(const uint16_t* w, int64_t ld, int K, int N, int KB, 
                            hipStream_t s);
 hipError_t llk_launch_zero_rows(void* y, int64_t ld_elems, int64_t M, int64_t N, int elem_bytes,
                                 const llk::ModuleFns* mod, hipStream_t s);
+hipError_t llk_launch_zero(void* p, size_t bytes, const llk::ModuleFns* mod, hipStream_t s);
 
 struct llk_packed_weights {
   // Reference metadata (PackedWeights.h:13-19).
@@ -274,7 +277,21 @@ struct Plan {
   size_t ws_bytes = 0;   // workspace the plan needs
   bool too_large = false;  // tile path: K beyond the kernel's 32-bit offsets
   int64_t head_nb = 0;   // tile path: leading n-blocks launched unsplit (S applies to the rest)
+  int64_t kb_cut = 0;    // tile path, > 0: the columns from head_nb on run as two pieces per
+                         // tile, 64-k blocks [0, kb_cut) and [kb_cut, KB), finished in the kernel
+  size_t fix_bytes = 0;  // tile path: the two-piece slots (after the padded X)
 };
+
+// Every workspace begins with this many bytes of per-tile arrival counters
+// for the two-piece k split, which no other use of the workspace touches:
+// the library's workspaces (zeroed when allocated) and the no-allocation
+// entry point's array (zero when loaded) keep them at zero between launches
+// (the second piece of each tile resets its counter); a caller's scratch is
+// cleared before each two-piece launch.
+constexpr size_t kCounterBytes = 64 << 10;
+
+// Workspace bytes of a plan whose other buffers take `body` bytes.
+size_t with_counters(size_t body) { return body ? kCounterBytes + body : 0; }
 
 // k splits of the tile kernel for `rows` rows: the S that minimises the
 // modelled time  waves(S) * (ceil(KB / S) + 2) + partial traffic  in units
@@ -314,26 +331,74 @@ SplitCost best_split(int nmat, int64_t rows, int64_t KB, int64_t NB, int64_t for
 // remaining columns take a k split -- one short balanced wave instead of a
 // nearly empty long one, with partial planes for the tail columns only.
 // Used when the model puts it 3% or more below the best single launch.
+//
+// Two-piece tail (SwiGLU): the T tiles of a partial wave (T < CUs; all
+// tiles when there is no whole wave) run as two pieces each, k blocks
+// [0, kb_cut) and [kb_cut, KB), finished by whichever piece arrives second
+// (the kernel adds the other's accumulators: no reduce launch, no planes).
+// The T long pieces start on T CUs; the other CUs work through the short
+// ones, r = ceil(T / (CUs - T)) each, so the wave takes
+//   max(kb_cut + 3, r * (KB - kb_cut + 2) + 1)
+// steps (fill and epilogue 2, publishing and adding the other piece 1)
+// instead of KB + 2: config 3 (176 tail tiles of 688, r = 3) cuts at 49 of
+// 64 blocks.  Used, when the knob tile_two_piece is 1, where the model puts
+// it 3% or more below the other plans.  The knob is 0 by default: measured
+// on MI355X each piece's epilogue (256 KiB of fp32 slot written, and the
+// second piece's 512 KiB read back) costs several times the model's step,
+// so the two-piece tail is slower (config 3: 287 vs 259 us, config 5's
+// SwiGLU at M = 1000: 238 vs 218 us, at M = 255: 87.5 vs 85.5 us).
 struct TilePlan {
   int S;
   int64_t head_nb;
+  int64_t kb_cut = 0;
 };
 
-TilePlan tile_plan(int nmat, int64_t rows, int64_t KB, int64_t NB, int64_t db_splits) {
+// Cost and cut of the two-piece form for T tiles (infinity if it cannot run).
+double two_piece_cost(int64_t T, int64_t KB, int64_t per_wave, int64_t* kb_cut) {
+  const int64_t spare = per_wave - T;
+  *kb_cut = 0;
+  if (T < 1 || spare < 1 || KB < 2 || T > llk_tile_fix_max_tiles()) return 1e300;
+  const int64_t r = (T + spare - 1) / spare;
+  double best = 1e300;
+  for (int64_t cut = (KB + 1) / 2; cut < KB; ++cut) {
+    const double c = std::max((double)(cut + 3), (double)(r * (KB - cut + 2) + 1));
+    if (c < best) {
+      best = c;
+      *kb_cut = cut;
+    }
+  }
+  return best;
+}
+
+TilePlan tile_plan(int nmat, int64_t rows, int64_t KB, int64_t NB, int64_t db_splits,
+                   bool allow_two_piece) {
   int64_t forced = llk::tunable("tile_splits");
   if (forced <= 0) forced = db_splits;
   const SplitCost all = best_split(nmat, rows, KB, NB, forced);
-  if (forced > 0 || llk::tunable("tile_tail_split") == 0) return {all.S, 0};
+  if (forced > 0) return {all.S, 0};
   const int64_t nb_per_tile = nmat == 2 ? 1 : 2;
   const int64_t tm = (rows + 255) / 256, tn = (NB + nb_per_tile - 1) / nb_per_tile;
   const int64_t per_wave = std::max<int64_t>(1, llk::tunable("tile_wgs_per_wave"));
   const int64_t head_tn = tm * tn / per_wave * per_wave / tm;  // columns of q whole waves
-  if (head_tn <= 0 || head_tn >= tn) return {all.S, 0};
-  const int64_t head_nb = head_tn * nb_per_tile;
-  const double head = (double)((tm * head_tn + per_wave - 1) / per_wave) * (double)(KB + 2);
-  const SplitCost tail = best_split(nmat, rows, KB, NB - head_nb, 0);
-  if (head + tail.cost <= 0.97 * all.cost) return {tail.S, head_nb};
-  return {all.S, 0};
+  TilePlan best{all.S, 0};
+  double best_cost = all.cost;
+  if (llk::tunable("tile_tail_split") != 0 && head_tn > 0 && head_tn < tn) {
+    const int64_t head_nb = head_tn * nb_per_tile;
+    const double head = (double)((tm * head_tn + per_wave - 1) / per_wave) * (double)(KB + 2);
+    const SplitCost tail = best_split(nmat, rows, KB, NB - head_nb, 0);
+    if (head + tail.cost <= 0.97 * best_cost) {
+      best = {tail.S, head_nb};
+      best_cost = head + tail.cost;
+    }
+  }
+  if (allow_two_piece && nmat == 2 && llk::tunable("tile_two_piece") != 0 && head_tn < tn) {
+    int64_t cut = 0;
+    const double tail = two_piece_cost(tm * (tn - head_tn), KB, per_wave, &cut);
+    const double head =
+        (double)((tm * head_tn + per_wave - 1) / per_wave) * (double)(KB + 2);
+    if (cut > 0 && head + tail <= 0.97 * best_cost) best = {1, head_tn * nb_per_tile, cut};
+  }
+  return best;
 }
 
 // Active schedule DB (llk_set_schedule_db, or the file named by the
@@ -435,9 +500,10 @@ SmallMChoice small_m_choice(int nmat, int64_t M, int64_t KB, int64_t NB, int64_t
 // entry point's fixed buffer); a plan that needs more takes fewer k splits
 // and, for a padded X, shorter row chunks.
 // accumulate (GEMM, C += A B): the tile path takes the partial planes at any
-// S (the reduce adds C) and no tail split.
+// S (the reduce adds C) and no tail split.  two_piece: the two-piece tail
+// may be used (it needs vector Y stores).
 Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const llk_tensor2d* x,
-                 size_t max_ws = SIZE_MAX, bool accumulate = false) {
+                 size_t max_ws = SIZE_MAX, bool accumulate = false, bool two_piece = true) {
   Plan p;
   llk::ScheduleEntry se;
   const bool have_db = db_entry(nmat, M, &se);
@@ -450,10 +516,10 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
     const SmallMChoice c = small_m_choice(nmat, M, KB, NB, gw, S);
     p.G = c.width;
     p.S = c.splits;
-    p.ws_bytes = llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), p.S);
+    p.ws_bytes = with_counters(llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), p.S));
     while (p.ws_bytes > max_ws && p.S > 1) {
       --p.S;
-      p.ws_bytes = llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), p.S);
+      p.ws_bytes = with_counters(llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), p.S));
     }
     return p;
   }
@@ -470,28 +536,48 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
     p.chunk = std::max<int64_t>(256, (((int64_t)1 << 31) - 1) / (p.ld * 2) / 256 * 256 - 256);
   const int64_t rows = std::min(p.chunk, M);
   if (p.pad) p.pad_bytes = ((size_t)rows * p.ld * 2 + 255) / 256 * 256;
-  const TilePlan tp = tile_plan(nmat, rows, KB, NB, have_db ? se.grain_size : 0);
+  // The two-piece tail runs over one row chunk only (its counters and slots
+  // are per launch).
+  const TilePlan tp = tile_plan(nmat, rows, KB, NB, have_db ? se.grain_size : 0,
+                                two_piece && !accumulate && rows == M);
   p.S = tp.S;
   p.head_nb = accumulate ? 0 : tp.head_nb;
   if (accumulate && tp.head_nb > 0) p.S = best_split(nmat, rows, KB, NB, 0).S;
-  p.ws_bytes = p.pad_bytes + llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)rows,
-                                                  (int)(NB - p.head_nb), p.S, accumulate);
+  p.kb_cut = tp.kb_cut;
+  if (p.kb_cut > 0)
+    p.fix_bytes = llk_tile_fix_bytes((int)((rows + 255) / 256 * (NB - p.head_nb)));
+  auto body = [&](int64_t crows) {
+    return p.pad_bytes + (p.kb_cut > 0 ? p.fix_bytes
+                                       : llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)crows,
+                                                              (int)(NB - p.head_nb), p.S,
+                                                              accumulate));
+  };
+  p.ws_bytes = with_counters(body(rows));
   if (p.ws_bytes <= max_ws) return p;
-  // Over the caller's limit: a padded X in row chunks that fit (whole
-  // 256-row tiles; fewer than 256 rows do not fit: ws_bytes stays above
-  // max_ws and the call is rejected), then the most k splits whose partial
-  // planes fit beside it.
-  if (p.pad && p.pad_bytes > max_ws) {
-    const int64_t fit = (int64_t)(max_ws / ((size_t)p.ld * 2)) / 256 * 256;
-    if (fit < 256) return p;
+  // Over the caller's limit: no two-piece tail, a padded X in row chunks
+  // that fit (whole 256-row tiles; fewer than 256 rows do not fit: ws_bytes
+  // stays above max_ws and the call is rejected), then the most k splits
+  // whose partial planes fit beside it.
+  if (p.kb_cut > 0) {
+    p.kb_cut = 0;
+    p.fix_bytes = 0;
+    p.head_nb = 0;
+    p.S = best_split(nmat, rows, KB, NB, 0).S;
+  }
+  const size_t room = max_ws > kCounterBytes ? max_ws - kCounterBytes : 0;
+  if (p.pad && p.pad_bytes > room) {
+    const int64_t fit = (int64_t)(room / ((size_t)p.ld * 2)) / 256 * 256;
+    if (fit < 256) {
+      p.ws_bytes = with_counters(body(rows));
+      return p;
+    }
     p.chunk = std::min(p.chunk, fit);
     p.pad_bytes = ((size_t)std::min(p.chunk, M) * p.ld * 2 + 255) / 256 * 256;
   }
   const int64_t crows = std::min(p.chunk, M);
   for (; p.S >= 1; --p.S) {
     if (p.S == 1) p.head_nb = 0;
-    p.ws_bytes = p.pad_bytes + llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)crows,
-                                                    (int)(NB - p.head_nb), p.S, accumulate);
+    p.ws_bytes = with_counters(body(crows));
     if (p.ws_bytes <= max_ws || p.S == 1) break;
   }
   return p;
@@ -508,14 +594,18 @@ int empty_reduction(llk_tensor2d* y, int out_dtype, llk_kernel_context* ctx, con
   return e == hipSuccess ? LLK_OK : fail_hip(e, what);
 }
 
+// counters_clean: the workspace is the library's or the no-allocation
+// array, whose counter area is zero between launches (else it is cleared
+// before a two-piece launch).
 int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w0,
                     const llk_packed_weights* w1, llk_tensor2d* y, int out_dtype,
                     llk_kernel_context* ctx, int dev, const char* what,
                     const llk::ModuleFns* mod, size_t max_ws = SIZE_MAX,
-                    bool accumulate = false) {
+                    bool accumulate = false, bool counters_clean = false) {
   const int64_t M = x->dim0, K = x->dim1, N = w0->N;
   const int nmat = mode == 1 ? 2 : 1;
-  const Plan p = plan_launch(nmat, M, K, w0->KB, w0->NB, x, max_ws, accumulate);
+  const bool yvec = y_vec_ok(y, out_dtype);
+  const Plan p = plan_launch(nmat, M, K, w0->KB, w0->NB, x, max_ws, accumulate, yvec);
   if (p.too_large)
     return fail(LLK_ERR_SHAPE, "%s: K=%lld too large for M=%lld (the tile kernel needs K <= %lld)",
                 what, (long long)K, (long long)M, (long long)(((int64_t)1 << 31) / 512 - 64));
@@ -526,13 +616,15 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
   void* ws = nullptr;
   int rc = get_workspace(dev, p.ws_bytes, ctx, &ws);
   if (rc) return rc;
+  if (!(ctx && ctx->scratch)) counters_clean = true;  // the library's workspace
+  // [counters: kCounterBytes][padded X][partial planes or two-piece slots]
+  uint8_t* const body = ws ? static_cast<uint8_t*>(ws) + kCounterBytes : nullptr;
   hipStream_t s = stream_of(ctx);
-  const bool yvec = y_vec_ok(y, out_dtype);
   hipError_t e = hipSuccess;
   if (p.skinny) {
     e = llk_launch_skinny(mode, static_cast<const uint16_t*>(x->data), x->stride0, w0->dev,
                           w1 ? w1->dev : nullptr, y->data, y->stride0, (int)M, (int)N, (int)K,
-                          (int)w0->KB, (int)w0->NB, p.S, p.G, ws, out_dtype, x_vec_ok(x), yvec,
+                          (int)w0->KB, (int)w0->NB, p.S, p.G, body, out_dtype, x_vec_ok(x), yvec,
                           accumulate, mod, s);
     if (e != hipSuccess) return fail_hip(e, what);
     return LLK_OK;
@@ -542,16 +634,16 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
     const int rows = (int)std::min(p.chunk, M - m0);
     const uint16_t* xp = static_cast<const uint16_t*>(x->data) + m0 * x->stride0;
     if (p.pad) {
-      e = llk_launch_pad_rows(xp, x->stride0, rows, (int)K, static_cast<uint16_t*>(ws), p.ld, mod,
-                              s);
+      e = llk_launch_pad_rows(xp, x->stride0, rows, (int)K, reinterpret_cast<uint16_t*>(body),
+                              p.ld, mod, s);
       if (e != hipSuccess) break;
-      xp = static_cast<const uint16_t*>(ws);
+      xp = reinterpret_cast<const uint16_t*>(body);
     }
     uint8_t* yp = static_cast<uint8_t*>(y->data) + m0 * y->stride0 * ysz;
     if (p.head_nb > 0) {
       e = llk_launch_tile(mode, xp, p.ld, w0->dev, w1 ? w1->dev : nullptr, yp, y->stride0, rows,
                           (int)(p.head_nb * 128), (int)w0->KB, (int)p.head_nb, 1, nullptr,
-                          out_dtype, yvec, accumulate, mod, s);
+                          out_dtype, yvec, accumulate, 0, nullptr, mod, s);
       if (e != hipSuccess) break;
     }
     // Columns from n-block head_nb on: the packed payload of a matrix is
@@ -559,12 +651,18 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
     // head_nb * KB blocks in.
     const size_t w_off = (size_t)p.head_nb * w0->KB * 16384;
     const int64_t n0 = p.head_nb * 128;
+    unsigned* const cnt = p.kb_cut > 0 ? static_cast<unsigned*>(ws) : nullptr;
+    if (cnt && !counters_clean) {
+      const int64_t tiles = (rows + 255) / 256 * (w0->NB - p.head_nb);
+      e = llk_launch_zero(cnt, (size_t)tiles * sizeof(unsigned), mod, s);
+      if (e != hipSuccess) break;
+    }
     e = llk_launch_tile(mode, xp, p.ld, static_cast<const uint8_t*>(w0->dev) + w_off,
                         w1 ? static_cast<const uint8_t*>(w1->dev) + w_off : nullptr,
                         yp + n0 * ysz, y->stride0, rows, (int)(N - n0), (int)w0->KB,
                         (int)(w0->NB - p.head_nb), p.S,
-                        p.S > 1 || accumulate ? static_cast<uint8_t*>(ws) + p.pad_bytes : nullptr,
-                        out_dtype, yvec, accumulate, mod, s);
+                        p.S > 1 || accumulate || cnt ? body + p.pad_bytes : nullptr, out_dtype,
+                        yvec, accumulate, (int)p.kb_cut, cnt, mod, s);
   }
   if (e != hipSuccess) return fail_hip(e, what);
   return LLK_OK;
@@ -1001,12 +1099,15 @@ int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, int x_al
   const int64_t rows = std::min(p.chunk, M);
   const int64_t chunks = (M + p.chunk - 1) / p.chunk;
   const int64_t nb_per_tile = nmat == 2 ? 1 : 2, tail_nb = NB - p.head_nb;
+  const int64_t pieces = p.kb_cut > 0 ? 2 : p.S;
   out->workgroups = (rows + 255) / 256 *
-                    (p.head_nb / nb_per_tile + (tail_nb + nb_per_tile - 1) / nb_per_tile * p.S);
+                    (p.head_nb / nb_per_tile + (tail_nb + nb_per_tile - 1) / nb_per_tile * pieces);
   out->threads_per_workgroup = 256;
   out->launches =
       chunks * (1 + (p.head_nb > 0 ? 1 : 0) + (p.pad ? 1 : 0) + (p.S > 1 ? 1 : 0));
   out->head_blocks_n = p.head_nb;
+  out->two_piece_kb = p.kb_cut;
+  if (p.kb_cut > 0) out->splits = 2;
   return LLK_OK;
 }
 
@@ -1065,7 +1166,7 @@ int swiglu_entry(const llk_tensor2d* x, const llk_packed_weights* wg,
   llk_kernel_context fixed{nullptr, kNoAllocScratchBytes, ctx ? ctx->stream : nullptr};
   if ((rc = noalloc_scratch(dev, &fixed.scratch))) return rc;
   return run_contraction(1, x, wg, wu, y, y_dtype, &fixed, dev, "swiglu (no allocation)", mod,
-                         kNoAllocScratchBytes);
+                         kNoAllocScratchBytes, false, true);
 }
 
 // llk_gemm_bf16 (accumulate: llk_gemm_bf16_accumulate, C += A B).

@@ -23,6 +23,11 @@ struct Knob {
 // tile_min_kb:       fewest 64-k steps per tile-kernel split.
 // tile_tail_split:   1 = the tile kernel may run the columns of its last,
 //                    partial wave as a separate k-split launch; 0 = never.
+// tile_two_piece:    1 = SwiGLU's partial last wave may run as two pieces
+//                    per tile finished in the kernel; 0 = never (the
+//                    default: on MI355X the slots' fp32 traffic and the
+//                    finishing piece's read-back cost more than the short
+//                    last wave they replace -- config 3 287 vs 259 us).
 Knob g_knobs[] = {
     {"decode_max_m", {64}},
     {"decode_splits", {0}},
@@ -33,6 +38,7 @@ Knob g_knobs[] = {
     {"tile_wgs_per_wave", {256}},
     {"tile_min_kb", {4}},
     {"tile_tail_split", {1}},
+    {"tile_two_piece", {0}},
 };
 
 }  // namespace

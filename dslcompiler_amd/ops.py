@@ -305,7 +305,8 @@ def describe_launch(op: str, M: int, N: int, K: int, x_aligned: bool = True) -> 
     return {"kernel": ("small_m", "tile")[p.kernel], "splits": p.splits,
             "group_width": p.group_width, "pad_x": bool(p.pad_x), "workgroups": p.workgroups,
             "threads_per_workgroup": p.threads_per_workgroup, "launches": p.launches,
-            "workspace_bytes": p.workspace_bytes, "head_blocks_n": p.head_blocks_n}
+            "workspace_bytes": p.workspace_bytes, "head_blocks_n": p.head_blocks_n,
+            "two_piece_kb": p.two_piece_kb}
 
 
 def classify_m(M: int) -> int:

@@ -209,10 +209,15 @@ typedef struct llk_launch_plan {
   int64_t workgroups;            /* of the main kernel, per row chunk (all its launches) */
   int64_t threads_per_workgroup; /* of the main kernel */
   int64_t launches;              /* kernel launches per call */
-  size_t workspace_bytes;        /* = ctx->scratch size the call needs */
+  size_t workspace_bytes;        /* = ctx->scratch size the call needs (Y rows
+                                    assumed 16-byte aligned) */
   int64_t head_blocks_n;         /* tile kernel: leading 128-column blocks launched
                                     without k split before the rest takes `splits`
                                     (0 = one launch over all columns) */
+  int64_t two_piece_kb;          /* tile kernel, > 0: the columns from head_blocks_n on
+                                    run as two pieces per tile (64-k blocks [0, this)
+                                    and the rest), finished in the kernel by the
+                                    second to arrive (splits = 2, no reduce launch) */
 } llk_launch_plan;
 int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, int x_aligned,
                         llk_launch_plan* out);
@@ -318,8 +323,11 @@ int llk_fill_normal_bf16(uint64_t seed, uint64_t stream, float sigma,
  * "tile_splits" (force the tile kernel's k-split count, 0 = cost model),
  * "tile_wgs_per_wave", "tile_min_kb", "tile_tail_split" (1: the columns
  * of a partial last wave of tiles may run as a separate k-split launch;
- * 0: never; a forced "tile_splits" also turns it off).  Returns LLK_OK or
- * LLK_ERR_INVALID_ARGUMENT for an unknown name. */
+ * 0: never; a forced "tile_splits" also turns it off), "tile_two_piece"
+ * (1: SwiGLU's partial last wave may run as two pieces per tile finished
+ * in the kernel, see llk_launch_plan.two_piece_kb; 0, the default: never,
+ * measured slower on MI355X; also off with a forced "tile_splits").
+ * Returns LLK_OK or LLK_ERR_INVALID_ARGUMENT for an unknown name. */
 int llk_set_tunable(const char* name, int64_t value);
 int llk_get_tunable(const char* name, int64_t* value);
 

@@ -81,7 +81,7 @@ int main(void) {
   CHECK(strstr(llk_last_error(), "M dimension mismatch") != NULL);
   CHECK(llk_classify_m(1) == 0 && llk_classify_m(4097) == 4);
   CHECK(llk_describe_launch(0, 2048, 11008, 4096, 1, &plan) == LLK_OK);
-  CHECK(plan.kernel == 1 && plan.workgroups == 688);
+  CHECK(plan.kernel == 1 && plan.workgroups == 688 && plan.two_piece_kb == 0);
   CHECK(llk_select_schedule("/nonexistent.json", "fused_swiglu", 0, &se, &n) == LLK_ERR_NOT_FOUND);
   CHECK(se.BM == 8 && se.BN == 32 && n == 0); /* built-in default */
 

@@ -49,6 +49,7 @@ def test_entry_matches_library_kernels(llk, gpu, op, M, N, K, out, what):
     assert plan["pad_x"] == ("padded" in what)
     splits = re.search(r"S = (\d+)", what)
     assert plan["splits"] == (int(splits.group(1)) if splits else 1)
+    assert (plan["two_piece_kb"] > 0) == ("two pieces" in what)
     dtype = {"bf16": gpu.bfloat16, "fp32": gpu.float32}[out]
     cache = llk.JitCache()
     fn = _entry(llk, cache, op, N, K, out)

@@ -185,11 +185,10 @@ def test_tile_tail_split_plans():
     off; a forced split count wins."""
     p = llk.describe_launch("matmul", 4097, 5120, 13824)
     assert (p["head_blocks_n"], p["splits"], p["workgroups"], p["launches"]) == (30, 3, 510, 3)
-    assert p["workspace_bytes"] == 3 * 4097 * 10 * 128 * 4
+    assert p["workspace_bytes"] == 64 * 1024 + 3 * 4097 * 10 * 128 * 4  # counters + planes
     p = llk.describe_launch("fused_swiglu", 4097, 13824, 5120)
     assert (p["head_blocks_n"], p["splits"], p["workgroups"], p["launches"]) == (105, 5, 2040, 3)
-    for op, M, N, K in [("fused_swiglu", 2048, 11008, 4096), ("matmul", 4096, 4096, 4096),
-                        ("fused_swiglu", 1000, 13824, 5120), ("matmul", 1000, 5120, 13824),
+    for op, M, N, K in [("matmul", 4096, 4096, 4096), ("matmul", 1000, 5120, 13824),
                         ("matmul", 255, 5120, 13824)]:
         assert llk.describe_launch(op, M, N, K)["head_blocks_n"] == 0, (op, M)
     for name, value in [("tile_tail_split", 0), ("tile_splits", 2)]:
@@ -200,6 +199,36 @@ def test_tile_tail_split_plans():
             assert p["head_blocks_n"] == 0 and p["workgroups"] == 340 * p["splits"]
         finally:
             llk.set_tunable(name, old)
+
+
+def test_two_piece_plans():
+    """SwiGLU's partial last wave as two pieces per tile (T tail tiles on T
+    CUs for the long pieces, r = ceil(T / (256 - T)) short ones on each
+    other CU): config 3 (176 tail tiles, r = 3: cut 49 of 64), config 5 at
+    M = 1000 (176, cut 61 of 80) and M = 255 (all 108 tiles, r = 1: an even
+    cut, one launch, no reduce).  Never for the GEMM, a forced split count,
+    the knob at 0 (its default: measured slower on MI355X), or a workspace
+    limit the slots do not fit (the no-allocation entry point's 64 MiB)."""
+    assert llk.get_tunable("tile_two_piece") == 0
+    assert llk.describe_launch("fused_swiglu", 2048, 11008, 4096)["two_piece_kb"] == 0
+    llk.set_tunable("tile_two_piece", 1)
+    try:
+        for M, N, K, head, cut, wgs, launches in [(2048, 11008, 4096, 64, 49, 864, 2),
+                                                  (1000, 13824, 5120, 64, 61, 608, 2),
+                                                  (255, 13824, 5120, 0, 40, 216, 1)]:
+            p = llk.describe_launch("fused_swiglu", M, N, K)
+            assert (p["head_blocks_n"], p["two_piece_kb"], p["workgroups"], p["launches"],
+                    p["splits"]) == (head, cut, wgs, launches, 2), M
+        assert all(llk.describe_launch("matmul", M, 5120, 13824)["two_piece_kb"] == 0
+                   for M in (255, 1000, 2048))
+        llk.set_tunable("tile_splits", 1)
+        try:
+            p = llk.describe_launch("fused_swiglu", 2048, 11008, 4096)
+            assert (p["two_piece_kb"], p["workgroups"], p["splits"]) == (0, 688, 1)
+        finally:
+            llk.set_tunable("tile_splits", 0)
+    finally:
+        llk.set_tunable("tile_two_piece", 0)
 
 
 def test_small_m_cost_model_choices():
