@@ -100,15 +100,19 @@ struct TileArgs {
   // partial planes (S >= 1), which keeps the tile kernel's epilogue, and its
   // registers, those of C = A B.
   int accumulate;
-  // Two-piece k split finished in the kernel (FIX, SwiGLU): workgroup b <
-  // tiles runs the 64-k blocks [0, kb_cut) of a tile, b >= tiles the blocks
-  // [kb_cut, KB) of one; each writes its raw fp32 accumulators to its slot
-  // part + (2 tile + piece) * 64 Ki floats (planes [gate, up][256 rows][128
-  // columns] of the tile) and counts itself in cnt[tile]; the second to
-  // arrive resets cnt[tile] to 0 and writes the tile's outputs from
-  // 0 + slot 0 + slot 1.  cnt must be zero at launch.
+  // Two-piece k split finished in the kernel (FIX, SwiGLU).  The grid holds
+  // first the H = tiles_m * head_tn whole tiles of the leading head_tn
+  // n-tile columns, then the T tiles of the other columns twice: workgroup
+  // H + b runs the 64-k blocks [0, kb_cut) of tail tile b, H + T + b the
+  // blocks [kb_cut, KB) of tail tile b.  The first piece of a tail tile to
+  // finish writes its raw fp32 accumulators to the tile's slot, part + b *
+  // 64 Ki floats, in register order; the second adds them to its own and
+  // runs the epilogue (see the kernel).  One grid, so the pieces start as
+  // soon as CUs free up from the whole tiles.  cnt: two counters per tail
+  // tile, zero at launch and again after it.
   unsigned* cnt;
   int kb_cut;
+  int head_tn;
 };
 
 constexpr int kThreads = 256;
@@ -122,7 +126,7 @@ constexpr int kXRingOff = kWStages * kWStageBytes;
 constexpr int kLdsBytes = kXRingOff + kXBlocks * kXBlockBytes;  // 160 KiB
 // Per wave: 4 buffer_load ... lds per weight stage, 8 per X block.
 constexpr int kStripRow = 144;        // epilogue staging: 128-byte rows + 16-byte pad
-constexpr int kFixMaxTiles = 16384;   // two-piece k split: counters (4 bytes each) per launch
+constexpr int kFixMaxTiles = 8192;    // two-piece k split: two counters (8 bytes) per tail tile
 
 // s_waitcnt with vmcnt(n) (n < 64) and the other counters left alone.
 template <int N>
@@ -206,13 +210,27 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   // Workgroup -> (split s, tile): tiles of one split are contiguous, so
   // after the XCD remap the tiles that share X's k slice (and, m fastest,
   // the tiles that share W columns) run on one XCD.
-  // FIX: the long pieces first, in launch order, so that they all start in
-  // the first wave; the remap keeps each piece class within itself.
+  // FIX: whole tiles first, then the long pieces, then the short ones, in
+  // launch order, so that the long pieces start on the first CUs to free up;
+  // the remap keeps each class within itself.
   const int tiles = a.tiles_m * a.tiles_n;
-  int split, tile;
+  // FIX: split -1 for a whole tile, else the piece; tile is then the index
+  // among the tail tiles, and the tile grid of either part starts at
+  // n-tile column n_base and is ntn columns wide.
+  int split, tile, n_base = 0, ntn = a.tiles_n;
   if constexpr (FIX) {
-    split = (int)blockIdx.x >= tiles ? 1 : 0;
-    tile = xcd_remap((int)blockIdx.x - split * tiles, tiles);
+    const int H = a.tiles_m * a.head_tn;
+    if ((int)blockIdx.x < H) {
+      split = -1;
+      tile = xcd_remap(blockIdx.x, H);
+      ntn = a.head_tn;
+    } else {
+      const int b = (int)blockIdx.x - H, T = tiles - H;
+      split = b >= T ? 1 : 0;
+      tile = xcd_remap(b - split * T, T);
+      n_base = a.head_tn;
+      ntn = a.tiles_n - a.head_tn;
+    }
   } else {
     const int idx = xcd_remap(blockIdx.x, tiles * (SPLIT ? a.S : 1));
     split = SPLIT ? idx / tiles : 0;
@@ -220,18 +238,19 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   }
   int tm, tn;
   if (a.group_m > 0 && a.tiles_m > a.group_m) {
-    const int span = a.group_m * a.tiles_n;  // tiles of one full group
+    const int span = a.group_m * ntn;  // tiles of one full group
     const int g = tile / span, r = tile - g * span;
     const int gm = min(a.group_m, a.tiles_m - g * a.group_m);  // last group may be short
     tm = g * a.group_m + r % gm;
-    tn = r / gm;
+    tn = n_base + r / gm;
   } else {
     tm = tile % a.tiles_m;
-    tn = tile / a.tiles_m;
+    tn = n_base + tile / a.tiles_m;
   }
   const int m0 = tm * kTileM;
-  const int kb0 = FIX ? (split ? a.kb_cut : 0) : SPLIT ? split * a.kbs : 0;
-  const int nkb = FIX ? (split ? a.KB - a.kb_cut : a.kb_cut) : SPLIT ? min(a.KB - kb0, a.kbs) : a.KB;
+  const int kb0 = FIX ? (split > 0 ? a.kb_cut : 0) : SPLIT ? split * a.kbs : 0;
+  const int nkb = FIX ? (split < 0 ? a.KB : split ? a.KB - a.kb_cut : a.kb_cut)
+                      : SPLIT ? min(a.KB - kb0, a.kbs) : a.KB;
 
   // ---- operand streams ----------------------------------------------------
   // Stage t holds k range [32 t, 32 t + 32); X block u = k [64 u, 64 u + 64)
@@ -458,110 +477,94 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   mfma_drain();
   acc_fence(acc);   // the epilogue reads the accumulators only after the drain
 
-  // ---- FIX: publish this piece, and finish the tile if it is the second.
-  // Each piece writes its raw accumulators to its slot as tile-local fp32
-  // planes [mat][256 rows][128 columns] (SwiGLU: gate, up), staged through
-  // the LDS strips like the k-split planes (whole 128-byte row segments per
-  // store; the accumulators only ever go to registers and LDS, so the K
-  // loop's register allocation is that of the other forms).  Slots are
-  // written and read with agent-scope coherent accesses (sc1: through every
-  // XCD's L2), and each thread's writes have completed (vmcnt 0) before the
-  // workgroup barrier that precedes the count, so the second piece, which
-  // reads only after seeing the first's count, reads the first's data.  It
-  // then finishes the tile from the two slots, adding piece 0 then piece 1
-  // to zero as split_reduce_kernel does (the same bits whichever piece
-  // arrives second).
+  // ---- FIX: the first piece of a tail tile to finish publishes its raw
+  // accumulators; the second waits for them and finishes the tile.  Each
+  // tail tile has two counters: cnt[2 tile] hands out tickets (0:
+  // publisher, 1: finisher), cnt[2 tile + 1] says the publisher's slot is
+  // complete.  The slot holds the publisher's accumulators in register order
+  // -- quad (i, j) of thread t at byte ((8 i + j) * 256 + t) * 16, so every
+  // store moves 1 KiB of consecutive bytes straight from the accumulators --
+  // and both pieces map threads to outputs alike, so the finisher reads the
+  // quads of its own positions at the same offsets.  The publisher stores
+  // with agent-scope coherent stores (sc1), waits for them (vmcnt 0) and a
+  // workgroup barrier, then counts the slot ready after an agent-scope
+  // release (L2 written back); the finisher polls that count with
+  // agent-scope acquire loads, resets both counters to 0 for the next
+  // launch, and adds the slot to its accumulators with coherent loads
+  // before the epilogue (fp32 addition commutes: the sum does not depend on
+  // which piece finishes).  The finisher only ever waits for a workgroup
+  // that already holds ticket 0, so is running, and has its stores and one
+  // atomic left; the poll is bounded all the same (about a second), past
+  // which it goes on.
   if constexpr (FIX) {
-    constexpr int kSlotBytes = kThreads * 64 * 16;
-    constexpr int kSc1 = 16;  // cache policy bits: sc1
-    float* const slots = a.part + (size_t)tile * 2 * (kSlotBytes / 4);
-    const int h4f = 4 * (lane >> 4), mrf = lane & 15;
-    __syncthreads();  // every wave is past its last operand read: the ring is free
-    {
-      uint8_t* const strip = smem + wave * (128 * kStripRow);
-      const __amdgpu_buffer_rsrc_t mine = __builtin_amdgcn_make_buffer_rsrc(
-          slots + (size_t)split * (kSlotBytes / 4), 0, kSlotBytes, kBufferWord3);
+    if (split >= 0) {
+      constexpr int kSlotBytes = kThreads * 64 * 16;
+      constexpr int kSc1 = 16;  // cache policy bits: sc1
+      const __amdgpu_buffer_rsrc_t slot = __builtin_amdgcn_make_buffer_rsrc(
+          a.part + (size_t)tile * (kSlotBytes / 4), 0, kSlotBytes, kBufferWord3);
+      const int t16 = (int)threadIdx.x * 16;
+      uint32_t* const flag = reinterpret_cast<uint32_t*>(smem);
+      __syncthreads();  // every wave is past its last operand read: the ring is free
+      if (threadIdx.x == 0)
+        *reinterpret_cast<volatile uint32_t*>(flag) =
+            __hip_atomic_fetch_add(a.cnt + 2 * tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      if (*reinterpret_cast<volatile uint32_t*>(flag) == 0u) {  // publisher
 #pragma unroll
-      for (int sp = 0; sp < 4; ++sp) {
-        // strip sp: accumulator rows i = 2 sp, 2 sp + 1 -> matrix sp / 2,
-        // tile-local columns wn * 64 + (sp % 2) * 32 .. + 32
-#pragma unroll
-        for (int ii = 0; ii < 2; ++ii)
+        for (int i = 0; i < 8; ++i)
 #pragma unroll
           for (int j = 0; j < 8; ++j)
-            *reinterpret_cast<f32x4*>(strip + (j * 16 + mrf) * kStripRow + (ii * 16 + h4f) * 4) =
-                acc[2 * sp + ii][j];
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        __builtin_amdgcn_wave_barrier();
-        asm volatile("" ::: "memory");
-        const int col0 = wn * 64 + (sp & 1) * 32;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-          const int row = k * 8 + (lane >> 3);
-          const u32x4 d =
-              *reinterpret_cast<const u32x4*>(strip + row * kStripRow + (lane & 7) * 16);
-          __builtin_amdgcn_raw_buffer_store_b128(
-              d, mine, (((sp >> 1) * 256 + wm * 128 + row) * 128 + col0) * 4 + (lane & 7) * 16, 0,
-              kSc1);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), slot,
+                                                   (i * 8 + j) * kThreads * 16 + t16, 0, kSc1);
+        wait_vmcnt<0>();
+        __syncthreads();
+        if (threadIdx.x == 0) {
+          // Release: the L2 write-back (buffer_wbl2) has completed before the
+          // count.  The wait is explicit: the compiler drops its own vmcnt
+          // wait after the write-back when the counter already reads zero.
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          __hip_atomic_fetch_add(a.cnt + 2 * tile + 1, 1u, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
         }
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        __builtin_amdgcn_wave_barrier();
-        asm volatile("" ::: "memory");
+        return;
+      }
+      if (threadIdx.x == 0) {
+        for (int it = 0; it < (1 << 24); ++it) {
+          if (__hip_atomic_load(a.cnt + 2 * tile + 1, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) !=
+              0u)
+            break;
+          __builtin_amdgcn_s_sleep(2);
+        }
+        __hip_atomic_store(a.cnt + 2 * tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.cnt + 2 * tile + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // The acquire's cache invalidate (buffer_inv) has completed before
+        // the barrier lets the other waves load the slot.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      __syncthreads();
+      // One accumulator row i (eight quads j) at a time, the next row's loads
+      // in flight while one is added; each sum goes back to its AGPRs (the
+      // epilogue then runs as for a whole tile, with its registers).
+      f32x4 pub[2][8];
+      auto load_row = [&](int i, f32x4 (&dst)[8]) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          dst[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 slot, (i * 8 + j) * kThreads * 16 + t16, 0, kSc1));
+      };
+      load_row(0, pub[0]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (i + 1 < 8) load_row(i + 1, pub[(i + 1) & 1]);
+        asm volatile("" ::: "memory");  // the next row's loads stay below this point
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          acc[i][j] += pub[i & 1][j];
+          asm volatile("" : "+a"(acc[i][j]));
+        }
       }
     }
-    wait_vmcnt<0>();
-    __syncthreads();
-    uint32_t* const flag = reinterpret_cast<uint32_t*>(smem);
-    if (threadIdx.x == 0) {
-      const unsigned prev =
-          __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (prev == 1u) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      *reinterpret_cast<volatile uint32_t*>(flag) = prev;
-    }
-    __syncthreads();
-    if (*reinterpret_cast<volatile uint32_t*>(flag) != 1u) return;  // the other piece finishes
-    const __amdgpu_buffer_rsrc_t p0 =
-        __builtin_amdgcn_make_buffer_rsrc(slots, 0, kSlotBytes, kBufferWord3);
-    const __amdgpu_buffer_rsrc_t p1 =
-        __builtin_amdgcn_make_buffer_rsrc(slots + kSlotBytes / 4, 0, kSlotBytes, kBufferWord3);
-    const int n_t = tn * 128;  // the tile's first column (MODE 1: one 128-column block)
-    // Thread t handles quads q = t + 256 s, s = 0..31 (row q / 32, columns
-    // 4 (q % 32) ..): four batches of eight, the next batch's 32 loads in
-    // flight while one is finished (the accumulators are dead here).
-    constexpr int kQ = 8;
-    f32x4 ld[2][kQ][4];
-    auto load_batch = [&](int b, f32x4 (&dst)[kQ][4]) {
-#pragma unroll
-      for (int k = 0; k < kQ; ++k) {
-        const int qd = (int)threadIdx.x + (b * kQ + k) * kThreads;
-        const int r = qd >> 5, c4 = (qd & 31) * 4;
-        const int og = (r * 128 + c4) * 4, ou = ((256 + r) * 128 + c4) * 4;
-        dst[k][0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(p0, og, 0, kSc1));
-        dst[k][1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(p1, og, 0, kSc1));
-        dst[k][2] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(p0, ou, 0, kSc1));
-        dst[k][3] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(p1, ou, 0, kSc1));
-      }
-    };
-    load_batch(0, ld[0]);
-#pragma unroll
-    for (int b = 0; b < 32 / kQ; ++b) {
-      if (b + 1 < 32 / kQ) load_batch(b + 1, ld[(b + 1) & 1]);
-      asm volatile("" ::: "memory");  // the next batch's loads stay below this point
-#pragma unroll
-      for (int k = 0; k < kQ; ++k) {
-        const int qd = (int)threadIdx.x + (b * kQ + k) * kThreads;
-        const int m = m0 + (qd >> 5), n = n_t + (qd & 31) * 4;
-        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-        const f32x4 g = zero + ld[b & 1][k][0] + ld[b & 1][k][1];
-        const f32x4 u = zero + ld[b & 1][k][2] + ld[b & 1][k][3];
-        float v[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = swiglu_act(g[q], u[q]);
-        store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, YVEC);  // bounds-checked (m < M, n < N)
-      }
-      asm volatile("" ::: "memory");
-    }
-    return;
   }
 
   // ---- epilogue: acc[i][j] holds, in lane l, output row m = m0 + wm*128 +
@@ -651,12 +654,14 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         float v[4];
+        const f32x4 g = acc[i][j];
+        const f32x4 u = acc[(MODE == 1) ? i + 4 : i][j];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           if constexpr (MODE == 1)
-            v[q] = swiglu_act(acc[i][j][q], acc[i + 4][j][q]);
+            v[q] = swiglu_act(g[q], u[q]);
           else
-            v[q] = acc[i][j][q];
+            v[q] = g[q];
         }
         uint8_t* const dst = strip + (j * 16 + mr) * kStripRow + (ii * 16 + h4) * kElem;
         if constexpr (OUT == kOutF32) {
@@ -738,7 +743,9 @@ static hipError_t launch_tile_t(const TileArgs& a, const llk::ModuleFns* mod, hi
     hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(fn), kLdsBytes, lds_set);
     if (e != hipSuccess) return e;
   }
-  dim3 grid(a.tiles_m * a.tiles_n * (FIX ? 2 : SPLIT ? a.S : 1)), block(kThreads);
+  const int tiles = a.tiles_m * a.tiles_n;
+  const int wgs = FIX ? 2 * tiles - a.tiles_m * a.head_tn : tiles * (SPLIT ? a.S : 1);
+  dim3 grid(wgs), block(kThreads);
   return launch_kernel(mod, reinterpret_cast<const void*>(fn),
                        &tile_symbol<MODE, OUT, YVEC, SPLIT, FIX>, grid, block, kLdsBytes, s, a);
 }
@@ -786,10 +793,11 @@ bool llk_tile_x_fits(int M, int64_t ldx) {
   return rows * ldx * 2 < ((int64_t)1 << 31);
 }
 
-// Two-piece k split (TileArgs::kb_cut): its largest tile count (the counters
-// it needs: 4 bytes per tile) and the slot bytes of `tiles` tiles.
+// Two-piece k split (TileArgs::kb_cut): its largest tail tile count (the
+// counters it needs: 8 bytes per tail tile) and the slot bytes of `tiles`
+// tail tiles (256 KiB each).
 int llk_tile_fix_max_tiles() { return llk_gfx950::kFixMaxTiles; }
-size_t llk_tile_fix_bytes(int tiles) { return (size_t)tiles * 2 * llk_gfx950::kThreads * 64 * 16; }
+size_t llk_tile_fix_bytes(int tiles) { return (size_t)tiles * llk_gfx950::kThreads * 64 * 16; }
 
 // Bytes of the partial planes of a k split over S workgroups (0 if S <= 1
 // and the launch does not accumulate: an accumulating GEMM launch always
@@ -805,13 +813,15 @@ size_t llk_tile_split_bytes(int mode, int M, int NB, int S, bool accumulate) {
 // non-empty: the caller guarantees (S - 1) * kbs < KB); `part` (16-byte
 // aligned) holds llk_tile_split_bytes(mode, M, NB, S, accumulate) bytes.
 // accumulate (GEMM only): y += x w instead of y = x w.  kb_cut > 0 (SwiGLU,
-// vector Y, S = 1): the two-piece k split finished in the kernel, with
-// `part` (256-byte aligned) holding llk_tile_fix_bytes(tiles) bytes and
-// `cnt` one zeroed counter per tile (tiles <= llk_tile_fix_max_tiles()).
+// vector Y, S = 1): the n-blocks [0, head_nb) run as whole tiles and the
+// others as the two-piece k split finished in the kernel, all in one grid,
+// with `part` (256-byte aligned) holding llk_tile_fix_bytes(tail) bytes and
+// `cnt` two zeroed counters per tail tile (tail = ceil(M / 256) * (NB -
+// head_nb) <= llk_tile_fix_max_tiles()); head_nb is 0 otherwise.
 hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                            const void* w1, void* y, int64_t ldy, int M, int N, int KB, int NB,
                            int S, void* part, int out, bool yvec, bool accumulate, int kb_cut,
-                           unsigned* cnt, const llk::ModuleFns* mod, hipStream_t s) {
+                           int head_nb, unsigned* cnt, const llk::ModuleFns* mod, hipStream_t s) {
   using namespace llk_gfx950;
   TileArgs a;
   a.x = x;
@@ -834,11 +844,13 @@ hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void*
   a.accumulate = accumulate ? 1 : 0;
   a.cnt = cnt;
   a.kb_cut = kb_cut;
+  a.head_tn = head_nb;
   if (a.S > 1 && (part == nullptr || (int64_t)(a.S - 1) * a.kbs >= KB)) return hipErrorInvalidValue;
   if (accumulate && (mode != 0 || part == nullptr)) return hipErrorInvalidValue;
+  if (kb_cut == 0 && head_nb != 0) return hipErrorInvalidValue;
   if (kb_cut != 0 && (mode != 1 || kb_cut < 0 || kb_cut >= KB || part == nullptr ||
-                      cnt == nullptr || accumulate || a.S > 1 ||
-                      (int64_t)a.tiles_m * a.tiles_n > kFixMaxTiles))
+                      cnt == nullptr || accumulate || a.S > 1 || head_nb < 0 || head_nb >= NB ||
+                      (int64_t)a.tiles_m * (a.tiles_n - head_nb) > kFixMaxTiles))
     return hipErrorInvalidValue;
 #if !defined(LLK_CO_OP) || LLK_CO_OP == 1
   if (mode == 1) return launch_mode<1>(a, out, yvec, mod, s);

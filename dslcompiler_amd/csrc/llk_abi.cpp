@@ -31,7 +31,8 @@ struct ModuleFns;  // functions of a loaded code object (code_object.cpp)
 hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                            const void* w1, void* y, int64_t ldy, int M, int N, int KB, int NB,
                            int S, void* part, int out_dtype, bool yvec, bool accumulate,
-                           int kb_cut, unsigned* cnt, const llk::ModuleFns* mod, hipStream_t s);
+                           int kb_cut, int head_nb, unsigned* cnt, const llk::ModuleFns* mod,
+                           hipStream_t s);
 int llk_tile_fix_max_tiles();
 size_t llk_tile_fix_bytes(int tiles);
 size_t llk_tile_split_bytes(int mode, int M, int NB, int S, bool accumulate);
@@ -282,8 +283,8 @@ struct Plan {
   size_t fix_bytes = 0;  // tile path: the two-piece slots (after the padded X)
 };
 
-// Every workspace begins with this many bytes of per-tile arrival counters
-// for the two-piece k split, which no other use of the workspace touches:
+// Every workspace begins with this many bytes of per-tile counters (two per
+// tile) for the two-piece k split, which no other use of the workspace touches:
 // the library's workspaces (zeroed when allocated) and the no-allocation
 // entry point's array (zero when loaded) keep them at zero between launches
 // (the second piece of each tile resets its counter); a caller's scratch is
@@ -341,12 +342,13 @@ SplitCost best_split(int nmat, int64_t rows, int64_t KB, int64_t NB, int64_t for
 //   max(kb_cut + 3, r * (KB - kb_cut + 2) + 1)
 // steps (fill and epilogue 2, publishing and adding the other piece 1)
 // instead of KB + 2: config 3 (176 tail tiles of 688, r = 3) cuts at 49 of
-// 64 blocks.  Used, when the knob tile_two_piece is 1, where the model puts
-// it 3% or more below the other plans.  The knob is 0 by default: measured
-// on MI355X each piece's epilogue (256 KiB of fp32 slot written, and the
-// second piece's 512 KiB read back) costs several times the model's step,
-// so the two-piece tail is slower (config 3: 287 vs 259 us, config 5's
-// SwiGLU at M = 1000: 238 vs 218 us, at M = 255: 87.5 vs 85.5 us).
+// 64 blocks.  The head's whole tiles run in the same grid, before the
+// pieces.  Used, when the knob tile_two_piece is 1, where the model puts it
+// 3% or more below the other plans.  The knob is 0 by default: measured on
+// MI355X a short piece's fill and 256 KiB publish, and the finisher's 256
+// KiB read-back, cost several times the model's step, so the two-piece tail
+// is slower (config 3: 280 vs 258-261 us; config 5's MLP at M = 1000: 351
+// vs 340-349 us, at M = 255: 158 vs 147 us).
 struct TilePlan {
   int S;
   int64_t head_nb;
@@ -640,10 +642,24 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
       xp = reinterpret_cast<const uint16_t*>(body);
     }
     uint8_t* yp = static_cast<uint8_t*>(y->data) + m0 * y->stride0 * ysz;
+    if (p.kb_cut > 0) {
+      // Two-piece tail: the head's whole tiles and the tail's pieces in one
+      // grid (the counters of the tail tiles lead the workspace).
+      unsigned* const cnt = static_cast<unsigned*>(ws);
+      if (!counters_clean) {
+        const int64_t tiles = (rows + 255) / 256 * (w0->NB - p.head_nb);
+        e = llk_launch_zero(cnt, (size_t)tiles * 2 * sizeof(unsigned), mod, s);
+        if (e != hipSuccess) break;
+      }
+      e = llk_launch_tile(mode, xp, p.ld, w0->dev, w1 ? w1->dev : nullptr, yp, y->stride0, rows,
+                          (int)N, (int)w0->KB, (int)w0->NB, 1, body + p.pad_bytes, out_dtype, yvec,
+                          false, (int)p.kb_cut, (int)p.head_nb, cnt, mod, s);
+      continue;
+    }
     if (p.head_nb > 0) {
       e = llk_launch_tile(mode, xp, p.ld, w0->dev, w1 ? w1->dev : nullptr, yp, y->stride0, rows,
                           (int)(p.head_nb * 128), (int)w0->KB, (int)p.head_nb, 1, nullptr,
-                          out_dtype, yvec, accumulate, 0, nullptr, mod, s);
+                          out_dtype, yvec, accumulate, 0, 0, nullptr, mod, s);
       if (e != hipSuccess) break;
     }
     // Columns from n-block head_nb on: the packed payload of a matrix is
@@ -651,18 +667,12 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
     // head_nb * KB blocks in.
     const size_t w_off = (size_t)p.head_nb * w0->KB * 16384;
     const int64_t n0 = p.head_nb * 128;
-    unsigned* const cnt = p.kb_cut > 0 ? static_cast<unsigned*>(ws) : nullptr;
-    if (cnt && !counters_clean) {
-      const int64_t tiles = (rows + 255) / 256 * (w0->NB - p.head_nb);
-      e = llk_launch_zero(cnt, (size_t)tiles * sizeof(unsigned), mod, s);
-      if (e != hipSuccess) break;
-    }
     e = llk_launch_tile(mode, xp, p.ld, static_cast<const uint8_t*>(w0->dev) + w_off,
                         w1 ? static_cast<const uint8_t*>(w1->dev) + w_off : nullptr,
                         yp + n0 * ysz, y->stride0, rows, (int)(N - n0), (int)w0->KB,
                         (int)(w0->NB - p.head_nb), p.S,
-                        p.S > 1 || accumulate || cnt ? body + p.pad_bytes : nullptr, out_dtype,
-                        yvec, accumulate, (int)p.kb_cut, cnt, mod, s);
+                        p.S > 1 || accumulate ? body + p.pad_bytes : nullptr, out_dtype, yvec,
+                        accumulate, 0, 0, nullptr, mod, s);
   }
   if (e != hipSuccess) return fail_hip(e, what);
   return LLK_OK;
@@ -1103,8 +1113,9 @@ int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, int x_al
   out->workgroups = (rows + 255) / 256 *
                     (p.head_nb / nb_per_tile + (tail_nb + nb_per_tile - 1) / nb_per_tile * pieces);
   out->threads_per_workgroup = 256;
-  out->launches =
-      chunks * (1 + (p.head_nb > 0 ? 1 : 0) + (p.pad ? 1 : 0) + (p.S > 1 ? 1 : 0));
+  // (the two-piece form runs its head in the same grid as its pieces)
+  out->launches = chunks * (1 + (p.head_nb > 0 && p.kb_cut == 0 ? 1 : 0) + (p.pad ? 1 : 0) +
+                            (p.S > 1 ? 1 : 0));
   out->head_blocks_n = p.head_nb;
   out->two_piece_kb = p.kb_cut;
   if (p.kb_cut > 0) out->splits = 2;

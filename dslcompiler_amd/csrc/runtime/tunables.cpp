@@ -25,9 +25,10 @@ struct Knob {
 //                    partial wave as a separate k-split launch; 0 = never.
 // tile_two_piece:    1 = SwiGLU's partial last wave may run as two pieces
 //                    per tile finished in the kernel; 0 = never (the
-//                    default: on MI355X the slots' fp32 traffic and the
-//                    finishing piece's read-back cost more than the short
-//                    last wave they replace -- config 3 287 vs 259 us).
+//                    default: on MI355X each short piece's fill and 256 KiB
+//                    publish, and the finisher's read-back, cost more than
+//                    the short last wave they replace -- config 3 280 vs
+//                    258-261 us).
 Knob g_knobs[] = {
     {"decode_max_m", {64}},
     {"decode_splits", {0}},

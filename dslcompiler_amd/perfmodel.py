@@ -87,7 +87,7 @@ def _two_piece_launch(cal: dict, cus: int, M: int, N: int, K: int, tiles: int,
     r = math.ceil(tiles / max(1, cus - tiles))
     cl, pl = piece(kb_cut * 64)
     cs, ps = piece((KB - kb_cut) * 64)
-    slots = tiles * 2 * 256 * 1024 * 2.0
+    slots = tiles * 256 * 1024 * 2.0  # one 256 KiB slot per tile, written and read back
     nbytes = 4.0 * K * N + 2.0 * M * K + 2.0 * M * N + slots
     return max(cl, r * cs), nbytes / cal["stream_bytes_per_s"], max(pl, r * ps) + \
         slots / cal["stream_bytes_per_s"], 0.0

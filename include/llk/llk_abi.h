@@ -217,7 +217,8 @@ typedef struct llk_launch_plan {
   int64_t two_piece_kb;          /* tile kernel, > 0: the columns from head_blocks_n on
                                     run as two pieces per tile (64-k blocks [0, this)
                                     and the rest), finished in the kernel by the
-                                    second to arrive (splits = 2, no reduce launch) */
+                                    second to arrive (splits = 2, no reduce launch;
+                                    the head's whole tiles in the same launch) */
 } llk_launch_plan;
 int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, int x_aligned,
                         llk_launch_plan* out);

@@ -206,15 +206,16 @@ def test_two_piece_plans():
     CUs for the long pieces, r = ceil(T / (256 - T)) short ones on each
     other CU): config 3 (176 tail tiles, r = 3: cut 49 of 64), config 5 at
     M = 1000 (176, cut 61 of 80) and M = 255 (all 108 tiles, r = 1: an even
-    cut, one launch, no reduce).  Never for the GEMM, a forced split count,
+    cut); one launch each (the whole tiles of the head in the same grid as
+    the pieces), no reduce.  Never for the GEMM, a forced split count,
     the knob at 0 (its default: measured slower on MI355X), or a workspace
     limit the slots do not fit (the no-allocation entry point's 64 MiB)."""
     assert llk.get_tunable("tile_two_piece") == 0
     assert llk.describe_launch("fused_swiglu", 2048, 11008, 4096)["two_piece_kb"] == 0
     llk.set_tunable("tile_two_piece", 1)
     try:
-        for M, N, K, head, cut, wgs, launches in [(2048, 11008, 4096, 64, 49, 864, 2),
-                                                  (1000, 13824, 5120, 64, 61, 608, 2),
+        for M, N, K, head, cut, wgs, launches in [(2048, 11008, 4096, 64, 49, 864, 1),
+                                                  (1000, 13824, 5120, 64, 61, 608, 1),
                                                   (255, 13824, 5120, 0, 40, 216, 1)]:
             p = llk.describe_launch("fused_swiglu", M, N, K)
             assert (p["head_blocks_n"], p["two_piece_kb"], p["workgroups"], p["launches"],
