@@ -162,6 +162,21 @@ __device__ __forceinline__ void dma16(const u32x4& rsrc, int voff, int soff, uin
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :: "s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
 }
+// The same load in two statements, for the K loop: set_m0 writes the LDS
+// address and dma16_m0 issues the load that reads it.  The caller puts at
+// least one instruction (an MFMA) between them -- the wait state M0 needs
+// before an LDS-DMA load -- so that no s_nop is needed and the four
+// instructions of a refill (offset add, M0 write, load) never queue up
+// between two MFMAs: a wave issues at most one instruction per 4 cycles, so
+// only three others fit in the 16 cycles of one MFMA.  Nothing else in these
+// kernels writes M0 between the two (checked by tests/test_isa_cpu.py).
+__device__ __forceinline__ void set_m0(uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0" :: "s"(lds) : "m0");
+}
+__device__ __forceinline__ void dma16_m0(const u32x4& rsrc, int voff, int soff) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" :: "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory");
+}
 #pragma clang diagnostic pop
 
 // LDS byte address of a pointer into the kernel's dynamic shared memory.
@@ -316,17 +331,18 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   int x_off[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) x_off[i] = x_voff[i & 1] + i * x_rowstep;
-  // Refill load i (0..3) of weight stage s into ring slot wb: the stage
-  // offset in the VGPR operand, so the range check covers it.
-  auto dma_rw = [&](int s, int wb, int i) {
-    const uint8_t* st = smem + wb * kWStageBytes + (wave * 4) * kSubBytes;
-    dma16(wrsrc, w_voff + s * 8 * kSubBytes, i * kSubBytes, lds_addr(st + i * kSubBytes));
+  // Refill load i (0..3) of weight stage s into ring slot wb, as its M0
+  // write (rw_m0) and its load (rw_ld): the stage offset in the VGPR operand,
+  // so the range check covers it.
+  auto rw_m0 = [&](int wb, int i) {
+    set_m0(lds_addr(smem + wb * kWStageBytes + (wave * 4 + i) * kSubBytes));
   };
+  auto rw_ld = [&](int s, int i) { dma16_m0(wrsrc, w_voff + s * 8 * kSubBytes, i * kSubBytes); };
   // Refill load i (0..7) of X block u into ring slot xb.
-  auto dma_rx = [&](int u, int xb, int i) {
-    const uint8_t* st = smem + kXRingOff + xb * kXBlockBytes + (wave * 8) * kSubBytes;
-    dma16(xrsrc, x_off[i] + u * (kPackK * 2), 0, lds_addr(st + i * kSubBytes));
+  auto rx_m0 = [&](int xb, int i) {
+    set_m0(lds_addr(smem + kXRingOff + xb * kXBlockBytes + (wave * 8 + i) * kSubBytes));
   };
+  auto rx_ld = [&](int u, int i) { dma16_m0(xrsrc, x_off[i] + u * (kPackK * 2), 0); };
 
   // Operands of v_mfma_f32_16x16x32_bf16 (stage-local k 0..31).
   // A operand i: 16 MFMA rows; SwiGLU i < 4 -> Wg rows wn*64 + 16 i, i >= 4
@@ -405,14 +421,16 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
 
   // Stage t (= g + KS, KS = t % 12 a compile-time constant, H = t % 2, X
   // block u = t / 2).  Half 0: A0..3 x B0..7, A outer; A4..7 of stage t are
-  // read meanwhile, and one refill load follows the first MFMA of each A.
-  // Half 1: A4..7 x B0..7, B outer; a refill load follows the second MFMA of
-  // every other column, and after column j's four MFMAs B[j] (and A[j],
+  // read meanwhile, and one refill per A: its M0 write after the A's first
+  // MFMA, its load after the second.  Half 1: A4..7 x B0..7, B outer; a
+  // refill in every other column (M0 after the column's first MFMA, the
+  // load after its second), and after column j's four MFMAs B[j] (and A[j],
   // j < 4) of stage t+1 are read -- their registers' last use this stage.
-  // The weight ring (4 slots) and the X ring (3 slots of two stages) repeat
-  // every 12 stages, so with KS constant every slot index is too.
-  // Before stage 0: rw at weight stage 3, rx at X block 2 (the prologue
-  // issued their first loads).
+  // Splitting each refill around an MFMA keeps at most three other
+  // instructions between two MFMAs almost everywhere (1186 -> 1156 cycles
+  // per stage on config 3).  The weight ring (4 slots) and the X ring (3
+  // slots of two stages) repeat every 12 stages, so with KS constant every
+  // slot index is too.
   int g = 0;  // first stage of the current group of 12
   auto stage = [&](auto KSc) {
     constexpr int KS = decltype(KSc)::value;
@@ -427,11 +445,15 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       A[4 + i] = rd_a(wb, 4 + i);
+      constexpr int xi0 = kH == 0 ? 2 : 6;
       mfma16(A[i], B[0], acc[i][0]);
-      if (i < 2) dma_rw(g + KS + 3, wb0, 2 + i);
-      else dma_rx(g / 2 + KS / 2 + 2, xb0, (kH == 0 ? 2 : 6) + (i - 2));
+      if (i < 2) rw_m0(wb0, 2 + i);
+      else rx_m0(xb0, xi0 + (i - 2));
+      mfma16(A[i], B[1], acc[i][1]);
+      if (i < 2) rw_ld(g + KS + 3, 2 + i);
+      else rx_ld(g / 2 + KS / 2 + 2, xi0 + (i - 2));
 #pragma unroll
-      for (int j = 1; j < 8; ++j) mfma16(A[i], B[j], acc[i][j]);
+      for (int j = 2; j < 8; ++j) mfma16(A[i], B[j], acc[i][j]);
     }
     wait_lgkmcnt0();   // this wave's reads of stage t are done
     wait_vmcnt<16>();  // stage t+1 landed
@@ -440,12 +462,15 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
     // u + 2 (H = 0) or loads 0-1 of block u + 3 into slot u % 3 (H = 1)
     constexpr int xb1 = kH == 0 ? xb0 : xb;
     constexpr int du1 = kH == 0 ? 2 : 3;  // block u + 2 or u + 3
+    constexpr int xi1 = kH == 0 ? 4 : 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       mfma16(A[4], B[j], acc[4][j]);
+      if (j == 0 || j == 2) rw_m0(wb, j / 2);
+      else if (j == 4 || j == 6) rx_m0(xb1, xi1 + (j - 4) / 2);
       mfma16(A[5], B[j], acc[5][j]);
-      if (j == 0 || j == 2) dma_rw(g + KS + 4, wb, j / 2);
-      else if (j == 4 || j == 6) dma_rx(g / 2 + KS / 2 + du1, xb1, (kH == 0 ? 4 : 0) + (j - 4) / 2);
+      if (j == 0 || j == 2) rw_ld(g + KS + 4, j / 2);
+      else if (j == 4 || j == 6) rx_ld(g / 2 + KS / 2 + du1, xi1 + (j - 4) / 2);
       mfma16(A[6], B[j], acc[6][j]);
       mfma16(A[7], B[j], acc[7][j]);
       B[j] = rd_b(nxb, nh, j);

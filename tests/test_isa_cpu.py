@@ -14,7 +14,8 @@ compiler actually emitted, for every instantiation:
 * its only vector-memory waits are the twelve barriers' (16 loads
   outstanding each: the refills are spread evenly; the LDS-DMA loads are
   inline assembly too, so that the compiler adds no waits of its own), and M0
-  is written only by those loads' own s_mov;
+  is written only by the loads' own s_mov, each followed by exactly one
+  LDS-DMA load with at least one instruction (the wait state) between them;
 * no VALU instruction writes an MFMA's A/B operand registers shortly before
   it (operands must come from LDS loads, whose waits the compiler places);
 * nothing writes an AGPR between the MFMAs except the MFMAs themselves;
@@ -134,12 +135,14 @@ def test_k_loop_waits_and_m0(asm):
         assert [re.search(r"vmcnt\((\d+)\)", b).group(1) for b in vm] == ["16"] * 12, (name, vm)
         assert sum(b == "s_barrier" for b in body) == 12, name
         insns = [b for b in lines if is_insn(b)]
-        for k, b in enumerate(insns):
-            if "m0" in b:
-                assert b.startswith("s_mov_b32 m0,"), (name, b)
-                assert insns[k + 1] == "s_nop 0" and insns[k + 2].startswith("buffer_load_dwordx4"), \
-                    (name, insns[k:k + 3])
-                assert insns[k + 2].endswith(" lds"), (name, insns[k + 2])
+        m0 = [k for k, b in enumerate(insns) if "m0" in b]
+        assert all(insns[k].startswith("s_mov_b32 m0,") for k in m0), name
+        dma = [k for k, b in enumerate(insns)
+               if b.startswith("buffer_load_dwordx4") and b.endswith(" lds")]
+        assert len(dma) == len(m0), name
+        for a, b in zip(m0, m0[1:] + [len(insns)]):
+            loads = [k for k in dma if a < k < b]
+            assert len(loads) == 1 and loads[0] >= a + 2, (name, insns[a:a + 4])
 
 
 def test_no_valu_writes_mfma_operands_just_before(asm):
