@@ -4,7 +4,10 @@
 For one call the model takes the dispatcher's launch plan
 (llk_describe_launch) and returns
     compute = rounds x per-workgroup MFMA work / per-CU rate,
-              rounds = ceil(workgroups / CUs)  (one workgroup per CU at a time)
+              rounds = ceil(workgroups / CUs)  (one workgroup per CU at a time);
+              in the tile kernel a partly filled last round counts
+              f_full / f(busy fraction), the clock rising linearly from
+              f_full (every CU busy) toward f_idle as CUs fall idle
     memory  = (weights + X + Y, or the partial planes written instead of Y) / stream rate
     per_cu  = per-CU loads.  Tile kernel: rounds x (weight panel / weight rate
               + X panel / L2 rate), the weight rate being HBM's when there is
@@ -52,7 +55,14 @@ def _tile_launch(cal: dict, cus: int, nmat: int, M: int, N: int, K: int, S: int,
     # Workgroup tile: 256 m x 256 MFMA rows (SwiGLU: 128 n of Wg + 128 n of Wu).
     kpart = math.ceil(K / 64) * 64 / S
     rounds = math.ceil(workgroups / cus)
-    compute = rounds * 2.0 * 256 * 256 * kpart / cal["tile_flops_per_cu"]
+    # A partly filled round runs at a higher clock: the board holds
+    # tile_clock_full_hz with every CU busy and climbs toward
+    # tile_clock_idle_hz as CUs fall idle (linear in the busy fraction).
+    full, occ = divmod(workgroups, cus)
+    occ /= cus
+    f_full, f_idle = cal["tile_clock_full_hz"], cal["tile_clock_idle_hz"]
+    eff_rounds = full + (f_full / (f_idle - (f_idle - f_full) * occ) if occ else 0.0)
+    compute = eff_rounds * 2.0 * 256 * 256 * kpart / cal["tile_flops_per_cu"]
     # Per-CU loads: one m tile means every weight byte comes from HBM
     # once; with more m tiles the panels are re-read from L2 / MALL.
     w_rate = (cal["tile_hbm_weight_bytes_per_cu_s"] if math.ceil(M / 256) == 1
