@@ -283,12 +283,13 @@ struct Plan {
   size_t fix_bytes = 0;  // tile path: the two-piece slots (after the padded X)
 };
 
-// Every workspace begins with this many bytes of per-tile counters (two per
-// tile) for the two-piece k split, which no other use of the workspace touches:
-// the library's workspaces (zeroed when allocated) and the no-allocation
-// entry point's array (zero when loaded) keep them at zero between launches
-// (the second piece of each tile resets its counter); a caller's scratch is
-// cleared before each two-piece launch.
+// Every workspace begins with this many bytes of counters for the
+// two-piece k split (two per tail tile: llk_tile_fix_max_tiles() tiles),
+// which no other use of the workspace touches: the library's workspaces
+// (zeroed when allocated) and the no-allocation entry point's array (zero
+// when loaded) keep them at zero between launches (the finishing piece of
+// each tail tile resets both of its counters); a caller's scratch is cleared
+// before each two-piece launch.
 constexpr size_t kCounterBytes = 64 << 10;
 
 // Workspace bytes of a plan whose other buffers take `body` bytes.
