@@ -70,18 +70,31 @@ def test_two_piece_parity(llk, gpu, orc, M, N, K):
 
 def test_two_piece_tail_after_whole_waves(llk, gpu, orc):
     """Config 5's SwiGLU at M = 1000: 256 whole tiles, then 176 as two
-    pieces (cut at 61 of 80 blocks); every row against the oracle."""
+    pieces (cut at 61 of 80 blocks), in one grid; every row against the
+    oracle, and the head's columns bit-identical to the one-launch form."""
     M, N, K = 1000, 13824, 5120
     print(f"case two-piece tail M={M}", flush=True)
     p = _plan(llk, M, N, K)
     assert (p["head_blocks_n"], p["two_piece_kb"]) == (64, 61)
     x, wg, wu = swiglu_inputs(M, K, N, seed=32)
     pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
-    yf = from_dev(llk.fused_swiglu(to_dev(gpu, x), pg, pu, out_dtype=gpu.float32))
+    xd = to_dev(gpu, x)
+    yf = from_dev(llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.float32))
     _, yf_ref = orc.swiglu_avx2(x, wg, wu, 16, want_f32=True)
     assert_parity(yf, yf_ref, "M=1000 fp32 (all rows)")
     for n0 in range(64 * 128, N, 128):  # every tail column block on its own
         assert_parity(yf[:, n0:n0 + 128], yf_ref[:, n0:n0 + 128], f"tail columns {n0}..")
+    # The head's whole tiles run in the two-piece grid with the plain
+    # kernel's arithmetic: bit-identical to the one-launch form there.
+    llk.set_tunable("tile_two_piece", 0)
+    try:
+        yf1 = from_dev(llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.float32))
+    finally:
+        llk.set_tunable("tile_two_piece", 1)
+    head = 64 * 128
+    assert np.array_equal(yf[:, :head].view(np.uint32), yf1[:, :head].view(np.uint32)), \
+        "head columns differ from the one-launch form"
+    assert_parity(yf[:, head:], yf1[:, head:], "tail vs one piece (order of the k sum only)")
 
 
 def test_caller_scratch_with_garbage_counters(llk, gpu):
