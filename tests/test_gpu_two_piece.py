@@ -7,7 +7,8 @@ accumulators.
 - Parity with the oracle on every row, for shapes with ragged rows and
   columns and for a whole-wave head plus a two-piece tail.
 - The same inputs without the two-piece form (knob tile_two_piece = 0)
-  differ only by the order of the k sum: fp32 outputs within the bar.
+  differ only by the order of the k sum: fp32 outputs within the bar, and
+  bit-identical where the two-piece grid runs whole tiles (the head).
 - Bit-identical reruns (the sum P0 + P1 does not depend on which piece
   arrives second: fp32 addition commutes).
 - A caller scratch whose counter area holds garbage (the library clears it
