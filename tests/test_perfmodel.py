@@ -93,3 +93,23 @@ def test_matrix_engines_match_spec_and_measurements():
     workers = doc["compute"]["owners"]["worker"]["count"]
     assert float(cal["tile_flops_per_cu"]) * workers < eng["mfma-bf16-16x16x32"][
         "sustained_flops_random_operands"]
+
+
+def test_partial_round_runs_at_a_higher_clock():
+    """The tile kernel's partly filled last round costs f_full / f(busy)
+    of a full round (the clock climbs from 1.80 GHz with every CU busy
+    toward 2.4 GHz as CUs fall idle, profiles/tile_kernel_cycles_per_stage.md):
+    config 3's 688 tiles (2 full rounds + 176 of 256) cost between 2.69 and
+    3 rounds, a single full round (GEMM 4096^3) exactly one."""
+    cal = {k: float(v) for k, v in perfmodel.machine()["calibration"].items() if k != "measured_us"}
+    t_round = 2.0 * 256 * 256 * 4096 / cal["tile_flops_per_cu"] * 1e6
+    p3 = perfmodel.predict("fused_swiglu", 2048, 11008, 4096)
+    assert p3["plan"]["workgroups"] == 688
+    f_full, f_idle = cal["tile_clock_full_hz"], cal["tile_clock_idle_hz"]
+    occ = (688 - 512) / 256
+    want = (2 + f_full / (f_idle - (f_idle - f_full) * occ)) * t_round
+    assert abs(p3["compute_us"] - want) < 1e-6 * want
+    assert 2.69 * t_round < p3["compute_us"] < 3 * t_round
+    p2 = perfmodel.predict("matmul", 4096, 4096, 4096)
+    assert p2["plan"]["workgroups"] == 256
+    assert abs(p2["compute_us"] - t_round) < 1e-6 * t_round
