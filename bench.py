@@ -48,11 +48,13 @@ EXTRA_WARM_S = 0.1
 
 
 def _time_loop(torch, fn, steps: int, warmup: int, min_warm_s: float = 0.0,
-               warm_info: dict | None = None) -> float:
+               warm_info: dict | None = None, per_launch: list | None = None) -> float:
     """Average ms per call, HIP events on the launch (current) stream.  After
     `warmup` untimed calls, keeps warming until `min_warm_s` seconds have
     passed (the GPU needs ~35 ms of load to reach its steady clock).
-    `warm_info`, if given, receives the untimed launch count and seconds."""
+    `warm_info`, if given, receives the untimed launch count and seconds.
+    `per_launch`, if given, receives each call's ms: an event is recorded
+    between consecutive calls, so call i spans events i and i + 1."""
     t0 = time.perf_counter()
     n = 0
     for i in range(warmup):
@@ -67,13 +69,22 @@ def _time_loop(torch, fn, steps: int, warmup: int, min_warm_s: float = 0.0,
     if warm_info is not None:
         warm_info.update(launches=n, seconds=round(time.perf_counter() - t0, 3))
     s = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(s)
+    if per_launch is None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for i in range(steps):
+            fn(i)
+        e1.record(s)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record(s)
     for i in range(steps):
         fn(i)
-    e1.record(s)
+        ev[i + 1].record(s)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    per_launch.extend(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+    return ev[0].elapsed_time(ev[steps]) / steps
 
 
 def bench_prefill(torch, llk, steps, warmup, fill="normal"):
@@ -94,11 +105,15 @@ def bench_prefill(torch, llk, steps, warmup, fill="normal"):
     pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
     xd = to_dev(torch, x)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-    warm = {}
+    warm, per = {}, []
     ms = _time_loop(torch, lambda i: llk.fused_swiglu(xd, pg, pu, out=y), steps, warmup,
-                    PREFILL_WARM_S, warm)
+                    PREFILL_WARM_S, warm, per)
     flops = 4.0 * M * K * N
-    return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, inputs=(x, wg, wu), y=y, warm=warm)
+    per_us = np.array(per) * 1e3
+    launch_us = {"min": round(float(per_us.min()), 2), "median": round(float(np.median(per_us)), 2),
+                 "max": round(float(per_us.max()), 2), "launches": len(per)}
+    return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, inputs=(x, wg, wu), y=y, warm=warm,
+                launch_us=launch_us)
 
 
 def _rand_w(torch, g, K, N):
@@ -190,6 +205,48 @@ def bench_vendor(torch, steps, warmup):
 def _unfused_swiglu(torch, F, x, w, gu, N):
     torch.matmul(x, w, out=gu)
     return F.silu(gu[:, :N]) * gu[:, N:]
+
+
+def bench_kernel_fn(torch, llk, M, K, N, calls=10):
+    """The reference-shaped KernelFn (llk_swiglu_kernel_fn, synchronous, raw
+    row-major weights in device memory) on an M x K x N SwiGLU: us per call
+    with the default per-call pack of Wg and Wu, and with packed weights
+    reused (llk_kernel_fn_assume_immutable_weights); beside them the same
+    shape through llk_swiglu_bf16 with packed handles; the difference of the
+    first two is the two packs (GB/s over their bytes read and written)."""
+    from dslcompiler_amd import cache as cmod
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    x = torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16)
+    wg, wu = _rand_w(torch, g, K, N), _rand_w(torch, g, K, N)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+
+    def per_call(fn):
+        fn()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t) / calls * 1e6
+
+    out = {}
+    out["pack_every_call_us"] = round(per_call(lambda: cmod.swiglu_kernel_fn(x, wg, wu, y, y)), 1)
+    old = cmod.kernel_fn_assume_immutable_weights(True)
+    try:
+        out["reuse_packed_us"] = round(per_call(lambda: cmod.swiglu_kernel_fn(x, wg, wu, y, y)), 1)
+    finally:
+        cmod.kernel_fn_assume_immutable_weights(old)
+        llk.lib().llk_cache_clear(llk.lib().llk_kernel_fn_cache())
+    pg, pu = llk.PackedWeights.from_device(wg), llk.PackedWeights.from_device(wu)
+    out["swiglu_bf16_us"] = round(_time_loop(torch, lambda i: llk.fused_swiglu(x, pg, pu, out=y),
+                                             calls, 5) * 1e3, 1)
+    # the two packs' share of a call, and their rate over 2 x K x N x 2 bytes
+    # read + the same written
+    pack_us = out["pack_every_call_us"] - out["reuse_packed_us"]
+    out["packs_us"] = round(pack_us, 1)
+    out["packs_gbs"] = round(2 * 2.0 * 2 * K * N / max(pack_us, 1e-3) / 1e3, 1)
+    return out
 
 
 def model_vs_measured(pre: dict, extra: dict) -> dict:
@@ -343,7 +400,7 @@ def main() -> None:
                                     "config 5's)")
     ap.add_argument("--set", action="append", default=[], metavar="NAME=VALUE",
                     help="set a dispatcher knob (llk_set_tunable) before a --only run, e.g. "
-                         "tile_two_piece=1; repeatable")
+                         "tile_splits=2; repeatable")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this hot path runs on one GPU; multi-GPU runs are not part of this "
@@ -399,6 +456,9 @@ def main() -> None:
         extra["gemm_4096_bf16_out"] = {"us": round(g16["ms"] * 1e3, 1),
                                        "tflops": round(g16["tflops"], 1)}
         extra["model_vs_measured"] = model_vs_measured(pre, extra)
+        extra["kernel_fn_c3"] = bench_kernel_fn(torch, llk, PREFILL["M"], PREFILL["K"],
+                                                PREFILL["N"])
+        extra["kernel_fn_decode_m8"] = bench_kernel_fn(torch, llk, 8, DECODE["K"], DECODE["N"])
     cpu = None if a.no_cpu_baseline else cpu_baseline(x, wg, wu)
     if not a.no_cpu_baseline and not a.no_extra:
         extra["cpu_port_other_configs"] = cpu_port_configs(llk)
@@ -414,6 +474,7 @@ def main() -> None:
         "warm_untimed": {**pre["warm"], "rule": f"--warmup launches, then more until "
                                                 f"{PREFILL_WARM_S} s have passed"},
         "ms_per_step": round(pre["ms"], 5),
+        "launch_us": pre["launch_us"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

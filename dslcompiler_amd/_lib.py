@@ -29,6 +29,8 @@ LLK_ERR_NOT_FOUND = -11
 LLK_BF16, LLK_FP16, LLK_FP32 = 0, 1, 2
 LLK_PACK_KEEP_HOST = 1
 LLK_PACK_HOST_ONLY = 2
+LLK_PLAN_X_ALIGNED = 1
+LLK_PLAN_ACCUMULATE = 2
 
 STATUS_NAMES = {
     0: "LLK_OK", -1: "LLK_ERR_INVALID_ARGUMENT", -2: "LLK_ERR_SHAPE", -3: "LLK_ERR_DTYPE",
@@ -82,8 +84,7 @@ class LaunchPlan(C.Structure):
     _fields_ = [("kernel", C.c_int), ("splits", C.c_int), ("group_width", C.c_int),
                 ("pad_x", C.c_int), ("workgroups", C.c_int64),
                 ("threads_per_workgroup", C.c_int64), ("launches", C.c_int64),
-                ("workspace_bytes", C.c_size_t), ("head_blocks_n", C.c_int64),
-                ("two_piece_kb", C.c_int64)]
+                ("workspace_bytes", C.c_size_t), ("head_blocks_n", C.c_int64)]
 
 
 class MemRef2D(C.Structure):
@@ -111,6 +112,8 @@ WKP = C.POINTER(WeightKeyC)
 KERNEL_FN = C.CFUNCTYPE(C.c_int, T2, P, P, T2, C.c_int, CTX)
 
 MR = C.POINTER(MemRef2D)
+# llk_memref_kernel_fn: JitCache::KernelFn (JitCache.h:79-81)
+MEMREF_FN = C.CFUNCTYPE(None, MR, MR, MR, MR, MR)
 
 # name -> (restype, argtypes); every function declared in include/llk/llk_abi.h.
 SIGNATURES = {
@@ -138,8 +141,10 @@ SIGNATURES = {
     "llk_swiglu_scratch_size": (C.c_size_t, [C.c_int64, C.c_int64, C.c_int64]),
     "llk_verify_fused_swiglu": (C.c_int, [C.c_int64] * 8),
     "llk_verify_matmul": (C.c_int, [C.c_int64, C.c_int64]),
-    "llk_describe_launch": (C.c_int, [C.c_int, C.c_int64, C.c_int64, C.c_int64, C.c_int,
+    "llk_describe_launch": (C.c_int, [C.c_int, C.c_int64, C.c_int64, C.c_int64, C.c_uint,
                                       C.POINTER(LaunchPlan)]),
+    "llk_workspace_stats": (C.c_int, [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
+    "llk_workspace_trim": (C.c_int, []),
     "llk_gemm_bf16": (C.c_int, [T2, P, T2, C.c_int, CTX]),
     "llk_gemm_bf16_accumulate": (C.c_int, [T2, P, T2, C.c_int, CTX]),
     "llk_mlp_bf16": (C.c_int, [T2, P, P, P, T2, T2, CTX]),
@@ -164,9 +169,13 @@ SIGNATURES = {
     "llk_swiglu_kernel_fn": (None, [MR, MR, MR, MR, MR]),
     "llk_kernel_fn_status": (C.c_int, []),
     "llk_kernel_fn_cache": (C.c_void_p, []),
+    "llk_kernel_fn_assume_immutable_weights": (C.c_int, [C.c_int]),
     "llk_cache_create": (C.c_int, [PP]),
     "llk_cache_destroy": (None, [P]),
-    "llk_cache_lookup_or_compile": (C.c_int, [P, KKP, C.POINTER(KERNEL_FN)]),
+    "llk_cache_lookup_or_compile": (C.c_int, [P, KKP, C.POINTER(MEMREF_FN)]),
+    "llk_cache_lookup_or_compile_packed": (C.c_int, [P, KKP, C.POINTER(KERNEL_FN)]),
+    "llk_cache_lookup_or_compile_str": (C.c_int, [P, C.c_char_p, C.c_char_p, C.c_size_t,
+                                                  C.POINTER(MEMREF_FN)]),
     "llk_cache_set_object_dir": (C.c_int, [P, C.c_char_p]),
     "llk_code_object_path": (C.c_int, [C.c_int, C.c_char_p, C.c_char_p, C.c_size_t]),
     "llk_code_object_info": (C.c_int, [C.c_char_p, C.POINTER(C.c_int), C.c_char_p, C.c_size_t,
@@ -180,6 +189,8 @@ SIGNATURES = {
     "llk_cache_insert_packed_weights": (C.c_int, [P, WKP, P]),
     "llk_cache_lookup_packed_weights": (C.c_int, [P, WKP, PP]),
     "llk_cache_get_packed_weights": (C.c_int, [P, T2, C.c_int64, C.c_int, C.c_uint, PP]),
+    "llk_cache_acquire_packed_weights": (C.c_int, [P, T2, C.c_int64, C.c_int, C.c_uint, PP]),
+    "llk_cache_release_packed_weights": (C.c_int, [P, P]),
     "llk_cache_evict_lru": (C.c_int, [P, C.c_int, C.c_size_t]),
     "llk_cache_set_max_entries": (C.c_int, [P, C.c_int, C.c_size_t]),
     "llk_cache_get_stats": (C.c_int, [P, C.POINTER(CacheStatsC)]),

@@ -9,8 +9,8 @@ from dataclasses import dataclass, fields
 import numpy as np
 
 from . import _lib
-from ._lib import (KERNEL_FN, CacheStatsC, KernelContext, KernelKeyC, WeightKeyC, check, lib,
-                   tensor2d)
+from ._lib import (KERNEL_FN, MEMREF_FN, CacheStatsC, KernelContext, KernelKeyC, MemRef2D,
+                   WeightKeyC, check, lib, tensor2d)
 from .ops import PackedWeights, _check_operand, _ctx, _out_dtype_code, _t2d, _torch
 
 # Enum values (KernelKey.h:22-38, plus this backend's additions).
@@ -55,8 +55,9 @@ class WeightKey:
         return WeightKeyC(self.weight_ptr or None, self.shape_hash, self.BK, self.BN)
 
 
-class KernelFn:
-    """A gfx950 entry point from the object-code level."""
+class PackedEntry:
+    """An object-code entry in its packed-handle shape (llk_kernel_fn: the
+    signature of llk_swiglu_bf16)."""
 
     def __init__(self, fn: KERNEL_FN):
         self._fn = fn
@@ -73,6 +74,64 @@ class KernelFn:
         ctx = _ctx(stream, scratch)
         check(self._fn(C.byref(_t2d(x)), w0.handle, w1.handle if w1 is not None else None,
                        C.byref(_t2d(y)), _out_dtype_code(y.dtype), C.byref(ctx)))
+
+
+def memref(t) -> MemRef2D:
+    """MemRef2D (JitCache.h:43-51) over a 2-D torch tensor (any device) or
+    numpy array; strides in elements, offset 0."""
+    if isinstance(t, np.ndarray):
+        if t.ndim != 2:
+            raise ValueError("memref operands are 2-D")
+        ptr, (d0, d1) = t.ctypes.data, t.shape
+        s0, s1 = (st // t.itemsize for st in t.strides)
+    else:
+        if t.dim() != 2:
+            raise ValueError("memref operands are 2-D")
+        ptr, (d0, d1), (s0, s1) = t.data_ptr(), t.shape, t.stride()
+    return MemRef2D(ptr, ptr, 0, d0, d1, s0, s1)
+
+
+def kernel_fn_status() -> int:
+    """Status of the calling thread's last KernelFn-shaped call."""
+    return int(lib().llk_kernel_fn_status())
+
+
+def _check_kernel_fn() -> None:
+    st = kernel_fn_status()
+    if st != _lib.LLK_OK:
+        check(st)
+
+
+class KernelFn:
+    """JitCache::KernelFn (JitCache.h:79-81): fn(x, wg, wu, init, result)
+    over five MemRef2D, no return value (status: llk_kernel_fn_status)."""
+
+    def __init__(self, fn: MEMREF_FN):
+        self._fn = fn
+
+    @property
+    def address(self) -> int:
+        return C.cast(self._fn, C.c_void_p).value or 0
+
+    def __call__(self, x, wg, wu, init, result) -> None:
+        """Operands: 2-D torch tensors or numpy arrays (wu None for a
+        matmul entry); raises LLKError on a failed call."""
+        m = [memref(t) if t is not None else None for t in (x, wg, wu, init, result)]
+        if result is init:
+            m[4] = m[3]
+        self._fn(*(C.byref(v) if v is not None else None for v in m))
+        _check_kernel_fn()
+
+
+def swiglu_kernel_fn(x, wg, wu, init, result) -> None:
+    """llk_swiglu_kernel_fn (the library's KernelFn for the fused SwiGLU)."""
+    KernelFn(C.cast(lib().llk_swiglu_kernel_fn, MEMREF_FN))(x, wg, wu, init, result)
+
+
+def kernel_fn_assume_immutable_weights(on: bool) -> bool:
+    """Opt-in reuse of packed weights by KernelFn calls; returns the previous
+    setting."""
+    return bool(lib().llk_kernel_fn_assume_immutable_weights(int(on)))
 
 
 def code_object_path(operation: int, directory: str | None = None) -> str:
@@ -122,19 +181,35 @@ class JitCache:
         check(lib().llk_cache_set_object_dir(self._c, path.encode() if path else None))
 
     def lookup_or_compile(self, key: KernelKey) -> KernelFn:
-        fn = KERNEL_FN()
+        """lookupOrCompile(KernelKey): the key's KernelFn (MemRef2D shape)."""
+        fn = MEMREF_FN()
         check(lib().llk_cache_lookup_or_compile(self._c, C.byref(key.c()), C.byref(fn)))
         return KernelFn(fn)
 
-    def lookup_object_code(self, key: KernelKey) -> KernelFn | None:
+    def lookup_or_compile_packed(self, key: KernelKey) -> PackedEntry:
+        """The same L3 entry in its packed-handle shape."""
+        fn = KERNEL_FN()
+        check(lib().llk_cache_lookup_or_compile_packed(self._c, C.byref(key.c()), C.byref(fn)))
+        return PackedEntry(fn)
+
+    def lookup_or_compile_str(self, cache_key: str, module: str) -> KernelFn:
+        """lookupOrCompile(std::string, ModuleOp): the KernelFn of the
+        module's first llk op, cached under `cache_key`."""
+        fn = MEMREF_FN()
+        text = module.encode()
+        check(lib().llk_cache_lookup_or_compile_str(self._c, cache_key.encode(), text, len(text),
+                                                    C.byref(fn)))
+        return KernelFn(fn)
+
+    def lookup_object_code(self, key: KernelKey) -> PackedEntry | None:
         fn = KERNEL_FN()
         r = lib().llk_cache_lookup_object_code(self._c, C.byref(key.c()), C.byref(fn))
         if r < 0:
             check(r)
-        return KernelFn(fn) if r == 1 else None
+        return PackedEntry(fn) if r == 1 else None
 
-    def insert_object_code(self, key: KernelKey, fn: KernelFn | int) -> None:
-        f = fn._fn if isinstance(fn, KernelFn) else KERNEL_FN(fn)
+    def insert_object_code(self, key: KernelKey, fn: PackedEntry | int) -> None:
+        f = fn._fn if isinstance(fn, PackedEntry) else KERNEL_FN(fn)
         check(lib().llk_cache_insert_object_code(self._c, C.byref(key.c()), f))
 
     # -- L1 / L2 --------------------------------------------------------------
@@ -187,18 +262,32 @@ class JitCache:
         host uint16 ndarray (bf16 bits) or a CUDA bfloat16 tensor.  The
         result is borrowed from the cache."""
         out = C.c_void_p()
+        t, on_device, flags = self._weight_args(w, host_only)
+        check(lib().llk_cache_get_packed_weights(self._c, C.byref(t), bk, on_device, flags,
+                                                  C.byref(out)))
+        return PackedWeights(out.value, owned=False)
+
+    def acquire_packed_weights(self, w, bk: int = 64, host_only: bool = False) -> PackedWeights:
+        """get_packed_weights with a counted reference: valid whatever the
+        level does until release_packed_weights."""
+        out = C.c_void_p()
+        t, on_device, flags = self._weight_args(w, host_only)
+        check(lib().llk_cache_acquire_packed_weights(self._c, C.byref(t), bk, on_device, flags,
+                                                      C.byref(out)))
+        return PackedWeights(out.value, owned=False)
+
+    def release_packed_weights(self, pw: PackedWeights) -> None:
+        check(lib().llk_cache_release_packed_weights(self._c, pw.handle))
+
+    @staticmethod
+    def _weight_args(w, host_only: bool):
         if isinstance(w, np.ndarray):
             if w.dtype != np.uint16 or w.ndim != 2 or w.strides[1] != 2:
                 raise ValueError("w must be a 2-D uint16 array with unit inner stride")
             t = tensor2d(w.ctypes.data, w.shape[0], w.shape[1], w.strides[0] // 2)
-            flags = _lib.LLK_PACK_HOST_ONLY if host_only else 0
-            check(lib().llk_cache_get_packed_weights(self._c, C.byref(t), bk, 0, flags,
-                                                      C.byref(out)))
-        else:
-            _check_operand(w, "w", (_torch().bfloat16,))
-            check(lib().llk_cache_get_packed_weights(self._c, C.byref(_t2d(w)), bk, 1, 0,
-                                                      C.byref(out)))
-        return PackedWeights(out.value, owned=False)
+            return t, 0, _lib.LLK_PACK_HOST_ONLY if host_only else 0
+        _check_operand(w, "w", (_torch().bfloat16,))
+        return _t2d(w), 1, 0
 
     # -- management -----------------------------------------------------------
     def evict_lru(self, level: int, max_entries: int) -> None:

@@ -48,7 +48,12 @@ int swiglu_with_module(const llk_tensor2d* x, const llk_packed_weights* wg,
                        const llk_packed_weights* wu, llk_tensor2d* y, int y_dtype,
                        llk_kernel_context* ctx, const ModuleFns* mod);
 int gemm_with_module(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor2d* c,
-                     int c_dtype, llk_kernel_context* ctx, const ModuleFns* mod);
+                     int c_dtype, llk_kernel_context* ctx, const ModuleFns* mod,
+                     bool accumulate);
+// The KernelFn-shaped call (kernel_fn.cpp) and its thread's status.
+int memref_call(int op, int out_dtype, const ModuleFns* mod, llk_memref2d* x, llk_memref2d* wg,
+                llk_memref2d* wu, llk_memref2d* init, llk_memref2d* result);
+void set_kernel_fn_status(int rc);
 
 hipFunction_t module_function(const ModuleFns* m, const char* symbol) {
   auto it = m->fns.find(symbol);
@@ -198,7 +203,9 @@ int module_on_current_device(CodeObject* obj, const llk::ModuleFns** out) {
 }
 
 // Entry points: a fixed pool of functions, each bound to one (object,
-// output type) pair when first handed out.
+// output type) pair when first handed out; slot i has an entry of each
+// shape, kEntries[i] (llk_kernel_fn: packed handles, a context) and
+// kMemrefEntries[i] (the reference's KernelFn: five MemRef2D).
 struct Slot {
   CodeObject* obj = nullptr;
   int out_dtype = 0;
@@ -207,14 +214,15 @@ constexpr int kSlots = 64;
 std::array<Slot, kSlots> g_slots;
 int g_nslots = 0;
 
+Slot slot_of(int i) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return g_slots[i];
+}
+
 int run_slot(int i, const llk_tensor2d* x, const llk_packed_weights* w0,
              const llk_packed_weights* w1, llk_tensor2d* y, int y_dtype,
              llk_kernel_context* ctx) {
-  Slot sl;
-  {
-    std::lock_guard<std::mutex> lk(g_mu);
-    sl = g_slots[i];
-  }
+  const Slot sl = slot_of(i);
   if (!sl.obj) return err(LLK_ERR_INVALID_ARGUMENT, "unbound code-object entry %d", i);
   if (y_dtype != sl.out_dtype)
     return err(LLK_ERR_DTYPE, "entry of a key with output type %d called with output type %d",
@@ -223,7 +231,25 @@ int run_slot(int i, const llk_tensor2d* x, const llk_packed_weights* w0,
   int rc = module_on_current_device(sl.obj, &m);
   if (rc) return rc;
   if (sl.obj->operation == kOpSwiglu) return llk::swiglu_with_module(x, w0, w1, y, y_dtype, ctx, m);
-  return llk::gemm_with_module(x, w0, y, y_dtype, ctx, m);
+  return llk::gemm_with_module(x, w0, y, y_dtype, ctx, m, false);
+}
+
+// The KernelFn shape: no return value; the status is the thread's
+// llk_kernel_fn_status().
+void run_memref_slot(int i, llk_memref2d* x, llk_memref2d* wg, llk_memref2d* wu,
+                     llk_memref2d* init, llk_memref2d* result) {
+  const Slot sl = slot_of(i);
+  if (!sl.obj) {
+    llk::set_kernel_fn_status(err(LLK_ERR_INVALID_ARGUMENT, "unbound code-object entry %d", i));
+    return;
+  }
+  const llk::ModuleFns* m = nullptr;
+  const int rc = module_on_current_device(sl.obj, &m);
+  if (rc) {
+    llk::set_kernel_fn_status(rc);
+    return;
+  }
+  (void)llk::memref_call(sl.obj->operation, sl.out_dtype, m, x, wg, wu, init, result);
 }
 
 template <int I>
@@ -232,12 +258,25 @@ int slot_entry(const llk_tensor2d* x, const llk_packed_weights* w0, const llk_pa
   return run_slot(I, x, w0, w1, y, y_dtype, ctx);
 }
 
+template <int I>
+void memref_slot_entry(llk_memref2d* x, llk_memref2d* wg, llk_memref2d* wu, llk_memref2d* init,
+                       llk_memref2d* result) {
+  run_memref_slot(I, x, wg, wu, init, result);
+}
+
 template <int... I>
 constexpr std::array<llk_kernel_fn, sizeof...(I)> slot_entries(std::integer_sequence<int, I...>) {
   return {&slot_entry<I>...};
 }
+template <int... I>
+constexpr std::array<llk_memref_kernel_fn, sizeof...(I)> memref_slot_entries(
+    std::integer_sequence<int, I...>) {
+  return {&memref_slot_entry<I>...};
+}
 constexpr std::array<llk_kernel_fn, kSlots> kEntries =
     slot_entries(std::make_integer_sequence<int, kSlots>{});
+constexpr std::array<llk_memref_kernel_fn, kSlots> kMemrefEntries =
+    memref_slot_entries(std::make_integer_sequence<int, kSlots>{});
 
 const char* object_file(int operation) {
   return operation == kOpSwiglu ? "llk_fused_swiglu_gfx950.hsaco"
@@ -265,11 +304,13 @@ std::string object_path(int operation, const char* dir) {
 
 namespace llk {
 
-// The entry point of (operation, out_dtype) from the operation's code object
-// in `dir` (empty: the default directory).  The caller has checked the key.
-// The object is read and checked here; with a device present it is also
-// loaded on the current device, so that a bad object is reported now.
-int code_object_entry(int operation, int out_dtype, const std::string& dir, llk_kernel_fn* out) {
+// The entry points of (operation, out_dtype) from the operation's code
+// object in `dir` (empty: the default directory), in both shapes.  The
+// caller has checked the key.  The object is read and checked here; with a
+// device present it is also loaded on the current device, so that a bad
+// object is reported now.
+int code_object_entry(int operation, int out_dtype, const std::string& dir, llk_kernel_fn* packed,
+                      llk_memref_kernel_fn* memref) {
   if (!object_file(operation))
     return err(LLK_ERR_INVALID_ARGUMENT, "operation %d has no gfx950 code object", operation);
   CodeObject* obj = nullptr;
@@ -283,15 +324,16 @@ int code_object_entry(int operation, int out_dtype, const std::string& dir, llk_
     (void)hipGetLastError();
   }
   std::lock_guard<std::mutex> lk(g_mu);
-  for (int i = 0; i < g_nslots; ++i)
-    if (g_slots[i].obj == obj && g_slots[i].out_dtype == out_dtype) {
-      *out = kEntries[i];
-      return LLK_OK;
-    }
-  if (g_nslots == kSlots)
-    return err(LLK_ERR_OUT_OF_MEMORY, "more than %d (code object, output type) entry points", kSlots);
-  g_slots[g_nslots] = Slot{obj, out_dtype};
-  *out = kEntries[g_nslots++];
+  int i = 0;
+  while (i < g_nslots && !(g_slots[i].obj == obj && g_slots[i].out_dtype == out_dtype)) ++i;
+  if (i == g_nslots) {
+    if (g_nslots == kSlots)
+      return err(LLK_ERR_OUT_OF_MEMORY, "more than %d (code object, output type) entry points",
+                 kSlots);
+    g_slots[g_nslots++] = Slot{obj, out_dtype};
+  }
+  *packed = kEntries[i];
+  *memref = kMemrefEntries[i];
   return LLK_OK;
 }
 

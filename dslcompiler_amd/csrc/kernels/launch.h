@@ -25,15 +25,14 @@ namespace llk_gfx950 {
 
 // Launches with the host stub `stub` when mod is null, else the function
 // `symbol()` of the loaded object.  args are the kernel's parameters, by
-// value, in order.
+// value, in order.  Returns the launch call's own status, so an error left
+// by an unrelated earlier call on the thread is neither reported here nor
+// cleared.
 template <class... Args>
 hipError_t launch_kernel(const llk::ModuleFns* mod, const void* stub, const char* (*symbol)(),
                          dim3 grid, dim3 block, unsigned lds, hipStream_t s, Args... args) {
   void* params[] = {static_cast<void*>(&args)...};
-  if (!mod) {
-    (void)hipLaunchKernel(stub, grid, block, params, lds, s);
-    return hipGetLastError();
-  }
+  if (!mod) return hipLaunchKernel(stub, grid, block, params, lds, s);
   hipFunction_t f = llk::module_function(mod, symbol());
   if (!f) return hipErrorNotFound;
   return hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, lds, s,

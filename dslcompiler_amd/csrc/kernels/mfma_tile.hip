@@ -57,10 +57,8 @@
 //
 // Optional k split across workgroups (SPLIT): raw fp32 partial planes plus
 // split_reduce_kernel, which sums them in split order and applies the
-// epilogue.  Or (FIX) two pieces of unequal k length per tile, finished by
-// the second piece to arrive: the long pieces of a partial last wave of
-// tiles run on as many CUs while the remaining CUs work through the short
-// ones, so the wave takes max(long, rounds x short) instead of a whole tile.
+// epilogue.  No workgroup ever waits for another: the kernel boundary
+// orders the planes before the reduce reads them.
 //
 // X must be padded to whole 64-k steps with 16-byte aligned rows (the host
 // copies it into a padded buffer otherwise); rows >= M read as zero through
@@ -100,19 +98,6 @@ struct TileArgs {
   // partial planes (S >= 1), which keeps the tile kernel's epilogue, and its
   // registers, those of C = A B.
   int accumulate;
-  // Two-piece k split finished in the kernel (FIX, SwiGLU).  The grid holds
-  // first the H = tiles_m * head_tn whole tiles of the leading head_tn
-  // n-tile columns, then the T tiles of the other columns twice: workgroup
-  // H + b runs the 64-k blocks [0, kb_cut) of tail tile b, H + T + b the
-  // blocks [kb_cut, KB) of tail tile b.  The first piece of a tail tile to
-  // finish writes its raw fp32 accumulators to the tile's slot, part + b *
-  // 64 Ki floats, in register order; the second adds them to its own and
-  // runs the epilogue (see the kernel).  One grid, so the pieces start as
-  // soon as CUs free up from the whole tiles.  cnt: two counters per tail
-  // tile, zero at launch and again after it.
-  unsigned* cnt;
-  int kb_cut;
-  int head_tn;
 };
 
 constexpr int kThreads = 256;
@@ -126,7 +111,6 @@ constexpr int kXRingOff = kWStages * kWStageBytes;
 constexpr int kLdsBytes = kXRingOff + kXBlocks * kXBlockBytes;  // 160 KiB
 // Per wave: 4 buffer_load ... lds per weight stage, 8 per X block.
 constexpr int kStripRow = 144;        // epilogue staging: 128-byte rows + 16-byte pad
-constexpr int kFixMaxTiles = 8192;    // two-piece k split: two counters (8 bytes) per tail tile
 
 // s_waitcnt with vmcnt(n) (n < 64) and the other counters left alone.
 template <int N>
@@ -212,8 +196,7 @@ __device__ __forceinline__ void acc_fence(f32x4 (&acc)[8][8]) {
 // OUT: output element type (kOutBF16, kOutF16 (GEMM only), kOutF32).
 // YVEC: Y rows allow a 4-element vector store (aligned base, ldy % 4 == 0).
 // SPLIT: store raw fp32 partial accumulators of k split s (see TileArgs).
-// FIX: two-piece k split finished in the kernel (see TileArgs).
-template <int MODE, int OUT, bool YVEC, bool SPLIT, bool FIX = false>
+template <int MODE, int OUT, bool YVEC, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
@@ -225,47 +208,24 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   // Workgroup -> (split s, tile): tiles of one split are contiguous, so
   // after the XCD remap the tiles that share X's k slice (and, m fastest,
   // the tiles that share W columns) run on one XCD.
-  // FIX: whole tiles first, then the long pieces, then the short ones, in
-  // launch order, so that the long pieces start on the first CUs to free up;
-  // the remap keeps each class within itself.
   const int tiles = a.tiles_m * a.tiles_n;
-  // FIX: split -1 for a whole tile, else the piece; tile is then the index
-  // among the tail tiles, and the tile grid of either part starts at
-  // n-tile column n_base and is ntn columns wide.
-  int split, tile, n_base = 0, ntn = a.tiles_n;
-  if constexpr (FIX) {
-    const int H = a.tiles_m * a.head_tn;
-    if ((int)blockIdx.x < H) {
-      split = -1;
-      tile = xcd_remap(blockIdx.x, H);
-      ntn = a.head_tn;
-    } else {
-      const int b = (int)blockIdx.x - H, T = tiles - H;
-      split = b >= T ? 1 : 0;
-      tile = xcd_remap(b - split * T, T);
-      n_base = a.head_tn;
-      ntn = a.tiles_n - a.head_tn;
-    }
-  } else {
-    const int idx = xcd_remap(blockIdx.x, tiles * (SPLIT ? a.S : 1));
-    split = SPLIT ? idx / tiles : 0;
-    tile = SPLIT ? idx - split * tiles : idx;
-  }
+  const int idx = xcd_remap(blockIdx.x, tiles * (SPLIT ? a.S : 1));
+  const int split = SPLIT ? idx / tiles : 0;
+  const int tile = SPLIT ? idx - split * tiles : idx;
   int tm, tn;
   if (a.group_m > 0 && a.tiles_m > a.group_m) {
-    const int span = a.group_m * ntn;  // tiles of one full group
+    const int span = a.group_m * a.tiles_n;  // tiles of one full group
     const int g = tile / span, r = tile - g * span;
     const int gm = min(a.group_m, a.tiles_m - g * a.group_m);  // last group may be short
     tm = g * a.group_m + r % gm;
-    tn = n_base + r / gm;
+    tn = r / gm;
   } else {
     tm = tile % a.tiles_m;
-    tn = n_base + tile / a.tiles_m;
+    tn = tile / a.tiles_m;
   }
   const int m0 = tm * kTileM;
-  const int kb0 = FIX ? (split > 0 ? a.kb_cut : 0) : SPLIT ? split * a.kbs : 0;
-  const int nkb = FIX ? (split < 0 ? a.KB : split ? a.KB - a.kb_cut : a.kb_cut)
-                      : SPLIT ? min(a.KB - kb0, a.kbs) : a.KB;
+  const int kb0 = SPLIT ? split * a.kbs : 0;
+  const int nkb = SPLIT ? min(a.KB - kb0, a.kbs) : a.KB;
 
   // ---- operand streams ----------------------------------------------------
   // Stage t holds k range [32 t, 32 t + 32); X block u = k [64 u, 64 u + 64)
@@ -502,96 +462,6 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   mfma_drain();
   acc_fence(acc);   // the epilogue reads the accumulators only after the drain
 
-  // ---- FIX: the first piece of a tail tile to finish publishes its raw
-  // accumulators; the second waits for them and finishes the tile.  Each
-  // tail tile has two counters: cnt[2 tile] hands out tickets (0:
-  // publisher, 1: finisher), cnt[2 tile + 1] says the publisher's slot is
-  // complete.  The slot holds the publisher's accumulators in register order
-  // -- quad (i, j) of thread t at byte ((8 i + j) * 256 + t) * 16, so every
-  // store moves 1 KiB of consecutive bytes straight from the accumulators --
-  // and both pieces map threads to outputs alike, so the finisher reads the
-  // quads of its own positions at the same offsets.  The publisher stores
-  // with agent-scope coherent stores (sc1), waits for them (vmcnt 0) and a
-  // workgroup barrier, then counts the slot ready after an agent-scope
-  // release (L2 written back); the finisher polls that count with
-  // agent-scope acquire loads, resets both counters to 0 for the next
-  // launch, and adds the slot to its accumulators with coherent loads
-  // before the epilogue (fp32 addition commutes: the sum does not depend on
-  // which piece finishes).  The finisher only ever waits for a workgroup
-  // that already holds ticket 0, so is running, and has its stores and one
-  // atomic left; the poll is bounded all the same (about a second), past
-  // which it goes on.
-  if constexpr (FIX) {
-    if (split >= 0) {
-      constexpr int kSlotBytes = kThreads * 64 * 16;
-      constexpr int kSc1 = 16;  // cache policy bits: sc1
-      const __amdgpu_buffer_rsrc_t slot = __builtin_amdgcn_make_buffer_rsrc(
-          a.part + (size_t)tile * (kSlotBytes / 4), 0, kSlotBytes, kBufferWord3);
-      const int t16 = (int)threadIdx.x * 16;
-      uint32_t* const flag = reinterpret_cast<uint32_t*>(smem);
-      __syncthreads();  // every wave is past its last operand read: the ring is free
-      if (threadIdx.x == 0)
-        *reinterpret_cast<volatile uint32_t*>(flag) =
-            __hip_atomic_fetch_add(a.cnt + 2 * tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __syncthreads();
-      if (*reinterpret_cast<volatile uint32_t*>(flag) == 0u) {  // publisher
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), slot,
-                                                   (i * 8 + j) * kThreads * 16 + t16, 0, kSc1);
-        wait_vmcnt<0>();
-        __syncthreads();
-        if (threadIdx.x == 0) {
-          // Release: the L2 write-back (buffer_wbl2) has completed before the
-          // count.  The wait is explicit: the compiler drops its own vmcnt
-          // wait after the write-back when the counter already reads zero.
-          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-          __hip_atomic_fetch_add(a.cnt + 2 * tile + 1, 1u, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-        }
-        return;
-      }
-      if (threadIdx.x == 0) {
-        for (int it = 0; it < (1 << 24); ++it) {
-          if (__hip_atomic_load(a.cnt + 2 * tile + 1, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) !=
-              0u)
-            break;
-          __builtin_amdgcn_s_sleep(2);
-        }
-        __hip_atomic_store(a.cnt + 2 * tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(a.cnt + 2 * tile + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // The acquire's cache invalidate (buffer_inv) has completed before
-        // the barrier lets the other waves load the slot.
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      }
-      __syncthreads();
-      // One accumulator row i (eight quads j) at a time, the next row's loads
-      // in flight while one is added; each sum goes back to its AGPRs (the
-      // epilogue then runs as for a whole tile, with its registers).
-      f32x4 pub[2][8];
-      auto load_row = [&](int i, f32x4 (&dst)[8]) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          dst[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                 slot, (i * 8 + j) * kThreads * 16 + t16, 0, kSc1));
-      };
-      load_row(0, pub[0]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (i + 1 < 8) load_row(i + 1, pub[(i + 1) & 1]);
-        asm volatile("" ::: "memory");  // the next row's loads stay below this point
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          acc[i][j] += pub[i & 1][j];
-          asm volatile("" : "+a"(acc[i][j]));
-        }
-      }
-    }
-  }
-
   // ---- epilogue: acc[i][j] holds, in lane l, output row m = m0 + wm*128 +
   // 16 j + l%16 and the four consecutive n = (wave's first n) + 16 i' +
   // 4*(l/16) + 0..3, i' = i (GEMM) or i % 4 (SwiGLU: i >= 4 is the up half).
@@ -753,11 +623,11 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(TileArgs a) {
 // library's own kernels).  A build of one operation's code object
 // (LLK_CO_OP: 1 SwiGLU, 0 GEMM) instantiates that operation's kernels only.
 // ---------------------------------------------------------------------------
-template <int MODE, int OUT, bool YVEC, bool SPLIT, bool FIX>
+template <int MODE, int OUT, bool YVEC, bool SPLIT>
 const char* tile_symbol() {
   static const std::string name = "_ZN10llk_gfx95016mfma_tile_kernelI" + mangle_int(MODE) +
                                   mangle_int(OUT) + mangle_bool(YVEC) + mangle_bool(SPLIT) +
-                                  mangle_bool(FIX) + "EEvNS_8TileArgsE";
+                                  "EEvNS_8TileArgsE";
   return name.c_str();
 }
 
@@ -768,27 +638,22 @@ const char* split_reduce_symbol() {
   return name.c_str();
 }
 
-template <int MODE, int OUT, bool YVEC, bool SPLIT, bool FIX = false>
+template <int MODE, int OUT, bool YVEC, bool SPLIT>
 static hipError_t launch_tile_t(const TileArgs& a, const llk::ModuleFns* mod, hipStream_t s) {
-  auto fn = mfma_tile_kernel<MODE, OUT, YVEC, SPLIT, FIX>;
+  auto fn = mfma_tile_kernel<MODE, OUT, YVEC, SPLIT>;
   if (!mod) {
     static std::atomic<uint64_t> lds_set{0};  // devices configured, per instantiation
     hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(fn), kLdsBytes, lds_set);
     if (e != hipSuccess) return e;
   }
   const int tiles = a.tiles_m * a.tiles_n;
-  const int wgs = FIX ? 2 * tiles - a.tiles_m * a.head_tn : tiles * (SPLIT ? a.S : 1);
-  dim3 grid(wgs), block(kThreads);
+  dim3 grid(tiles * (SPLIT ? a.S : 1)), block(kThreads);
   return launch_kernel(mod, reinterpret_cast<const void*>(fn),
-                       &tile_symbol<MODE, OUT, YVEC, SPLIT, FIX>, grid, block, kLdsBytes, s, a);
+                       &tile_symbol<MODE, OUT, YVEC, SPLIT>, grid, block, kLdsBytes, s, a);
 }
 
 template <int MODE, int OUT, bool YVEC>
 static hipError_t launch_t(const TileArgs& a, const llk::ModuleFns* mod, hipStream_t s) {
-  if constexpr (MODE == 1 && YVEC) {
-    if (a.kb_cut > 0) return launch_tile_t<MODE, OUT, YVEC, false, true>(a, mod, s);
-  }
-  if (a.kb_cut > 0) return hipErrorInvalidValue;  // the two-piece form is SwiGLU's, vector Y
   if (a.S <= 1 && !a.accumulate) return launch_tile_t<MODE, OUT, YVEC, false>(a, mod, s);
   // Partials are fp32 planes with 16-byte aligned rows: one instantiation.
   hipError_t e = launch_tile_t<MODE, kOutF32, true, true>(a, mod, s);
@@ -826,12 +691,6 @@ bool llk_tile_x_fits(int M, int64_t ldx) {
   return rows * ldx * 2 < ((int64_t)1 << 31);
 }
 
-// Two-piece k split (TileArgs::kb_cut): its largest tail tile count (the
-// counters it needs: 8 bytes per tail tile) and the slot bytes of `tiles`
-// tail tiles (256 KiB each).
-int llk_tile_fix_max_tiles() { return llk_gfx950::kFixMaxTiles; }
-size_t llk_tile_fix_bytes(int tiles) { return (size_t)tiles * llk_gfx950::kThreads * 64 * 16; }
-
 // Bytes of the partial planes of a k split over S workgroups (0 if S <= 1
 // and the launch does not accumulate: an accumulating GEMM launch always
 // takes the planes, one at S = 1).
@@ -845,16 +704,11 @@ size_t llk_tile_split_bytes(int mode, int M, int NB, int S, bool accumulate) {
 // S > 1 splits K over S workgroups of kbs = ceil(KB / S) blocks (every split
 // non-empty: the caller guarantees (S - 1) * kbs < KB); `part` (16-byte
 // aligned) holds llk_tile_split_bytes(mode, M, NB, S, accumulate) bytes.
-// accumulate (GEMM only): y += x w instead of y = x w.  kb_cut > 0 (SwiGLU,
-// vector Y, S = 1): the n-blocks [0, head_nb) run as whole tiles and the
-// others as the two-piece k split finished in the kernel, all in one grid,
-// with `part` (256-byte aligned) holding llk_tile_fix_bytes(tail) bytes and
-// `cnt` two zeroed counters per tail tile (tail = ceil(M / 256) * (NB -
-// head_nb) <= llk_tile_fix_max_tiles()); head_nb is 0 otherwise.
+// accumulate (GEMM only): y += x w instead of y = x w.
 hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                            const void* w1, void* y, int64_t ldy, int M, int N, int KB, int NB,
-                           int S, void* part, int out, bool yvec, bool accumulate, int kb_cut,
-                           int head_nb, unsigned* cnt, const llk::ModuleFns* mod, hipStream_t s) {
+                           int S, void* part, int out, bool yvec, bool accumulate,
+                           const llk::ModuleFns* mod, hipStream_t s) {
   using namespace llk_gfx950;
   TileArgs a;
   a.x = x;
@@ -875,16 +729,8 @@ hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void*
   a.n_pad = NB * 128;
   a.part = static_cast<float*>(part);
   a.accumulate = accumulate ? 1 : 0;
-  a.cnt = cnt;
-  a.kb_cut = kb_cut;
-  a.head_tn = head_nb;
   if (a.S > 1 && (part == nullptr || (int64_t)(a.S - 1) * a.kbs >= KB)) return hipErrorInvalidValue;
   if (accumulate && (mode != 0 || part == nullptr)) return hipErrorInvalidValue;
-  if (kb_cut == 0 && head_nb != 0) return hipErrorInvalidValue;
-  if (kb_cut != 0 && (mode != 1 || kb_cut < 0 || kb_cut >= KB || part == nullptr ||
-                      cnt == nullptr || accumulate || a.S > 1 || head_nb < 0 || head_nb >= NB ||
-                      (int64_t)a.tiles_m * (a.tiles_n - head_nb) > kFixMaxTiles))
-    return hipErrorInvalidValue;
 #if !defined(LLK_CO_OP) || LLK_CO_OP == 1
   if (mode == 1) return launch_mode<1>(a, out, yvec, mod, s);
 #endif

@@ -17,6 +17,7 @@
 #include <string>
 #include <vector>
 
+#include "packed_weights.h"
 #include "runtime/kernel_key.h"
 #include "runtime/packed_layout.h"
 #include "runtime/schedule.h"
@@ -31,10 +32,7 @@ struct ModuleFns;  // functions of a loaded code object (code_object.cpp)
 hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                            const void* w1, void* y, int64_t ldy, int M, int N, int KB, int NB,
                            int S, void* part, int out_dtype, bool yvec, bool accumulate,
-                           int kb_cut, int head_nb, unsigned* cnt, const llk::ModuleFns* mod,
-                           hipStream_t s);
-int llk_tile_fix_max_tiles();
-size_t llk_tile_fix_bytes(int tiles);
+                           const llk::ModuleFns* mod, hipStream_t s);
 size_t llk_tile_split_bytes(int mode, int M, int NB, int S, bool accumulate);
 bool llk_tile_x_fits(int M, int64_t ldx);
 hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const void* w0,
@@ -47,23 +45,9 @@ int llk_skinny_threads(int nmat, int M, int G);
 hipError_t llk_launch_pad_rows(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* out,
                                int64_t ldo, const llk::ModuleFns* mod, hipStream_t s);
 hipError_t llk_launch_pack(const uint16_t* w, int64_t ld, int K, int N, int KB, int NB, void* out,
-                           hipStream_t s);
+                           const llk::ModuleFns* mod, hipStream_t s);
 hipError_t llk_launch_zero_rows(void* y, int64_t ld_elems, int64_t M, int64_t N, int elem_bytes,
                                 const llk::ModuleFns* mod, hipStream_t s);
-hipError_t llk_launch_zero(void* p, size_t bytes, const llk::ModuleFns* mod, hipStream_t s);
-
-struct llk_packed_weights {
-  // Reference metadata (PackedWeights.h:13-19).
-  int64_t K_blocks = 0, N = 0, block_size = 0, BK = 0;
-  int dtype = LLK_BF16;
-  // Backend fields.
-  int64_t K = 0;
-  std::vector<uint16_t> host;  // reference layout, when kept
-  void* dev = nullptr;
-  size_t dev_bytes = 0;
-  int device = -1;
-  int64_t KB = 0, NB = 0;  // device layout blocks (64 k, 128 n)
-};
 
 namespace {
 
@@ -89,6 +73,10 @@ constexpr int kMaxDevices = 64;
 struct Workspace {
   void* ptr = nullptr;
   size_t bytes = 0;
+  hipEvent_t done = nullptr;  // recorded on the stream after the last call that used it
+  bool pinned = false;        // used under graph capture: a graph may name it, never freed
+  int busy = 0;               // calls between get_workspace and release_workspace
+  uint64_t tick = 0;          // last use, for LRU eviction
 };
 
 struct DeviceState {
@@ -97,9 +85,11 @@ struct DeviceState {
   char arch[64] = {0};
   int cu_count = 0, lds = 0, clock_khz = 0;
   // Library-owned workspaces, one per stream (the per-thread default stream:
-  // one per thread), so launches on different streams never share one.
+  // one per thread), so launches on different streams never share one; at
+  // most max_workspaces of them, least recently used evicted first.
   std::map<std::pair<uintptr_t, uint64_t>, Workspace> ws;
-  std::vector<void*> retired;  // outgrown workspaces, kept until process exit
+  uint64_t tick = 0;
+  std::vector<void*> retired;  // outgrown pinned workspaces, kept until process exit
   void* noalloc_scratch = nullptr;  // device address of `scratch` (below)
 };
 DeviceState g_dev[kMaxDevices];
@@ -177,19 +167,52 @@ std::pair<uintptr_t, uint64_t> workspace_key(hipStream_t s) {
   return {reinterpret_cast<uintptr_t>(s), s == hipStreamPerThread ? thread_id : 0};
 }
 
+// Frees a library workspace's buffer once the last call that used it has
+// finished on the GPU (its `done` event; a workspace never used yet has
+// none).  Called with the device mutex held, for idle, unpinned entries.
+void free_workspace_buffer(Workspace* w) {
+  if (w->done) (void)hipEventSynchronize(w->done);
+  if (w->ptr) (void)hipFree(w->ptr);
+  w->ptr = nullptr;
+  w->bytes = 0;
+}
+
+// Evicts the least recently used idle, unpinned workspace of `st` other
+// than `keep`; false if there is none.
+bool evict_one_workspace(DeviceState& st, const Workspace* keep) {
+  auto victim = st.ws.end();
+  for (auto it = st.ws.begin(); it != st.ws.end(); ++it) {
+    const Workspace& w = it->second;
+    if (&w == keep || w.busy > 0 || w.pinned) continue;
+    if (victim == st.ws.end() || w.tick < victim->second.tick) victim = it;
+  }
+  if (victim == st.ws.end()) return false;
+  free_workspace_buffer(&victim->second);
+  if (victim->second.done) (void)hipEventDestroy(victim->second.done);
+  st.ws.erase(victim);
+  return true;
+}
+
 // Workspace: the caller's (ctx->scratch) if given, else the library's own
 // buffer for the launch stream, grown on demand.  Launches are ordered on
 // their stream, so work on one stream never overlaps in its workspace, and
 // two streams never share one.  (A HIP graph captured on a stream keeps
 // that stream's workspace: replaying it concurrently with direct launches
 // on the capture stream is the caller's race, as with any captured buffer.)
-// An outgrown buffer is retired, not freed: launches still queued, captured
-// in a graph or about to be issued by another thread may name it, and
-// freeing would need a device-wide synchronisation.  Growth is geometric
-// (x1.5 at least), so the retired buffers of a stream add up to less than
-// twice its current one.
-int get_workspace(int dev, size_t need, llk_kernel_context* ctx, void** out) {
+// The library keeps at most `max_workspaces` of them per device (tunable,
+// default 16): a new stream (or thread, on the per-thread default stream)
+// beyond that evicts the least recently used idle one.  A buffer is freed
+// (on eviction, on growth, or by llk_workspace_trim) only after the event
+// recorded behind the last call that used it has completed, so work still
+// queued on a stream -- even one destroyed since -- never loses its
+// buffer; a workspace that a call used while its stream was capturing a
+// graph is pinned instead (the graph names it) and is never freed.  Growth
+// is geometric (x1.5 at least).  *held is the library workspace handed out
+// (null for a caller's scratch or when nothing is needed): the caller gives
+// it back with release_workspace after enqueuing its launches.
+int get_workspace(int dev, size_t need, llk_kernel_context* ctx, void** out, Workspace** held) {
   *out = nullptr;
+  *held = nullptr;
   if (need == 0) return LLK_OK;
   if (ctx && ctx->scratch) {
     if (ctx->scratch_size < need)
@@ -204,15 +227,41 @@ int get_workspace(int dev, size_t need, llk_kernel_context* ctx, void** out) {
   const auto key = workspace_key(ctx ? static_cast<hipStream_t>(ctx->stream) : nullptr);
   std::lock_guard<std::mutex> lk(st.mu);
   Workspace* w = nullptr;
+  const bool fresh_key = st.ws.find(key) == st.ws.end();
+  if (fresh_key) {
+    const size_t cap = (size_t)std::max<int64_t>(1, llk::tunable("max_workspaces"));
+    while (st.ws.size() >= cap && evict_one_workspace(st, nullptr)) {
+    }
+  }
   try {
     w = &st.ws[key];
   } catch (const std::bad_alloc&) {
     return fail(LLK_ERR_OUT_OF_MEMORY, "workspace bookkeeping");
   }
+  if (!w->done) {
+    const hipError_t e = hipEventCreateWithFlags(&w->done, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      w->done = nullptr;
+      if (fresh_key) st.ws.erase(key);
+      return fail_hip(e, "hipEventCreate(workspace)");
+    }
+  }
   if (w->bytes < need) {
     const size_t bytes = std::max({need, w->bytes + w->bytes / 2, (size_t)1 << 20});
+    if (w->ptr && !w->pinned && w->busy == 0) {
+      free_workspace_buffer(w);  // this stream's earlier calls have finished with it
+    } else if (w->ptr) {
+      try {
+        st.retired.push_back(w->ptr);  // a graph or a concurrent call may still name it
+      } catch (const std::bad_alloc&) {
+        return fail(LLK_ERR_OUT_OF_MEMORY, "workspace bookkeeping");
+      }
+      w->ptr = nullptr;
+      w->bytes = 0;
+    }
     void* fresh = nullptr;
     hipError_t e = hipMalloc(&fresh, bytes);
+    if (e != hipSuccess && evict_one_workspace(st, w)) e = hipMalloc(&fresh, bytes);
     if (e != hipSuccess)
       return fail(LLK_ERR_OUT_OF_MEMORY, "hipMalloc(%zu) for workspace: %s", bytes,
                   hipGetErrorString(e));
@@ -221,17 +270,33 @@ int get_workspace(int dev, size_t need, llk_kernel_context* ctx, void** out) {
       (void)hipFree(fresh);
       return fail_hip(e, "hipMemset(workspace)");
     }
-    try {
-      if (w->ptr) st.retired.push_back(w->ptr);
-    } catch (const std::bad_alloc&) {
-      (void)hipFree(fresh);
-      return fail(LLK_ERR_OUT_OF_MEMORY, "workspace bookkeeping");
-    }
     w->ptr = fresh;
     w->bytes = bytes;
+    w->pinned = false;
   }
+  ++w->busy;
+  w->tick = ++st.tick;
   *out = w->ptr;
+  *held = w;
   return LLK_OK;
+}
+
+// Gives back a workspace from get_workspace once the call's launches are
+// enqueued on `s`: records its `done` event there, or pins it when `s` is
+// capturing a graph (an event recorded under capture would be a graph node,
+// not a point the host can wait for).
+void release_workspace(int dev, Workspace* w, hipStream_t s) {
+  if (!w) return;
+  DeviceState& st = g_dev[dev];
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  // Pinned too when the capture state or the record cannot be had: no event
+  // then marks this call's end, so the buffer must outlive it.
+  bool pin = hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone;
+  if (!pin && hipEventRecord(w->done, s) != hipSuccess) pin = true;
+  if (pin) (void)hipGetLastError();  // a failed query leaves no error for the next call
+  std::lock_guard<std::mutex> lk(st.mu);
+  if (pin) w->pinned = true;
+  --w->busy;
 }
 
 // Workspace of llk_swiglu_bf16_noalloc: a fixed device array, one copy per
@@ -278,22 +343,7 @@ struct Plan {
   size_t ws_bytes = 0;   // workspace the plan needs
   bool too_large = false;  // tile path: K beyond the kernel's 32-bit offsets
   int64_t head_nb = 0;   // tile path: leading n-blocks launched unsplit (S applies to the rest)
-  int64_t kb_cut = 0;    // tile path, > 0: the columns from head_nb on run as two pieces per
-                         // tile, 64-k blocks [0, kb_cut) and [kb_cut, KB), finished in the kernel
-  size_t fix_bytes = 0;  // tile path: the two-piece slots (after the padded X)
 };
-
-// Every workspace begins with this many bytes of counters for the
-// two-piece k split (two per tail tile: llk_tile_fix_max_tiles() tiles),
-// which no other use of the workspace touches: the library's workspaces
-// (zeroed when allocated) and the no-allocation entry point's array (zero
-// when loaded) keep them at zero between launches (the finishing piece of
-// each tail tile resets both of its counters); a caller's scratch is cleared
-// before each two-piece launch.
-constexpr size_t kCounterBytes = 64 << 10;
-
-// Workspace bytes of a plan whose other buffers take `body` bytes.
-size_t with_counters(size_t body) { return body ? kCounterBytes + body : 0; }
 
 // k splits of the tile kernel for `rows` rows: the S that minimises the
 // modelled time  waves(S) * (ceil(KB / S) + 2) + partial traffic  in units
@@ -333,48 +383,12 @@ SplitCost best_split(int nmat, int64_t rows, int64_t KB, int64_t NB, int64_t for
 // remaining columns take a k split -- one short balanced wave instead of a
 // nearly empty long one, with partial planes for the tail columns only.
 // Used when the model puts it 3% or more below the best single launch.
-//
-// Two-piece tail (SwiGLU): the T tiles of a partial wave (T < CUs; all
-// tiles when there is no whole wave) run as two pieces each, k blocks
-// [0, kb_cut) and [kb_cut, KB), finished by whichever piece arrives second
-// (the kernel adds the other's accumulators: no reduce launch, no planes).
-// The T long pieces start on T CUs; the other CUs work through the short
-// ones, r = ceil(T / (CUs - T)) each, so the wave takes
-//   max(kb_cut + 3, r * (KB - kb_cut + 2) + 1)
-// steps (fill and epilogue 2, publishing and adding the other piece 1)
-// instead of KB + 2: config 3 (176 tail tiles of 688, r = 3) cuts at 49 of
-// 64 blocks.  The head's whole tiles run in the same grid, before the
-// pieces.  Used, when the knob tile_two_piece is 1, where the model puts it
-// 3% or more below the other plans.  The knob is 0 by default: measured on
-// MI355X a short piece's fill and 256 KiB publish, and the finisher's 256
-// KiB read-back, cost several times the model's step, so the two-piece tail
-// is slower (config 3: 280 vs 258-261 us; config 5's MLP at M = 1000: 351
-// vs 340-349 us, at M = 255: 158 vs 147 us).
 struct TilePlan {
   int S;
   int64_t head_nb;
-  int64_t kb_cut = 0;
 };
 
-// Cost and cut of the two-piece form for T tiles (infinity if it cannot run).
-double two_piece_cost(int64_t T, int64_t KB, int64_t per_wave, int64_t* kb_cut) {
-  const int64_t spare = per_wave - T;
-  *kb_cut = 0;
-  if (T < 1 || spare < 1 || KB < 2 || T > llk_tile_fix_max_tiles()) return 1e300;
-  const int64_t r = (T + spare - 1) / spare;
-  double best = 1e300;
-  for (int64_t cut = (KB + 1) / 2; cut < KB; ++cut) {
-    const double c = std::max((double)(cut + 3), (double)(r * (KB - cut + 2) + 1));
-    if (c < best) {
-      best = c;
-      *kb_cut = cut;
-    }
-  }
-  return best;
-}
-
-TilePlan tile_plan(int nmat, int64_t rows, int64_t KB, int64_t NB, int64_t db_splits,
-                   bool allow_two_piece) {
+TilePlan tile_plan(int nmat, int64_t rows, int64_t KB, int64_t NB, int64_t db_splits) {
   int64_t forced = llk::tunable("tile_splits");
   if (forced <= 0) forced = db_splits;
   const SplitCost all = best_split(nmat, rows, KB, NB, forced);
@@ -393,13 +407,6 @@ TilePlan tile_plan(int nmat, int64_t rows, int64_t KB, int64_t NB, int64_t db_sp
       best = {tail.S, head_nb};
       best_cost = head + tail.cost;
     }
-  }
-  if (allow_two_piece && nmat == 2 && llk::tunable("tile_two_piece") != 0 && head_tn < tn) {
-    int64_t cut = 0;
-    const double tail = two_piece_cost(tm * (tn - head_tn), KB, per_wave, &cut);
-    const double head =
-        (double)((tm * head_tn + per_wave - 1) / per_wave) * (double)(KB + 2);
-    if (cut > 0 && head + tail <= 0.97 * best_cost) best = {1, head_tn * nb_per_tile, cut};
   }
   return best;
 }
@@ -503,10 +510,9 @@ SmallMChoice small_m_choice(int nmat, int64_t M, int64_t KB, int64_t NB, int64_t
 // entry point's fixed buffer); a plan that needs more takes fewer k splits
 // and, for a padded X, shorter row chunks.
 // accumulate (GEMM, C += A B): the tile path takes the partial planes at any
-// S (the reduce adds C) and no tail split.  two_piece: the two-piece tail
-// may be used (it needs vector Y stores).
+// S (the reduce adds C) and no tail split.
 Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const llk_tensor2d* x,
-                 size_t max_ws = SIZE_MAX, bool accumulate = false, bool two_piece = true) {
+                 size_t max_ws = SIZE_MAX, bool accumulate = false) {
   Plan p;
   llk::ScheduleEntry se;
   const bool have_db = db_entry(nmat, M, &se);
@@ -519,10 +525,10 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
     const SmallMChoice c = small_m_choice(nmat, M, KB, NB, gw, S);
     p.G = c.width;
     p.S = c.splits;
-    p.ws_bytes = with_counters(llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), p.S));
+    p.ws_bytes = llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), p.S);
     while (p.ws_bytes > max_ws && p.S > 1) {
       --p.S;
-      p.ws_bytes = with_counters(llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), p.S));
+      p.ws_bytes = llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), p.S);
     }
     return p;
   }
@@ -539,48 +545,30 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
     p.chunk = std::max<int64_t>(256, (((int64_t)1 << 31) - 1) / (p.ld * 2) / 256 * 256 - 256);
   const int64_t rows = std::min(p.chunk, M);
   if (p.pad) p.pad_bytes = ((size_t)rows * p.ld * 2 + 255) / 256 * 256;
-  // The two-piece tail runs over one row chunk only (its counters and slots
-  // are per launch).
-  const TilePlan tp = tile_plan(nmat, rows, KB, NB, have_db ? se.grain_size : 0,
-                                two_piece && !accumulate && rows == M);
+  const TilePlan tp = tile_plan(nmat, rows, KB, NB, have_db ? se.grain_size : 0);
   p.S = tp.S;
   p.head_nb = accumulate ? 0 : tp.head_nb;
   if (accumulate && tp.head_nb > 0) p.S = best_split(nmat, rows, KB, NB, 0).S;
-  p.kb_cut = tp.kb_cut;
-  if (p.kb_cut > 0)
-    p.fix_bytes = llk_tile_fix_bytes((int)((rows + 255) / 256 * (NB - p.head_nb)));
   auto body = [&](int64_t crows) {
-    return p.pad_bytes + (p.kb_cut > 0 ? p.fix_bytes
-                                       : llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)crows,
-                                                              (int)(NB - p.head_nb), p.S,
-                                                              accumulate));
+    return p.pad_bytes + llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)crows,
+                                              (int)(NB - p.head_nb), p.S, accumulate);
   };
-  p.ws_bytes = with_counters(body(rows));
+  p.ws_bytes = body(rows);
   if (p.ws_bytes <= max_ws) return p;
-  // Over the caller's limit: no two-piece tail, a padded X in row chunks
-  // that fit (whole 256-row tiles; fewer than 256 rows do not fit: ws_bytes
-  // stays above max_ws and the call is rejected), then the most k splits
-  // whose partial planes fit beside it.
-  if (p.kb_cut > 0) {
-    p.kb_cut = 0;
-    p.fix_bytes = 0;
-    p.head_nb = 0;
-    p.S = best_split(nmat, rows, KB, NB, 0).S;
-  }
-  const size_t room = max_ws > kCounterBytes ? max_ws - kCounterBytes : 0;
-  if (p.pad && p.pad_bytes > room) {
-    const int64_t fit = (int64_t)(room / ((size_t)p.ld * 2)) / 256 * 256;
-    if (fit < 256) {
-      p.ws_bytes = with_counters(body(rows));
-      return p;
-    }
+  // Over the caller's limit: a padded X in row chunks that fit (whole
+  // 256-row tiles; fewer than 256 rows do not fit: ws_bytes stays above
+  // max_ws and the call is rejected), then the most k splits whose partial
+  // planes fit beside it.
+  if (p.pad && p.pad_bytes > max_ws) {
+    const int64_t fit = (int64_t)(max_ws / ((size_t)p.ld * 2)) / 256 * 256;
+    if (fit < 256) return p;
     p.chunk = std::min(p.chunk, fit);
     p.pad_bytes = ((size_t)std::min(p.chunk, M) * p.ld * 2 + 255) / 256 * 256;
   }
   const int64_t crows = std::min(p.chunk, M);
   for (; p.S >= 1; --p.S) {
     if (p.S == 1) p.head_nb = 0;
-    p.ws_bytes = with_counters(body(crows));
+    p.ws_bytes = body(crows);
     if (p.ws_bytes <= max_ws || p.S == 1) break;
   }
   return p;
@@ -597,18 +585,19 @@ int empty_reduction(llk_tensor2d* y, int out_dtype, llk_kernel_context* ctx, con
   return e == hipSuccess ? LLK_OK : fail_hip(e, what);
 }
 
-// counters_clean: the workspace is the library's or the no-allocation
-// array, whose counter area is zero between launches (else it is cleared
-// before a two-piece launch).
+int launch_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w0,
+                       const llk_packed_weights* w1, llk_tensor2d* y, int out_dtype,
+                       const Plan& p, uint8_t* ws, hipStream_t s, const char* what,
+                       const llk::ModuleFns* mod, bool accumulate);
+
 int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w0,
                     const llk_packed_weights* w1, llk_tensor2d* y, int out_dtype,
                     llk_kernel_context* ctx, int dev, const char* what,
                     const llk::ModuleFns* mod, size_t max_ws = SIZE_MAX,
-                    bool accumulate = false, bool counters_clean = false) {
-  const int64_t M = x->dim0, K = x->dim1, N = w0->N;
+                    bool accumulate = false) {
+  const int64_t M = x->dim0, K = x->dim1;
   const int nmat = mode == 1 ? 2 : 1;
-  const bool yvec = y_vec_ok(y, out_dtype);
-  const Plan p = plan_launch(nmat, M, K, w0->KB, w0->NB, x, max_ws, accumulate, yvec);
+  const Plan p = plan_launch(nmat, M, K, w0->KB, w0->NB, x, max_ws, accumulate);
   if (p.too_large)
     return fail(LLK_ERR_SHAPE, "%s: K=%lld too large for M=%lld (the tile kernel needs K <= %lld)",
                 what, (long long)K, (long long)M, (long long)(((int64_t)1 << 31) / 512 - 64));
@@ -617,12 +606,23 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
                 "%s: M=%lld K=%lld needs %zu workspace bytes, more than the %zu available",
                 what, (long long)M, (long long)K, p.ws_bytes, max_ws);
   void* ws = nullptr;
-  int rc = get_workspace(dev, p.ws_bytes, ctx, &ws);
+  Workspace* held = nullptr;
+  int rc = get_workspace(dev, p.ws_bytes, ctx, &ws, &held);
   if (rc) return rc;
-  if (!(ctx && ctx->scratch)) counters_clean = true;  // the library's workspace
-  // [counters: kCounterBytes][padded X][partial planes or two-piece slots]
-  uint8_t* const body = ws ? static_cast<uint8_t*>(ws) + kCounterBytes : nullptr;
   hipStream_t s = stream_of(ctx);
+  rc = launch_contraction(mode, x, w0, w1, y, out_dtype, p, static_cast<uint8_t*>(ws), s, what,
+                          mod, accumulate);
+  release_workspace(dev, held, s);
+  return rc;
+}
+
+// Enqueues the plan's launches.  Workspace layout: [padded X][partial planes].
+int launch_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w0,
+                       const llk_packed_weights* w1, llk_tensor2d* y, int out_dtype,
+                       const Plan& p, uint8_t* body, hipStream_t s, const char* what,
+                       const llk::ModuleFns* mod, bool accumulate) {
+  const int64_t M = x->dim0, K = x->dim1, N = w0->N;
+  const bool yvec = y_vec_ok(y, out_dtype);
   hipError_t e = hipSuccess;
   if (p.skinny) {
     e = llk_launch_skinny(mode, static_cast<const uint16_t*>(x->data), x->stride0, w0->dev,
@@ -643,24 +643,10 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
       xp = reinterpret_cast<const uint16_t*>(body);
     }
     uint8_t* yp = static_cast<uint8_t*>(y->data) + m0 * y->stride0 * ysz;
-    if (p.kb_cut > 0) {
-      // Two-piece tail: the head's whole tiles and the tail's pieces in one
-      // grid (the counters of the tail tiles lead the workspace).
-      unsigned* const cnt = static_cast<unsigned*>(ws);
-      if (!counters_clean) {
-        const int64_t tiles = (rows + 255) / 256 * (w0->NB - p.head_nb);
-        e = llk_launch_zero(cnt, (size_t)tiles * 2 * sizeof(unsigned), mod, s);
-        if (e != hipSuccess) break;
-      }
-      e = llk_launch_tile(mode, xp, p.ld, w0->dev, w1 ? w1->dev : nullptr, yp, y->stride0, rows,
-                          (int)N, (int)w0->KB, (int)w0->NB, 1, body + p.pad_bytes, out_dtype, yvec,
-                          false, (int)p.kb_cut, (int)p.head_nb, cnt, mod, s);
-      continue;
-    }
     if (p.head_nb > 0) {
       e = llk_launch_tile(mode, xp, p.ld, w0->dev, w1 ? w1->dev : nullptr, yp, y->stride0, rows,
                           (int)(p.head_nb * 128), (int)w0->KB, (int)p.head_nb, 1, nullptr,
-                          out_dtype, yvec, accumulate, 0, 0, nullptr, mod, s);
+                          out_dtype, yvec, accumulate, mod, s);
       if (e != hipSuccess) break;
     }
     // Columns from n-block head_nb on: the packed payload of a matrix is
@@ -673,7 +659,7 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
                         yp + n0 * ysz, y->stride0, rows, (int)(N - n0), (int)w0->KB,
                         (int)(w0->NB - p.head_nb), p.S,
                         p.S > 1 || accumulate ? body + p.pad_bytes : nullptr, out_dtype, yvec,
-                        accumulate, 0, 0, nullptr, mod, s);
+                        accumulate, mod, s);
   }
   if (e != hipSuccess) return fail_hip(e, what);
   return LLK_OK;
@@ -811,7 +797,7 @@ int llk_pack_weights_device(const llk_tensor2d* w, int64_t bk, void* stream,
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
     e = llk_launch_pack(static_cast<const uint16_t*>(w->data), w->stride0, (int)pw->K, (int)pw->N,
-                        (int)pw->KB, (int)pw->NB, pw->dev, s);
+                        (int)pw->KB, (int)pw->NB, pw->dev, nullptr, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
       llk_packed_weights_free(pw);
@@ -827,6 +813,8 @@ int llk_repack(llk_packed_weights* pw, const llk_tensor2d* w) {
   if (!pw) return fail(LLK_ERR_INVALID_ARGUMENT, "handle is NULL");
   int rc = check_weight_input(w, pw->BK);
   if (rc) return rc;
+  if (!pw->owns_dev)
+    return fail(LLK_ERR_INVALID_ARGUMENT, "handle is a view over memory it does not own");
   if (w->dim0 != pw->K || w->dim1 != pw->N)
     return fail(LLK_ERR_SHAPE, "repack shape (%lld, %lld) differs from packed (%lld, %lld)",
                 (long long)w->dim0, (long long)w->dim1, (long long)pw->K, (long long)pw->N);
@@ -860,7 +848,7 @@ int llk_repack(llk_packed_weights* pw, const llk_tensor2d* w) {
 
 void llk_packed_weights_free(llk_packed_weights* pw) {
   if (!pw) return;
-  if (pw->dev) (void)hipFree(pw->dev);
+  if (pw->dev && pw->owns_dev) (void)hipFree(pw->dev);
   delete pw;
 }
 
@@ -1077,20 +1065,26 @@ size_t llk_swiglu_scratch_size(int64_t M, int64_t N, int64_t K) {
   return plan_launch(2, M, K, llk::deviceBlocksK(K), llk::deviceBlocksN(N), nullptr).ws_bytes;
 }
 
-int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, int x_aligned,
+int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, unsigned flags,
                         llk_launch_plan* out) {
   if (!out) return fail(LLK_ERR_INVALID_ARGUMENT, "out is NULL");
   *out = llk_launch_plan{};
   if (operation != 0 && operation != 3)
     return fail(LLK_ERR_INVALID_ARGUMENT, "operation %d has no gfx950 kernel", operation);
+  if (flags & ~(LLK_PLAN_X_ALIGNED | LLK_PLAN_ACCUMULATE))
+    return fail(LLK_ERR_INVALID_ARGUMENT, "unknown plan flags 0x%x", flags);
+  const bool accumulate = (flags & LLK_PLAN_ACCUMULATE) != 0;
+  if (accumulate && operation != 3)
+    return fail(LLK_ERR_INVALID_ARGUMENT, "LLK_PLAN_ACCUMULATE applies to the matmul only");
   if (M < 1 || N < 1 || K < 1 || M > kMaxDim || N > kMaxDim || K > kMaxDim)
     return fail(LLK_ERR_SHAPE, "M, N, K must be in [1, 2^30]");
   const int nmat = operation == 0 ? 2 : 1;
   const int64_t KB = llk::deviceBlocksK(K), NB = llk::deviceBlocksN(N);
   // A stand-in X with the requested alignment (plan_launch reads only the
   // pointer's alignment, the row stride and K).
+  const bool x_aligned = (flags & LLK_PLAN_X_ALIGNED) != 0;
   llk_tensor2d x{reinterpret_cast<void*>(x_aligned ? 256 : 2), M, K, x_aligned ? K : K + 1, 1};
-  const Plan p = plan_launch(nmat, M, K, KB, NB, &x);
+  const Plan p = plan_launch(nmat, M, K, KB, NB, &x, SIZE_MAX, accumulate);
   if (p.too_large)
     return fail(LLK_ERR_SHAPE, "K=%lld too large for M=%lld (the tile kernel needs K <= %lld)",
                 (long long)K, (long long)M, (long long)(((int64_t)1 << 31) / 512 - 64));
@@ -1110,16 +1104,41 @@ int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, int x_al
   const int64_t rows = std::min(p.chunk, M);
   const int64_t chunks = (M + p.chunk - 1) / p.chunk;
   const int64_t nb_per_tile = nmat == 2 ? 1 : 2, tail_nb = NB - p.head_nb;
-  const int64_t pieces = p.kb_cut > 0 ? 2 : p.S;
   out->workgroups = (rows + 255) / 256 *
-                    (p.head_nb / nb_per_tile + (tail_nb + nb_per_tile - 1) / nb_per_tile * pieces);
+                    (p.head_nb / nb_per_tile + (tail_nb + nb_per_tile - 1) / nb_per_tile * p.S);
   out->threads_per_workgroup = 256;
-  // (the two-piece form runs its head in the same grid as its pieces)
-  out->launches = chunks * (1 + (p.head_nb > 0 && p.kb_cut == 0 ? 1 : 0) + (p.pad ? 1 : 0) +
-                            (p.S > 1 ? 1 : 0));
+  // An accumulating launch always ends with the reduce (it adds C).
+  out->launches = chunks * (1 + (p.head_nb > 0 ? 1 : 0) + (p.pad ? 1 : 0) +
+                            (p.S > 1 || accumulate ? 1 : 0));
   out->head_blocks_n = p.head_nb;
-  out->two_piece_kb = p.kb_cut;
-  if (p.kb_cut > 0) out->splits = 2;
+  return LLK_OK;
+}
+
+int llk_workspace_stats(size_t* count, size_t* bytes) {
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  DeviceState& st = g_dev[dev];
+  std::lock_guard<std::mutex> lk(st.mu);
+  size_t n = 0, b = 0;
+  for (const auto& kv : st.ws) {
+    if (!kv.second.ptr) continue;
+    ++n;
+    b += kv.second.bytes;
+  }
+  if (count) *count = n;
+  if (bytes) *bytes = b;
+  return LLK_OK;
+}
+
+int llk_workspace_trim(void) {
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  DeviceState& st = g_dev[dev];
+  std::lock_guard<std::mutex> lk(st.mu);
+  while (evict_one_workspace(st, nullptr)) {
+  }
   return LLK_OK;
 }
 
@@ -1178,7 +1197,7 @@ int swiglu_entry(const llk_tensor2d* x, const llk_packed_weights* wg,
   llk_kernel_context fixed{nullptr, kNoAllocScratchBytes, ctx ? ctx->stream : nullptr};
   if ((rc = noalloc_scratch(dev, &fixed.scratch))) return rc;
   return run_contraction(1, x, wg, wu, y, y_dtype, &fixed, dev, "swiglu (no allocation)", mod,
-                         kNoAllocScratchBytes, false, true);
+                         kNoAllocScratchBytes);
 }
 
 // llk_gemm_bf16 (accumulate: llk_gemm_bf16_accumulate, C += A B).
@@ -1247,6 +1266,45 @@ int llk_mlp_bf16(const llk_tensor2d* x, const llk_packed_weights* wg, const llk_
 }  // extern "C"
 
 namespace llk {
+
+int pack_into(const llk_tensor2d* w, int64_t bk, bool w_on_device, void* dst, hipStream_t s,
+              const ModuleFns* mod, llk_packed_weights** view) {
+  if (!view) return fail(LLK_ERR_INVALID_ARGUMENT, "view is NULL");
+  int rc = check_weight_input(w, bk);
+  if (rc) return rc;
+  int dev = -1;
+  if ((rc = current_device(&dev))) return rc;
+  if (!*view) {
+    *view = new (std::nothrow) llk_packed_weights();
+    if (!*view) return fail(LLK_ERR_OUT_OF_MEMORY, "handle allocation");
+  }
+  llk_packed_weights* v = *view;
+  fill_meta(v, w->dim0, w->dim1, bk);
+  v->host.clear();
+  v->owns_dev = false;
+  v->dev = dst;
+  v->dev_bytes = llk::deviceLayoutBytes(v->K, v->N);
+  v->device = dev;
+  if (v->dev_bytes == 0) return LLK_OK;
+  if (!dst) return fail(LLK_ERR_INVALID_ARGUMENT, "pack destination is NULL");
+  const uint16_t* src = static_cast<const uint16_t*>(w->data);
+  hipError_t e;
+  if (w_on_device) {
+    e = llk_launch_pack(src, w->stride0, (int)v->K, (int)v->N, (int)v->KB, (int)v->NB, dst, mod, s);
+    return e == hipSuccess ? LLK_OK : fail_hip(e, "pack kernel");
+  }
+  std::vector<uint8_t> staging;
+  try {
+    staging.resize(v->dev_bytes);
+  } catch (const std::bad_alloc&) {
+    return fail(LLK_ERR_OUT_OF_MEMORY, "host allocation while packing");
+  }
+  llk::packDeviceLayout(src, v->K, v->N, w->stride0, staging.data());
+  e = hipMemcpyAsync(dst, staging.data(), v->dev_bytes, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);  // staging is freed on return
+  return e == hipSuccess ? LLK_OK : fail_hip(e, "upload of packed weights");
+}
+
 // The SwiGLU and GEMM entry points with the kernels of a loaded code object
 // (code_object.cpp).
 int swiglu_with_module(const llk_tensor2d* x, const llk_packed_weights* wg,
@@ -1255,8 +1313,9 @@ int swiglu_with_module(const llk_tensor2d* x, const llk_packed_weights* wg,
   return swiglu_entry(x, wg, wu, y, y_dtype, ctx, false, mod);
 }
 int gemm_with_module(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor2d* c,
-                     int c_dtype, llk_kernel_context* ctx, const ModuleFns* mod) {
-  return gemm_entry(a, b, c, c_dtype, ctx, mod);
+                     int c_dtype, llk_kernel_context* ctx, const ModuleFns* mod,
+                     bool accumulate) {
+  return gemm_entry(a, b, c, c_dtype, ctx, mod, accumulate);
 }
 }  // namespace llk
 

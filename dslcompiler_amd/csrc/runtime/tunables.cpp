@@ -23,12 +23,10 @@ struct Knob {
 // tile_min_kb:       fewest 64-k steps per tile-kernel split.
 // tile_tail_split:   1 = the tile kernel may run the columns of its last,
 //                    partial wave as a separate k-split launch; 0 = never.
-// tile_two_piece:    1 = SwiGLU's partial last wave may run as two pieces
-//                    per tile finished in the kernel; 0 = never (the
-//                    default: on MI355X each short piece's fill and 256 KiB
-//                    publish, and the finisher's read-back, cost more than
-//                    the short last wave they replace -- config 3 280 vs
-//                    258-261 us).
+// max_workspaces:    library-owned workspaces kept per device (one per
+//                    stream, or per thread on the per-thread default
+//                    stream); beyond it the least recently used idle one is
+//                    freed once its last call has finished.
 Knob g_knobs[] = {
     {"decode_max_m", {64}},
     {"decode_splits", {0}},
@@ -39,7 +37,7 @@ Knob g_knobs[] = {
     {"tile_wgs_per_wave", {256}},
     {"tile_min_kb", {4}},
     {"tile_tail_split", {1}},
-    {"tile_two_piece", {0}},
+    {"max_workspaces", {16}},
 };
 
 }  // namespace

@@ -5,8 +5,17 @@
 // SwiGLU / matmul launches with HIP events instead of a CPU stand-in.
 //
 //   llk-bench [--op=fused_swiglu|matmul] [--M=128] [--N=4096] [--K=4096]
-//             [--out=bf16|f32] [--warmup-ms=500] [--measure-ms=2000]
-//             [--reps=5] [--copies=1] [--seed=42]
+//             [--threads=8] [--out=bf16|f32] [--warmup-ms=500]
+//             [--measure-ms=2000] [--reps=5] [--copies=1] [--seed=42]
+//             [--dry-run]
+//
+// --dry-run prints the parsed shape and the launch the dispatcher would make
+// (llk_describe_launch), and times nothing (no GPU needed).
+//
+// Options take llvm::cl's forms (-M 2048, --M=2048, -M=2048; cl_opts.h);
+// an unknown option exits 1.  --threads is the reference's CPU thread
+// count: accepted so that its scripts run unchanged, and reported as not
+// used (the GPU launch takes its parallelism from the grid).
 //
 // Inputs: X ~ N(0,1), weights ~ N(0, 1/sqrt(K)) in bf16 (llk_fill_normal_bf16),
 // resident in HBM before timing.  --copies rotates that many weight sets so
@@ -21,21 +30,10 @@
 #include <string>
 #include <vector>
 
+#include "cl_opts.h"
 #include "llk/llk_abi.h"
 
 namespace {
-
-std::string opt(int argc, char** argv, const char* name, const char* dflt) {
-  const size_t n = std::strlen(name);
-  for (int i = 1; i < argc; ++i)
-    if (std::strncmp(argv[i], name, n) == 0 && argv[i][n] == '=') return argv[i] + n + 1;
-  return dflt;
-}
-
-int64_t opt_i(int argc, char** argv, const char* name, int64_t dflt) {
-  const std::string v = opt(argc, argv, name, "");
-  return v.empty() ? dflt : std::strtoll(v.c_str(), nullptr, 10);
-}
 
 [[noreturn]] void die(const char* what, const char* msg) {
   std::fprintf(stderr, "llk-bench: %s: %s\n", what, msg);
@@ -59,34 +57,55 @@ double now_ms() {
 }  // namespace
 
 int main(int argc, char** argv) {
-  for (int i = 1; i < argc; ++i)
-    if (!std::strcmp(argv[i], "--help") || !std::strcmp(argv[i], "-h")) {
-      std::printf("llk-bench [--op=fused_swiglu|matmul] [--M=128] [--N=4096] [--K=4096] "
-                  "[--out=bf16|f32] [--warmup-ms=500] [--measure-ms=2000] [--reps=5] "
-                  "[--copies=1] [--seed=42]\n");
-      return 0;
-    }
-  const std::string op = opt(argc, argv, "--op", "fused_swiglu");
-  const int64_t M = opt_i(argc, argv, "--M", 128), N = opt_i(argc, argv, "--N", 4096),
-                K = opt_i(argc, argv, "--K", 4096);
-  const std::string out = opt(argc, argv, "--out", "bf16");
-  const int64_t warmup_ms = opt_i(argc, argv, "--warmup-ms", 500);
-  const int64_t measure_ms = opt_i(argc, argv, "--measure-ms", 2000);
-  const int reps = (int)opt_i(argc, argv, "--reps", 5);
-  const int copies = (int)std::max<int64_t>(1, opt_i(argc, argv, "--copies", 1));
-  const uint64_t seed = (uint64_t)opt_i(argc, argv, "--seed", 42);
+  std::string op = "fused_swiglu", out = "bf16";
+  int64_t M = 128, N = 4096, K = 4096, threads = 8, warmup_ms = 500, measure_ms = 2000, reps = 5,
+          copies = 1, seed_opt = 42;
+  llk_tools::Options cl("llk-bench", "LLK kernel benchmark (gfx950)");
+  cl.add_str("op", &op, "Operation: fused_swiglu or matmul");
+  cl.add_int("M", &M, "M dimension (rows)");
+  cl.add_int("N", &N, "N dimension (hidden)");
+  cl.add_int("K", &K, "K dimension (input)");
+  cl.add_int("threads", &threads, "Thread count (CPU; not used by the GPU launch)");
+  cl.add_str("out", &out, "Output type: bf16 or f32");
+  cl.add_int("warmup-ms", &warmup_ms, "Warmup milliseconds");
+  cl.add_int("measure-ms", &measure_ms, "Measurement milliseconds");
+  cl.add_int("reps", &reps, "Measurement repetitions");
+  cl.add_int("copies", &copies, "Weight sets rotated between launches");
+  cl.add_int("seed", &seed_opt, "Input generator seed");
+  bool dry = false;
+  cl.add_flag("dry-run", &dry, "Print the shape and launch plan; time nothing");
+  if (!cl.parse(argc, argv)) return 1;
+  copies = std::max<int64_t>(1, copies);
+  const uint64_t seed = (uint64_t)seed_opt;
   const bool swiglu = op == "fused_swiglu";
   if (!swiglu && op != "matmul") die("--op", "fused_swiglu or matmul");
   if (out != "bf16" && out != "f32") die("--out", "bf16 or f32");
   if (M < 1 || N < 1 || K < 1 || reps < 1) die("shape", "M, N, K and reps must be positive");
+  if (threads < 1) die("--threads", "must be positive");
   const int y_dtype = out == "bf16" ? LLK_BF16 : LLK_FP32;
+  if (dry) {
+    llk_launch_plan plan;
+    check_llk(llk_describe_launch(swiglu ? 0 : 3, M, N, K, LLK_PLAN_X_ALIGNED, &plan), "plan");
+    std::printf("LLK Bench (dry run) — op=%s M=%lld N=%lld K=%lld threads=%lld out=%s "
+                "warmup-ms=%lld measure-ms=%lld reps=%lld copies=%lld\n",
+                op.c_str(), (long long)M, (long long)N, (long long)K, (long long)threads,
+                out.c_str(), (long long)warmup_ms, (long long)measure_ms, (long long)reps,
+                (long long)copies);
+    std::printf("plan: kernel=%s splits=%d group_width=%d workgroups=%lld launches=%lld "
+                "workspace=%zu\n",
+                plan.kernel ? "mfma_tile" : "small_m", plan.splits, plan.group_width,
+                (long long)plan.workgroups, (long long)plan.launches, plan.workspace_bytes);
+    return 0;
+  }
 
   char arch[64] = {0};
   int cus = 0, lds = 0, clk = 0;
   check_llk(llk_device_info(arch, sizeof arch, &cus, &lds, &clk), "device");
-  std::printf("LLK Bench — op=%s M=%lld N=%lld K=%lld out=%s device=%s CUs=%d copies=%d\n",
-              op.c_str(), (long long)M, (long long)N, (long long)K, out.c_str(), arch, cus,
-              copies);
+  std::printf("LLK Bench — op=%s M=%lld N=%lld K=%lld threads=%lld out=%s device=%s CUs=%d "
+              "copies=%lld\n",
+              op.c_str(), (long long)M, (long long)N, (long long)K, (long long)threads,
+              out.c_str(), arch, cus, (long long)copies);
+  std::printf("note: --threads is not used on the GPU (the launch grid covers %d CUs)\n", cus);
 
   // Host inputs (generator streams: X 0, Wg 1, Wu 2), packed once per copy.
   std::vector<uint16_t> x((size_t)M * K), w((size_t)K * N);
@@ -148,8 +167,8 @@ int main(int argc, char** argv) {
   const double flops = 2.0 * nmat * (double)M * N * K;
   const double bytes = 2.0 * nmat * (double)K * N + 2.0 * M * K +
                        (double)M * N * (y_dtype == LLK_BF16 ? 2 : 4);
-  std::printf("Best: %.1f GFLOPS (%.6f ms/iter, %d reps)\n", flops / (best_ms * 1e-3) / 1e9,
-              best_ms, reps);
+  std::printf("Best: %.1f GFLOPS (%.6f ms/iter, %lld reps)\n", flops / (best_ms * 1e-3) / 1e9,
+              best_ms, (long long)reps);
   std::printf("      %.1f TFLOP/s, %.1f GB/s of algorithmic bytes (%.0f B/launch)\n",
               flops / (best_ms * 1e-3) / 1e12, bytes / (best_ms * 1e-3) / 1e9, bytes);
   for (auto* pw : packed) llk_packed_weights_free(pw);

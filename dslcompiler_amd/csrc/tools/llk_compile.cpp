@@ -4,6 +4,8 @@
 //   llk-compile <input.mlir> [--M=<dim>] [--N=<dim>] [--K=<dim>]
 //               [--schedule-db=<path>] [--quiet]
 //
+// Options take llvm::cl's forms (-M 2048, --M=2048; cl_opts.h); an unknown
+// option or a missing input exits 1.
 // Reads an MLIR module with llk.fused_swiglu / llk.matmul ops in the
 // reference's textual form, checks every op with the reference verifier's
 // rules (llk_verify_fused_swiglu / llk_verify_matmul), resolves dynamic
@@ -20,138 +22,19 @@
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
+#include <functional>
 #include <sstream>
 #include <string>
 #include <vector>
 
+#include "cl_opts.h"
 #include "llk/llk_abi.h"
+#include "runtime/mlir_scan.h"
 
 namespace {
 
-struct TensorType {
-  std::vector<int64_t> dims;  // -1 = dynamic
-  std::string elem;
-};
-
-struct OpInfo {
-  std::string func, kind;  // kind: fused_swiglu | matmul
-  std::vector<TensorType> ins, outs;
-  std::string math_mode = "bounded_fast";
-  int line = 0;
-};
-
-bool parse_tensor(const std::string& s, size_t pos, TensorType* t, size_t* end) {
-  // tensor<AxBx...xELEM>
-  const size_t open = s.find('<', pos), close = s.find('>', pos);
-  if (open == std::string::npos || close == std::string::npos || close < open) return false;
-  const std::string body = s.substr(open + 1, close - open - 1);
-  std::vector<std::string> parts;
-  std::stringstream ss(body);
-  std::string p;
-  while (std::getline(ss, p, 'x')) parts.push_back(p);
-  if (parts.empty()) return false;
-  t->elem = parts.back();
-  t->dims.clear();
-  for (size_t i = 0; i + 1 < parts.size(); ++i) {
-    if (parts[i] == "?") {
-      t->dims.push_back(-1);
-    } else {
-      char* e = nullptr;
-      const long long v = std::strtoll(parts[i].c_str(), &e, 10);
-      if (!e || *e) return false;
-      t->dims.push_back(v);
-    }
-  }
-  *end = close + 1;
-  return true;
-}
-
-// Tensor types after the ':' of an ins(...) / outs(...) group.
-bool parse_group(const std::string& s, size_t start, const char* tag, std::vector<TensorType>* out,
-                 size_t* end) {
-  const size_t g = s.find(tag, start);
-  if (g == std::string::npos) return false;
-  const size_t close = s.find(')', g);
-  const size_t colon = s.find(':', g);
-  if (close == std::string::npos || colon == std::string::npos || colon > close) return false;
-  size_t pos = colon;
-  while (true) {
-    const size_t t = s.find("tensor<", pos);
-    if (t == std::string::npos || t > close) break;
-    TensorType tt;
-    size_t e;
-    if (!parse_tensor(s, t, &tt, &e)) return false;
-    out->push_back(tt);
-    pos = e;
-  }
-  *end = close + 1;
-  return true;
-}
-
-std::vector<OpInfo> scan(const std::string& text, std::string* err) {
-  std::vector<OpInfo> ops;
-  std::string func = "<module>";
-  size_t pos = 0;
-  while (pos < text.size()) {
-    const size_t f = text.find("func.func @", pos);
-    const size_t a = text.find("llk.fused_swiglu", pos);
-    const size_t b = text.find("llk.matmul", pos);
-    const size_t op = std::min(a, b);
-    if (op == std::string::npos) break;
-    if (f != std::string::npos && f < op) {
-      const size_t n0 = f + 11, n1 = text.find_first_of("( ", n0);
-      func = "@" + text.substr(n0, n1 - n0);
-      pos = n1;
-      continue;
-    }
-    OpInfo o;
-    o.func = func;
-    o.kind = (op == a) ? "fused_swiglu" : "matmul";
-    o.line = 1 + (int)std::count(text.begin(), text.begin() + op, '\n');
-    size_t e1, e2;
-    if (!parse_group(text, op, "ins(", &o.ins, &e1) ||
-        !parse_group(text, e1, "outs(", &o.outs, &e2)) {
-      *err = "line " + std::to_string(o.line) + ": cannot parse operands of llk." + o.kind;
-      return {};
-    }
-    const size_t attr = text.find('{', e2), arrow = text.find("->", e2);
-    if (attr != std::string::npos && (arrow == std::string::npos || attr < arrow)) {
-      const size_t close = text.find('}', attr);
-      const std::string dict = text.substr(attr, close - attr);
-      const size_t mm = dict.find("#llk.math_mode<");
-      if (mm != std::string::npos) {
-        const size_t s0 = mm + 15, s1 = dict.find('>', s0);
-        o.math_mode = dict.substr(s0, s1 - s0);
-      }
-    }
-    ops.push_back(o);
-    pos = e2;
-  }
-  return ops;
-}
-
-int64_t arg_value(int argc, char** argv, const char* name, int64_t dflt, bool* ok) {
-  const size_t n = std::strlen(name);
-  for (int i = 1; i < argc; ++i) {
-    if (std::strncmp(argv[i], name, n) != 0) continue;
-    const char* v = nullptr;
-    if (argv[i][n] == '=') v = argv[i] + n + 1;
-    else if (argv[i][n] == '\0' && i + 1 < argc) v = argv[i + 1];
-    if (!v) continue;
-    char* e = nullptr;
-    const long long x = std::strtoll(v, &e, 10);
-    if (!e || *e) *ok = false;
-    return x;
-  }
-  return dflt;
-}
-
-std::string arg_string(int argc, char** argv, const char* name, const std::string& dflt) {
-  const size_t n = std::strlen(name);
-  for (int i = 1; i < argc; ++i)
-    if (std::strncmp(argv[i], name, n) == 0 && argv[i][n] == '=') return argv[i] + n + 1;
-  return dflt;
-}
+using llk::mlir_scan::OpInfo;
+using llk::mlir_scan::scan;
 
 std::string default_db(const char* argv0) {
   std::string exe = argv0;
@@ -168,28 +51,17 @@ int fail(const std::string& msg) {
 }  // namespace
 
 int main(int argc, char** argv) {
-  std::string input;
-  for (int i = 1; i < argc; ++i) {
-    if (argv[i][0] != '-') {
-      // a bare value following "--M" etc. is not the input
-      if (i > 1 && argv[i - 1][0] == '-' && std::strchr(argv[i - 1], '=') == nullptr &&
-          std::strcmp(argv[i - 1], "--quiet") != 0)
-        continue;
-      input = argv[i];
-      break;
-    }
-  }
-  if (input.empty())
-    return fail("usage: llk-compile <input.mlir> [--M=<dim>] [--N=<dim>] [--K=<dim>] "
-                "[--schedule-db=<path>] [--quiet]");
-  bool ok = true;
-  const int64_t optM = arg_value(argc, argv, "--M", 0, &ok);
-  const int64_t optN = arg_value(argc, argv, "--N", 0, &ok);
-  const int64_t optK = arg_value(argc, argv, "--K", 0, &ok);
-  if (!ok) return fail("--M/--N/--K take integers");
-  const std::string db = arg_string(argc, argv, "--schedule-db", default_db(argv[0]));
+  std::string input, db = default_db(argv[0]);
+  int64_t optM = 0, optN = 0, optK = 0;
   bool quiet = false;
-  for (int i = 1; i < argc; ++i) quiet |= std::strcmp(argv[i], "--quiet") == 0;
+  llk_tools::Options cl("llk-compile", "LLK compiler driver (gfx950)");
+  cl.add_positional(&input, "<input .mlir>", true);
+  cl.add_int("M", &optM, "M dimension (rows)");
+  cl.add_int("N", &optN, "N dimension (cols)");
+  cl.add_int("K", &optK, "K dimension (hidden)");
+  cl.add_str("schedule-db", &db, "Schedule database (schedule_db.json)");
+  cl.add_flag("quiet", &quiet, "Print only the final line");
+  if (!cl.parse(argc, argv)) return 1;
 
   std::ifstream f(input);
   if (!f) return fail("Failed to parse " + input);
@@ -279,8 +151,8 @@ int main(int argc, char** argv) {
     key.thread_count = 1;
     key.compiler_version = 1;
     key.schedule_version = 1;
-    llk_kernel_fn fn = nullptr;
-    if (llk_cache_lookup_or_compile(cache, &key, &fn) != LLK_OK) {
+    llk_kernel_fn fn = nullptr;  // the key's entry (also checks the op has a gfx950 kernel)
+    if (llk_cache_lookup_or_compile_packed(cache, &key, &fn) != LLK_OK) {
       rc = fail(where + llk_last_error());
       break;
     }
@@ -308,6 +180,23 @@ int main(int argc, char** argv) {
                   plan.kernel ? "mfma_tile" : "small_m", plan.splits, plan.group_width, plan.pad_x,
                   (long long)plan.workgroups, (long long)plan.threads_per_workgroup,
                   (long long)plan.launches, plan.workspace_bytes);
+    }
+  }
+  if (!rc) {
+    // The module's KernelFn under the key the reference's driver derives
+    // (llk-compile.cpp:298-310): "llk_" + hash of the module text + the
+    // --M/--N/--K values.  (The reference hashes the module as printed after
+    // its pipeline; here the input text is hashed.)
+    const std::string text = buf.str();
+    const std::string cacheKey = "llk_" + std::to_string(std::hash<std::string>{}(text)) + "_M" +
+                                 std::to_string(optM) + "_N" + std::to_string(optN) + "_K" +
+                                 std::to_string(optK);
+    llk_memref_kernel_fn fn = nullptr;
+    if (llk_cache_lookup_or_compile_str(cache, cacheKey.c_str(), text.data(), text.size(), &fn) !=
+        LLK_OK) {
+      rc = fail(std::string("JIT compilation failed: ") + llk_last_error());
+    } else if (!quiet) {
+      std::printf("entry: %s\n", cacheKey.c_str());
     }
   }
   llk_cache_destroy(cache);

@@ -5,8 +5,11 @@
 // candidate is launched and timed on the GPU.
 //
 //   llk-tune [--op=fused_swiglu|matmul] [--M=128] [--N=4096] [--K=4096]
-//            [-o=tune_result.json] [--top=3] [--measure-ms=200]
+//            [-o tune_result.json] [--top=3] [--measure-ms=200]
 //            [--copies=0] [--dry-run]
+//
+// Options take llvm::cl's forms (-M 2048, --M=2048, -o out.json;
+// cl_opts.h); an unknown option exits 1.
 //
 // Candidates are the dispatcher's launch knobs for the shape's kernel:
 // small-M kernel (M <= 64): the dispatcher's own choice (width and splits
@@ -30,25 +33,11 @@
 #include <string>
 #include <vector>
 
+#include "cl_opts.h"
 #include "llk/llk_abi.h"
 
 namespace {
 
-std::string opt(int argc, char** argv, const char* name, const char* dflt) {
-  const size_t n = std::strlen(name);
-  for (int i = 1; i < argc; ++i)
-    if (std::strncmp(argv[i], name, n) == 0 && argv[i][n] == '=') return argv[i] + n + 1;
-  return dflt;
-}
-int64_t opt_i(int argc, char** argv, const char* name, int64_t dflt) {
-  const std::string v = opt(argc, argv, name, "");
-  return v.empty() ? dflt : std::strtoll(v.c_str(), nullptr, 10);
-}
-bool flag(int argc, char** argv, const char* name) {
-  for (int i = 1; i < argc; ++i)
-    if (!std::strcmp(argv[i], name)) return true;
-  return false;
-}
 [[noreturn]] void die(const char* what, const char* msg) {
   std::fprintf(stderr, "llk-tune: %s: %s\n", what, msg);
   std::exit(1);
@@ -75,14 +64,21 @@ struct Candidate {
 }  // namespace
 
 int main(int argc, char** argv) {
-  const std::string op = opt(argc, argv, "--op", "fused_swiglu");
-  const int64_t M = opt_i(argc, argv, "--M", 128), N = opt_i(argc, argv, "--N", 4096),
-                K = opt_i(argc, argv, "--K", 4096);
-  std::string outp = opt(argc, argv, "-o", "");
-  if (outp.empty()) outp = opt(argc, argv, "--output", "tune_result.json");
-  const int top = (int)std::max<int64_t>(1, opt_i(argc, argv, "--top", 3));
-  const int64_t measure_ms = opt_i(argc, argv, "--measure-ms", 200);
-  const bool dry = flag(argc, argv, "--dry-run");
+  std::string op = "fused_swiglu", outp = "tune_result.json";
+  int64_t M = 128, N = 4096, K = 4096, top_opt = 3, measure_ms = 200, copies_opt = 0;
+  bool dry = false;
+  llk_tools::Options cl("llk-tune", "LLK autotuning search (gfx950, measured)");
+  cl.add_str("op", &op, "Operation: fused_swiglu or matmul");
+  cl.add_int("M", &M, "M dimension (rows)");
+  cl.add_int("N", &N, "N dimension (hidden)");
+  cl.add_int("K", &K, "K dimension (input)");
+  cl.add_str("o", &outp, "Output JSON file");
+  cl.add_int("top", &top_opt, "Records written, best first");
+  cl.add_int("measure-ms", &measure_ms, "Measurement milliseconds per window");
+  cl.add_int("copies", &copies_opt, "Weight sets rotated between launches (0: automatic)");
+  cl.add_flag("dry-run", &dry, "Generate configs without measuring");
+  if (!cl.parse(argc, argv)) return 1;
+  const int top = (int)std::max<int64_t>(1, top_opt);
   const bool swiglu = op == "fused_swiglu";
   if (!swiglu && op != "matmul") die("--op", "fused_swiglu or matmul");
   if (M < 1 || N < 1 || K < 1) die("shape", "M, N, K must be positive");
@@ -91,7 +87,7 @@ int main(int argc, char** argv) {
   const int bucket = llk_classify_m(M);
   const bool small = M <= 64;
   const int64_t KB = (K + 63) / 64;
-  int copies = (int)opt_i(argc, argv, "--copies", 0);
+  int copies = (int)copies_opt;
   if (copies <= 0) {
     const double wbytes = 2.0 * nmat * (double)K * N;
     copies = small ? (int)std::min(8.0, std::ceil(3.0 * 256e6 / wbytes)) : 1;

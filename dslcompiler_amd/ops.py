@@ -297,16 +297,31 @@ def swiglu_scratch_size(M: int, N: int, K: int) -> int:
     return int(lib().llk_swiglu_scratch_size(M, N, K))
 
 
-def describe_launch(op: str, M: int, N: int, K: int, x_aligned: bool = True) -> dict:
-    """The dispatcher's launch for op 'fused_swiglu' or 'matmul' (host only)."""
+def describe_launch(op: str, M: int, N: int, K: int, x_aligned: bool = True,
+                    accumulate: bool = False) -> dict:
+    """The dispatcher's launch for op 'fused_swiglu' or 'matmul' (host only);
+    accumulate: the plan of the C += A B matmul."""
     code = {"fused_swiglu": 0, "matmul": 3}[op]
+    flags = (_lib.LLK_PLAN_X_ALIGNED if x_aligned else 0) | (
+        _lib.LLK_PLAN_ACCUMULATE if accumulate else 0)
     p = _lib.LaunchPlan()
-    check(lib().llk_describe_launch(code, M, N, K, int(x_aligned), C.byref(p)))
+    check(lib().llk_describe_launch(code, M, N, K, flags, C.byref(p)))
     return {"kernel": ("small_m", "tile")[p.kernel], "splits": p.splits,
             "group_width": p.group_width, "pad_x": bool(p.pad_x), "workgroups": p.workgroups,
             "threads_per_workgroup": p.threads_per_workgroup, "launches": p.launches,
-            "workspace_bytes": p.workspace_bytes, "head_blocks_n": p.head_blocks_n,
-            "two_piece_kb": p.two_piece_kb}
+            "workspace_bytes": p.workspace_bytes, "head_blocks_n": p.head_blocks_n}
+
+
+def workspace_stats() -> tuple[int, int]:
+    """(count, bytes) of the library-owned workspaces on the current device."""
+    n, b = C.c_size_t(), C.c_size_t()
+    check(lib().llk_workspace_stats(C.byref(n), C.byref(b)))
+    return n.value, b.value
+
+
+def workspace_trim() -> None:
+    """Frees every idle, uncaptured library workspace of the current device."""
+    check(lib().llk_workspace_trim())
 
 
 def classify_m(M: int) -> int:

@@ -22,11 +22,7 @@ For one call the model takes the dispatcher's launch plan
     time    = max(compute, memory, per_cu, shortest launch) + reduce
               + (launches - 1) x launch gap.
 A tile-kernel tail split (head_blocks_n > 0) is two such launches in a row:
-the leading columns unsplit, the remaining columns with the k split.  A
-two-piece tail (two_piece_kb > 0) runs its T tiles' long pieces (kb_cut 64-k
-blocks) on T CUs while the other CUs take r = ceil(T / (CUs - T)) short
-pieces each: max(long piece, r short pieces), plus the slots (two 256 KiB
-per tile) written and read back at the stream rate.
+the leading columns unsplit, the remaining columns with the k split.
 The small-M kernel's MFMA work counts whole 32-row groups.
 """
 from __future__ import annotations
@@ -81,28 +77,6 @@ def _tile_launch(cal: dict, cus: int, nmat: int, M: int, N: int, K: int, S: int,
     return compute, nbytes / cal["stream_bytes_per_s"], per_cu, reduce
 
 
-def _two_piece_launch(cal: dict, cus: int, M: int, N: int, K: int, tiles: int,
-                      kb_cut: int) -> tuple[float, float, float, float]:
-    """(compute, memory, per_cu, reduce) seconds of a two-piece SwiGLU launch."""
-    KB = math.ceil(K / 64)
-    w_rate = (cal["tile_hbm_weight_bytes_per_cu_s"] if math.ceil(M / 256) == 1
-              else cal["tile_l2_bytes_per_cu_s"])
-
-    def piece(kpart):
-        c = 2.0 * 256 * 256 * kpart / cal["tile_flops_per_cu"]
-        pc = (256 * kpart * 2.0 / w_rate
-              + min(M, 256) * kpart * 2.0 / cal["tile_l2_bytes_per_cu_s"])
-        return c, pc
-
-    r = math.ceil(tiles / max(1, cus - tiles))
-    cl, pl = piece(kb_cut * 64)
-    cs, ps = piece((KB - kb_cut) * 64)
-    slots = tiles * 256 * 1024 * 2.0  # one 256 KiB slot per tile, written and read back
-    nbytes = 4.0 * K * N + 2.0 * M * K + 2.0 * M * N + slots
-    return max(cl, r * cs), nbytes / cal["stream_bytes_per_s"], max(pl, r * ps) + \
-        slots / cal["stream_bytes_per_s"], 0.0
-
-
 def predict(op: str, M: int, N: int, K: int, machine_path: str = str(MACHINE)) -> dict:
     m = machine(machine_path)
     # YAML 1.1 reads 1.0e12 as a string: convert explicitly
@@ -121,10 +95,6 @@ def predict(op: str, M: int, N: int, K: int, machine_path: str = str(MACHINE)) -
             segs = [(head_nb * 128, 1, head_wgs),
                     (N - head_nb * 128, S, plan["workgroups"] - head_wgs)]
         parts = [_tile_launch(cal, cus, nmat, M, n, K, s, wgs) for n, s, wgs in segs]
-        if plan.get("two_piece_kb", 0) > 0:
-            tail_tiles = (plan["workgroups"] - head_wgs) // 2
-            parts[-1] = _two_piece_launch(cal, cus, M, N - head_nb * 128, K, tail_tiles,
-                                          plan["two_piece_kb"])
         compute, memory, per_cu, reduce = (sum(p[i] for p in parts) for i in range(4))
         t = sum(max(c, mem, pc, cal["launch_min_s"]) + r for c, mem, pc, r in parts) + gap
     else:

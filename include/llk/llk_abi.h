@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define LLK_ABI_VERSION 3
+#define LLK_ABI_VERSION 4
 
 /* Status codes.  The reference returns errors as llvm::Expected /
  * StringError (JitCache.cpp:200-224); this ABI uses negative integers. */
@@ -199,8 +199,14 @@ size_t llk_swiglu_scratch_size(int64_t M, int64_t N, int64_t K);
  * values: 0 fused SwiGLU, 3 matmul) on an M x N x K problem -- the role of
  * the reference's ShapeSpecialization + ScheduleSelection passes
  * (ShapeSpecialization.cpp:38-48, ScheduleSelection.cpp:46-67) for this
- * backend.  x_aligned: X rows are 16-byte aligned with K % 8 == 0 (else the
- * worst case is assumed).  Host-only, no HIP call. */
+ * backend.  flags: LLK_PLAN_X_ALIGNED -- X rows are 16-byte aligned with
+ * K % 8 == 0 (else the worst case, a padded copy of X, is assumed);
+ * LLK_PLAN_ACCUMULATE -- the plan of llk_gemm_bf16_accumulate (matmul only),
+ * which always ends with the reduce launch that adds C and needs its
+ * partial planes even unsplit.  workspace_bytes is then exactly the
+ * ctx->scratch size that call needs.  Host-only, no HIP call. */
+#define LLK_PLAN_X_ALIGNED 1u
+#define LLK_PLAN_ACCUMULATE 2u
 typedef struct llk_launch_plan {
   int kernel;                    /* 0 small-M bandwidth kernel, 1 MFMA tile kernel */
   int splits;                    /* k splits across workgroups (1 = none) */
@@ -209,19 +215,27 @@ typedef struct llk_launch_plan {
   int64_t workgroups;            /* of the main kernel, per row chunk (all its launches) */
   int64_t threads_per_workgroup; /* of the main kernel */
   int64_t launches;              /* kernel launches per call */
-  size_t workspace_bytes;        /* = ctx->scratch size the call needs (Y rows
-                                    assumed 16-byte aligned) */
+  size_t workspace_bytes;        /* = ctx->scratch size the call needs */
   int64_t head_blocks_n;         /* tile kernel: leading 128-column blocks launched
                                     without k split before the rest takes `splits`
                                     (0 = one launch over all columns) */
-  int64_t two_piece_kb;          /* tile kernel, > 0: the columns from head_blocks_n on
-                                    run as two pieces per tile (64-k blocks [0, this)
-                                    and the rest), finished in the kernel by the
-                                    second to arrive (splits = 2, no reduce launch;
-                                    the head's whole tiles in the same launch) */
 } llk_launch_plan;
-int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, int x_aligned,
+int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, unsigned flags,
                         llk_launch_plan* out);
+
+/* Library-owned workspaces of the current device (no reference
+ * counterpart; for long-running callers that watch device memory).  When a
+ * call gets no ctx->scratch, the library uses a workspace of its own per
+ * stream (per thread for the per-thread default stream), grown on demand,
+ * and keeps at most the tunable "max_workspaces" (default 16) per device:
+ * a further stream evicts the least recently used idle one.  A buffer is
+ * freed only after the last call that used it has finished on the GPU; one
+ * used while its stream was capturing a HIP graph is kept until the process
+ * ends.  llk_workspace_stats reports the live workspaces and their bytes;
+ * llk_workspace_trim frees every idle, uncaptured one (waiting for its last
+ * call). */
+int llk_workspace_stats(size_t* count, size_t* bytes);
+int llk_workspace_trim(void);
 
 /* micro.mma matmul  C = A B  (MicroOps.td:196-222, MicroOps.cpp:246-291;
  * llk.matmul, LLKOps.td:210-255, accumulator f32), i.e. with a zero initial
@@ -324,10 +338,8 @@ int llk_fill_normal_bf16(uint64_t seed, uint64_t stream, float sigma,
  * "tile_splits" (force the tile kernel's k-split count, 0 = cost model),
  * "tile_wgs_per_wave", "tile_min_kb", "tile_tail_split" (1: the columns
  * of a partial last wave of tiles may run as a separate k-split launch;
- * 0: never; a forced "tile_splits" also turns it off), "tile_two_piece"
- * (1: SwiGLU's partial last wave may run as two pieces per tile finished
- * in the kernel, see llk_launch_plan.two_piece_kb; 0, the default: never,
- * measured slower on MI355X; also off with a forced "tile_splits").
+ * 0: never; a forced "tile_splits" also turns it off), "max_workspaces"
+ * (library-owned workspaces kept per device, see llk_workspace_stats).
  * Returns LLK_OK or LLK_ERR_INVALID_ARGUMENT for an unknown name. */
 int llk_set_tunable(const char* name, int64_t value);
 int llk_get_tunable(const char* name, int64_t* value);
@@ -395,9 +407,27 @@ typedef struct llk_cache_stats {
   size_t evictions[4];
 } llk_cache_stats;
 
-/* A gfx950 entry point as held by the object-code level: the shape of
- * llk_swiglu_bf16 (w1 is ignored by GEMM entries).  Counterpart of
- * JitCache::KernelFn (JitCache.h:79-81). */
+/* MemRef2D (JitCache.h:43-51): the same seven fields in the same order (56
+ * bytes).  Element strides; the data address is aligned + offset elements. */
+typedef struct llk_memref2d {
+  void* allocated;
+  void* aligned;
+  int64_t offset;
+  int64_t size0;
+  int64_t size1;
+  int64_t stride0;
+  int64_t stride1;
+} llk_memref2d;
+
+/* JitCache::KernelFn (JitCache.h:79-81): x, wg, wu, init, result.  No
+ * return value: the calling thread's status of its last KernelFn call is
+ * llk_kernel_fn_status(), its message llk_last_error(). */
+typedef void (*llk_memref_kernel_fn)(llk_memref2d* x, llk_memref2d* wg, llk_memref2d* wu,
+                                     llk_memref2d* init, llk_memref2d* result);
+
+/* The other shape of an object-code entry: packed-weight handles, a
+ * stream and a workspace, with llk_swiglu_bf16's signature (w1 is ignored
+ * by matmul entries).  No reference counterpart. */
 typedef int (*llk_kernel_fn)(const llk_tensor2d* x, const llk_packed_weights* w0,
                              const llk_packed_weights* w1, llk_tensor2d* y, int y_dtype,
                              llk_kernel_context* ctx);
@@ -405,29 +435,51 @@ typedef int (*llk_kernel_fn)(const llk_tensor2d* x, const llk_packed_weights* w0
 typedef struct llk_jit_cache llk_jit_cache;
 
 /* JitCache() / ~JitCache().  Destroying the cache frees the packed-weight
- * handles it owns. */
+ * handles it owns (release acquired references first). */
 int llk_cache_create(llk_jit_cache** out);
 void llk_cache_destroy(llk_jit_cache* c);
 
-/* lookupOrCompile(KernelKey) (JitCache.cpp:182-250): the L3 entry for the
- * key, or on a miss the entry point of the key's gfx950 code object
- * (inserted into L3).  Code objects are compiled ahead of time, one per
- * operation (llk_fused_swiglu_gfx950.hsaco, llk_matmul_gfx950.hsaco; see
- * llk_code_object_path): on a miss the key's object is read and checked
- * (64-bit AMDGPU ELF, gfx950, defines kernels) and, when a HIP device is
- * present, loaded on the current device with hipModuleLoadData and its
- * kernels resolved with hipModuleGetFunction (else at the entry's first
- * call on a device; each device loads it once, and it stays loaded until
- * the process ends).  The entry runs the operation with that object's
- * kernels, for the key's output type only (another y_dtype:
- * LLK_ERR_DTYPE).  Errors: LLK_ERR_UNSUPPORTED_ARCH (isa != 7, or the
- * object is not for gfx950), LLK_ERR_DTYPE (input not bf16, output not
- * bf16/fp32), LLK_ERR_INVALID_ARGUMENT (RoPE, Attention or an unknown
+/* lookupOrCompile(const KernelKey&, ModuleOp) (JitCache.h:107-109,
+ * JitCache.cpp:247-250): the KernelFn of the key -- from L3, or on a miss
+ * from the key's gfx950 code object, inserted into L3.  Code objects are
+ * compiled ahead of time, one per operation (llk_fused_swiglu_gfx950.hsaco,
+ * llk_matmul_gfx950.hsaco; see llk_code_object_path), so no module is
+ * passed: on a miss the key's object is read and checked (64-bit AMDGPU
+ * ELF, gfx950, defines kernels) and, when a HIP device is present, loaded
+ * on the current device with hipModuleLoadData and its kernels resolved
+ * with hipModuleGetFunction (else at the entry's first call on a device;
+ * each device loads it once, and it stays loaded until the process ends).
+ * The entry has the reference's KernelFn shape and behaviour -- that of
+ * llk_swiglu_kernel_fn (below), result element type = the key's output
+ * type -- but runs the kernels of the loaded code object, the pack kernel
+ * included.  For a matmul key the entry computes result = init + x wg
+ * (linalg.matmul's outs(init) semantics; wu is unused and may be NULL).
+ * Errors: LLK_ERR_UNSUPPORTED_ARCH (isa != 7, or the object is not for
+ * gfx950), LLK_ERR_DTYPE (input not bf16; output not bf16/f32, or f16 for
+ * a matmul), LLK_ERR_INVALID_ARGUMENT (RoPE, Attention or an unknown
  * operation; N or K < 1; a file that is no code object), LLK_ERR_NOT_FOUND
  * (the key's code object is missing), LLK_ERR_HIP (the load failed).  On an
  * error nothing is inserted. */
 int llk_cache_lookup_or_compile(llk_jit_cache* c, const llk_kernel_key* key,
-                                llk_kernel_fn* out);
+                                llk_memref_kernel_fn* out);
+
+/* The same L3 entry in its packed-handle shape (llk_kernel_fn), bound to
+ * the key's output type (another y_dtype: LLK_ERR_DTYPE).  No reference
+ * counterpart. */
+int llk_cache_lookup_or_compile_packed(llk_jit_cache* c, const llk_kernel_key* key,
+                                       llk_kernel_fn* out);
+
+/* lookupOrCompile(const std::string& cache_key, ModuleOp) (JitCache.h:
+ * 103-105, JitCache.cpp:182-245), the overload llk-compile calls with
+ * "llk_" + hash(module) + "_M<M>_N<N>_K<K>" (llk-compile.cpp:298-310): the
+ * L3 entry under `cache_key`, or on a miss the KernelFn of the module's
+ * entry -- its first llk.fused_swiglu or llk.matmul op, in the reference's
+ * MLIR text form (`module`, module_len bytes) -- with the op's result
+ * element type, inserted under cache_key.  A module without such an op is
+ * LLK_ERR_INVALID_ARGUMENT "No exported kernel entry point found in module"
+ * (JitCache.cpp:214-220); other errors as llk_cache_lookup_or_compile. */
+int llk_cache_lookup_or_compile_str(llk_jit_cache* c, const char* cache_key, const char* module,
+                                    size_t module_len, llk_memref_kernel_fn* out);
 
 /* Directory this cache reads code objects from (NULL or "": the default,
  * $LLK_CODE_OBJECT_DIR or else objects/ beside the library).  No
@@ -448,8 +500,9 @@ int llk_code_object_path(int operation, const char* dir, char* buf, size_t cap);
 int llk_code_object_info(const char* path, int* kernel_count, char* names, size_t cap,
                          size_t* len);
 
-/* L3 (JitCache.cpp:256-276): lookup returns 1 on a hit (*out set), 0 on a
- * miss; insert returns LLK_OK. */
+/* L3 (JitCache.cpp:256-276), packed-handle shape: lookup returns 1 on a hit
+ * (*out set), 0 on a miss; insert returns LLK_OK (a later
+ * llk_cache_lookup_or_compile of the key adds the KernelFn shape). */
 int llk_cache_lookup_object_code(llk_jit_cache* c, const llk_kernel_key* key, llk_kernel_fn* out);
 int llk_cache_insert_object_code(llk_jit_cache* c, const llk_kernel_key* key, llk_kernel_fn fn);
 
@@ -463,11 +516,11 @@ int llk_cache_lookup_blob(llk_jit_cache* c, int level, const char* key, size_t k
 
 /* L4 (JitCache.cpp:314-328), holding packed-weight handles instead of
  * blobs.  Insert transfers ownership of `pw` to the cache: a replaced or
- * evicted handle is freed; inserting the handle its key already holds only
- * refreshes the entry; a handle belongs under one key at a time; on
- * LLK_ERR_OUT_OF_MEMORY the handle has been freed.  Lookup returns 1 with
- * a borrowed handle, valid until the entry is evicted or the cache is
- * cleared or destroyed, or 0 on a miss. */
+ * evicted handle is freed once no acquired reference holds it; inserting
+ * the handle its key already holds only refreshes the entry; a handle
+ * belongs under one key at a time; on LLK_ERR_OUT_OF_MEMORY the handle has
+ * been freed.  Lookup returns 1 with a borrowed handle, valid until the
+ * entry is evicted or the cache is cleared or destroyed, or 0 on a miss. */
 int llk_cache_insert_packed_weights(llk_jit_cache* c, const llk_weight_key* key,
                                     llk_packed_weights* pw);
 int llk_cache_lookup_packed_weights(llk_jit_cache* c, const llk_weight_key* key,
@@ -475,9 +528,20 @@ int llk_cache_lookup_packed_weights(llk_jit_cache* c, const llk_weight_key* key,
 /* L4 lookup by (w->data, shape, bk), packing on a miss: from host memory
  * (llk_pack_weights, flags as there) or, with on_device != 0, from device
  * memory (llk_pack_weights_device on the default stream).  The WeightKey is
- * {w->data, hash of (K, N, stride0), bk, 128}.  *out is borrowed as above. */
+ * {w->data, hash of (K, N, stride0), bk, 128}.  One pack per key: callers
+ * that miss on a key being packed wait for that pack and share its handle.
+ * *out is borrowed as above. */
 int llk_cache_get_packed_weights(llk_jit_cache* c, const llk_tensor2d* w, int64_t bk,
                                  int on_device, unsigned flags, llk_packed_weights** out);
+/* llk_cache_get_packed_weights with a counted reference instead of a
+ * borrowed handle (the reference's L4 hands out copies: JitCache.cpp:
+ * 314-320): the handle stays valid, whatever eviction, replacement or
+ * clear does to the level, until every acquire of it on this cache has
+ * been matched by a release.  Release returns LLK_ERR_INVALID_ARGUMENT for
+ * a handle with no reference held. */
+int llk_cache_acquire_packed_weights(llk_jit_cache* c, const llk_tensor2d* w, int64_t bk,
+                                     int on_device, unsigned flags, llk_packed_weights** out);
+int llk_cache_release_packed_weights(llk_jit_cache* c, llk_packed_weights* pw);
 
 /* evictLRU / setMaxEntries (JitCache.cpp:332-363): level 1..4; trims the
  * level to at most max_entries and makes that its capacity.  Returns
@@ -493,43 +557,41 @@ size_t llk_cache_size(const llk_jit_cache* c);
 /* The reference's KernelFn calling convention (JitCache.h:43-51, 79-81)    */
 /* ----------------------------------------------------------------------- */
 
-/* MemRef2D (JitCache.h:43-51): the same seven fields in the same order (56
- * bytes).  Element strides; the data address is aligned + offset elements. */
-typedef struct llk_memref2d {
-  void* allocated;
-  void* aligned;
-  int64_t offset;
-  int64_t size0;
-  int64_t size1;
-  int64_t stride0;
-  int64_t stride1;
-} llk_memref2d;
-
-/* JitCache::KernelFn (JitCache.h:79-81): x, wg, wu, init, result. */
-typedef void (*llk_memref_kernel_fn)(llk_memref2d* x, llk_memref2d* wg, llk_memref2d* wu,
-                                     llk_memref2d* init, llk_memref2d* result);
-
 /* The fused SwiGLU with exactly the KernelFn shape, a drop-in for the
  * function JitCache::lookupOrCompile returns for an llk.fused_swiglu module
  * (JitCache.h:79-109): bf16 x [M, K], raw row-major bf16 wg, wu [K, N],
  * init and result [M, N] (callers pass init == result; init is only
- * shape-checked), result = bf16(SiLU(x wg) * (x wu)).  wg and wu are
- * resolved through the L4 weight level of the current device's cache
- * (llk_kernel_fn_cache; WeightKey = address, shape, BK 64: JitCache.h:143-146,
- * KernelKey.h:114-124), packed on a miss, so repeated calls with the same
- * weight buffers reuse the packed handles (a caller that rewrites a weight
- * buffer in place clears the cache, as with the reference's L4).  Operands
- * may be device memory (used in place) or host memory (staged through
- * device buffers).  Runs on the null stream with the library's workspace
- * for that stream and returns when the result is written, like the
- * reference's JIT'd function.  No return value: the status of the calling
- * thread's last call is llk_kernel_fn_status(), its message llk_last_error(). */
+ * shape-checked), result = bf16(SiLU(x wg) * (x wu)).  Like the JIT'd
+ * function, every call reads wg and wu as they are at the call: they are
+ * packed into the MFMA operand layout on the device (one pack launch per
+ * matrix into a buffer the library owns per device), so a caller may
+ * rewrite a weight buffer in place or reuse its address between calls.
+ * Operands may be device memory (used in place) or host memory (staged
+ * through device buffers).  Runs on the null stream and returns when the
+ * result is written, like the reference's JIT'd function.  Calls on one
+ * device from several threads are safe: they run one at a time.  No return
+ * value: the status of the calling thread's last call is
+ * llk_kernel_fn_status(), its message llk_last_error(). */
 void llk_swiglu_kernel_fn(llk_memref2d* x, llk_memref2d* wg, llk_memref2d* wu,
                           llk_memref2d* init, llk_memref2d* result);
 int llk_kernel_fn_status(void);
-/* The cache llk_swiglu_kernel_fn uses on the current device (created on first
- * use, owned by the library; llk_cache_get_stats / llk_cache_clear apply),
- * or NULL without a device. */
+
+/* Opt-in reuse of packed weights by every KernelFn-shaped call of the
+ * process (llk_swiglu_kernel_fn and the entries of
+ * llk_cache_lookup_or_compile): with on != 0 the caller promises that a
+ * weight buffer's contents never change while its address is in use, and
+ * wg / wu are resolved through the L4 level of the current device's cache
+ * (llk_kernel_fn_cache; WeightKey = address, shape, BK 64: JitCache.h:
+ * 143-146, KernelKey.h:114-124) as counted references, packed on the first
+ * call only.  A caller that then rewrites a buffer in place clears that
+ * cache.  Returns the previous setting (0, the default: pack every call).
+ * No reference counterpart. */
+int llk_kernel_fn_assume_immutable_weights(int on);
+
+/* The cache the KernelFn-shaped calls use on the current device under
+ * llk_kernel_fn_assume_immutable_weights(1) (created on first use, owned by
+ * the library; llk_cache_get_stats / llk_cache_clear apply), or NULL
+ * without a device. */
 llk_jit_cache* llk_kernel_fn_cache(void);
 
 #ifdef __cplusplus

@@ -43,6 +43,7 @@ int main(void) {
   llk_jit_cache* cache = NULL;
   llk_kernel_key key;
   llk_kernel_fn fn = NULL;
+  llk_memref_kernel_fn kfn = NULL;
   llk_weight_key wk;
   (void)unused_size_check;
   CHECK(kernel_fn_shape != NULL);
@@ -80,8 +81,13 @@ int main(void) {
   CHECK(llk_verify_fused_swiglu(2, 4, 4, 8, 4, 8, 3, 8) == LLK_ERR_SHAPE);
   CHECK(strstr(llk_last_error(), "M dimension mismatch") != NULL);
   CHECK(llk_classify_m(1) == 0 && llk_classify_m(4097) == 4);
-  CHECK(llk_describe_launch(0, 2048, 11008, 4096, 1, &plan) == LLK_OK);
-  CHECK(plan.kernel == 1 && plan.workgroups == 688 && plan.two_piece_kb == 0);
+  CHECK(llk_describe_launch(0, 2048, 11008, 4096, LLK_PLAN_X_ALIGNED, &plan) == LLK_OK);
+  CHECK(plan.kernel == 1 && plan.workgroups == 688 && plan.workspace_bytes == 0);
+  /* the accumulating matmul always has its planes and the reduce launch */
+  CHECK(llk_describe_launch(3, 700, 384, 768, LLK_PLAN_X_ALIGNED | LLK_PLAN_ACCUMULATE, &plan) ==
+        LLK_OK);
+  CHECK(plan.workspace_bytes > 0 && plan.launches == 2);
+  CHECK(llk_describe_launch(0, 8, 8, 8, LLK_PLAN_ACCUMULATE, &plan) == LLK_ERR_INVALID_ARGUMENT);
   CHECK(llk_select_schedule("/nonexistent.json", "fused_swiglu", 0, &se, &n) == LLK_ERR_NOT_FOUND);
   CHECK(se.BM == 8 && se.BN == 32 && n == 0); /* built-in default */
 
@@ -93,13 +99,15 @@ int main(void) {
   /* the key's code object is missing from this directory: a status, and
      nothing is cached */
   CHECK(llk_cache_set_object_dir(cache, "/nonexistent-llk-objects") == LLK_OK);
-  CHECK(llk_cache_lookup_or_compile(cache, &key, &fn) == LLK_ERR_NOT_FOUND);
+  CHECK(llk_cache_lookup_or_compile(cache, &key, &kfn) == LLK_ERR_NOT_FOUND);
   CHECK(strstr(llk_last_error(), "/nonexistent-llk-objects/llk_fused_swiglu_gfx950.hsaco") != NULL);
   CHECK(llk_cache_lookup_object_code(cache, &key, &fn) == 0);
   /* the default directory (objects/ beside the library): read and checked
      on this host, loaded on a device at the entry's first call */
   CHECK(llk_cache_set_object_dir(cache, NULL) == LLK_OK);
-  CHECK(llk_cache_lookup_or_compile(cache, &key, &fn) == LLK_OK && fn != NULL &&
+  CHECK(llk_cache_lookup_or_compile(cache, &key, &kfn) == LLK_OK && kfn != NULL &&
+        kfn != llk_swiglu_kernel_fn);
+  CHECK(llk_cache_lookup_or_compile_packed(cache, &key, &fn) == LLK_OK && fn != NULL &&
         fn != llk_swiglu_bf16);
   CHECK(llk_cache_lookup_object_code(cache, &key, &fn) == 1);
   key.M_bucket = 3;
@@ -110,7 +118,7 @@ int main(void) {
   CHECK(llk_cache_insert_packed_weights(cache, &wk, pw) == LLK_OK); /* cache owns pw */
   CHECK(llk_cache_lookup_packed_weights(cache, &wk, &hit) == 1 && hit == pw);
   CHECK(llk_cache_get_stats(cache, &st) == LLK_OK);
-  CHECK(st.hits[2] == 2 && st.misses[2] == 3 && st.hits[3] == 1);
+  CHECK(st.hits[2] == 3 && st.misses[2] == 3 && st.hits[3] == 1);
   CHECK(llk_cache_size(cache) == 3);
   llk_cache_destroy(cache); /* frees pw */
   free(w);

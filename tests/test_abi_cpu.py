@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(llk):
 
 
 def test_abi_version(llk):
-    assert llk.lib().llk_abi_version() == 3
+    assert llk.lib().llk_abi_version() == 4
 
 
 def _t(arr, rows=None, cols=None, stride0=None, stride1=1):
@@ -153,8 +153,8 @@ def test_cache_and_scratch_paths_reject_host_tensors(llk):
     import torch
     from dslcompiler_amd import cache, ops
     jc = cache.JitCache()
-    fn = jc.lookup_or_compile(cache.KernelKey(operation=cache.OP_FUSED_SWIGLU, N=32, K=16,
-                                              isa=cache.ISA_GFX950))
+    fn = jc.lookup_or_compile_packed(cache.KernelKey(operation=cache.OP_FUSED_SWIGLU, N=32,
+                                                     K=16, isa=cache.ISA_GFX950))
     wg = llk.PackedWeights.from_host(normal_bf16(1, 1, (16, 32)), host_only=True)
     x = torch.zeros((4, 16), dtype=torch.bfloat16)
     y = torch.zeros((4, 32), dtype=torch.bfloat16)

@@ -213,20 +213,102 @@ def test_get_packed_weights_host_hits_on_same_buffer():
 def test_lookup_or_compile_selects_entries():
     """gfx950 keys resolve to entries of their operation's code object (read
     and checked here; loaded on a device at first call), one per (object,
-    output type), cached in L3."""
+    output type), cached in L3: the KernelFn shape (MemRef2D) from
+    lookup_or_compile, the packed-handle shape of the same L3 entry from
+    lookup_or_compile_packed."""
     c = JitCache()
     sw = KernelKey(operation=0, isa=7, N=11008, K=4096, M_bucket=4, weight_layout=2)
     mm = KernelKey(operation=3, isa=7, N=4096, K=4096, M_bucket=4, output_type=2)
     f1 = c.lookup_or_compile(sw)
     f2 = c.lookup_or_compile(mm)
+    p1 = c.lookup_or_compile_packed(sw)
+    lib_fn = C.cast(lib().llk_swiglu_kernel_fn, C.c_void_p).value
     swiglu_addr = C.cast(lib().llk_swiglu_bf16, C.c_void_p).value
-    assert len({f1.address, f2.address, swiglu_addr, 0}) == 4
+    assert len({f1.address, f2.address, p1.address, lib_fn, swiglu_addr, 0}) == 6
     assert c.lookup_or_compile(sw).address == f1.address  # L3 hit
+    assert c.lookup_object_code(sw).address == p1.address
     s = c.stats()
-    assert (s["hits"][2], s["misses"][2]) == (1, 2)
+    assert (s["hits"][2], s["misses"][2]) == (3, 2)
     # another key of the same object and output type shares the entry
     assert JitCache().lookup_or_compile(KernelKey(operation=0, isa=7, N=64, K=64)).address == \
         f1.address
+    # a matmul key may ask for f16 (llk.matmul's result types); SwiGLU may not
+    assert c.lookup_or_compile(KernelKey(operation=3, isa=7, N=64, K=64, output_type=1)).address
+    with pytest.raises(llk.LLKError, match="DTYPE"):
+        c.lookup_or_compile(KernelKey(operation=0, isa=7, N=64, K=64, output_type=1))
+
+
+SWIGLU_MODULE = """
+func.func @swiglu(%x: tensor<4x8xbf16>, %wg: tensor<8x16xbf16>, %wu: tensor<8x16xbf16>,
+                  %init: tensor<4x16xbf16>) -> tensor<4x16xbf16> {
+  %0 = llk.fused_swiglu ins(%x, %wg, %wu : tensor<4x8xbf16>, tensor<8x16xbf16>,
+                            tensor<8x16xbf16>) outs(%init : tensor<4x16xbf16>)
+       -> tensor<4x16xbf16>
+  return %0 : tensor<4x16xbf16>
+}
+"""
+MATMUL_F32_MODULE = """
+func.func @mm(%a: tensor<4x8xbf16>, %b: tensor<8x16xbf16>, %c: tensor<4x16xf32>) -> tensor<4x16xf32> {
+  %0 = llk.matmul ins(%a, %b : tensor<4x8xbf16>, tensor<8x16xbf16>) outs(%c : tensor<4x16xf32>)
+       -> tensor<4x16xf32>
+  return %0 : tensor<4x16xf32>
+}
+"""
+
+
+def test_lookup_or_compile_string_key():
+    """The string-keyed overload (JitCache.h:103-105) that llk-compile uses:
+    the module's first llk op picks the code object and output type, the
+    entry is cached under the caller's key, a repeat of the key hits L3
+    without reading the module, and a module with no llk op is the
+    reference's "No exported kernel entry point" error (JitCache.cpp:
+    214-220) with nothing inserted."""
+    c = JitCache()
+    sw_key = KernelKey(operation=0, isa=7, N=16, K=8)
+    f_sw = c.lookup_or_compile_str("llk_1_M4_N16_K8", SWIGLU_MODULE)
+    assert f_sw.address == c.lookup_or_compile(sw_key).address  # same (object, bf16) entry
+    f_mm = c.lookup_or_compile_str("llk_2_M4_N16_K8", MATMUL_F32_MODULE)
+    assert f_mm.address == c.lookup_or_compile(KernelKey(operation=3, isa=7, N=16, K=8,
+                                                         output_type=2)).address
+    assert f_mm.address != f_sw.address
+    n = c.size()
+    assert c.lookup_or_compile_str("llk_1_M4_N16_K8", "not read on a hit").address == f_sw.address
+    assert c.stats()["hits"][2] >= 1 and c.size() == n
+    with pytest.raises(llk.LLKError, match="No exported kernel entry point found in module"):
+        c.lookup_or_compile_str("llk_3", "func.func @f() { return }")
+    with pytest.raises(llk.LLKError, match="DTYPE"):
+        c.lookup_or_compile_str("llk_4", SWIGLU_MODULE.replace("x8xbf16>, tensor<8x16", "x8xf32>, tensor<8x16", 1))
+    assert c.size() == n
+
+
+def test_get_packed_weights_single_flight_threads():
+    """8 threads miss on one key at once (host-only packs of a 2048 x 2048
+    matrix, ~10 ms each, the GIL released in the C call): one pack, one
+    handle for all, one L4 entry; counted references survive a clear."""
+    w = normal_bf16(91, 1, (2048, 2048))
+    c = JitCache()
+    got, start = [None] * 8, threading.Barrier(8)
+
+    def run(i):
+        start.wait()
+        got[i] = c.get_packed_weights(w, 64, host_only=True).handle.value
+
+    th = [threading.Thread(target=run, args=(i,)) for i in range(8)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert len(set(got)) == 1 and got[0]
+    assert c.size() == 1 and c.stats()["evictions"][3] == 0
+    ref = c.acquire_packed_weights(w, 64, host_only=True)
+    assert ref.handle.value == got[0]
+    c.clear()
+    assert c.size() == 0
+    assert np.array_equal(ref.host_data(),
+                          llk.PackedWeights.from_host(w, 64, host_only=True).host_data())
+    c.release_packed_weights(ref)
+    with pytest.raises(llk.LLKError, match="no reference"):
+        c.release_packed_weights(ref)
 
 
 @pytest.mark.parametrize("kw,match", [

@@ -7,6 +7,7 @@ lowering or symbol lookup fails: JitCache.cpp:182-245).  Loading and running
 an entry is tests/test_gpu_code_object.py."""
 from __future__ import annotations
 
+import re
 import shutil
 import struct
 from pathlib import Path
@@ -20,7 +21,7 @@ from dslcompiler_amd.cache import JitCache, KernelKey
 PKG = Path(llk.__file__).resolve().parent
 TILE = "_ZN10llk_gfx95016mfma_tile_kernelI"
 # config 3's whole tiles: mfma_tile_kernel<1, 0, true, false, false>(TileArgs)
-CONFIG3 = TILE + "Li1ELi0ELb1ELb0ELb0EEEvNS_8TileArgsE"
+CONFIG3 = TILE + "Li1ELi0ELb1ELb0EEEvNS_8TileArgsE"
 
 
 def _key(op, out=0):
@@ -44,20 +45,22 @@ def test_objects_hold_their_operations_kernels():
     # tile kernels: MODE 1 only in the SwiGLU object, MODE 0 only in the GEMM one
     assert {k[len(TILE):len(TILE) + 4] for k in sw if k.startswith(TILE)} == {"Li1E"}
     assert {k[len(TILE):len(TILE) + 4] for k in mm if k.startswith(TILE)} == {"Li0E"}
-    # both operations' launchers: tile (5 / 7 instantiations, + the SwiGLU
-    # two-piece form for bf16 and fp32 output), k-split
+    # both operations' launchers: tile (5 / 7 instantiations), k-split
     # reduce, small-M kernels (2 x 3 widths x 2 X paths x output types) and
-    # their reduce, X padding and the K = 0 fill
+    # their reduce, X padding and the K = 0 fill; no tile form waits for
+    # another workgroup (every instantiation has four template arguments)
     def count(names, part):
         return sum(part in k for k in names)
-    assert (count(sw, "mfma_tile_kernel"), count(mm, "mfma_tile_kernel")) == (7, 7)
-    def two_piece(names):
-        return sum(k.startswith(TILE) and k.endswith("Lb1EEEvNS_8TileArgsE") for k in names)
-    assert (two_piece(sw), two_piece(mm)) == (2, 0)
+    assert (count(sw, "mfma_tile_kernel"), count(mm, "mfma_tile_kernel")) == (5, 7)
+    for k in sw + mm:
+        if k.startswith(TILE):
+            args = k[len(TILE):k.index("EEvNS_8TileArgsE")]
+            assert len(re.findall(r"L[ib]\d+E", args)) == 4, k
     assert (count(sw, "13skinny_kernel"), count(mm, "13skinny_kernel")) == (24, 36)
     for names in (sw, mm):
         assert "_Z15pad_rows_kernelPKtliiPtl" in names
         assert "_Z16zero_rows_kernelPhllil" in names
+        assert "_ZN10llk_gfx95016pack_tile_kernelEPKtliiiiPj" in names  # KernelFn entries pack
 
 
 def _expect(path_or_dir, key, match):

@@ -20,10 +20,10 @@ def test_lookup_or_compile_entries_run_on_gpu(llk, gpu):
     pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
     xd = to_dev(gpu, x)
     cache = llk.JitCache()
-    sw = cache.lookup_or_compile(llk.KernelKey(operation=0, isa=7, N=N, K=K, M_bucket=4,
-                                               weight_layout=2))
-    mm = cache.lookup_or_compile(llk.KernelKey(operation=3, isa=7, N=N, K=K, M_bucket=4,
-                                               weight_layout=2, output_type=2))
+    sw = cache.lookup_or_compile_packed(llk.KernelKey(operation=0, isa=7, N=N, K=K, M_bucket=4,
+                                                      weight_layout=2))
+    mm = cache.lookup_or_compile_packed(llk.KernelKey(operation=3, isa=7, N=N, K=K, M_bucket=4,
+                                                      weight_layout=2, output_type=2))
     y = gpu.empty((M, N), dtype=gpu.bfloat16, device="cuda")
     sw(xd, pg, pu, y)
     c = gpu.empty((M, N), dtype=gpu.float32, device="cuda")

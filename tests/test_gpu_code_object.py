@@ -37,7 +37,7 @@ CASES = [
 def _entry(llk, cache, op, N, K, out):
     key = llk.KernelKey(operation=0 if op == "fused_swiglu" else 3, isa=7, N=N, K=K,
                         output_type=OUT[out], M_bucket=llk.classify_m(1))
-    return cache.lookup_or_compile(key)
+    return cache.lookup_or_compile_packed(key)
 
 
 @pytest.mark.parametrize("op,M,N,K,out,what", CASES, ids=[f"{c[0]}-{c[1]}x{c[2]}x{c[3]}"
@@ -49,7 +49,6 @@ def test_entry_matches_library_kernels(llk, gpu, op, M, N, K, out, what):
     assert plan["pad_x"] == ("padded" in what)
     splits = re.search(r"S = (\d+)", what)
     assert plan["splits"] == (int(splits.group(1)) if splits else 1)
-    assert (plan["two_piece_kb"] > 0) == ("two pieces" in what)
     dtype = {"bf16": gpu.bfloat16, "fp32": gpu.float32}[out]
     cache = llk.JitCache()
     fn = _entry(llk, cache, op, N, K, out)

@@ -1,18 +1,26 @@
 """The reference's KernelFn calling convention (JitCache.h:79-81):
-llk_swiglu_kernel_fn(x, wg, wu, init, result) with five 56-byte MemRef2D
-descriptors (JitCache.h:43-51) built here in ctypes, init == result as the
-reference's callers pass them (swiglu_vector_avx2.cpp:278-285), raw
-row-major weights resolved through the L4 weight level (a miss packs, the
-next call with the same buffers hits), against the oracle; with device
-operands and with host operands (the reference's callers' own buffers)."""
+fn(x, wg, wu, init, result) with five 56-byte MemRef2D descriptors
+(JitCache.h:43-51) built here in ctypes, init == result as the reference's
+callers pass them (swiglu_vector_avx2.cpp:278-285), raw row-major weights,
+against the oracle; with device operands and with host operands (the
+reference's callers' own buffers).
+
+Like the reference's JIT'd function, every call reads the weights as they
+are at the call: a buffer rewritten in place gives the new result; two host
+threads calling at once both get right results.  Reuse of packed weights
+across calls is opt-in (llk_kernel_fn_assume_immutable_weights).  The
+object-code level hands out entries of the same shape that run the kernels
+of the key's loaded code object (JitCache.cpp:182-250), also by string key
+(JitCache.h:103-105)."""
 from __future__ import annotations
 
 import ctypes as C
+import threading
 
 import numpy as np
 import pytest
 
-from common import assert_parity_bf16, swiglu_inputs
+from common import assert_parity, assert_parity_bf16, swiglu_inputs
 from gpu_util import from_dev, to_dev
 
 pytestmark = pytest.mark.gpu
@@ -32,6 +40,12 @@ def _l4(llk):
     return st.hits[3], st.misses[3]
 
 
+def _call(llk, mx, mg, mu, my):
+    L = llk.lib()
+    L.llk_swiglu_kernel_fn(C.byref(mx), C.byref(mg), C.byref(mu), C.byref(my), C.byref(my))
+    assert L.llk_kernel_fn_status() == 0, L.llk_last_error()
+
+
 def test_memref_is_56_bytes():
     from dslcompiler_amd._lib import MemRef2D
     assert C.sizeof(MemRef2D) == 56
@@ -39,37 +53,134 @@ def test_memref_is_56_bytes():
 
 @pytest.mark.parametrize("M,K,N", [(8, 1024, 768), (300, 576, 392)])
 def test_kernel_fn_device_operands(llk, gpu, orc, M, K, N):
+    """Device operands used in place; by default the weights are packed on
+    every call (the L4 level is not consulted) and repeated calls give the
+    same bits."""
     print(f"case kernel_fn device M={M} K={K} N={N}", flush=True)
-    L = llk.lib()
     x, wg, wu = swiglu_inputs(M, K, N, seed=M + 5)
     xd, wgd, wud = to_dev(gpu, x), to_dev(gpu, wg), to_dev(gpu, wu)
     y = gpu.full((M, N), float("nan"), dtype=gpu.bfloat16, device="cuda")
-    mx = _memref(xd.data_ptr(), M, K, K)
-    mg = _memref(wgd.data_ptr(), K, N, N)
-    mu = _memref(wud.data_ptr(), K, N, N)
-    my = _memref(y.data_ptr(), M, N, N)
+    mx, mg = _memref(xd.data_ptr(), M, K, K), _memref(wgd.data_ptr(), K, N, N)
+    mu, my = _memref(wud.data_ptr(), K, N, N), _memref(y.data_ptr(), M, N, N)
     yf_ref, _ = orc.swiglu(x, wg, wu)
-    L.llk_cache_clear(L.llk_kernel_fn_cache())  # no stale entry at a reused address
-    hits0, miss0 = _l4(llk)
-    L.llk_swiglu_kernel_fn(C.byref(mx), C.byref(mg), C.byref(mu), C.byref(my), C.byref(my))
-    assert L.llk_kernel_fn_status() == 0, L.llk_last_error()
-    hits1, miss1 = _l4(llk)
-    assert (hits1 - hits0, miss1 - miss0) == (0, 2), "first call: both weights packed (L4 miss)"
+    l4_0 = _l4(llk)
+    _call(llk, mx, mg, mu, my)
     got1 = from_dev(y)
     assert_parity_bf16(got1, yf_ref, "KernelFn device, first call")
     y.fill_(float("nan"))
-    L.llk_swiglu_kernel_fn(C.byref(mx), C.byref(mg), C.byref(mu), C.byref(my), C.byref(my))
-    assert L.llk_kernel_fn_status() == 0, L.llk_last_error()
-    hits2, miss2 = _l4(llk)
-    assert (hits2 - hits1, miss2 - miss1) == (2, 0), "second call: both weights from L4"
+    _call(llk, mx, mg, mu, my)
     assert np.array_equal(from_dev(y), got1)
+    assert _l4(llk) == l4_0, "weights packed per call, not through L4"
+
+
+def test_kernel_fn_sees_weights_rewritten_in_place(llk, gpu, orc):
+    """The caller rewrites wg in place (same address, same shape) between
+    two calls: the second result is that of the new weights, as the
+    reference's JIT'd function, which reads its arguments every call, gives."""
+    print("case kernel_fn in-place weight rewrite", flush=True)
+    M, K, N = 200, 768, 640
+    x, wg, wu = swiglu_inputs(M, K, N, seed=31)
+    _, wg2, _ = swiglu_inputs(M, K, N, seed=32)
+    xd, wgd, wud = to_dev(gpu, x), to_dev(gpu, wg), to_dev(gpu, wu)
+    y = gpu.empty((M, N), dtype=gpu.bfloat16, device="cuda")
+    mx, mg = _memref(xd.data_ptr(), M, K, K), _memref(wgd.data_ptr(), K, N, N)
+    mu, my = _memref(wud.data_ptr(), K, N, N), _memref(y.data_ptr(), M, N, N)
+    _call(llk, mx, mg, mu, my)
+    assert_parity_bf16(from_dev(y), orc.swiglu(x, wg, wu)[0], "before the rewrite")
+    wgd.copy_(to_dev(gpu, wg2))  # same buffer, new contents
+    gpu.cuda.synchronize()
+    _call(llk, mx, mg, mu, my)
+    assert_parity_bf16(from_dev(y), orc.swiglu(x, wg2, wu)[0], "after the in-place rewrite")
+    # host weights likewise
+    wg_h = np.ascontiguousarray(wg)
+    mg_h = _memref(wg_h.ctypes.data, K, N, N)
+    _call(llk, mx, mg_h, mu, my)
+    assert_parity_bf16(from_dev(y), orc.swiglu(x, wg, wu)[0], "host wg")
+    wg_h[:] = wg2
+    _call(llk, mx, mg_h, mu, my)
+    assert_parity_bf16(from_dev(y), orc.swiglu(x, wg2, wu)[0], "host wg rewritten")
+
+
+def test_kernel_fn_two_threads_same_weights(llk, gpu, orc):
+    """Two host threads call the KernelFn at once on the same weight buffers
+    (each with its own X and result), several times each: every result
+    matches the oracle."""
+    print("case kernel_fn two threads", flush=True)
+    K, N = 1024, 1536
+    _, wg, wu = swiglu_inputs(8, K, N, seed=41)
+    wgd, wud = to_dev(gpu, wg), to_dev(gpu, wu)
+    jobs = []
+    for t, M in enumerate((8, 700)):  # one small-M and one tile-kernel shape
+        x, _, _ = swiglu_inputs(M, K, N, seed=50 + t)
+        xd = to_dev(gpu, x)
+        y = gpu.empty((M, N), dtype=gpu.bfloat16, device="cuda")
+        jobs.append((M, x, xd, y))
+    gpu.cuda.synchronize()
+    L = llk.lib()
+    errors, outs = [], [[] for _ in jobs]
+    start = threading.Barrier(len(jobs))
+
+    def run(i):
+        M, _, xd, y = jobs[i]
+        mx, my = _memref(xd.data_ptr(), M, K, K), _memref(y.data_ptr(), M, N, N)
+        mg, mu = _memref(wgd.data_ptr(), K, N, N), _memref(wud.data_ptr(), K, N, N)
+        start.wait()
+        for _ in range(4):
+            L.llk_swiglu_kernel_fn(C.byref(mx), C.byref(mg), C.byref(mu), C.byref(my),
+                                   C.byref(my))
+            if L.llk_kernel_fn_status() != 0:
+                errors.append(L.llk_last_error())
+                return
+            outs[i].append(from_dev(y))  # the call is synchronous: y is final here
+
+    th = [threading.Thread(target=run, args=(i,)) for i in range(len(jobs))]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert not errors, errors
+    for (M, x, _, _), got in zip(jobs, outs):
+        ref = orc.swiglu(x, wg, wu)[0]
+        assert len(got) == 4
+        for g in got:
+            assert_parity_bf16(g, ref, f"thread M={M}")
+            assert np.array_equal(g, got[0])
+
+
+def test_kernel_fn_opt_in_reuse(llk, gpu, orc):
+    """With llk_kernel_fn_assume_immutable_weights(1) the weights resolve
+    through the device cache's L4 level: the first call packs both (two
+    misses), the next hits both, and the result is unchanged."""
+    print("case kernel_fn immutable weights", flush=True)
+    M, K, N = 96, 512, 384
+    x, wg, wu = swiglu_inputs(M, K, N, seed=61)
+    xd, wgd, wud = to_dev(gpu, x), to_dev(gpu, wg), to_dev(gpu, wu)
+    y = gpu.empty((M, N), dtype=gpu.bfloat16, device="cuda")
+    mx, mg = _memref(xd.data_ptr(), M, K, K), _memref(wgd.data_ptr(), K, N, N)
+    mu, my = _memref(wud.data_ptr(), K, N, N), _memref(y.data_ptr(), M, N, N)
+    L = llk.lib()
+    assert L.llk_kernel_fn_assume_immutable_weights(1) == 0
+    try:
+        L.llk_cache_clear(L.llk_kernel_fn_cache())  # no entry at a reused address
+        h0, m0 = _l4(llk)
+        _call(llk, mx, mg, mu, my)
+        h1, m1 = _l4(llk)
+        assert (h1 - h0, m1 - m0) == (0, 2)
+        got = from_dev(y)
+        _call(llk, mx, mg, mu, my)
+        h2, m2 = _l4(llk)
+        assert (h2 - h1, m2 - m1) == (2, 0)
+        assert np.array_equal(from_dev(y), got)
+        assert_parity_bf16(got, orc.swiglu(x, wg, wu)[0], "KernelFn with L4 reuse")
+    finally:
+        assert L.llk_kernel_fn_assume_immutable_weights(0) == 1
+        L.llk_cache_clear(L.llk_kernel_fn_cache())
 
 
 def test_kernel_fn_host_operands_with_offset(llk, gpu, orc):
     """Host buffers as the reference's tests pass them, with a non-zero
     memref offset on X and a padded result row stride."""
     print("case kernel_fn host", flush=True)
-    L = llk.lib()
     M, K, N = 33, 200, 136
     x, wg, wu = swiglu_inputs(M, K, N, seed=77)
     xbuf = np.zeros(M * K + 5, np.uint16)
@@ -80,8 +191,7 @@ def test_kernel_fn_host_operands_with_offset(llk, gpu, orc):
     mg = _memref(wg_h.ctypes.data, K, N, N)
     mu = _memref(wu_h.ctypes.data, K, N, N)
     my = _memref(ybuf.ctypes.data, M, N, N + 8)
-    L.llk_swiglu_kernel_fn(C.byref(mx), C.byref(mg), C.byref(mu), C.byref(my), C.byref(my))
-    assert L.llk_kernel_fn_status() == 0, L.llk_last_error()
+    _call(llk, mx, mg, mu, my)
     yf_ref, _ = orc.swiglu(x, wg, wu)
     assert_parity_bf16(ybuf[:, :N], yf_ref, "KernelFn host operands")
     assert np.all(ybuf[:, N:] == 0xFFFF), "row padding written"
@@ -96,3 +206,60 @@ def test_kernel_fn_reports_errors(llk, gpu):
     L.llk_swiglu_kernel_fn(C.byref(mx), C.byref(mw), C.byref(mw), C.byref(mx), C.byref(mx))
     assert L.llk_kernel_fn_status() == llk._lib.LLK_ERR_SHAPE
     assert b"K dimension mismatch" in L.llk_last_error()
+
+
+def test_object_code_kernel_fn_entries(llk, gpu, orc):
+    """lookupOrCompile hands back the KernelFn of the key (JitCache.cpp:
+    182-250): a MemRef2D-shaped entry that runs the kernels of the key's
+    loaded code object, its pack kernel included.  SwiGLU: bit-equal to
+    llk_swiglu_kernel_fn and to the oracle's bar; matmul (fp32 key):
+    result = init + x wg (linalg.matmul's outs(init)), init != result."""
+    print("case object-code KernelFn entries", flush=True)
+    from dslcompiler_amd import cache as cmod
+    M, K, N = 300, 1000, 640
+    x, wg, wu = swiglu_inputs(M, K, N, seed=71)
+    xd, wgd, wud = to_dev(gpu, x), to_dev(gpu, wg), to_dev(gpu, wu)
+    jc = llk.JitCache()
+    fn = jc.lookup_or_compile(llk.KernelKey(operation=0, isa=7, N=N, K=K, M_bucket=4,
+                                            weight_layout=2))
+    y = gpu.full((M, N), float("nan"), dtype=gpu.bfloat16, device="cuda")
+    fn(xd, wgd, wud, y, y)
+    y_lib = gpu.empty_like(y)
+    cmod.swiglu_kernel_fn(xd, wgd, wud, y_lib, y_lib)
+    assert np.array_equal(from_dev(y), from_dev(y_lib))
+    assert_parity_bf16(from_dev(y), orc.swiglu(x, wg, wu)[0], "object-code KernelFn")
+    # fp32 matmul entry with a separate init
+    mm = jc.lookup_or_compile(llk.KernelKey(operation=3, isa=7, N=N, K=K, output_type=2))
+    init = gpu.randn((M, N), dtype=gpu.float32, device="cuda")
+    c = gpu.full((M, N), float("nan"), dtype=gpu.float32, device="cuda")
+    mm(xd, wgd, None, init, c)
+    ref, _ = orc.gemm(x, wg)
+    assert_parity(from_dev(c), ref + from_dev(init), "object-code matmul KernelFn")
+    # in place (init == result): accumulates again
+    mm(xd, wgd, None, c, c)
+    assert_parity(from_dev(c), 2 * ref + from_dev(init), "matmul KernelFn in place")
+    jc.close()
+
+
+def test_string_keyed_kernel_fn(llk, gpu, orc):
+    """The string-keyed lookupOrCompile (JitCache.h:103-105) with a module in
+    the reference's MLIR text: its KernelFn runs on the GPU."""
+    print("case string-keyed KernelFn", flush=True)
+    M, K, N = 64, 512, 1376
+    module = f"""
+func.func @swiglu(%x: tensor<{M}x{K}xbf16>, %wg: tensor<{K}x{N}xbf16>, %wu: tensor<{K}x{N}xbf16>,
+                  %init: tensor<{M}x{N}xbf16>) -> tensor<{M}x{N}xbf16> {{
+  %0 = llk.fused_swiglu ins(%x, %wg, %wu : tensor<{M}x{K}xbf16>, tensor<{K}x{N}xbf16>,
+                            tensor<{K}x{N}xbf16>) outs(%init : tensor<{M}x{N}xbf16>)
+       -> tensor<{M}x{N}xbf16>
+  return %0 : tensor<{M}x{N}xbf16>
+}}
+"""
+    x, wg, wu = swiglu_inputs(M, K, N, seed=81)
+    xd, wgd, wud = to_dev(gpu, x), to_dev(gpu, wg), to_dev(gpu, wu)
+    jc = llk.JitCache()
+    fn = jc.lookup_or_compile_str(f"llk_{hash(module) & 0xffff}_M{M}_N{N}_K{K}", module)
+    y = gpu.empty((M, N), dtype=gpu.bfloat16, device="cuda")
+    fn(xd, wgd, wud, y, y)
+    assert_parity_bf16(from_dev(y), orc.swiglu(x, wg, wu)[0], "string-keyed KernelFn")
+    jc.close()

@@ -7,7 +7,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from common import assert_parity, bf16_bits_to_f32, normal_bf16, swiglu_inputs
+from common import assert_parity, assert_parity_bf16, bf16_bits_to_f32, normal_bf16, swiglu_inputs
 from gpu_util import from_dev, to_dev
 
 pytestmark = pytest.mark.gpu
@@ -168,3 +168,94 @@ def test_graph_survives_workspace_growth(llk, gpu):
         del junk
     finally:
         llk.set_tunable("tile_splits", old)
+
+
+def test_workspaces_stay_bounded_per_thread_stream(llk, gpu, orc):
+    """Threads launching on the per-thread default stream each get a library
+    workspace of their own; the library keeps at most max_workspaces of
+    them (least recently used freed once its calls are done), every result
+    stays right, and llk_workspace_trim frees the idle ones.  Workspaces
+    that graphs captured earlier in this process are pinned (never freed):
+    the bound is set above what a trim leaves."""
+    import ctypes as C
+    import threading
+    from dslcompiler_amd._lib import KernelContext, tensor2d
+    print("case workspaces per thread bounded", flush=True)
+    M, K, N = 300, 2048, 640
+    x, wg, wu = swiglu_inputs(M, K, N, seed=91)
+    pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
+    xd = to_dev(gpu, x)
+    ref = orc.swiglu(x, wg, wu)[0]
+    old = llk.get_tunable("tile_splits"), llk.get_tunable("max_workspaces")
+    gpu.cuda.synchronize()
+    llk.workspace_trim()
+    pinned = llk.workspace_stats()[0]  # kept for graphs captured by earlier tests
+    llk.set_tunable("tile_splits", 3)  # partial planes: a workspace per call
+    llk.set_tunable("max_workspaces", pinned + 4)
+    L = llk.lib()
+    per_thread = 2  # hipStreamPerThread
+    ys = [gpu.empty((M, N), dtype=gpu.bfloat16, device="cuda") for _ in range(12)]
+    gpu.cuda.synchronize()
+    errors, counts = [], []
+    lock = threading.Lock()
+
+    def run(i):
+        ctx = KernelContext(None, 0, per_thread)
+        xt = tensor2d(xd.data_ptr(), M, K)
+        yt = tensor2d(ys[i].data_ptr(), M, N)
+        for _ in range(3):
+            rc = L.llk_swiglu_bf16(C.byref(xt), pg.handle, pu.handle, C.byref(yt), 0, C.byref(ctx))
+            if rc:
+                errors.append(L.llk_last_error())
+                return
+        with lock:
+            counts.append(llk.workspace_stats()[0])
+
+    try:
+        for batch in range(3):  # 4 threads at a time, 12 distinct threads in all
+            th = [threading.Thread(target=run, args=(4 * batch + i,)) for i in range(4)]
+            for t in th:
+                t.start()
+            for t in th:
+                t.join()
+        gpu.cuda.synchronize()
+        assert not errors, errors
+        assert max(counts) <= pinned + 4, (pinned, counts)
+        n, nbytes = llk.workspace_stats()
+        assert n <= pinned + 4 and nbytes > 0
+        for y in ys:
+            assert_parity_bf16(from_dev(y), ref, "per-thread stream, split 3")
+        llk.workspace_trim()
+        assert llk.workspace_stats()[0] == pinned
+    finally:
+        llk.set_tunable("tile_splits", old[0])
+        llk.set_tunable("max_workspaces", old[1])
+
+
+def test_accumulate_scratch_sized_from_plan(llk, gpu, orc):
+    """llk_describe_launch with LLK_PLAN_ACCUMULATE gives exactly the scratch
+    the accumulating GEMM needs (its partial planes exist even unsplit): a
+    caller buffer of that size works on the S = 1 tile case (M = 700, N =
+    768, K = 384: the plain plan needs no workspace at all), a smaller one is
+    LLK_ERR_SCRATCH, and the result equals the library-workspace call bit
+    for bit."""
+    print("case accumulate scratch from plan", flush=True)
+    M, K, N = 700, 384, 768
+    x, wb, _ = swiglu_inputs(M, K, N, seed=93)
+    xd, pb = to_dev(gpu, x), llk.PackedWeights.from_host(wb)
+    plan = llk.describe_launch("matmul", M, N, K, accumulate=True)
+    assert plan["splits"] == 1 and plan["workspace_bytes"] >= M * N * 4
+    assert llk.describe_launch("matmul", M, N, K)["workspace_bytes"] == 0
+    c0 = gpu.randn((M, N), dtype=gpu.float32, device="cuda")
+    c_lib = c0.clone()
+    llk.matmul(xd, pb, out=c_lib, accumulate=True)
+    c_own = c0.clone()
+    scratch = gpu.empty(plan["workspace_bytes"], dtype=gpu.uint8, device="cuda")
+    llk.matmul(xd, pb, out=c_own, accumulate=True, scratch=scratch)
+    gpu.cuda.synchronize()
+    assert np.array_equal(from_dev(c_own), from_dev(c_lib))
+    ref, _ = orc.gemm(x, wb)
+    assert_parity(from_dev(c_own), ref + from_dev(c0), "accumulate with plan-sized scratch")
+    small = gpu.empty(plan["workspace_bytes"] - 256, dtype=gpu.uint8, device="cuda")
+    with pytest.raises(llk.LLKError, match="SCRATCH"):
+        llk.matmul(xd, pb, out=c0.clone(), accumulate=True, scratch=small)

@@ -25,23 +25,12 @@ def test_model_bounds():
 def test_model_split_phases():
     """A k-split tile launch: the per-CU load term (one m tile: weights from
     HBM, X from L2) plus the partial-plane write burst of a single round,
-    then the reduce kernel as a serial phase.  The SwiGLU two-piece form has
-    no reduce phase: the longer of the long piece and r short ones, plus its
-    slots."""
+    then the reduce kernel as a serial phase."""
     p = perfmodel.predict("matmul", 255, 5120, 13824)
     assert p["plan"]["kernel"] == "tile" and p["plan"]["splits"] == 12
     assert p["per_cu_us"] > max(p["compute_us"], p["memory_us"])
     assert p["reduce_us"] > 0
     assert abs(p["predicted_us"] - (p["per_cu_us"] + p["reduce_us"] + 3.0)) < 1e-6
-    from dslcompiler_amd import get_tunable, set_tunable
-    assert get_tunable("tile_two_piece") == 0
-    set_tunable("tile_two_piece", 1)
-    try:
-        p = perfmodel.predict("fused_swiglu", 255, 13824, 5120)
-    finally:
-        set_tunable("tile_two_piece", 0)
-    assert p["plan"]["two_piece_kb"] == 40 and p["reduce_us"] == 0
-    assert abs(p["predicted_us"] - max(p["compute_us"], p["memory_us"], p["per_cu_us"])) < 1e-6
 
 
 def _engines():

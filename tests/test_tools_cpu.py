@@ -89,6 +89,71 @@ def test_compile_missing_input(tmp_path):
     assert r.returncode == 1 and "Failed to parse" in r.stderr
 
 
+def _tool(name, *args):
+    return subprocess.run([str(BIN / name), *args], capture_output=True, text=True, timeout=60)
+
+
+@pytest.mark.parametrize("args", [
+    ["--M", "2048", "--N", "11008", "--K", "4096"],   # --name value
+    ["-M=2048", "-N=11008", "-K=4096"],               # -name=value
+    ["-M", "2048", "--N=11008", "-K", "4096"],        # mixed
+])
+def test_bench_options_in_llvm_cl_forms(args):
+    """llk-bench takes the reference's llvm::cl options (llk-bench.cpp:21-35)
+    in every form cl accepts; --dry-run reports the parsed shape and plan
+    without a GPU.  --threads (the reference's CPU thread count) is
+    accepted."""
+    r = _tool("llk-bench", *args, "--threads", "16", "--dry-run")
+    assert r.returncode == 0, r.stderr
+    assert "M=2048 N=11008 K=4096 threads=16" in r.stdout
+    assert "kernel=mfma_tile splits=1" in r.stdout and "workgroups=688" in r.stdout
+
+
+@pytest.mark.parametrize("tool,args,msg", [
+    ("llk-bench", ["--bogus"], "Unknown command line argument '--bogus'"),
+    ("llk-bench", ["--threads=2", "-x"], "Unknown command line argument '-x'"),
+    ("llk-bench", ["-M"], "for the -M option: requires a value!"),
+    ("llk-bench", ["-M", "12x"], "'12x' value invalid for integer argument"),
+    ("llk-tune", ["--dry-run=maybe"], "invalid value for boolean argument"),
+    ("llk-tune", ["--threads=8", "--dry-run"], "Unknown command line argument '--threads=8'"),
+    ("llk-compile", [], "Not enough positional command line arguments"),
+    ("llk-compile", ["a.mlir", "b.mlir"], "Too many positional arguments"),
+])
+def test_tools_reject_bad_options(tool, args, msg):
+    """Unknown options and malformed values exit 1 with cl's message instead
+    of silently running the defaults."""
+    r = _tool(tool, *args)
+    assert r.returncode == 1, r.stdout
+    assert msg in r.stderr
+
+
+def test_tune_output_option_forms(tmp_path):
+    """llk-tune -o <file> (llk-tune.cpp:27-28) writes that file in every
+    form; the default stays tune_result.json in the working directory."""
+    for i, form in enumerate((["-o", "a.json"], ["-o=b.json"], ["--o", "c.json"])):
+        r = subprocess.run([str(BIN / "llk-tune"), "-M", "2048", "--N=11008", "-K", "4096",
+                            "--dry-run", *form], capture_output=True, text=True, timeout=60,
+                           cwd=tmp_path)
+        assert r.returncode == 0, r.stderr
+        name = "abc"[i] + ".json"
+        assert (tmp_path / name).exists() and f"to {name}" in r.stdout
+        assert "M=2048 (bucket 4) N=11008 K=4096" in r.stdout
+    r = subprocess.run([str(BIN / "llk-tune"), "--dry-run"], capture_output=True, text=True,
+                       timeout=60, cwd=tmp_path)
+    assert r.returncode == 0 and (tmp_path / "tune_result.json").exists()
+    assert "M=128 (bucket 4) N=4096 K=4096" in r.stdout  # the reference's defaults
+
+
+def test_compile_string_keyed_entry(tmp_path):
+    """llk-compile derives the reference's cache key, "llk_" + hash of the
+    module + "_M.._N.._K.." (llk-compile.cpp:298-310), and obtains the
+    module's KernelFn through the string-keyed lookupOrCompile."""
+    r = _compile(tmp_path, _swiglu_fn("f", 8, 4096, 14336), "-M", "8", "-N=14336", "--K", "4096")
+    assert r.returncode == 0, r.stderr
+    line = [l for l in r.stdout.splitlines() if l.startswith("entry: llk_")]
+    assert len(line) == 1 and line[0].endswith("_M8_N14336_K4096"), r.stdout
+
+
 def test_verifiers_exported():
     L = llk.lib()
     assert L.llk_verify_fused_swiglu(2, 4, 4, 8, 4, 8, 2, 8) == 0
@@ -185,7 +250,7 @@ def test_tile_tail_split_plans():
     off; a forced split count wins."""
     p = llk.describe_launch("matmul", 4097, 5120, 13824)
     assert (p["head_blocks_n"], p["splits"], p["workgroups"], p["launches"]) == (30, 3, 510, 3)
-    assert p["workspace_bytes"] == 64 * 1024 + 3 * 4097 * 10 * 128 * 4  # counters + planes
+    assert p["workspace_bytes"] == 3 * 4097 * 10 * 128 * 4  # the tail columns' planes
     p = llk.describe_launch("fused_swiglu", 4097, 13824, 5120)
     assert (p["head_blocks_n"], p["splits"], p["workgroups"], p["launches"]) == (105, 5, 2040, 3)
     for op, M, N, K in [("matmul", 4096, 4096, 4096), ("matmul", 1000, 5120, 13824),
@@ -199,37 +264,6 @@ def test_tile_tail_split_plans():
             assert p["head_blocks_n"] == 0 and p["workgroups"] == 340 * p["splits"]
         finally:
             llk.set_tunable(name, old)
-
-
-def test_two_piece_plans():
-    """SwiGLU's partial last wave as two pieces per tile (T tail tiles on T
-    CUs for the long pieces, r = ceil(T / (256 - T)) short ones on each
-    other CU): config 3 (176 tail tiles, r = 3: cut 49 of 64), config 5 at
-    M = 1000 (176, cut 61 of 80) and M = 255 (all 108 tiles, r = 1: an even
-    cut); one launch each (the whole tiles of the head in the same grid as
-    the pieces), no reduce.  Never for the GEMM, a forced split count,
-    the knob at 0 (its default: measured slower on MI355X), or a workspace
-    limit the slots do not fit (the no-allocation entry point's 64 MiB)."""
-    assert llk.get_tunable("tile_two_piece") == 0
-    assert llk.describe_launch("fused_swiglu", 2048, 11008, 4096)["two_piece_kb"] == 0
-    llk.set_tunable("tile_two_piece", 1)
-    try:
-        for M, N, K, head, cut, wgs, launches in [(2048, 11008, 4096, 64, 49, 864, 1),
-                                                  (1000, 13824, 5120, 64, 61, 608, 1),
-                                                  (255, 13824, 5120, 0, 40, 216, 1)]:
-            p = llk.describe_launch("fused_swiglu", M, N, K)
-            assert (p["head_blocks_n"], p["two_piece_kb"], p["workgroups"], p["launches"],
-                    p["splits"]) == (head, cut, wgs, launches, 2), M
-        assert all(llk.describe_launch("matmul", M, 5120, 13824)["two_piece_kb"] == 0
-                   for M in (255, 1000, 2048))
-        llk.set_tunable("tile_splits", 1)
-        try:
-            p = llk.describe_launch("fused_swiglu", 2048, 11008, 4096)
-            assert (p["two_piece_kb"], p["workgroups"], p["splits"]) == (0, 688, 1)
-        finally:
-            llk.set_tunable("tile_splits", 0)
-    finally:
-        llk.set_tunable("tile_two_piece", 0)
 
 
 def test_small_m_cost_model_choices():
