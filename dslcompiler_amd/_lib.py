@@ -31,6 +31,7 @@ LLK_PACK_KEEP_HOST = 1
 LLK_PACK_HOST_ONLY = 2
 LLK_PLAN_X_ALIGNED = 1
 LLK_PLAN_ACCUMULATE = 2
+LLK_PLAN_OUT_F32 = 4
 
 STATUS_NAMES = {
     0: "LLK_OK", -1: "LLK_ERR_INVALID_ARGUMENT", -2: "LLK_ERR_SHAPE", -3: "LLK_ERR_DTYPE",
@@ -84,7 +85,8 @@ class LaunchPlan(C.Structure):
     _fields_ = [("kernel", C.c_int), ("splits", C.c_int), ("group_width", C.c_int),
                 ("pad_x", C.c_int), ("workgroups", C.c_int64),
                 ("threads_per_workgroup", C.c_int64), ("launches", C.c_int64),
-                ("workspace_bytes", C.c_size_t), ("head_blocks_n", C.c_int64)]
+                ("workspace_bytes", C.c_size_t), ("head_blocks_n", C.c_int64),
+                ("tile_columns", C.c_int64)]
 
 
 class MemRef2D(C.Structure):

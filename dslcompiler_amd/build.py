@@ -43,6 +43,7 @@ INCLUDES = [f"-I{ROOT / 'include'}", f"-I{CSRC}"]
 
 HIP_SOURCES = [
     CSRC / "kernels" / "mfma_tile.hip",
+    CSRC / "kernels" / "swiglu_wide.hip",
     CSRC / "kernels" / "swiglu_decode.hip",
     CSRC / "kernels" / "pack.hip",
     CSRC / "llk_abi.cpp",  # host code that calls the HIP runtime

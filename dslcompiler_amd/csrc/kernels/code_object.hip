@@ -7,5 +7,6 @@
 #error "LLK_CO_OP must be 0 (GEMM) or 1 (fused SwiGLU)"
 #endif
 #include "mfma_tile.hip"
+#include "swiglu_wide.hip"
 #include "pack.hip"
 #include "swiglu_decode.hip"

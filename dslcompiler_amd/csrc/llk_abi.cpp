@@ -35,6 +35,10 @@ hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void*
                            const llk::ModuleFns* mod, hipStream_t s);
 size_t llk_tile_split_bytes(int mode, int M, int NB, int S, bool accumulate);
 bool llk_tile_x_fits(int M, int64_t ldx);
+hipError_t llk_launch_swiglu_wide(int B, const uint16_t* x, int64_t ldx, const void* wg,
+                                  const void* wu, void* y, int64_t ldy, int M, int N, int KB,
+                                  int NB, const llk::ModuleFns* mod, hipStream_t s);
+bool llk_swiglu_wide_fits(int B, int KB);
 hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                              const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
                              int NB, int S, int G, void* ws, int out_dtype, bool xvec,
@@ -343,6 +347,8 @@ struct Plan {
   size_t ws_bytes = 0;   // workspace the plan needs
   bool too_large = false;  // tile path: K beyond the kernel's 32-bit offsets
   int64_t head_nb = 0;   // tile path: leading n-blocks launched unsplit (S applies to the rest)
+  int wide = 0;          // tile path, fused SwiGLU with bf16 output: the wide kernel's B
+                         // (16 B columns per tile and matrix; 0 = the 128-column kernel)
 };
 
 // k splits of the tile kernel for `rows` rows: the S that minimises the
@@ -386,26 +392,55 @@ SplitCost best_split(int nmat, int64_t rows, int64_t KB, int64_t NB, int64_t for
 struct TilePlan {
   int S;
   int64_t head_nb;
+  double cost;  // modelled time, in the units of best_split
 };
 
 TilePlan tile_plan(int nmat, int64_t rows, int64_t KB, int64_t NB, int64_t db_splits) {
   int64_t forced = llk::tunable("tile_splits");
   if (forced <= 0) forced = db_splits;
   const SplitCost all = best_split(nmat, rows, KB, NB, forced);
-  if (forced > 0) return {all.S, 0};
+  if (forced > 0) return {all.S, 0, all.cost};
   const int64_t nb_per_tile = nmat == 2 ? 1 : 2;
   const int64_t tm = (rows + 255) / 256, tn = (NB + nb_per_tile - 1) / nb_per_tile;
   const int64_t per_wave = std::max<int64_t>(1, llk::tunable("tile_wgs_per_wave"));
   const int64_t head_tn = tm * tn / per_wave * per_wave / tm;  // columns of q whole waves
-  TilePlan best{all.S, 0};
+  TilePlan best{all.S, 0, all.cost};
   double best_cost = all.cost;
   if (llk::tunable("tile_tail_split") != 0 && head_tn > 0 && head_tn < tn) {
     const int64_t head_nb = head_tn * nb_per_tile;
     const double head = (double)((tm * head_tn + per_wave - 1) / per_wave) * (double)(KB + 2);
     const SplitCost tail = best_split(nmat, rows, KB, NB - head_nb, 0);
     if (head + tail.cost <= 0.97 * best_cost) {
-      best = {tail.S, head_nb};
+      best = {tail.S, head_nb, head + tail.cost};
       best_cost = head + tail.cost;
+    }
+  }
+  return best;
+}
+
+// Wide SwiGLU tiles (kernels/swiglu_wide.hip): B blocks of 16 columns per
+// matrix instead of 8, unsplit.  Modelled like best_split: waves of
+// workgroups x (64-k steps + 2), each workgroup B/8 times the work of a
+// 128-column tile.  Taken when 3% or more below the 128-column plan's cost
+// (config 3: 504 tiles in 2 waves x 1.375 against 688 in 3 waves; config 5 at
+// M = 1000: 496 tiles of B = 7 in 2 waves x 0.875 against 432 in 2 waves).
+// tile_wide = 7 or 11 forces that width; 0 turns the kernel off.
+int wide_choice(int64_t rows, int64_t N, int64_t KB, double std_cost) {
+  const int64_t knob = llk::tunable("tile_wide");
+  if (knob == 0) return 0;
+  const int64_t per_wave = std::max<int64_t>(1, llk::tunable("tile_wgs_per_wave"));
+  const int64_t tm = (rows + 255) / 256;
+  int best = 0;
+  double best_cost = 0.97 * std_cost;
+  for (int B : {11, 7}) {
+    if (!llk_swiglu_wide_fits(B, (int)KB)) continue;
+    if (knob == B) return B;
+    if (knob != 1) continue;
+    const int64_t tiles = tm * ((N + 16 * B - 1) / (16 * B));
+    const double cost = (double)((tiles + per_wave - 1) / per_wave) * (double)(KB + 2) * B / 8.0;
+    if (cost < best_cost) {
+      best = B;
+      best_cost = cost;
     }
   }
   return best;
@@ -512,7 +547,7 @@ SmallMChoice small_m_choice(int nmat, int64_t M, int64_t KB, int64_t NB, int64_t
 // accumulate (GEMM, C += A B): the tile path takes the partial planes at any
 // S (the reduce adds C) and no tail split.
 Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const llk_tensor2d* x,
-                 size_t max_ws = SIZE_MAX, bool accumulate = false) {
+                 size_t max_ws = SIZE_MAX, bool accumulate = false, bool out_bf16 = true) {
   Plan p;
   llk::ScheduleEntry se;
   const bool have_db = db_entry(nmat, M, &se);
@@ -548,6 +583,16 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
   const TilePlan tp = tile_plan(nmat, rows, KB, NB, have_db ? se.grain_size : 0);
   p.S = tp.S;
   p.head_nb = accumulate ? 0 : tp.head_nb;
+  // The wide kernel: fused SwiGLU, bf16 output, no k split (a forced split
+  // count or a DB entry with one keeps the 128-column kernel).
+  const bool split_forced = llk::tunable("tile_splits") > 0 || (have_db && se.grain_size > 1);
+  if (nmat == 2 && out_bf16 && !accumulate && !split_forced) {
+    p.wide = wide_choice(rows, NB * 128, KB, tp.cost);
+    if (p.wide) {
+      p.S = 1;
+      p.head_nb = 0;
+    }
+  }
   if (accumulate && tp.head_nb > 0) p.S = best_split(nmat, rows, KB, NB, 0).S;
   auto body = [&](int64_t crows) {
     return p.pad_bytes + llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)crows,
@@ -597,7 +642,8 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
                     bool accumulate = false) {
   const int64_t M = x->dim0, K = x->dim1;
   const int nmat = mode == 1 ? 2 : 1;
-  const Plan p = plan_launch(nmat, M, K, w0->KB, w0->NB, x, max_ws, accumulate);
+  const Plan p = plan_launch(nmat, M, K, w0->KB, w0->NB, x, max_ws, accumulate,
+                             out_dtype == LLK_BF16);
   if (p.too_large)
     return fail(LLK_ERR_SHAPE, "%s: K=%lld too large for M=%lld (the tile kernel needs K <= %lld)",
                 what, (long long)K, (long long)M, (long long)(((int64_t)1 << 31) / 512 - 64));
@@ -643,6 +689,11 @@ int launch_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights
       xp = reinterpret_cast<const uint16_t*>(body);
     }
     uint8_t* yp = static_cast<uint8_t*>(y->data) + m0 * y->stride0 * ysz;
+    if (p.wide) {
+      e = llk_launch_swiglu_wide(p.wide, xp, p.ld, w0->dev, w1->dev, yp, y->stride0, rows, (int)N,
+                                 (int)w0->KB, (int)w0->NB, mod, s);
+      continue;
+    }
     if (p.head_nb > 0) {
       e = llk_launch_tile(mode, xp, p.ld, w0->dev, w1 ? w1->dev : nullptr, yp, y->stride0, rows,
                           (int)(p.head_nb * 128), (int)w0->KB, (int)p.head_nb, 1, nullptr,
@@ -1062,7 +1113,11 @@ int llk_packed_weights_load(const char* path, unsigned flags, llk_packed_weights
 
 size_t llk_swiglu_scratch_size(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  return plan_launch(2, M, K, llk::deviceBlocksK(K), llk::deviceBlocksN(N), nullptr).ws_bytes;
+  // Either output type (the bf16 plan may take the wide kernel, which needs
+  // no partial planes).
+  const int64_t KB = llk::deviceBlocksK(K), NB = llk::deviceBlocksN(N);
+  return std::max(plan_launch(2, M, K, KB, NB, nullptr, SIZE_MAX, false, true).ws_bytes,
+                  plan_launch(2, M, K, KB, NB, nullptr, SIZE_MAX, false, false).ws_bytes);
 }
 
 int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, unsigned flags,
@@ -1071,7 +1126,7 @@ int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, unsigned
   *out = llk_launch_plan{};
   if (operation != 0 && operation != 3)
     return fail(LLK_ERR_INVALID_ARGUMENT, "operation %d has no gfx950 kernel", operation);
-  if (flags & ~(LLK_PLAN_X_ALIGNED | LLK_PLAN_ACCUMULATE))
+  if (flags & ~(LLK_PLAN_X_ALIGNED | LLK_PLAN_ACCUMULATE | LLK_PLAN_OUT_F32))
     return fail(LLK_ERR_INVALID_ARGUMENT, "unknown plan flags 0x%x", flags);
   const bool accumulate = (flags & LLK_PLAN_ACCUMULATE) != 0;
   if (accumulate && operation != 3)
@@ -1084,7 +1139,8 @@ int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, unsigned
   // pointer's alignment, the row stride and K).
   const bool x_aligned = (flags & LLK_PLAN_X_ALIGNED) != 0;
   llk_tensor2d x{reinterpret_cast<void*>(x_aligned ? 256 : 2), M, K, x_aligned ? K : K + 1, 1};
-  const Plan p = plan_launch(nmat, M, K, KB, NB, &x, SIZE_MAX, accumulate);
+  const Plan p = plan_launch(nmat, M, K, KB, NB, &x, SIZE_MAX, accumulate,
+                             (flags & LLK_PLAN_OUT_F32) == 0);
   if (p.too_large)
     return fail(LLK_ERR_SHAPE, "K=%lld too large for M=%lld (the tile kernel needs K <= %lld)",
                 (long long)K, (long long)M, (long long)(((int64_t)1 << 31) / 512 - 64));
@@ -1103,10 +1159,18 @@ int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, unsigned
   out->pad_x = p.pad ? 1 : 0;
   const int64_t rows = std::min(p.chunk, M);
   const int64_t chunks = (M + p.chunk - 1) / p.chunk;
+  out->threads_per_workgroup = 256;
+  if (p.wide) {
+    out->kernel = 2;
+    out->tile_columns = 16 * p.wide;
+    out->workgroups = (rows + 255) / 256 * ((N + 16 * p.wide - 1) / (16 * p.wide));
+    out->launches = chunks * (1 + (p.pad ? 1 : 0));
+    return LLK_OK;
+  }
+  out->tile_columns = nmat == 2 ? 128 : 256;
   const int64_t nb_per_tile = nmat == 2 ? 1 : 2, tail_nb = NB - p.head_nb;
   out->workgroups = (rows + 255) / 256 *
                     (p.head_nb / nb_per_tile + (tail_nb + nb_per_tile - 1) / nb_per_tile * p.S);
-  out->threads_per_workgroup = 256;
   // An accumulating launch always ends with the reduce (it adds C).
   out->launches = chunks * (1 + (p.head_nb > 0 ? 1 : 0) + (p.pad ? 1 : 0) +
                             (p.S > 1 || accumulate ? 1 : 0));

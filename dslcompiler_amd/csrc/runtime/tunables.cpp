@@ -23,6 +23,10 @@ struct Knob {
 // tile_min_kb:       fewest 64-k steps per tile-kernel split.
 // tile_tail_split:   1 = the tile kernel may run the columns of its last,
 //                    partial wave as a separate k-split launch; 0 = never.
+// tile_wide:         fused SwiGLU with bf16 output: 1 = the cost model may
+//                    take the wide tile kernel (16 B columns per matrix, B = 7
+//                    or 11) where its whole waves beat the 128-column tile;
+//                    0 = never; 7 or 11 = that width whenever it applies.
 // max_workspaces:    library-owned workspaces kept per device (one per
 //                    stream, or per thread on the per-thread default
 //                    stream); beyond it the least recently used idle one is
@@ -37,6 +41,7 @@ Knob g_knobs[] = {
     {"tile_wgs_per_wave", {256}},
     {"tile_min_kb", {4}},
     {"tile_tail_split", {1}},
+    {"tile_wide", {1}},
     {"max_workspaces", {16}},
 };
 

@@ -22,6 +22,11 @@
 
 namespace llk_tools {
 
+// Name of llk_launch_plan::kernel.
+inline const char* kernel_name(int kernel) {
+  return kernel == 0 ? "small_m" : kernel == 1 ? "mfma_tile" : "swiglu_wide";
+}
+
 class Options {
  public:
   Options(const char* tool, const char* overview) : tool_(tool), overview_(overview) {}

@@ -93,7 +93,7 @@ int main(int argc, char** argv) {
                 (long long)copies);
     std::printf("plan: kernel=%s splits=%d group_width=%d workgroups=%lld launches=%lld "
                 "workspace=%zu\n",
-                plan.kernel ? "mfma_tile" : "small_m", plan.splits, plan.group_width,
+                llk_tools::kernel_name(plan.kernel), plan.splits, plan.group_width,
                 (long long)plan.workgroups, (long long)plan.launches, plan.workspace_bytes);
     return 0;
   }

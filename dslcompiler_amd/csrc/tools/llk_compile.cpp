@@ -177,7 +177,7 @@ int main(int argc, char** argv) {
       std::printf("  key=0x%016llx math_mode=%s\n", (unsigned long long)h, o.math_mode.c_str());
       std::printf("  kernel=%s splits=%d group_width=%d pad_x=%d workgroups=%lld threads=%lld "
                   "launches=%lld workspace=%zu\n",
-                  plan.kernel ? "mfma_tile" : "small_m", plan.splits, plan.group_width, plan.pad_x,
+                  llk_tools::kernel_name(plan.kernel), plan.splits, plan.group_width, plan.pad_x,
                   (long long)plan.workgroups, (long long)plan.threads_per_workgroup,
                   (long long)plan.launches, plan.workspace_bytes);
     }

@@ -298,18 +298,20 @@ def swiglu_scratch_size(M: int, N: int, K: int) -> int:
 
 
 def describe_launch(op: str, M: int, N: int, K: int, x_aligned: bool = True,
-                    accumulate: bool = False) -> dict:
+                    accumulate: bool = False, out_f32: bool = False) -> dict:
     """The dispatcher's launch for op 'fused_swiglu' or 'matmul' (host only);
-    accumulate: the plan of the C += A B matmul."""
+    accumulate: the plan of the C += A B matmul; out_f32: SwiGLU with an fp32
+    result instead of bf16."""
     code = {"fused_swiglu": 0, "matmul": 3}[op]
     flags = (_lib.LLK_PLAN_X_ALIGNED if x_aligned else 0) | (
-        _lib.LLK_PLAN_ACCUMULATE if accumulate else 0)
+        _lib.LLK_PLAN_ACCUMULATE if accumulate else 0) | (_lib.LLK_PLAN_OUT_F32 if out_f32 else 0)
     p = _lib.LaunchPlan()
     check(lib().llk_describe_launch(code, M, N, K, flags, C.byref(p)))
-    return {"kernel": ("small_m", "tile")[p.kernel], "splits": p.splits,
+    return {"kernel": ("small_m", "tile", "wide_tile")[p.kernel], "splits": p.splits,
             "group_width": p.group_width, "pad_x": bool(p.pad_x), "workgroups": p.workgroups,
             "threads_per_workgroup": p.threads_per_workgroup, "launches": p.launches,
-            "workspace_bytes": p.workspace_bytes, "head_blocks_n": p.head_blocks_n}
+            "workspace_bytes": p.workspace_bytes, "head_blocks_n": p.head_blocks_n,
+            "tile_columns": p.tile_columns}
 
 
 def workspace_stats() -> tuple[int, int]:

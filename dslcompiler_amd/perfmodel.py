@@ -22,7 +22,9 @@ For one call the model takes the dispatcher's launch plan
     time    = max(compute, memory, per_cu, shortest launch) + reduce
               + (launches - 1) x launch gap.
 A tile-kernel tail split (head_blocks_n > 0) is two such launches in a row:
-the leading columns unsplit, the remaining columns with the k split.
+the leading columns unsplit, the remaining columns with the k split.  The
+wide SwiGLU kernel is the tile kernel's model with 2 x tile_columns MFMA
+rows per workgroup, unsplit.
 The small-M kernel's MFMA work counts whole 32-row groups.
 """
 from __future__ import annotations
@@ -45,10 +47,12 @@ def machine(path: str = str(MACHINE)) -> dict:
 
 
 def _tile_launch(cal: dict, cus: int, nmat: int, M: int, N: int, K: int, S: int,
-                 workgroups: int) -> tuple[float, float, float, float]:
+                 workgroups: int, rows: int = 256) -> tuple[float, float, float, float]:
     """(compute, memory, per_cu, reduce) seconds of one tile-kernel launch
-    over N columns with S k splits (and its reduce kernel when S > 1)."""
-    # Workgroup tile: 256 m x 256 MFMA rows (SwiGLU: 128 n of Wg + 128 n of Wu).
+    over N columns with S k splits (and its reduce kernel when S > 1).
+    rows: MFMA rows of the workgroup tile -- 256 for mfma_tile_kernel
+    (SwiGLU: 128 n of Wg + 128 n of Wu), 2 x 16 B for the wide SwiGLU kernel
+    (16 B columns of each matrix)."""
     kpart = math.ceil(K / 64) * 64 / S
     rounds = math.ceil(workgroups / cus)
     # A partly filled round runs at a higher clock: the board holds
@@ -58,12 +62,12 @@ def _tile_launch(cal: dict, cus: int, nmat: int, M: int, N: int, K: int, S: int,
     occ /= cus
     f_full, f_idle = cal["tile_clock_full_hz"], cal["tile_clock_idle_hz"]
     eff_rounds = full + (f_full / (f_idle - (f_idle - f_full) * occ) if occ else 0.0)
-    compute = eff_rounds * 2.0 * 256 * 256 * kpart / cal["tile_flops_per_cu"]
+    compute = eff_rounds * 2.0 * 256 * rows * kpart / cal["tile_flops_per_cu"]
     # Per-CU loads: one m tile means every weight byte comes from HBM
     # once; with more m tiles the panels are re-read from L2 / MALL.
     w_rate = (cal["tile_hbm_weight_bytes_per_cu_s"] if math.ceil(M / 256) == 1
               else cal["tile_l2_bytes_per_cu_s"])
-    per_cu = rounds * (256 * kpart * 2.0 / w_rate
+    per_cu = rounds * (rows * kpart * 2.0 / w_rate
                        + min(M, 256) * kpart * 2.0 / cal["tile_l2_bytes_per_cu_s"])
     reduce = 0.0
     if S > 1:  # split_reduce_kernel: reads the partial planes, writes Y
@@ -97,6 +101,10 @@ def predict(op: str, M: int, N: int, K: int, machine_path: str = str(MACHINE)) -
         parts = [_tile_launch(cal, cus, nmat, M, n, K, s, wgs) for n, s, wgs in segs]
         compute, memory, per_cu, reduce = (sum(p[i] for p in parts) for i in range(4))
         t = sum(max(c, mem, pc, cal["launch_min_s"]) + r for c, mem, pc, r in parts) + gap
+    elif plan["kernel"] == "wide_tile":
+        compute, memory, per_cu, reduce = _tile_launch(cal, cus, nmat, M, N, K, 1,
+                                                       plan["workgroups"], 2 * plan["tile_columns"])
+        t = max(compute, memory, per_cu, cal["launch_min_s"]) + gap
     else:
         groups = plan["workgroups"]
         mrows = 32 * math.ceil(M / 32)

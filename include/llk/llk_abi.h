@@ -203,12 +203,16 @@ size_t llk_swiglu_scratch_size(int64_t M, int64_t N, int64_t K);
  * K % 8 == 0 (else the worst case, a padded copy of X, is assumed);
  * LLK_PLAN_ACCUMULATE -- the plan of llk_gemm_bf16_accumulate (matmul only),
  * which always ends with the reduce launch that adds C and needs its
- * partial planes even unsplit.  workspace_bytes is then exactly the
- * ctx->scratch size that call needs.  Host-only, no HIP call. */
+ * partial planes even unsplit; LLK_PLAN_OUT_F32 -- fused SwiGLU with an fp32
+ * result (the pre-truncf value) instead of the op's bf16 one.  workspace_bytes
+ * is then exactly the ctx->scratch size that call needs.  Host-only, no HIP
+ * call. */
 #define LLK_PLAN_X_ALIGNED 1u
 #define LLK_PLAN_ACCUMULATE 2u
+#define LLK_PLAN_OUT_F32 4u
 typedef struct llk_launch_plan {
-  int kernel;                    /* 0 small-M bandwidth kernel, 1 MFMA tile kernel */
+  int kernel;                    /* 0 small-M bandwidth kernel, 1 MFMA tile kernel,
+                                    2 wide SwiGLU tile kernel (bf16 result) */
   int splits;                    /* k splits across workgroups (1 = none) */
   int group_width;               /* small-M kernel: 32-column groups per workgroup */
   int pad_x;                     /* tile kernel: X copied to a padded buffer first */
@@ -219,6 +223,8 @@ typedef struct llk_launch_plan {
   int64_t head_blocks_n;         /* tile kernel: leading 128-column blocks launched
                                     without k split before the rest takes `splits`
                                     (0 = one launch over all columns) */
+  int64_t tile_columns;          /* tile kernels: output columns per workgroup (each
+                                    matrix for SwiGLU); 0 for the small-M kernel */
 } llk_launch_plan;
 int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, unsigned flags,
                         llk_launch_plan* out);

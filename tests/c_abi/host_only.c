@@ -82,7 +82,11 @@ int main(void) {
   CHECK(strstr(llk_last_error(), "M dimension mismatch") != NULL);
   CHECK(llk_classify_m(1) == 0 && llk_classify_m(4097) == 4);
   CHECK(llk_describe_launch(0, 2048, 11008, 4096, LLK_PLAN_X_ALIGNED, &plan) == LLK_OK);
-  CHECK(plan.kernel == 1 && plan.workgroups == 688 && plan.workspace_bytes == 0);
+  CHECK(plan.kernel == 2 && plan.workgroups == 504 && plan.workspace_bytes == 0 &&
+        plan.tile_columns == 176);
+  CHECK(llk_describe_launch(0, 2048, 11008, 4096, LLK_PLAN_X_ALIGNED | LLK_PLAN_OUT_F32, &plan) ==
+        LLK_OK);
+  CHECK(plan.kernel == 1 && plan.workgroups == 688 && plan.tile_columns == 128);
   /* the accumulating matmul always has its planes and the reduce launch */
   CHECK(llk_describe_launch(3, 700, 384, 768, LLK_PLAN_X_ALIGNED | LLK_PLAN_ACCUMULATE, &plan) ==
         LLK_OK);

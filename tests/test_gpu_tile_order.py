@@ -1,7 +1,9 @@
 """Whole-output parity of the tile kernel where its grouped tile order is
 active: more than 8 m-tiles (M > 2048) together with several n-tiles, a short
 last group of m-tiles, with and without k splits, and with the tail split
-(the columns of a partial last wave as a separate k-split launch).  Every
+(the columns of a partial last wave as a separate k-split launch).  The
+wide SwiGLU kernel, which the dispatcher would take for some of these
+shapes, is switched off here (tests/test_gpu_wide.py covers it).  Every
 row is compared with the oracle, so a tile computed into the wrong place
 fails wherever it lands."""
 from __future__ import annotations
@@ -45,7 +47,7 @@ def _per_wave(llk, op, M, per_wave):
     if per_wave:
         return per_wave
     for w in TAIL_WAVES:
-        with _tunables(llk, tile_splits=0, tile_wgs_per_wave=w, tile_tail_split=1):
+        with _tunables(llk, tile_splits=0, tile_wgs_per_wave=w, tile_tail_split=1, tile_wide=0):
             if llk.describe_launch(op, M, N_ORDER, K_ORDER)["head_blocks_n"] > 0:
                 return w
     raise AssertionError(f"no workgroups-per-wave value engages the tail split for {op} M={M}")
@@ -59,7 +61,8 @@ def test_swiglu_grouped_order_whole_output(llk, gpu, orc, M, splits, per_wave, t
     print(f"case swiglu order M={M} S={splits} per_wave={per_wave}", flush=True)
     x, wg, wu = swiglu_inputs(M, K, N, seed=31)
     pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
-    with _tunables(llk, tile_splits=splits, tile_wgs_per_wave=per_wave, tile_tail_split=1):
+    with _tunables(llk, tile_splits=splits, tile_wgs_per_wave=per_wave, tile_tail_split=1,
+                   tile_wide=0):
         plan = llk.describe_launch("fused_swiglu", M, N, K)
         assert plan["kernel"] == "tile"
         assert (plan["head_blocks_n"] > 0) == tail, plan

@@ -90,14 +90,27 @@ def test_partial_round_runs_at_a_higher_clock():
     toward 2.4 GHz as CUs fall idle, profiles/tile_kernel_cycles_per_stage.md):
     config 3's 688 tiles (2 full rounds + 176 of 256) cost between 2.69 and
     3 rounds, a single full round (GEMM 4096^3) exactly one."""
+    import dslcompiler_amd as llk
     cal = {k: float(v) for k, v in perfmodel.machine()["calibration"].items() if k != "measured_us"}
     t_round = 2.0 * 256 * 256 * 4096 / cal["tile_flops_per_cu"] * 1e6
-    p3 = perfmodel.predict("fused_swiglu", 2048, 11008, 4096)
+    old = llk.get_tunable("tile_wide")
+    llk.set_tunable("tile_wide", 0)  # the 128-column kernel (the default plan is the wide one)
+    try:
+        p3 = perfmodel.predict("fused_swiglu", 2048, 11008, 4096)
+    finally:
+        llk.set_tunable("tile_wide", old)
     assert p3["plan"]["workgroups"] == 688
     f_full, f_idle = cal["tile_clock_full_hz"], cal["tile_clock_idle_hz"]
     occ = (688 - 512) / 256
     want = (2 + f_full / (f_idle - (f_idle - f_full) * occ)) * t_round
     assert abs(p3["compute_us"] - want) < 1e-6 * want
+    # the wide kernel (B = 11): 504 workgroups of 352 MFMA rows, 1 full round
+    # + 248 of 256
+    pw = perfmodel.predict("fused_swiglu", 2048, 11008, 4096)
+    assert (pw["plan"]["kernel"], pw["plan"]["workgroups"]) == ("wide_tile", 504)
+    occ = (504 - 256) / 256
+    want = (1 + f_full / (f_idle - (f_idle - f_full) * occ)) * t_round * 352 / 256
+    assert abs(pw["compute_us"] - want) < 1e-6 * want
     assert 2.69 * t_round < p3["compute_us"] < 3 * t_round
     p2 = perfmodel.predict("matmul", 4096, 4096, 4096)
     assert p2["plan"]["workgroups"] == 256

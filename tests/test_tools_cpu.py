@@ -50,7 +50,9 @@ def test_compile_buckets_follow_shape_specialization(tmp_path):
     for m, b in zip((1, 4, 16, 64, 128), range(5)):
         assert f"@bucket_M{m}: llk.fused_swiglu M={m} N=512 K=256 -> bucket {b}" in r.stdout
     assert r.stdout.rstrip().endswith("Compilation successful")
-    assert "kernel=small_m" in r.stdout and "kernel=mfma_tile" in r.stdout
+    # M <= 64: the small-M kernel; M = 128: a tile kernel (the wide SwiGLU one
+    # here: 5 tiles of 112 columns model below 4 of 128)
+    assert "kernel=small_m" in r.stdout and "kernel=swiglu_wide" in r.stdout
 
 
 @pytest.mark.parametrize("kw,msg", [
@@ -106,7 +108,7 @@ def test_bench_options_in_llvm_cl_forms(args):
     r = _tool("llk-bench", *args, "--threads", "16", "--dry-run")
     assert r.returncode == 0, r.stderr
     assert "M=2048 N=11008 K=4096 threads=16" in r.stdout
-    assert "kernel=mfma_tile splits=1" in r.stdout and "workgroups=688" in r.stdout
+    assert "kernel=swiglu_wide splits=1" in r.stdout and "workgroups=504" in r.stdout
 
 
 @pytest.mark.parametrize("tool,args,msg", [
@@ -225,7 +227,14 @@ def test_schedule_db_drives_launch(tmp_path):
 def test_describe_launch_configs():
     """Plans of the BASELINE configs (kernel choice and grid sizes)."""
     p = llk.describe_launch("fused_swiglu", 2048, 11008, 4096)
-    assert (p["kernel"], p["workgroups"], p["splits"], p["workspace_bytes"]) == ("tile", 688, 1, 0)
+    assert (p["kernel"], p["workgroups"], p["splits"], p["workspace_bytes"], p["tile_columns"]) == \
+        ("wide_tile", 504, 1, 0, 176)
+    # the fp32 result (pre-truncf) keeps the 128-column kernel: 688 tiles
+    p = llk.describe_launch("fused_swiglu", 2048, 11008, 4096, out_f32=True)
+    assert (p["kernel"], p["workgroups"], p["splits"], p["tile_columns"]) == ("tile", 688, 1, 128)
+    # config 5's SwiGLU at M = 1000: 112-column tiles, 496 of them
+    p = llk.describe_launch("fused_swiglu", 1000, 13824, 5120)
+    assert (p["kernel"], p["workgroups"], p["tile_columns"]) == ("wide_tile", 496, 112)
     p = llk.describe_launch("fused_swiglu", 8, 14336, 4096)
     assert p["kernel"] == "small_m" and p["workgroups"] * p["threads_per_workgroup"] >= 256 * 256
     p = llk.describe_launch("matmul", 4096, 4096, 4096)
