@@ -22,8 +22,9 @@
 // pair, so wave wn = 0 takes gate blocks 0..C and up blocks 0..C-1, wave
 // wn = 1 up blocks C..B-1 and gate blocks C+1..B-1 (C = (B-1)/2): each wave
 // holds both matrices of every block but C, whose gate sits in wave 0 and up
-// in wave 1; the epilogue exchanges half of block C through LDS (4 KiB per
-// wave), so that each wave finishes exactly half of the tile's outputs.
+// in wave 1; the epilogue exchanges half of block C through LDS (4 KiB each
+// way per wave pair), so that each wave finishes exactly half of the tile's
+// outputs.
 //
 // Weights: the packed payload (common.h) is in 128-column blocks; a tile
 // starting at a multiple of 16 B columns starts at a multiple of 16 inside
@@ -91,8 +92,8 @@ struct WideCfg {
   static constexpr int kLds = kWRing + 4 * kWSlot;
   static constexpr int kN = 16 * B;              // columns per tile (each matrix)
   static constexpr int kRowBytes = 2 * kN;       // one tile row of bf16 output
-  static constexpr int kXch = 0;                 // epilogue: block-C exchange (16 KiB)
-  static constexpr int kStage = 16384;           // epilogue: output staging
+  static constexpr int kXch = 0;                 // epilogue: block-C exchange (32 KiB)
+  static constexpr int kStage = 32768;           // epilogue: output staging
   static_assert(kStage + 256 * kRowBytes <= kLds, "staging fits the LDS");
   // Loads outstanding at the barrier of an even / odd stage, and before the
   // first stage (see the schedule above).
@@ -383,13 +384,16 @@ __global__ __launch_bounds__(256, 1) void mfma_swiglu_wide_kernel(WideArgs a) {
   const int h4 = 4 * (lane >> 4);
   // Block C: wave 0 finishes its m blocks 0-3 (gate here, up from wave 1's
   // row 0), wave 1 its m blocks 4-7 (up here, gate from wave 0's row C).
-  uint8_t* const xch = smem + Cfg::kXch + wm * 8192 + lane * 16;  // [dir][jj] x 1 KiB
-  if (wn == 0) {
+  // Every wave writes both halves a partner could need (wave-independent
+  // code: a branch on the wave that picked different accumulators made the
+  // compiler merge them through AGPR moves and scratch): row C's m blocks
+  // 4-7 and row 0's m blocks 0-3, to its own 8 KiB ([half][jj] x 1 KiB).
+  uint8_t* const xch_own = smem + Cfg::kXch + wave * 8192 + lane * 16;
+  uint8_t* const xch_peer = smem + Cfg::kXch + (wave ^ 2) * 8192 + lane * 16;
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) *reinterpret_cast<f32x4*>(xch + jj * 1024) = acc[C][4 + jj];
-  } else {
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) *reinterpret_cast<f32x4*>(xch + 4096 + jj * 1024) = acc[0][jj];
+  for (int jj = 0; jj < 4; ++jj) {
+    *reinterpret_cast<f32x4*>(xch_own + jj * 1024) = acc[C][4 + jj];
+    *reinterpret_cast<f32x4*>(xch_own + 4096 + jj * 1024) = acc[0][jj];
   }
   uint8_t* const stg = smem + Cfg::kStage;
   auto put = [&](const f32x4& gv, const f32x4& uv, int blk, int j) {
@@ -425,14 +429,14 @@ __global__ __launch_bounds__(256, 1) void mfma_swiglu_wide_kernel(WideArgs a) {
     static_for<C>([&](auto ic_) { pair1(ic<(decltype(ic_)::value + 7 - C) % C + 1>{}); });
   }
   __syncthreads();  // the block-C halves are in LDS
-  if (wn == 0) {
+  if (wn == 0) {  // up of block C, m blocks 0-3: the peer's row 0
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj)
-      put(acc[C][jj], *reinterpret_cast<const f32x4*>(xch + 4096 + jj * 1024), C, jj);
-  } else {
+      put(acc[C][jj], *reinterpret_cast<const f32x4*>(xch_peer + 4096 + jj * 1024), C, jj);
+  } else {  // gate of block C, m blocks 4-7: the peer's row C
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj)
-      put(*reinterpret_cast<const f32x4*>(xch + jj * 1024), acc[0][4 + jj], C, 4 + jj);
+      put(*reinterpret_cast<const f32x4*>(xch_peer + jj * 1024), acc[0][4 + jj], C, 4 + jj);
   }
   __syncthreads();
   // Copy-out: 256 rows x 2 B chunks of 16 bytes.
@@ -445,10 +449,16 @@ __global__ __launch_bounds__(256, 1) void mfma_swiglu_wide_kernel(WideArgs a) {
     const int row = c / kChunks, ch = c - row * kChunks;
     const uint4 d = *reinterpret_cast<const uint4*>(stg + row * Cfg::kRowBytes + ch * 16);
     const int m = m0 + row, n = n0 + ch * 8;
+    // Chunks wholly outside Y (the columns past N of the last tile column,
+    // rows past M) are skipped before any other test: on those lanes the
+    // element-wise path below would otherwise run its eight checks for
+    // nothing, and the last column's tiles, which run in the last round, set
+    // the launch's end.
+    if (!fast && (m >= a.M || n >= a.N)) continue;
     uint16_t* const out = a.y + (size_t)m * a.ldy + n;
-    if (fast || (al16 && m < a.M && n + 8 <= a.N)) {
+    if (fast || (al16 && n + 8 <= a.N)) {
       __builtin_nontemporal_store(u32x4{d.x, d.y, d.z, d.w}, reinterpret_cast<u32x4*>(out));
-    } else if (m < a.M) {
+    } else {
       const uint32_t w[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e)
