@@ -185,3 +185,138 @@ def test_wait_states_around_the_mfmas(asm):
                  if k > last and not b.startswith(MFMA) and reads_agpr(b)]
         assert reads, name
         assert _nops(insns[last:reads[0]]) >= 64, (name, "last MFMA -> first read")
+
+
+# ---------------------------------------------------------------------------
+# The wide SwiGLU tile kernel (kernels/swiglu_wide.hip): the same construction
+# with B row blocks per wave (B = 7, 11) -- rows 0-7 accumulate in AGPRs,
+# rows 8.. (B = 11) in VGPRs -- and a K-loop body of four 32-k stages whose
+# barriers wait for a constant number of loads per stage parity.
+# ---------------------------------------------------------------------------
+WIDE = re.compile(r"^(_ZN10llk_gfx95023mfma_swiglu_wide_kernelILi(\d+)EE\w+):", re.M)
+# loads outstanding at the barriers of an even / odd stage (the refill
+# schedule of the kernel's header comment)
+WIDE_WAITS = {11: ("13", "11"), 7: ("10", "8")}
+
+
+@pytest.fixture(scope="module")
+def wide_asm(tmp_path_factory) -> str:
+    out = tmp_path_factory.mktemp("isa") / "swiglu_wide.s"
+    cmd = [B.HIPCC, *B.HIP_FLAGS, *B.INCLUDES, "--cuda-device-only", "-S",
+           str(B.CSRC / "kernels" / "swiglu_wide.hip"), "-o", str(out)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    return out.read_text()
+
+
+def wide_kernels(asm: str) -> dict[int, list[str]]:
+    """B -> the kernel's instruction lines (as kernels())."""
+    out = {}
+    for m in WIDE.finditer(asm):
+        body = asm[m.end():]
+        body = body[:body.index("s_endpgm")]
+        lines = []
+        for ln in body.split("\n"):
+            ln = ln.split(";")[0].strip()
+            if ln and not ln.startswith(".") or re.match(r"^\.LBB\d+_\d+:", ln):
+                lines.append(ln)
+        out[int(m.group(2))] = lines
+    return out
+
+
+def _acc_regs(mfmas: list[str]) -> tuple[set[int], set[int]]:
+    """(AGPRs, VGPRs) used as MFMA accumulators."""
+    a, v = set(), set()
+    for b in mfmas:
+        kind, rs = regs(operands(b)[0])
+        (a if kind == "a" else v).update(rs)
+    return a, v
+
+
+def test_wide_instantiations_and_no_scratch(wide_asm):
+    assert sorted(wide_kernels(wide_asm)) == [7, 11]
+    # no spills anywhere in the kernels (the epilogue once spilled AGPRs):
+    # the metadata entry of each kernel, its name followed by its scratch size
+    meta = re.findall(r"\.name:\s+(_ZN10llk_gfx95023mfma_swiglu_wide_kernel\w+)\n"
+                      r"\s+\.private_segment_fixed_size:\s+(\d+)", wide_asm)
+    assert len(meta) == 2 and all(size == "0" for _, size in meta), meta
+    for count in ("sgpr_spill_count", "vgpr_spill_count"):
+        spills = re.findall(r"\." + count + r":\s+(\d+)", wide_asm)
+        assert spills and all(n == "0" for n in spills), (count, spills)
+
+
+def test_wide_k_loop_in_place_mfmas(wide_asm):
+    for Bw, lines in wide_kernels(wide_asm).items():
+        body = [b for b in k_loop(lines) if is_insn(b)]
+        mf = [b for b in body if b.startswith(MFMA)]
+        assert len(mf) == 4 * 8 * Bw, (Bw, len(mf))
+        assert not [b for b in body if b.startswith("v_accvgpr")], Bw
+        for b in mf:
+            ops = operands(b)
+            assert ops[0] == ops[3], (Bw, b)
+        a, v = _acc_regs(mf)
+        assert len(a) == 4 * 8 * min(Bw, 8), (Bw, len(a))
+        assert len(v) == 4 * 8 * max(0, Bw - 8), (Bw, len(v))
+        # nothing but the MFMAs writes a VGPR accumulator inside the loop
+        for b in body:
+            if not b.startswith(MFMA) and operands(b) and not re.match(
+                    r"^(ds_write|global_store|buffer_store|buffer_load|s_)", b):
+                kind, dst = regs(operands(b)[0])
+                assert not (kind == "v" and dst & v), (Bw, b)
+
+
+def test_wide_k_loop_waits_and_m0(wide_asm):
+    for Bw, lines in wide_kernels(wide_asm).items():
+        body = [b for b in k_loop(lines) if is_insn(b)]
+        vm = [re.search(r"vmcnt\((\d+)\)", b).group(1) for b in body if "vmcnt" in b]
+        even, odd = WIDE_WAITS[Bw]
+        assert sorted(vm) == sorted([even, odd, even, odd]), (Bw, vm)
+        assert sum(b == "s_barrier" for b in body) == 4, Bw
+        insns = [b for b in lines if is_insn(b)]
+        m0 = [k for k, b in enumerate(insns) if "m0" in b]
+        assert all(insns[k].startswith("s_mov_b32 m0,") for k in m0), Bw
+        dma = [k for k, b in enumerate(insns)
+               if b.startswith("buffer_load_dwordx4") and b.endswith(" lds")]
+        assert len(dma) == len(m0), Bw
+        for a, b in zip(m0, m0[1:] + [len(insns)]):
+            loads = [k for k in dma if a < k < b]
+            assert len(loads) == 1 and loads[0] >= a + 2, (Bw, insns[a:a + 4])
+
+
+def test_wide_wait_states_around_the_mfmas(wide_asm):
+    for Bw, lines in wide_kernels(wide_asm).items():
+        insns = [b for b in lines if is_insn(b)]
+        idx = [k for k, b in enumerate(insns) if b.startswith(MFMA)]
+        first, last = idx[0], idx[-1]
+        a, v = _acc_regs([insns[k] for k in idx])
+        # the last write of an accumulator (zeroing) before the first MFMA
+        zero = [k for k, b in enumerate(insns[:first]) if operands(b) and (
+            (b.startswith("v_accvgpr_write") and regs(operands(b)[0])[1] & a) or
+            (b.startswith("v_") and regs(operands(b)[0])[0] == "v" and regs(operands(b)[0])[1] & v))]
+        assert zero, Bw
+        assert _nops(insns[zero[-1]:first]) >= 64, (Bw, "zeroing -> first MFMA")
+        # the first read of an accumulator after the last MFMA
+        def reads_acc(b):
+            if b.startswith(MFMA) or not operands(b):
+                return False
+            ops = operands(b)
+            srcs = ops if re.match(r"^(ds_write|global_store|buffer_store|flat_store)", b) else ops[1:]
+            return any((regs(o)[0] == "a" and regs(o)[1] & a) or (regs(o)[0] == "v" and regs(o)[1] & v)
+                       for o in srcs)
+        reads = [k for k, b in enumerate(insns) if k > last and reads_acc(b)]
+        assert reads, Bw
+        assert _nops(insns[last:reads[0]]) >= 64, (Bw, "last MFMA -> first read")
+
+
+def test_wide_no_valu_writes_mfma_operands_just_before(wide_asm):
+    for Bw, lines in wide_kernels(wide_asm).items():
+        insns = [b for b in lines if is_insn(b)]
+        for k, b in enumerate(insns):
+            if not b.startswith(MFMA):
+                continue
+            ops = operands(b)
+            src = regs(ops[1])[1] | regs(ops[2])[1]
+            for prev in insns[max(0, k - 4):k]:
+                if prev.startswith("v_") and not prev.startswith("v_mfma"):
+                    kind, dst = regs(operands(prev)[0]) if operands(prev) else ("", set())
+                    assert not (kind == "v" and dst & src), (Bw, prev, b)
