@@ -68,20 +68,25 @@ __device__ __forceinline__ uint32_t f32x2_to_bf16x2_rne(float lo, float hi) {
 // (FuseDoubleContraction.cpp:175-199, math.exp).  exp(-g) = 2^t with
 // t = -g log2(e): v_exp_f32 on the rounded t, times 2^err for the rounding
 // errors of the product and of log2(e) in fp32 (err < 2^-20, so 2^err =
-// 1 + err ln2 to fp32 precision); the reciprocal is v_rcp_f32.  12 VALU
-// operations against ~22 for expf and an IEEE divide, and on MI355X the
-// same bound: at most 3 ulp from the correctly rounded result for every
-// finite bf16 g with |g| <= 100 and 2^20 random fp32 g in [-20, 20].
-// Results below ~1e-36 (g < -87.3, where 1 / (1 + e) is subnormal) flush
-// to +-0; g = +-inf, NaN give what the exact formula gives.
+// 1 + err ln2 to fp32 precision); the reciprocal is v_rcp_f32.  Eight VALU
+// operations and two transcendentals against ~22 for expf and an IEEE
+// divide, and on MI355X the same bound: at most 3 ulp from the correctly
+// rounded result for every finite bf16 g with |g| <= 100 and 2^20 random
+// fp32 g in [-20, 20].  Results below ~1e-36 (g < -87.3, where
+// 1 / (1 + e) is subnormal) flush to +-0; g = +-inf, NaN give what the
+// exact formula gives.  The exponent is computed from g clamped to
+// [-88.75, 88.75] (one v_med3_f32): beyond it 2^t is already +inf or below
+// 2^-128, so 1 / (1 + e) is exactly 0 or 1 as for the unclamped g, and t
+// stays finite, so the error terms never meet inf - inf (the clamp replaced
+// a test of t for infinity, one VALU operation more, with the same results).
 __device__ __forceinline__ float swiglu_act(float g, float u) {
   constexpr float kL2E = 1.44269502162933349609375f;  // log2(e) rounded to fp32
   constexpr float kL2ELo = 1.925963033500011079e-8f;  // log2(e) - kL2E
   constexpr float kLn2 = 0.693147180559945309f;
-  const float t = g * -kL2E;
-  float err = __builtin_fmaf(g, -kL2E, -t);  // the product's rounding error
-  err = __builtin_fmaf(g, -kL2ELo, err);
-  err = __builtin_isinf(t) ? 0.0f : err;
+  const float gc = __builtin_amdgcn_fmed3f(g, -88.75f, 88.75f);
+  const float t = gc * -kL2E;
+  float err = __builtin_fmaf(gc, -kL2E, -t);  // the product's rounding error
+  err = __builtin_fmaf(gc, -kL2ELo, err);
   const float e = __builtin_amdgcn_exp2f(t) * __builtin_fmaf(err, kLn2, 1.0f);
   const float sig = __builtin_amdgcn_rcpf(1.0f + e);
   return (g * sig) * u;

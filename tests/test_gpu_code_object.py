@@ -4,8 +4,9 @@ hipModuleGetFunction (the reference's lookupOrCompile hands back the
 JIT-compiled entry of a key: JitCache.cpp:182-245).  The objects are built
 from the same sources as the library, so every launch path must give the
 library's own output bit for bit: small-M kernels with and without k
-splits, tile kernels with and without k splits, padded X and the K = 0
-fill; two cases are also held to the oracle."""
+splits, tile kernels with and without k splits, the wide SwiGLU kernel at
+both widths, padded X and the K = 0 fill; two cases are also held to the
+oracle."""
 from __future__ import annotations
 
 import re
@@ -25,7 +26,8 @@ CASES = [
     ("fused_swiglu", 1, 1024, 4096, "bf16", "small-M, S = 8"),
     ("fused_swiglu", 40, 640, 512, "fp32", "small-M, two row groups"),
     ("fused_swiglu", 300, 640, 1000, "bf16", "tile, S = 4, padded X"),
-    ("fused_swiglu", 600, 1280, 512, "bf16", "tile"),
+    ("fused_swiglu", 600, 1280, 512, "bf16", "wide tile, B = 7"),
+    ("fused_swiglu", 2048, 11008, 512, "bf16", "wide tile, B = 11"),
     ("fused_swiglu", 255, 13824, 5120, "bf16", "tile, S = 2 (config 5)"),
     ("matmul", 1, 5120, 13824, "bf16", "small-M, S = 3"),
     ("matmul", 64, 1024, 4096, "fp32", "small-M, S = 16"),
@@ -46,6 +48,10 @@ def test_entry_matches_library_kernels(llk, gpu, op, M, N, K, out, what):
     print(f"case code object {op} M={M} N={N} K={K} {out} ({what})", flush=True)
     plan = llk.describe_launch(op, M, N, K, x_aligned=K % 64 == 0)
     assert (plan["kernel"] == "small_m") == what.startswith("small-M")
+    assert (plan["kernel"] == "wide_tile") == what.startswith("wide")
+    wide = re.search(r"B = (\d+)", what)
+    if wide:
+        assert plan["tile_columns"] == 16 * int(wide.group(1)), plan
     assert plan["pad_x"] == ("padded" in what)
     splits = re.search(r"S = (\d+)", what)
     assert plan["splits"] == (int(splits.group(1)) if splits else 1)
