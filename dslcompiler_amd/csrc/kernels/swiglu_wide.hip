@@ -55,6 +55,15 @@
 // Epilogue: SiLU(g) * u on registers, bf16 rounding, the tile's output
 // staged whole in LDS (256 rows x 32 B bytes) and copied out in 16-byte
 // chunks with non-temporal stores.
+//
+// Optional k split (SPLIT, config 5's SwiGLU at M = 255: 124 tiles of B = 7
+// x 2 splits = 248 workgroups where the 128-column kernel runs 108 x 2 =
+// 216): workgroup (tile, s) covers the 64-k blocks [s kbs, (s + 1) kbs) and
+// stores its raw fp32 accumulators in register order -- each wave's R x 8
+// quads as R x 8 coalesced 1 KiB stores, no LDS staging -- and
+// wide_reduce_kernel sums the S partials of every output in split order
+// (fixed, so results are reproducible; with the same k ranges they equal
+// the 128-column kernel's split sums bit for bit) and applies the epilogue.
 #include <type_traits>
 
 #include "common.h"
@@ -74,6 +83,10 @@ struct WideArgs {
   int NB;              // packed n-blocks of 128
   int tiles_m, tiles_n;
   int group_m;         // tile order as TileArgs::group_m
+  // k split (S > 1): partials [S][tiles][4 waves][R][8][64 lanes] x f32x4,
+  // kbs 64-k blocks per split (every split non-empty).
+  float* part;
+  int S, kbs;
 };
 
 template <int B>
@@ -154,22 +167,9 @@ __device__ __forceinline__ void acc_order(f32x4& v) {
   else asm volatile("" : "+v"(v));
 }
 
-template <int B>
-__global__ __launch_bounds__(256, 1) void mfma_swiglu_wide_kernel(WideArgs a) {
-  using Cfg = WideCfg<B>;
-  constexpr int R = Cfg::R, C = Cfg::C, H0 = Cfg::H0, LW = Cfg::LW, LH = Cfg::LH;
-  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-  const int wm = wave & 1;
-  const int wn = wave >> 1;
-
-  // Workgroup -> tile: XCD-aware, m fastest inside groups of group_m m-tiles
-  // (as mfma_tile_kernel).
-  const int tiles = a.tiles_m * a.tiles_n;
-  const int tile = xcd_remap(blockIdx.x, tiles);
-  int tm, tn;
+// Tile index -> (m tile, n tile): XCD-aware order of mfma_tile_kernel, m
+// fastest inside groups of group_m m-tiles.
+__device__ __forceinline__ void wide_tile_mn(const WideArgs& a, int tile, int& tm, int& tn) {
   if (a.group_m > 0 && a.tiles_m > a.group_m) {
     const int span = a.group_m * a.tiles_n;
     const int g = tile / span, r = tile - g * span;
@@ -180,21 +180,46 @@ __global__ __launch_bounds__(256, 1) void mfma_swiglu_wide_kernel(WideArgs a) {
     tm = tile % a.tiles_m;
     tn = tile / a.tiles_m;
   }
+}
+
+template <int B, bool SPLIT>
+__global__ __launch_bounds__(256, 1) void mfma_swiglu_wide_kernel(WideArgs a) {
+  using Cfg = WideCfg<B>;
+  constexpr int R = Cfg::R, C = Cfg::C, H0 = Cfg::H0, LW = Cfg::LW, LH = Cfg::LH;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int wm = wave & 1;
+  const int wn = wave >> 1;
+
+  // Workgroup -> (split, tile): tiles of one split are contiguous, so after
+  // the XCD remap the tiles sharing X's k slice run on one XCD.
+  const int tiles = a.tiles_m * a.tiles_n;
+  const int idx = xcd_remap(blockIdx.x, tiles * (SPLIT ? a.S : 1));
+  const int split = SPLIT ? idx / tiles : 0;
+  const int tile = SPLIT ? idx - split * tiles : idx;
+  int tm, tn;
+  wide_tile_mn(a, tile, tm, tn);
   const int m0 = tm * 256;
   const int n0 = tn * Cfg::kN;
-  const int T = 2 * a.KB;  // 32-k stages
+  const int kb0 = SPLIT ? split * a.kbs : 0;
+  const int nkb = SPLIT ? min(a.KB - kb0, a.kbs) : a.KB;
+  const int T = 2 * nkb;  // 32-k stages
 
   // ---- weight stream --------------------------------------------------------
   // One resource per matrix from the first packed n-block the tile touches
   // to the payload's end (the host keeps three panels plus the stage offsets
   // below 2^31, so every real load is in range and the spare loads, at
   // 2^31 + ..., are not).
+  // A split starts kb0 blocks into every panel.
   const int nbf = n0 >> 7;
   const int64_t panel = (int64_t)a.KB * kBlockBytes;
-  const int64_t wspan = (int64_t)(a.NB - nbf) * panel;
+  const int64_t wspan = (int64_t)(a.NB - nbf) * panel - (int64_t)kb0 * kBlockBytes;
   const int wbytes = (int)(wspan < 0x7fffffff ? wspan : 0x7fffffff);
-  const u32x4 rg = buffer_rsrc(a.w0 + nbf * panel, wbytes);
-  const u32x4 ru = buffer_rsrc(a.w1 + nbf * panel, wbytes);
+  const size_t wbase = (size_t)nbf * panel + (size_t)kb0 * kBlockBytes;
+  const u32x4 rg = buffer_rsrc(a.w0 + wbase, wbytes);
+  const u32x4 ru = buffer_rsrc(a.w1 + wbase, wbytes);
   // Lane l of a fragment load fetches row l%16 of a 16-column block, k
   // 8*(l/16) .. +8 of the stage: sub-block k quarter l/32 (+4 KiB), slot half
   // (l/16)%2 (+512 bytes) of it.  Stage t adds t * 8 KiB (two k quarters).
@@ -215,8 +240,10 @@ __global__ __launch_bounds__(256, 1) void mfma_swiglu_wide_kernel(WideArgs a) {
   const uint32_t w_lds0 = lds_addr(smem + Cfg::kWRing) + (uint32_t)(wave * LH) * 1024;
 
   // ---- X stream (as mfma_tile_kernel) ---------------------------------------
+  // X from row m0, column 64 kb0, to row M (rows >= M read zero).
   const int rows_left = a.M - m0;
-  const u32x4 xrsrc = buffer_rsrc(a.x + (size_t)m0 * a.ldx, (int)((int64_t)rows_left * a.ldx * 2));
+  const u32x4 xrsrc = buffer_rsrc(a.x + (size_t)m0 * a.ldx + (size_t)kb0 * 64,
+                                 (int)((int64_t)rows_left * a.ldx * 2 - (int64_t)kb0 * 128));
   const int x_rowstep = 8 * (int)a.ldx * 2;
   int x_off[8];
 #pragma unroll
@@ -376,6 +403,19 @@ __global__ __launch_bounds__(256, 1) void mfma_swiglu_wide_kernel(WideArgs a) {
   mfma_drain();
   fence();
 
+  if constexpr (SPLIT) {
+    // Raw accumulators in register order: quad (r, j) of this wave, lane l,
+    // at ((split * tiles + tile) * 4 + wave) * R * 8 + r * 8 + j quads of
+    // 64 lanes -- one coalesced 1 KiB store per wave and quad.
+    f32x4* const dst = reinterpret_cast<f32x4*>(a.part) +
+                       ((size_t)(split * tiles + tile) * 4 + wave) * (R * 8 * 64) + lane;
+    static_for<R>([&](auto rc) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dst[(decltype(rc)::value * 8 + j) * 64] = acc[decltype(rc)::value][j];
+    });
+    return;
+  }
+
   // ---- epilogue -------------------------------------------------------------
   // acc[r][j], lane l: output row wm*128 + 16 j + l%16 of the tile, columns
   // 16 b + 4 (l/16) + 0..3 of block b (the wave's row block r).
@@ -467,42 +507,115 @@ __global__ __launch_bounds__(256, 1) void mfma_swiglu_wide_kernel(WideArgs a) {
   }
 }
 
+// Sums the S register-order partials of each output in split order and
+// applies the SiLU epilogue.  One wave per (tile, wave row wm, block b, m
+// block j): lane l owns output row m0 + wm*128 + 16 j + l%16, columns
+// n0 + 16 b + 4 (l/16) + 0..3; its gate and up quads sit in the wave and
+// row block that held them in the tile kernel (gate b: wave wm + 2 (b > C),
+// row b; up b: wave wm + 2 (b >= C), row b + C + 1 (b < C) or b - C).
 template <int B>
+__global__ __launch_bounds__(256) void wide_reduce_kernel(WideArgs a) {
+  using Cfg = WideCfg<B>;
+  constexpr int R = Cfg::R, C = Cfg::C;
+  const int lane = threadIdx.x & 63;
+  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int tiles = a.tiles_m * a.tiles_n;
+  if (unit >= (int64_t)tiles * 2 * B * 8) return;
+  const int j = (int)(unit % 8);
+  const int b = (int)(unit / 8 % B);
+  const int wm = (int)(unit / (8 * B) % 2);
+  const int tile = (int)(unit / (16 * B));
+  int tm, tn;
+  wide_tile_mn(a, tile, tm, tn);
+  const int m = tm * 256 + wm * 128 + 16 * j + (lane & 15);
+  const int n = tn * Cfg::kN + 16 * b + 4 * (lane >> 4);
+  const int wg = wm + (b > C ? 2 : 0), rg = b;
+  const int wu = wm + (b >= C ? 2 : 0), ru = b < C ? b + C + 1 : b - C;
+  const f32x4* const src = reinterpret_cast<const f32x4*>(a.part) + lane;
+  const size_t per_split = (size_t)tiles * 4 * R * 8 * 64;
+  const size_t og = ((size_t)tile * 4 + wg) * (R * 8 * 64) + (size_t)(rg * 8 + j) * 64;
+  const size_t ou = ((size_t)tile * 4 + wu) * (R * 8 * 64) + (size_t)(ru * 8 + j) * 64;
+  f32x4 g = src[og], u = src[ou];
+  for (int sp = 1; sp < a.S; ++sp) {
+    g += src[sp * per_split + og];
+    u += src[sp * per_split + ou];
+  }
+  if (m >= a.M || n >= a.N) return;
+  float v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) v[q] = swiglu_act(g[q], u[q]);
+  const bool vec = ((reinterpret_cast<uintptr_t>(a.y) | (uintptr_t)(a.ldy * 2)) & 7) == 0;
+  store4<kOutBF16>(a.y, a.ldy, a.M, a.N, m, n, v, vec);
+}
+
+template <int B, bool SPLIT>
 const char* wide_symbol() {
   static const std::string name = "_ZN10llk_gfx95023mfma_swiglu_wide_kernelI" + mangle_int(B) +
-                                  "EEvNS_8WideArgsE";
+                                  mangle_bool(SPLIT) + "EEvNS_8WideArgsE";
   return name.c_str();
 }
 
 template <int B>
-static hipError_t launch_wide_t(const WideArgs& a, const llk::ModuleFns* mod, hipStream_t s) {
-  auto fn = mfma_swiglu_wide_kernel<B>;
+const char* wide_reduce_symbol() {
+  static const std::string name = "_ZN10llk_gfx95018wide_reduce_kernelI" + mangle_int(B) +
+                                  "EEvNS_8WideArgsE";
+  return name.c_str();
+}
+
+template <int B, bool SPLIT>
+static hipError_t launch_wide_kernel(const WideArgs& a, const llk::ModuleFns* mod,
+                                     hipStream_t s) {
+  auto fn = mfma_swiglu_wide_kernel<B, SPLIT>;
   if (!mod) {
     static std::atomic<uint64_t> lds_set{0};
     hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(fn), WideCfg<B>::kLds, lds_set);
     if (e != hipSuccess) return e;
   }
-  return launch_kernel(mod, reinterpret_cast<const void*>(fn), &wide_symbol<B>,
-                       dim3(a.tiles_m * a.tiles_n), dim3(256), WideCfg<B>::kLds, s, a);
+  return launch_kernel(mod, reinterpret_cast<const void*>(fn), &wide_symbol<B, SPLIT>,
+                       dim3(a.tiles_m * a.tiles_n * (SPLIT ? a.S : 1)), dim3(256),
+                       WideCfg<B>::kLds, s, a);
+}
+
+template <int B>
+static hipError_t launch_wide_t(const WideArgs& a, const llk::ModuleFns* mod, hipStream_t s) {
+  if (a.S <= 1) return launch_wide_kernel<B, false>(a, mod, s);
+  hipError_t e = launch_wide_kernel<B, true>(a, mod, s);
+  if (e != hipSuccess) return e;
+  const int64_t waves = (int64_t)a.tiles_m * a.tiles_n * 2 * B * 8;
+  return launch_kernel(mod, reinterpret_cast<const void*>(wide_reduce_kernel<B>),
+                       &wide_reduce_symbol<B>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                       s, a);
 }
 
 }  // namespace llk_gfx950
 
-// Whether the wide kernel of B blocks can address its weight panels (three
-// 128-column panels of K plus the refill stages past the end, 32-bit
-// offsets) -- the host falls back to mfma_tile_kernel otherwise.
+// Whether the wide kernel can address its weight panels (a tile's columns
+// touch at most three 128-column panels of K; plus the refill stages past
+// the end; 32-bit offsets) -- the host falls back to mfma_tile_kernel
+// otherwise.  The same bound holds for any B and split.
 bool llk_swiglu_wide_fits(int B, int KB) {
   (void)B;
   return (int64_t)3 * KB * 16384 + (int64_t)(2 * KB + 8) * 8192 < ((int64_t)1 << 31);
 }
 
+// Bytes of the register-order partials of a k split over S workgroups per
+// tile (0 if S <= 1).
+size_t llk_swiglu_wide_split_bytes(int B, int M, int N, int S) {
+  if (S <= 1) return 0;
+  const size_t tiles = (size_t)((M + 255) / 256) * ((N + 16 * B - 1) / (16 * B));
+  return (size_t)S * tiles * 4 * B * 8 * 64 * 16;
+}
+
 // Internal (not part of the C ABI).  Fused SwiGLU with bf16 output over
 // 16 B-column tiles.  x: [M, 64*KB] bf16, ldx % 8 == 0, 16-byte aligned,
 // columns >= K zero; llk_tile_x_fits(M, ldx) and llk_swiglu_wide_fits(B, KB)
-// must hold.
+// must hold.  S > 1 splits K over S workgroups of kbs = ceil(KB / S) blocks
+// (every split non-empty: the caller guarantees (S - 1) * kbs < KB); `part`
+// (16-byte aligned) holds llk_swiglu_wide_split_bytes(B, M, N, S) bytes.
 hipError_t llk_launch_swiglu_wide(int B, const uint16_t* x, int64_t ldx, const void* wg,
                                   const void* wu, void* y, int64_t ldy, int M, int N, int KB,
-                                  int NB, const llk::ModuleFns* mod, hipStream_t s) {
+                                  int NB, int S, void* part, const llk::ModuleFns* mod,
+                                  hipStream_t s) {
   using namespace llk_gfx950;
   WideArgs a;
   a.x = x;
@@ -518,7 +631,11 @@ hipError_t llk_launch_swiglu_wide(int B, const uint16_t* x, int64_t ldx, const v
   a.tiles_m = (M + 255) / 256;
   a.tiles_n = (N + 16 * B - 1) / (16 * B);
   a.group_m = 8;
+  a.S = S > 1 ? S : 1;
+  a.kbs = (KB + a.S - 1) / a.S;
+  a.part = static_cast<float*>(part);
   if (KB < 1 || !llk_swiglu_wide_fits(B, KB)) return hipErrorInvalidValue;
+  if (a.S > 1 && (part == nullptr || (int64_t)(a.S - 1) * a.kbs >= KB)) return hipErrorInvalidValue;
 #if !defined(LLK_CO_OP) || LLK_CO_OP == 1
   if (B == 11) return launch_wide_t<11>(a, mod, s);
   if (B == 7) return launch_wide_t<7>(a, mod, s);

@@ -37,8 +37,10 @@ size_t llk_tile_split_bytes(int mode, int M, int NB, int S, bool accumulate);
 bool llk_tile_x_fits(int M, int64_t ldx);
 hipError_t llk_launch_swiglu_wide(int B, const uint16_t* x, int64_t ldx, const void* wg,
                                   const void* wu, void* y, int64_t ldy, int M, int N, int KB,
-                                  int NB, const llk::ModuleFns* mod, hipStream_t s);
+                                  int NB, int S, void* part, const llk::ModuleFns* mod,
+                                  hipStream_t s);
 bool llk_swiglu_wide_fits(int B, int KB);
+size_t llk_swiglu_wide_split_bytes(int B, int M, int N, int S);
 hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const void* w0,
                              const void* w1, void* y, int64_t ldy, int M, int N, int K, int KB,
                              int NB, int S, int G, void* ws, int out_dtype, bool xvec,
@@ -419,28 +421,52 @@ TilePlan tile_plan(int nmat, int64_t rows, int64_t KB, int64_t NB, int64_t db_sp
 }
 
 // Wide SwiGLU tiles (kernels/swiglu_wide.hip): B blocks of 16 columns per
-// matrix instead of 8, unsplit.  Modelled like best_split: waves of
-// workgroups x (64-k steps + 2), each workgroup B/8 times the work of a
-// 128-column tile.  Taken when 3% or more below the 128-column plan's cost
-// (config 3: 504 tiles in 2 waves x 1.375 against 688 in 3 waves; config 5 at
-// M = 1000: 496 tiles of B = 7 in 2 waves x 0.875 against 432 in 2 waves).
-// tile_wide = 7 or 11 forces that width; 0 turns the kernel off.
-int wide_choice(int64_t rows, int64_t N, int64_t KB, double std_cost) {
+// matrix instead of 8, with S k splits.  Modelled like best_split: waves of
+// workgroups x (64-k steps per split + 2), each workgroup B/8 times the work
+// of a 128-column tile, plus for S > 1 the register-order partials written
+// and read back at ~4 TB/s and one reduce launch.  Taken when 3% or more
+// below the 128-column plan's cost (config 3: 504 tiles in 2 waves x 1.375
+// against 688 in 3 waves; config 5 at M = 1000: 496 tiles of B = 7 in 2 waves
+// x 0.875 against 432 in 2 waves; at M = 255: 124 tiles of B = 7 x 2 splits,
+// 248 workgroups, against 108 x 2 = 216).  tile_wide = 7 or 11 forces that
+// width (with the forced tile_splits, if any, else the modelled S); 0 turns
+// the kernel off.
+struct WideChoice {
+  int B = 0, S = 1;
+};
+
+WideChoice wide_choice(int64_t rows, int64_t N, int64_t KB, double std_cost, int64_t forced_s) {
   const int64_t knob = llk::tunable("tile_wide");
-  if (knob == 0) return 0;
+  if (knob == 0) return {};
   const int64_t per_wave = std::max<int64_t>(1, llk::tunable("tile_wgs_per_wave"));
+  const int64_t min_kb = std::max<int64_t>(1, llk::tunable("tile_min_kb"));
   const int64_t tm = (rows + 255) / 256;
-  int best = 0;
+  WideChoice best;
   double best_cost = 0.97 * std_cost;
   for (int B : {11, 7}) {
     if (!llk_swiglu_wide_fits(B, (int)KB)) continue;
-    if (knob == B) return B;
-    if (knob != 1) continue;
+    if (knob != 1 && knob != B) continue;
     const int64_t tiles = tm * ((N + 16 * B - 1) / (16 * B));
-    const double cost = (double)((tiles + per_wave - 1) / per_wave) * (double)(KB + 2) * B / 8.0;
-    if (cost < best_cost) {
-      best = B;
-      best_cost = cost;
+    WideChoice own;
+    double own_cost = 0.0;
+    int64_t s_lo = 1, s_hi = std::min<int64_t>(64, std::max<int64_t>(1, KB / min_kb));
+    if (forced_s > 0) s_lo = s_hi = std::min(forced_s, KB);
+    for (int64_t S = s_lo; S <= s_hi; ++S) {
+      const int64_t kbs = (KB + S - 1) / S;
+      const int64_t s_eff = (KB + kbs - 1) / kbs;  // no empty splits
+      double cost = (double)((tiles * s_eff + per_wave - 1) / per_wave) * (double)(kbs + 2) * B / 8.0;
+      if (s_eff > 1)
+        cost += 2.0 * (double)llk_swiglu_wide_split_bytes(B, (int)rows, (int)N, (int)s_eff) /
+                    (4e12 * 1.6e-6) + 1.0;
+      if (S == s_lo || cost < own_cost) {
+        own = {B, (int)s_eff};
+        own_cost = cost;
+      }
+    }
+    if (knob == B) return own;
+    if (own_cost < best_cost) {
+      best = own;
+      best_cost = own_cost;
     }
   }
   return best;
@@ -583,18 +609,24 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
   const TilePlan tp = tile_plan(nmat, rows, KB, NB, have_db ? se.grain_size : 0);
   p.S = tp.S;
   p.head_nb = accumulate ? 0 : tp.head_nb;
-  // The wide kernel: fused SwiGLU, bf16 output, no k split (a forced split
-  // count or a DB entry with one keeps the 128-column kernel).
-  const bool split_forced = llk::tunable("tile_splits") > 0 || (have_db && se.grain_size > 1);
-  if (nmat == 2 && out_bf16 && !accumulate && !split_forced) {
-    p.wide = wide_choice(rows, NB * 128, KB, tp.cost);
-    if (p.wide) {
-      p.S = 1;
+  // The wide kernel: fused SwiGLU, bf16 output.  A forced split count or a
+  // DB entry with one keeps the 128-column kernel unless tile_wide forces a
+  // width (which then takes the forced split count).
+  const int64_t forced_s = llk::tunable("tile_splits");
+  const bool split_forced = forced_s > 0 || (have_db && se.grain_size > 1);
+  const bool wide_forced = llk::tunable("tile_wide") == 7 || llk::tunable("tile_wide") == 11;
+  if (nmat == 2 && out_bf16 && !accumulate && (!split_forced || wide_forced)) {
+    const WideChoice wc = wide_choice(rows, NB * 128, KB, tp.cost, forced_s);
+    if (wc.B) {
+      p.wide = wc.B;
+      p.S = wc.S;
       p.head_nb = 0;
     }
   }
   if (accumulate && tp.head_nb > 0) p.S = best_split(nmat, rows, KB, NB, 0).S;
   auto body = [&](int64_t crows) {
+    if (p.wide)
+      return p.pad_bytes + llk_swiglu_wide_split_bytes(p.wide, (int)crows, (int)(NB * 128), p.S);
     return p.pad_bytes + llk_tile_split_bytes(nmat == 2 ? 1 : 0, (int)crows,
                                               (int)(NB - p.head_nb), p.S, accumulate);
   };
@@ -612,6 +644,10 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
   }
   const int64_t crows = std::min(p.chunk, M);
   for (; p.S >= 1; --p.S) {
+    // a split count whose splits would not all be non-empty runs as the
+    // count it effectively is (KB = 7, S = 5: 4 splits of 2 blocks)
+    const int64_t kbs = (KB + p.S - 1) / p.S;
+    p.S = (int)((KB + kbs - 1) / kbs);
     if (p.S == 1) p.head_nb = 0;
     p.ws_bytes = body(crows);
     if (p.ws_bytes <= max_ws || p.S == 1) break;
@@ -691,7 +727,8 @@ int launch_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights
     uint8_t* yp = static_cast<uint8_t*>(y->data) + m0 * y->stride0 * ysz;
     if (p.wide) {
       e = llk_launch_swiglu_wide(p.wide, xp, p.ld, w0->dev, w1->dev, yp, y->stride0, rows, (int)N,
-                                 (int)w0->KB, (int)w0->NB, mod, s);
+                                 (int)w0->KB, (int)w0->NB, p.S,
+                                 p.S > 1 ? body + p.pad_bytes : nullptr, mod, s);
       continue;
     }
     if (p.head_nb > 0) {
@@ -1163,8 +1200,8 @@ int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, unsigned
   if (p.wide) {
     out->kernel = 2;
     out->tile_columns = 16 * p.wide;
-    out->workgroups = (rows + 255) / 256 * ((N + 16 * p.wide - 1) / (16 * p.wide));
-    out->launches = chunks * (1 + (p.pad ? 1 : 0));
+    out->workgroups = (rows + 255) / 256 * ((N + 16 * p.wide - 1) / (16 * p.wide)) * p.S;
+    out->launches = chunks * (1 + (p.pad ? 1 : 0) + (p.S > 1 ? 1 : 0));
     return LLK_OK;
   }
   out->tile_columns = nmat == 2 ? 128 : 256;

@@ -24,7 +24,8 @@ For one call the model takes the dispatcher's launch plan
 A tile-kernel tail split (head_blocks_n > 0) is two such launches in a row:
 the leading columns unsplit, the remaining columns with the k split.  The
 wide SwiGLU kernel is the tile kernel's model with 2 x tile_columns MFMA
-rows per workgroup, unsplit.
+rows per workgroup (its k split's register-order partials counted like the
+partial planes).
 The small-M kernel's MFMA work counts whole 32-row groups.
 """
 from __future__ import annotations
@@ -102,9 +103,9 @@ def predict(op: str, M: int, N: int, K: int, machine_path: str = str(MACHINE)) -
         compute, memory, per_cu, reduce = (sum(p[i] for p in parts) for i in range(4))
         t = sum(max(c, mem, pc, cal["launch_min_s"]) + r for c, mem, pc, r in parts) + gap
     elif plan["kernel"] == "wide_tile":
-        compute, memory, per_cu, reduce = _tile_launch(cal, cus, nmat, M, N, K, 1,
+        compute, memory, per_cu, reduce = _tile_launch(cal, cus, nmat, M, N, K, S,
                                                        plan["workgroups"], 2 * plan["tile_columns"])
-        t = max(compute, memory, per_cu, cal["launch_min_s"]) + gap
+        t = max(compute, memory, per_cu, cal["launch_min_s"]) + reduce + gap
     else:
         groups = plan["workgroups"]
         mrows = 32 * math.ceil(M / 32)

@@ -5,8 +5,8 @@ JIT-compiled entry of a key: JitCache.cpp:182-245).  The objects are built
 from the same sources as the library, so every launch path must give the
 library's own output bit for bit: small-M kernels with and without k
 splits, tile kernels with and without k splits, the wide SwiGLU kernel at
-both widths, padded X and the K = 0 fill; two cases are also held to the
-oracle."""
+both widths and with a k split, padded X and the K = 0 fill; two cases are
+also held to the oracle."""
 from __future__ import annotations
 
 import re
@@ -28,7 +28,7 @@ CASES = [
     ("fused_swiglu", 300, 640, 1000, "bf16", "tile, S = 4, padded X"),
     ("fused_swiglu", 600, 1280, 512, "bf16", "wide tile, B = 7"),
     ("fused_swiglu", 2048, 11008, 512, "bf16", "wide tile, B = 11"),
-    ("fused_swiglu", 255, 13824, 5120, "bf16", "tile, S = 2 (config 5)"),
+    ("fused_swiglu", 255, 13824, 5120, "bf16", "wide tile, B = 7, S = 2 (config 5)"),
     ("matmul", 1, 5120, 13824, "bf16", "small-M, S = 3"),
     ("matmul", 64, 1024, 4096, "fp32", "small-M, S = 16"),
     ("matmul", 300, 640, 1000, "fp32", "tile, S = 4, padded X"),

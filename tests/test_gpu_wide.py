@@ -60,9 +60,9 @@ def _wide_and_tile(llk, gpu, x, wg, wu, B, x_stride=None):
     N = wg.shape[1]
     pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
     xd = to_dev(gpu, x, x_stride)
-    with _tunables(llk, tile_wide=B):
+    with _tunables(llk, tile_wide=B, tile_splits=1):
         plan = llk.describe_launch("fused_swiglu", M, N, K, x_aligned=x_stride is None and K % 64 == 0)
-        assert (plan["kernel"], plan["tile_columns"]) == ("wide_tile", 16 * B), plan
+        assert (plan["kernel"], plan["tile_columns"], plan["splits"]) == ("wide_tile", 16 * B, 1), plan
         yw = from_dev(llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.bfloat16))
     with _tunables(llk, tile_wide=0, tile_splits=1):
         plan = llk.describe_launch("fused_swiglu", M, N, K)
@@ -111,7 +111,7 @@ def test_wide_misaligned_y(llk, gpu, orc, B):
     xd = to_dev(gpu, x)
     buf = gpu.full((M, N + 7), 7.0, dtype=gpu.bfloat16, device="cuda")
     y = buf[:, 1:N + 1]
-    with _tunables(llk, tile_wide=B):
+    with _tunables(llk, tile_wide=B, tile_splits=1):
         assert llk.describe_launch("fused_swiglu", M, N, K)["kernel"] == "wide_tile"
         llk.fused_swiglu(xd, pg, pu, out=y)
     with _tunables(llk, tile_wide=0, tile_splits=1):
@@ -179,3 +179,55 @@ def test_wide_config3_whole_output(llk, gpu, orc):
     _, yf_ref = orc.swiglu_avx2(x, wg, wu, _threads(), want_f32=True)
     for m0 in range(0, M, 256):
         assert_parity_bf16(yw[m0:m0 + 256], yf_ref[m0:m0 + 256], f"config 3 rows {m0}..")
+
+
+# (M, N, K, S): k splits of the wide kernel; config 5's SwiGLU at M = 255 is
+# the dispatcher's own choice (B = 7, S = 2)
+SPLIT_SHAPES = [
+    (255, 13824, 5120, 2),
+    (100, 1000, 1000, 3),   # padded X, ragged M and N, odd block count per split
+    (300, 700, 640, 2),     # two m tiles, last n tile partial
+    (513, 2200, 320, 3),    # three m tiles, 5 blocks over 3 splits
+]
+
+
+@pytest.mark.parametrize("B", [7, 11])
+@pytest.mark.parametrize("M,N,K,S", SPLIT_SHAPES)
+def test_wide_split_matches_tile_split_and_oracle(llk, gpu, orc, B, M, N, K, S):
+    """The k split sums register-order partials in split order over the same
+    k ranges as the 128-column kernel's split, so the two agree bit for bit;
+    every output at the bar against the oracle."""
+    print(f"case wide split B={B} M={M} N={N} K={K} S={S}", flush=True)
+    x, wg, wu = swiglu_inputs(M, K, N, seed=7 * B + S)
+    pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
+    xd = to_dev(gpu, x)
+    with _tunables(llk, tile_wide=B, tile_splits=S):
+        plan = llk.describe_launch("fused_swiglu", M, N, K, x_aligned=K % 64 == 0)
+        assert (plan["kernel"], plan["tile_columns"], plan["splits"]) == ("wide_tile", 16 * B, S), plan
+        yw = from_dev(llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.bfloat16))
+    with _tunables(llk, tile_wide=0, tile_splits=S):
+        plan = llk.describe_launch("fused_swiglu", M, N, K)
+        assert (plan["kernel"], plan["splits"]) == ("tile", S), plan
+        yt = from_dev(llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.bfloat16))
+    gpu.cuda.synchronize()
+    assert np.array_equal(yw, yt), f"B={B} S={S} {M}x{N}x{K}: differs from the 128-column split"
+    _, yf_ref = orc.swiglu_avx2(x, wg, wu, _threads(), want_f32=True)
+    assert_parity_bf16(yw, yf_ref, f"wide split B={B} S={S} {M}x{N}x{K}")
+
+
+def test_wide_split_default_plan_config5(llk, gpu):
+    """The dispatcher's plan for config 5's SwiGLU at M = 255 (B = 7, S = 2,
+    248 workgroups, register-order partials in the workspace), run twice:
+    reruns bit-identical."""
+    M, N, K = 255, 13824, 5120
+    plan = llk.describe_launch("fused_swiglu", M, N, K)
+    assert (plan["kernel"], plan["tile_columns"], plan["splits"], plan["workgroups"]) == \
+        ("wide_tile", 112, 2, 248), plan
+    assert plan["workspace_bytes"] == 2 * 124 * 4 * 7 * 8 * 64 * 16
+    x, wg, wu = swiglu_inputs(M, K, N, seed=5)
+    pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
+    xd = to_dev(gpu, x)
+    y1 = from_dev(llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.bfloat16))
+    y2 = from_dev(llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.bfloat16))
+    gpu.cuda.synchronize()
+    assert np.array_equal(y1, y2)

@@ -191,9 +191,11 @@ def test_wait_states_around_the_mfmas(asm):
 # The wide SwiGLU tile kernel (kernels/swiglu_wide.hip): the same construction
 # with B row blocks per wave (B = 7, 11) -- rows 0-7 accumulate in AGPRs,
 # rows 8.. (B = 11) in VGPRs -- and a K-loop body of four 32-k stages whose
-# barriers wait for a constant number of loads per stage parity.
+# barriers wait for a constant number of loads per stage parity; with and
+# without the k split (same K loop, register-order partial stores instead of
+# the SiLU epilogue).
 # ---------------------------------------------------------------------------
-WIDE = re.compile(r"^(_ZN10llk_gfx95023mfma_swiglu_wide_kernelILi(\d+)EE\w+):", re.M)
+WIDE = re.compile(r"^(_ZN10llk_gfx95023mfma_swiglu_wide_kernelILi(\d+)ELb([01])EE\w+):", re.M)
 # loads outstanding at the barriers of an even / odd stage (the refill
 # schedule of the kernel's header comment)
 WIDE_WAITS = {11: ("13", "11"), 7: ("10", "8")}
@@ -209,8 +211,8 @@ def wide_asm(tmp_path_factory) -> str:
     return out.read_text()
 
 
-def wide_kernels(asm: str) -> dict[int, list[str]]:
-    """B -> the kernel's instruction lines (as kernels())."""
+def wide_kernels(asm: str) -> dict[tuple[int, int], list[str]]:
+    """(B, split) -> the kernel's instruction lines (as kernels())."""
     out = {}
     for m in WIDE.finditer(asm):
         body = asm[m.end():]
@@ -220,7 +222,7 @@ def wide_kernels(asm: str) -> dict[int, list[str]]:
             ln = ln.split(";")[0].strip()
             if ln and not ln.startswith(".") or re.match(r"^\.LBB\d+_\d+:", ln):
                 lines.append(ln)
-        out[int(m.group(2))] = lines
+        out[(int(m.group(2)), int(m.group(3)))] = lines
     return out
 
 
@@ -234,19 +236,19 @@ def _acc_regs(mfmas: list[str]) -> tuple[set[int], set[int]]:
 
 
 def test_wide_instantiations_and_no_scratch(wide_asm):
-    assert sorted(wide_kernels(wide_asm)) == [7, 11]
+    assert sorted(wide_kernels(wide_asm)) == [(7, 0), (7, 1), (11, 0), (11, 1)]
     # no spills anywhere in the kernels (the epilogue once spilled AGPRs):
     # the metadata entry of each kernel, its name followed by its scratch size
     meta = re.findall(r"\.name:\s+(_ZN10llk_gfx95023mfma_swiglu_wide_kernel\w+)\n"
                       r"\s+\.private_segment_fixed_size:\s+(\d+)", wide_asm)
-    assert len(meta) == 2 and all(size == "0" for _, size in meta), meta
+    assert len(meta) == 4 and all(size == "0" for _, size in meta), meta
     for count in ("sgpr_spill_count", "vgpr_spill_count"):
         spills = re.findall(r"\." + count + r":\s+(\d+)", wide_asm)
         assert spills and all(n == "0" for n in spills), (count, spills)
 
 
 def test_wide_k_loop_in_place_mfmas(wide_asm):
-    for Bw, lines in wide_kernels(wide_asm).items():
+    for (Bw, _split), lines in wide_kernels(wide_asm).items():
         body = [b for b in k_loop(lines) if is_insn(b)]
         mf = [b for b in body if b.startswith(MFMA)]
         assert len(mf) == 4 * 8 * Bw, (Bw, len(mf))
@@ -266,7 +268,7 @@ def test_wide_k_loop_in_place_mfmas(wide_asm):
 
 
 def test_wide_k_loop_waits_and_m0(wide_asm):
-    for Bw, lines in wide_kernels(wide_asm).items():
+    for (Bw, _split), lines in wide_kernels(wide_asm).items():
         body = [b for b in k_loop(lines) if is_insn(b)]
         vm = [re.search(r"vmcnt\((\d+)\)", b).group(1) for b in body if "vmcnt" in b]
         even, odd = WIDE_WAITS[Bw]
@@ -284,7 +286,7 @@ def test_wide_k_loop_waits_and_m0(wide_asm):
 
 
 def test_wide_wait_states_around_the_mfmas(wide_asm):
-    for Bw, lines in wide_kernels(wide_asm).items():
+    for (Bw, _split), lines in wide_kernels(wide_asm).items():
         insns = [b for b in lines if is_insn(b)]
         idx = [k for k, b in enumerate(insns) if b.startswith(MFMA)]
         first, last = idx[0], idx[-1]
@@ -309,7 +311,7 @@ def test_wide_wait_states_around_the_mfmas(wide_asm):
 
 
 def test_wide_no_valu_writes_mfma_operands_just_before(wide_asm):
-    for Bw, lines in wide_kernels(wide_asm).items():
+    for (Bw, _split), lines in wide_kernels(wide_asm).items():
         insns = [b for b in lines if is_insn(b)]
         for k, b in enumerate(insns):
             if not b.startswith(MFMA):
