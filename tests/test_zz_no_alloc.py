@@ -45,7 +45,9 @@ def _both(llk, torch, x, wg, wu, out_dtype, x_stride=None):
 
 # (M, K, N, X row stride or None): each pair is a larger call then a smaller one.
 PAIRS = [
-    ((255, 5120, 13824, None), (100, 1000, 500, 1003)),   # tile k split; then padded X
+    # k splits (bf16: the wide kernel's register-order partials, fp32: the
+    # 128-column kernel's planes); then padded X
+    ((255, 5120, 13824, None), (100, 1000, 500, 1003)),
     ((8, 13824, 5120, None), (3, 4096, 384, None)),       # small-M k split; then unsplit
     ((9000, 4000, 256, None), (300, 4000, 256, 4008)),    # padded X beyond the array: chunks
 ]
