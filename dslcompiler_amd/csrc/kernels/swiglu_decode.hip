@@ -81,7 +81,8 @@ constexpr bool skinny_one_pass(int NMAT, int red_floats) {
 // PIPE: the weight loads of the next 64-k step are issued before this
 // step's MFMAs (one step of weights in flight per wave beyond the one being
 // used; UNROLL is then unused) -- the form for the shapes whose register
-// budget holds two steps, measured 1.5% faster at decode M = 8.
+// budget holds two steps, measured 1.5% faster at decode M = 8 and 3-8%
+// faster for SwiGLU at M = 40-64 (N = 14336, K = 4096).
 template <int NMAT, int MT, int KS, int G, int GW, int OUT, bool XVEC, int UNROLL, bool PIPE>
 __global__ __launch_bounds__(KS * G * 64) void skinny_kernel(SkinnyArgs a) {
   extern __shared__ __attribute__((aligned(16))) float red[];  // [1 or NMAT][KS][G][GW][MT][16][64]
@@ -310,8 +311,8 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(SkinnyArgs a, int ro
 // traffic, the deeper wave count wins); with M > 32 both use GW = 2 (at
 // M = 64 X traffic equals the weights').  Register budgets: KS * G * 64
 // threads with at most 512 / waves-per-SIMD VGPRs each; the SwiGLU M > 32
-// form holds 2 x 2 x 2 accumulators plus 2 k steps of loads (~312 VGPRs, one
-// wave per SIMD).  LDS: KS * G * GW * MT * 4 KiB per matrix, both matrices
+// form holds 2 x 2 x 2 accumulators (128 AGPRs) plus 2 k steps of loads
+// (376 VGPRs with the pipelined loop, one wave per SIMD).  LDS: KS * G * GW * MT * 4 KiB per matrix, both matrices
 // at once when that fits 128 KiB.
 template <int NMAT, int MT, int W>
 struct SkinnyCfg {
@@ -323,9 +324,12 @@ struct SkinnyCfg {
               : (NMAT == 2 ? 4 / G : (MT == 1 ? 16 / G : 4));
   static constexpr int UNROLL = (GW == 2 && NMAT == 1 && MT == 1) ? 1 : 2;
   // M <= 32 with one group per wave or one wave group, up to 8 waves per
-  // wave group: two steps of weights in flight fit the registers (the
-  // 4-group forms with 4 waves per group spill).
-  static constexpr bool PIPE = MT == 1 && (GW == 1 || G == 1) && G * GW <= 2;
+  // wave group, and SwiGLU with M > 32 (one wave group of two groups, four
+  // waves): two steps of weights in flight fit the registers (the 4-group
+  // forms with 4 waves per group spill).  The GEMM with M > 32 keeps the
+  // plain loop, 1-4% faster there (M = 48, 64).
+  static constexpr bool PIPE =
+      (MT == 1 && (GW == 1 || G == 1) && G * GW <= 2) || (NMAT == 2 && MT == 2 && G == 1 && GW == 2);
   static constexpr size_t lds = (size_t)skinny_red_floats(KS, G, GW, MT) * sizeof(float) *
                                 (skinny_one_pass(NMAT, skinny_red_floats(KS, G, GW, MT)) ? 2 : 1);
   static_assert(G * GW == W && KS * G <= 16 && lds <= 131072, "small-M launch shape");

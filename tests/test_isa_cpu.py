@@ -1,5 +1,6 @@
-"""Checks on the gfx950 code object of the tile kernel (CPU only: hipcc
-cross-compiles the kernel source to assembly).
+"""Checks on the gfx950 code objects of the tile kernels, and the small-M
+kernel's resource use (CPU only: hipcc cross-compiles the kernel sources to
+assembly).
 
 The tile kernel issues its v_mfma_f32_16x16x32_bf16 instructions from inline
 assembly with the accumulators tied to AGPRs, so the compiler's hazard
@@ -322,3 +323,40 @@ def test_wide_no_valu_writes_mfma_operands_just_before(wide_asm):
                 if prev.startswith("v_") and not prev.startswith("v_mfma"):
                     kind, dst = regs(operands(prev)[0]) if operands(prev) else ("", set())
                     assert not (kind == "v" and dst & src), (Bw, prev, b)
+
+
+# ---- small-M kernel ---------------------------------------------------------
+
+@pytest.fixture(scope="module")
+def skinny_asm(tmp_path_factory) -> str:
+    out = tmp_path_factory.mktemp("isa") / "swiglu_decode.s"
+    cmd = [B.HIPCC, *B.HIP_FLAGS, *B.INCLUDES, "--cuda-device-only", "-S",
+           str(B.CSRC / "kernels" / "swiglu_decode.hip"), "-o", str(out)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    return out.read_text()
+
+
+def test_small_m_kernels_no_scratch_and_pipelined_forms(skinny_asm):
+    """Every small-M instantiation with vector X loads runs without scratch
+    (the pipelined loop holds two 64-k steps of weights in registers); the
+    element-wise X forms (unaligned X rows) of the 16-wave SwiGLU shapes keep
+    one 8-byte spill, stored before the K loop and reloaded after it, within
+    12 bytes of scratch.  The SwiGLU form for M > 32 (two 32-row tiles, one
+    wave group of two column groups, four waves) with vector X loads is the
+    pipelined one, the GEMM's is not."""
+    meta = dict(re.findall(r"\.name:\s+(_ZN10llk_gfx95013skinny_kernel\w+)\n"
+                           r"\s+\.private_segment_fixed_size:\s+(\d+)", skinny_asm))
+    assert len(meta) >= 24, sorted(meta)
+    # NMAT, MT, KS, G, GW, OUT, XVEC, UNROLL, PIPE
+    sym = re.compile(r"skinny_kernelILi(\d)ELi(\d)ELi(\d+)ELi(\d)ELi(\d)ELi(\d)ELb(\d)ELi(\d)ELb(\d)E")
+    forms = [tuple(int(v) for v in sym.search(name).groups()) for name in meta]
+    for f, size in zip(forms, meta.values()):
+        if f[6] == 1:
+            assert size == "0", (f, size)
+        else:
+            assert int(size) <= 12 and (size == "0" or f[2] * f[3] == 16), (f, size)
+    swiglu_m64 = [f for f in forms if f[:5] == (2, 2, 4, 1, 2) and f[6] == 1]
+    gemm_m64 = [f for f in forms if f[:5] == (1, 2, 4, 1, 2) and f[6] == 1]
+    assert swiglu_m64 and all(f[8] == 1 for f in swiglu_m64), swiglu_m64
+    assert gemm_m64 and all(f[8] == 0 for f in gemm_m64), gemm_m64
