@@ -21,6 +21,7 @@
 // orders the two, so no device-scope fences are needed.
 #include "common.h"
 #include "launch.h"
+#include "tile_ops.h"
 
 namespace llk_gfx950 {
 
@@ -412,6 +413,220 @@ static int skinny_threads_w(int W) {
   return SkinnyCfg<NMAT, MT, 1>::KS * SkinnyCfg<NMAT, MT, 1>::G * 64;
 }
 
+
+// ---- decode tile kernel ------------------------------------------------------
+//
+// The small-M form for K a multiple of 64 and X rows 16-byte aligned
+// (ldx % 8 == 0): a workgroup streams its columns' weights and all of X
+// through a ring of three 64-k step slots in LDS, every byte by LDS-DMA
+// (buffer_load_dwordx4 ... lds, as the tile kernels), two steps ahead of the
+// MFMAs.  Weights are the packed payload's contiguous 1 KiB sub-blocks, read
+// non-temporal: each weight byte is read once, and streaming them past L2
+// keeps X there (decode M = 64, N = 14336, K = 4096: 43.3 us with ordinary
+// weight loads, 37.7 us with `nt`).  X moves as whole 128-byte row segments
+// (64 rows; rows >= M read zero through the buffer range check), its 16-byte
+// chunks XOR-swizzled by row & 7 in LDS, so that an MFMA B operand (32 rows x
+// 16 bytes per half wave) hits every bank once.  Every wave issues four
+// weight loads, then two X loads per step, so "step kb has landed" is
+// vmcnt(6) for each wave, then one barrier for the workgroup; the slot the
+// barrier frees (step kb - 1's) takes step kb + 2, and X, like the weights,
+// is loaded two steps ahead of its use.  (Issuing only the X loads that have
+// rows < M, X first with vmcnt(4), left X one step ahead: at M = 16 and 32,
+// where a few waves read the same X lines as every other workgroup, 46 and
+// 45 us instead of 37 and 38.)  The kernel has no k parts inside a workgroup
+// and no partial sums in LDS.
+//
+// A step is 16 weight sub-blocks (16 KiB) + 8 KiB of X.  SwiGLU (NMAT 2): a
+// workgroup covers 64 columns (half an n-block) of Wg and Wu; GEMM (NMAT 1):
+// 128 columns (one n-block).  Wave w = (column group c = w & 1, m tile
+// h = w >> 1) accumulates acc[p] = 32 columns x 32 rows, p = 0, 1 (SwiGLU:
+// gate and up of the same columns, so the epilogue is register-local; GEMM:
+// column groups c and 2 + c).  With S > 1 workgroup (columns, s) covers the
+// 64-k blocks [s kbs, (s + 1) kbs) and writes fp32 partials in the layout of
+// skinny_kernel's, which skinny_reduce_kernel adds in split order.
+struct DecTileArgs {
+  const uint16_t* x;  // [M, K], row stride ldx
+  const uint8_t* w0;  // packed (Wg, or B for the GEMM)
+  const uint8_t* w1;  // packed (Wu), NMAT == 2
+  void* y;            // [M, N]
+  float* part;        // [S][NMAT][rows][n_pad] fp32 partials (S > 1)
+  int64_t ldx, ldy;
+  int M, N, KB, NB, S, kbs, n_pad, rows;
+  bool yvec;
+  bool accumulate;  // GEMM only, S == 1: y += x w (the existing y read in its type)
+};
+
+constexpr int kDecSlots = 3;                   // ring slots (64-k steps)
+constexpr int kDecW = 16384, kDecSlot = 24576; // weights, then X (8 KiB), per slot
+constexpr int kDecLds = kDecSlots * kDecSlot;  // 72 KiB
+
+template <int NMAT, int OUT>
+__global__ __launch_bounds__(256) void decode_tile_kernel(DecTileArgs a) {
+  constexpr int kAhead = kDecSlots - 1;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int cg = wave & 1, mh = wave >> 1;
+  const int per_split = NMAT == 2 ? a.NB * 2 : a.NB;
+  const int grp = blockIdx.x % per_split;
+  const int split = blockIdx.x / per_split;
+  const int nb = NMAT == 2 ? grp >> 1 : grp;
+  const int kb0 = split * a.kbs;
+  const int nkb = min(a.KB - kb0, a.kbs);
+
+  // Weight resources: this n-block's panel from 64-k block kb0 (loads past
+  // the panel read zero); X from column 64 kb0, up to row M.
+  const int64_t panel = (int64_t)a.KB * kBlockBytes;
+  const int64_t woff = (int64_t)nb * panel + (int64_t)kb0 * kBlockBytes;
+  const int wbytes = (int)(panel - (int64_t)kb0 * kBlockBytes);
+  const u32x4 rw_lo = buffer_rsrc(a.w0 + woff, wbytes);
+  const u32x4 rw_hi = buffer_rsrc((NMAT == 2 ? a.w1 : a.w0) + woff, wbytes);
+  const u32x4 rx = buffer_rsrc(a.x + (size_t)kb0 * 64,
+                               (int)((int64_t)a.M * a.ldx * 2 - (int64_t)kb0 * 128));
+  // This wave's weight loads: sub-blocks i = 4 wave + q of the step, i.e.
+  // operand p = i >> 3, k quarter (i >> 1) & 3, column group c = i & 1 --
+  // packed 32-column group 2 (grp & 1) + c of matrix p (SwiGLU) or 2 p + c
+  // (GEMM) -- placed at ((p * 2 + c) * 4 + kq) KiB of the slot.
+  int w_vo[4];
+  uint32_t w_lds[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int i = wave * 4 + q, p = i >> 3, kq = (i >> 1) & 3, c = i & 1;
+    const int n32 = NMAT == 2 ? 2 * (grp & 1) + c : 2 * p + c;
+    w_vo[q] = (kq * 4 + n32) * kSubBytes + lane * 16;
+    w_lds[q] = (uint32_t)(((p * 2 + c) * 4 + kq) * 1024);
+  }
+  // This wave's X loads: rows 8 f .. 8 f + 7 for f = 2 wave + q, lane l
+  // fetching physical chunk l & 7 of row 8 f + l / 8, i.e. logical chunk
+  // (l & 7) ^ (row & 7).  Loads of rows >= M read zeros (no memory traffic)
+  // but are issued all the same, so that every wave waits for one count.
+  int x_vo[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int row = 8 * (wave * 2 + q) + (lane >> 3);
+    x_vo[q] = (row * (int)a.ldx + (((lane & 7) ^ (row & 7)) * 8)) * 2;
+  }
+  const uint32_t lds0 = lds_addr(smem);
+  const u32x4 rw_mine = wave < 2 ? rw_lo : rw_hi;  // operand p = wave >> 1
+  auto issue = [&](int kb, int slot) {
+    const uint32_t base = lds0 + (uint32_t)(slot * kDecSlot);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dma16_nt(rw_mine, w_vo[q] + kb * kBlockBytes, 0, base + w_lds[q]);
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      dma16(rx, x_vo[q] + kb * 128, 0, base + kDecW + (uint32_t)(wave * 2 + q) * 1024);
+  };
+  // Steps past the split's end read zeros (weights) or unused X into slots
+  // no MFMA reads: the load count per step stays uniform.
+#pragma unroll
+  for (int s = 0; s < kAhead; ++s) issue(s, s);
+
+  f32x16 acc[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[p][r] = 0.0f;
+  const uint8_t* const a_rd = smem + cg * 4096 + lane * 16;  // + slot + p * 8 KiB + kq KiB
+  const int xm = mh * 32 + (lane & 31);                       // the B operand's row
+  const uint8_t* const b_rd = smem + kDecW + xm * 128;
+  int slot = 0, fill = kAhead;
+  for (int kb = 0; kb < nkb; ++kb) {
+    wait_vmcnt<6 * (kAhead - 1)>();  // this wave's loads of step kb have landed
+    __syncthreads();                 // ... every wave's; slot `fill` (step kb - 1) is free
+    issue(kb + kAhead, fill);
+    fill = fill + 1 == kDecSlots ? 0 : fill + 1;
+    const int off = slot * kDecSlot;
+    bf16x8 A[2][4], Bx[4];
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) {
+      Bx[kq] = *reinterpret_cast<const bf16x8*>(b_rd + off +
+                                                (((2 * kq + (lane >> 5)) ^ (xm & 7)) * 16));
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+        A[p][kq] = *reinterpret_cast<const bf16x8*>(a_rd + off + p * 8192 + kq * 1024);
+    }
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) acc[p] = mfma32(A[p][kq], Bx[kq], acc[p]);
+    slot = slot + 1 == kDecSlots ? 0 : slot + 1;
+  }
+  wait_vmcnt<0>();  // the trailing loads have landed before the workgroup ends
+
+  // acc[p] register r, lane l: row m = 32 h + l % 32, column 8 (r / 4) +
+  // 4 (l / 32) + r % 4 of the wave's 32-column group of operand p.
+  const int m = xm;
+  const int n_col = NMAT == 2 ? grp * 64 + cg * 32 : nb * kPackN + cg * 32;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int n_off = 8 * g + 4 * (lane >> 5);
+    if (a.S > 1) {
+      if (m < a.rows) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const int mat = NMAT == 2 ? p : 0;
+          const int n = n_col + (NMAT == 2 ? 0 : p * 64) + n_off;
+          float* dst = a.part + (((size_t)split * NMAT + mat) * a.rows + m) * a.n_pad + n;
+          *reinterpret_cast<f32x4*>(dst) =
+              f32x4{acc[p][4 * g], acc[p][4 * g + 1], acc[p][4 * g + 2], acc[p][4 * g + 3]};
+        }
+      }
+    } else if constexpr (NMAT == 2) {
+      float v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = swiglu_act(acc[0][4 * g + q], acc[1][4 * g + q]);
+      store4<OUT>(a.y, a.ldy, a.M, a.N, m, n_col + n_off, v, a.yvec);
+    } else {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = acc[p][4 * g + q];
+        const int n = n_col + p * 64 + n_off;
+        if (a.accumulate) add_existing4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
+        store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
+      }
+    }
+  }
+}
+
+template <int NMAT, int OUT>
+const char* decode_tile_symbol() {
+  static const std::string name = "_ZN10llk_gfx95018decode_tile_kernelI" + mangle_int(NMAT) +
+                                  mangle_int(OUT) + "EEvNS_11DecTileArgsE";
+  return name.c_str();
+}
+
+template <int NMAT, int OUT>
+static hipError_t launch_decode_tile_t(const DecTileArgs& a, const llk::ModuleFns* mod,
+                                       hipStream_t s) {
+  auto fn = decode_tile_kernel<NMAT, OUT>;
+  if (!mod) {
+    static std::atomic<uint64_t> lds_set{0};
+    hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(fn), kDecLds, lds_set);
+    if (e != hipSuccess) return e;
+  }
+  const unsigned groups = (unsigned)((NMAT == 2 ? a.NB * 2 : a.NB) * a.S);
+  hipError_t e = launch_kernel(mod, reinterpret_cast<const void*>(fn),
+                               &decode_tile_symbol<NMAT, OUT>, dim3(groups), dim3(256), kDecLds,
+                               s, a);
+  if (e != hipSuccess || a.S == 1) return e;
+  SkinnyArgs r{};
+  r.y = a.y;
+  r.part = a.part;
+  r.ldy = a.ldy;
+  r.M = a.M;
+  r.N = a.N;
+  r.S = a.S;
+  r.n_pad = a.n_pad;
+  r.yvec = a.yvec;
+  r.accumulate = a.accumulate;
+  const int64_t threads = (int64_t)a.M * (a.n_pad / 4);
+  return launch_kernel(mod, reinterpret_cast<const void*>(skinny_reduce_kernel<NMAT, OUT>),
+                       &skinny_reduce_symbol<NMAT, OUT>,
+                       dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, r, a.rows);
+}
+
 }  // namespace llk_gfx950
 
 // Rows of the partial buffer for M rows (whole 32-row MFMA groups).
@@ -474,6 +689,65 @@ hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const voi
   if (mode == 0)
     return mt == 1 ? launch_skinny_mt<1, 1>(a, G, out, xvec, mod, s)
                    : launch_skinny_mt<1, 2>(a, G, out, xvec, mod, s);
+#endif
+  return hipErrorInvalidValue;
+}
+
+// Whether the decode tile kernel takes a shape: M <= 64, K a multiple of
+// 64, X rows 16-byte aligned (ldx % 8 == 0 and a 16-byte aligned base, the
+// caller's check), and the 32-bit buffer offsets: 64 rows of X plus the
+// trailing steps, and one weight panel plus them.
+bool llk_decode_tile_fits(int M, int64_t K, int64_t ldx) {
+  if (M < 1 || M > 64 || K < 64 || K % 64 != 0 || ldx < K || ldx % 8 != 0) return false;
+  const int64_t KB = K / 64;
+  return 64 * ldx * 2 + (KB + 2) * 128 < ((int64_t)1 << 31) &&
+         (KB + 2) * (int64_t)llk_gfx950::kBlockBytes < ((int64_t)1 << 31);
+}
+
+// Internal: the decode tile kernel.  mode 1 = SwiGLU (w0 = Wg, w1 = Wu),
+// mode 0 = GEMM (w0 = B); llk_decode_tile_fits(M, 64 * KB, ldx) must hold.
+// S > 1 splits K over S workgroups of kbs = ceil(KB / S) blocks (every split
+// non-empty: (S - 1) * kbs < KB) through `ws`, which holds
+// llk_skinny_workspace_bytes(nmat, M, 128 * NB, S) bytes; accumulate (GEMM
+// only) adds the existing y.
+hipError_t llk_launch_decode_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
+                                  const void* w1, void* y, int64_t ldy, int M, int N, int KB,
+                                  int NB, int S, void* ws, int out, bool yvec, bool accumulate,
+                                  const llk::ModuleFns* mod, hipStream_t s) {
+  using namespace llk_gfx950;
+  if (!llk_decode_tile_fits(M, (int64_t)KB * 64, ldx) || NB < 1 || (accumulate && mode != 0))
+    return hipErrorInvalidValue;
+  DecTileArgs a{};
+  a.x = x;
+  a.w0 = static_cast<const uint8_t*>(w0);
+  a.w1 = static_cast<const uint8_t*>(w1);
+  a.y = y;
+  a.part = static_cast<float*>(ws);
+  a.ldx = ldx;
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.KB = KB;
+  a.NB = NB;
+  a.S = S < 1 ? 1 : S;
+  a.kbs = (KB + a.S - 1) / a.S;
+  a.n_pad = NB * kPackN;
+  a.rows = skinny_rows(M);
+  a.yvec = yvec;
+  a.accumulate = accumulate;
+  if (a.S > 1 && (ws == nullptr || (int64_t)(a.S - 1) * a.kbs >= KB)) return hipErrorInvalidValue;
+#if !defined(LLK_CO_OP) || LLK_CO_OP == 1
+  if (mode == 1) {
+    if (out == kOutBF16) return launch_decode_tile_t<2, kOutBF16>(a, mod, s);
+    if (out == kOutF32) return launch_decode_tile_t<2, kOutF32>(a, mod, s);
+  }
+#endif
+#if !defined(LLK_CO_OP) || LLK_CO_OP == 0
+  if (mode == 0) {
+    if (out == kOutBF16) return launch_decode_tile_t<1, kOutBF16>(a, mod, s);
+    if (out == kOutF32) return launch_decode_tile_t<1, kOutF32>(a, mod, s);
+    if (out == kOutF16) return launch_decode_tile_t<1, kOutF16>(a, mod, s);
+  }
 #endif
   return hipErrorInvalidValue;
 }

@@ -41,6 +41,13 @@ __device__ __forceinline__ void dma16(const u32x4& rsrc, int voff, int soff, uin
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :: "s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
 }
+// The same load, non-temporal (`nt`): for data each workgroup reads once
+// and no other workgroup reads again (a decode step's weights), so that it
+// streams past L2 rather than evicting what is reused there.
+__device__ __forceinline__ void dma16_nt(const u32x4& rsrc, int voff, int soff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
+               :: "s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
+}
 // The same load in two statements, for the K loops: set_m0 writes the LDS
 // address and dma16_m0 issues the load that reads it.  The caller puts at
 // least one instruction (an MFMA) between them -- the wait state M0 needs

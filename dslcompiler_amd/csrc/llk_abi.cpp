@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <tuple>
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
@@ -48,6 +49,11 @@ hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const voi
                              hipStream_t s);
 size_t llk_skinny_workspace_bytes(int nmat, int M, int N_pad, int S);
 int llk_skinny_threads(int nmat, int M, int G);
+bool llk_decode_tile_fits(int M, int64_t K, int64_t ldx);
+hipError_t llk_launch_decode_tile(int mode, const uint16_t* x, int64_t ldx, const void* w0,
+                                  const void* w1, void* y, int64_t ldy, int M, int N, int KB,
+                                  int NB, int S, void* ws, int out, bool yvec, bool accumulate,
+                                  const llk::ModuleFns* mod, hipStream_t s);
 hipError_t llk_launch_pad_rows(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* out,
                                int64_t ldo, const llk::ModuleFns* mod, hipStream_t s);
 hipError_t llk_launch_pack(const uint16_t* w, int64_t ld, int K, int N, int KB, int NB, void* out,
@@ -340,6 +346,7 @@ hipStream_t stream_of(const llk_kernel_context* ctx) {
 // Launch plan of one contraction (SwiGLU: nmat 2, GEMM: nmat 1).
 struct Plan {
   bool skinny = false;   // small-M bandwidth kernel
+  bool dtile = false;    // ... on the decode tile kernel (with skinny)
   int S = 1;             // k splits across workgroups (either kernel)
   int G = 1;             // small-M kernel: 32-column groups per workgroup
   bool pad = false;      // tile path: copy X into a padded buffer first
@@ -562,6 +569,36 @@ SmallMChoice small_m_choice(int nmat, int64_t M, int64_t KB, int64_t NB, int64_t
   return best;
 }
 
+// Decode tile kernel k splits: the S minimising
+//   rounds x per-workgroup bytes / 30 GB/s
+//   + (S > 1: reduce launch ~4 us + partial planes written and read at 4 TB/s)
+// with rounds = ceil(workgroups / decode_target_wgs) and per-workgroup bytes
+// = the split's k steps x 24 KiB (16 KiB of weights + 8 KiB of X per 64-k
+// step: 64 columns of both SwiGLU matrices, 128 of the GEMM's).  A forced
+// split count (> 0) is kept.
+int decode_tile_splits(int nmat, int64_t M, int64_t KB, int64_t NB, int64_t force_s) {
+  const int64_t target = std::max<int64_t>(1, llk::tunable("decode_target_wgs"));
+  const int64_t min_kb = std::max<int64_t>(1, llk::tunable("decode_min_kb"));
+  const int64_t rows = (M + 31) / 32 * 32;
+  const int64_t groups = nmat == 2 ? NB * 2 : NB;
+  int64_t s_lo = 1, s_hi = std::min<int64_t>(64, std::max<int64_t>(1, KB / min_kb));
+  if (force_s > 0) s_lo = s_hi = std::min(force_s, KB);
+  int best_s = 1;
+  double best_t = 0.0;
+  for (int64_t S = s_lo; S <= s_hi; ++S) {
+    const int64_t kbs = (KB + S - 1) / S;
+    const int64_t s_eff = (KB + kbs - 1) / kbs;  // no empty splits
+    const int64_t wgs = groups * s_eff;
+    double t = (double)((wgs + target - 1) / target) * (double)kbs * 24576.0 / 30e9;
+    if (s_eff > 1) t += 4e-6 + 2.0 * s_eff * nmat * rows * NB * 128 * 4 / 4e12;
+    if (best_t == 0.0 || t < best_t) {
+      best_t = t;
+      best_s = (int)s_eff;
+    }
+  }
+  return best_s;
+}
+
 // x == nullptr: plan for the worst case (X needs padding).  Precedence for
 // each knob: a forced tunable, then the active schedule DB's entry
 // (small-M: group width = BN / 32, splits = grain_size; tile: splits =
@@ -583,13 +620,26 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
     if (gw <= 0 && have_db && (se.BN == 32 || se.BN == 64 || se.BN == 128)) gw = se.BN / 32;
     int64_t S = llk::tunable("decode_splits");
     if (S <= 0 && have_db && se.grain_size > 0) S = se.grain_size;
+    auto fit_splits = [&](int s) {
+      size_t ws = llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), s);
+      while (ws > max_ws && s > 1) ws = llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), --s);
+      return std::make_pair(s, ws);
+    };
     const SmallMChoice c = small_m_choice(nmat, M, KB, NB, gw, S);
     p.G = c.width;
-    p.S = c.splits;
-    p.ws_bytes = llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), p.S);
-    while (p.ws_bytes > max_ws && p.S > 1) {
-      --p.S;
-      p.ws_bytes = llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), p.S);
+    std::tie(p.S, p.ws_bytes) = fit_splits(c.splits);
+    // The decode tile kernel unless a width is forced (the small-M kernel's
+    // own knob, or its schedule record) or the shape does not fit it; when
+    // X is unknown (sizing), the larger of the two workspaces.
+    if (llk::tunable("decode_tile") != 0 && gw <= 0 &&
+        llk_decode_tile_fits((int)M, K, x ? x->stride0 : K)) {
+      const auto d = fit_splits(decode_tile_splits(nmat, M, KB, NB, S));
+      if (!x) {
+        p.ws_bytes = std::max(p.ws_bytes, d.second);
+      } else if (x_vec_ok(x)) {
+        p.dtile = true;
+        std::tie(p.S, p.ws_bytes) = d;
+      }
     }
     return p;
   }
@@ -706,6 +756,14 @@ int launch_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights
   const int64_t M = x->dim0, K = x->dim1, N = w0->N;
   const bool yvec = y_vec_ok(y, out_dtype);
   hipError_t e = hipSuccess;
+  if (p.dtile) {
+    e = llk_launch_decode_tile(mode, static_cast<const uint16_t*>(x->data), x->stride0, w0->dev,
+                               w1 ? w1->dev : nullptr, y->data, y->stride0, (int)M, (int)N,
+                               (int)w0->KB, (int)w0->NB, p.S, body, out_dtype, yvec, accumulate,
+                               mod, s);
+    if (e != hipSuccess) return fail_hip(e, what);
+    return LLK_OK;
+  }
   if (p.skinny) {
     e = llk_launch_skinny(mode, static_cast<const uint16_t*>(x->data), x->stride0, w0->dev,
                           w1 ? w1->dev : nullptr, y->data, y->stride0, (int)M, (int)N, (int)K,
@@ -1183,6 +1241,15 @@ int llk_describe_launch(int operation, int64_t M, int64_t N, int64_t K, unsigned
                 (long long)K, (long long)M, (long long)(((int64_t)1 << 31) / 512 - 64));
   out->splits = p.S;
   out->workspace_bytes = p.ws_bytes;
+  if (p.dtile) {
+    out->kernel = 3;
+    out->group_width = 0;
+    out->tile_columns = nmat == 2 ? 64 : 128;
+    out->workgroups = (nmat == 2 ? NB * 2 : NB) * p.S;
+    out->threads_per_workgroup = 256;
+    out->launches = p.S > 1 ? 2 : 1;
+    return LLK_OK;
+  }
   if (p.skinny) {
     out->kernel = 0;
     out->group_width = p.G;

@@ -17,7 +17,11 @@ struct Knob {
 // decode_target_wgs: workgroups per round in the small-M cost model (1 per CU).
 // decode_min_kb:     fewest 64-k steps per split.
 // decode_group_width: force the 32-column groups per small-M workgroup (1, 2
-//                    or 4; 0 = cost model, 2 or 1).
+//                    or 4; 0 = cost model, 2 or 1); a forced width runs the
+//                    small-M kernel of that width.
+// decode_tile:       1 = M <= 64 with K a multiple of 64 and 16-byte aligned
+//                    X rows runs on the decode tile kernel (LDS-DMA ring);
+//                    0 = always the small-M kernel.
 // tile_splits:       force the tile kernel's k-split count (0 = cost model).
 // tile_wgs_per_wave: workgroups the tile kernel runs at once (1 per CU).
 // tile_min_kb:       fewest 64-k steps per tile-kernel split.
@@ -37,6 +41,7 @@ Knob g_knobs[] = {
     {"decode_target_wgs", {256}},
     {"decode_min_kb", {2}},
     {"decode_group_width", {0}},
+    {"decode_tile", {1}},
     {"tile_splits", {0}},
     {"tile_wgs_per_wave", {256}},
     {"tile_min_kb", {4}},

@@ -24,7 +24,8 @@ namespace llk_tools {
 
 // Name of llk_launch_plan::kernel.
 inline const char* kernel_name(int kernel) {
-  return kernel == 0 ? "small_m" : kernel == 1 ? "mfma_tile" : "swiglu_wide";
+  return kernel == 0 ? "small_m" : kernel == 1 ? "mfma_tile" : kernel == 2 ? "swiglu_wide"
+                                                                          : "decode_tile";
 }
 
 class Options {

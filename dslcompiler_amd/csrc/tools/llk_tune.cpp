@@ -12,14 +12,17 @@
 // cl_opts.h); an unknown option exits 1.
 //
 // Candidates are the dispatcher's launch knobs for the shape's kernel:
-// small-M kernel (M <= 64): the dispatcher's own choice (width and splits
-// from its cost model), then 32-column groups per workgroup G in {1, 2, 4}
-// x k splits S in {auto, 1, 2, 3, 4, 6, 8}; tile kernel: S in {auto, 1, 2,
-// 3, 4, 6, 8, 12, 16} (at least 4 k-steps of 64 per split).  Each is timed
-// with HIP events (best of 3 windows of --measure-ms after a warm-up); the
-// --top fastest are written as schedule_db.json records in the reference
-// schema with this target's field meaning (BN = 32 G for the small-M
-// kernel, grain_size = S; 0 = the dispatcher chooses), best first, so that
+// M <= 64: the dispatcher's own choice (the decode tile kernel where it
+// applies, else the small-M kernel's width, and splits from the cost
+// models), the same kernel at k splits S in {1, 2, 3, 4, 6, 8}, then the
+// small-M kernel at 32-column groups per workgroup G in {1, 2, 4} x S in
+// {auto, 1, 2, 3, 4, 6, 8}; tile kernels: S in {auto, 1, 2, 3, 4, 6, 8, 12,
+// 16} (at least 4 k-steps of 64 per split).  Each is timed with HIP events
+// (best of 3 windows of --measure-ms after a warm-up); the --top fastest
+// are written as schedule_db.json records in the reference schema with this
+// target's field meaning (BN = 32 G for the small-M kernel, 0 for the
+// decode tile kernel, the tile's columns for the tile kernels; grain_size =
+// S; 0 = the dispatcher chooses), best first, so that
 // the loader's first-match rule picks the best.  --copies rotates weight sets (default:
 // enough to exceed the 256 MB MALL for small M, 1 otherwise).
 #include <hip/hip_runtime_api.h>
@@ -113,7 +116,9 @@ int main(int argc, char** argv) {
     (void)llk_set_tunable("tile_splits", saved_ts);
   };
   if (small) {
-    cands.push_back({0, 0});  // the dispatcher's own choice (width and splits)
+    cands.push_back({0, 0});  // the dispatcher's own choice (kernel, width and splits)
+    for (int s : small_s)     // its kernel (the decode tile kernel where it applies) at S
+      if (s > 0 && s <= KB) cands.push_back({0, s});
     for (int g : gs)
       for (int s : small_s)
         if (s <= KB) cands.push_back({g, s});
@@ -236,11 +241,14 @@ int main(int argc, char** argv) {
   const int count = std::min<int>(top, (int)cands.size());
   for (int i = 0; i < count; ++i) {
     const auto& c = cands[i];
-    const bool sm = c.plan.kernel == 0;
-    const int64_t BM = sm ? (M <= 32 ? 32 : 64) : 256;
-    // BN 0 / grain_size 0: the dispatcher chooses for each shape; VM x VN is
-    // the MFMA tile (small-M kernel 32x32x16, tile kernel 16x16x32)
-    const int64_t BN = sm ? (c.G ? 32 * c.plan.group_width : 0) : (swiglu ? 128 : 256);
+    const bool sm = c.plan.kernel == 0 || c.plan.kernel == 3;  // small-M or decode tile
+    const int64_t BM = c.plan.kernel == 0 ? (M <= 32 ? 32 : 64) : sm ? 64 : 256;
+    // BN 0 / grain_size 0: the dispatcher chooses for each shape (for M <= 64
+    // the decode tile kernel where it applies, else the small-M kernel's
+    // width); VM x VN is the MFMA tile (small-M and decode tile kernels
+    // 32x32x16, tile kernels 16x16x32)
+    const int64_t BN = c.plan.kernel == 0 ? (c.G ? 32 * c.plan.group_width : 0)
+                                          : sm ? 0 : c.plan.tile_columns;
     std::fprintf(f,
                  "    {\"operation\": \"%s\", \"target\": \"gfx950\", \"shape\": {\"M_bucket\": %d, "
                  "\"N\": %lld, \"K\": %lld}, \"dtype\": \"bf16\", \"math_mode\": \"strict\",\n"

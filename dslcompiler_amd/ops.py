@@ -307,7 +307,7 @@ def describe_launch(op: str, M: int, N: int, K: int, x_aligned: bool = True,
         _lib.LLK_PLAN_ACCUMULATE if accumulate else 0) | (_lib.LLK_PLAN_OUT_F32 if out_f32 else 0)
     p = _lib.LaunchPlan()
     check(lib().llk_describe_launch(code, M, N, K, flags, C.byref(p)))
-    return {"kernel": ("small_m", "tile", "wide_tile")[p.kernel], "splits": p.splits,
+    return {"kernel": ("small_m", "tile", "wide_tile", "decode_tile")[p.kernel], "splits": p.splits,
             "group_width": p.group_width, "pad_x": bool(p.pad_x), "workgroups": p.workgroups,
             "threads_per_workgroup": p.threads_per_workgroup, "launches": p.launches,
             "workspace_bytes": p.workspace_bytes, "head_blocks_n": p.head_blocks_n,

@@ -16,7 +16,11 @@ For one call the model takes the dispatcher's launch plan
               burst that every workgroup issues at the same moment.
               Small-M kernel: rounds x max(weight share / per-CU weight rate,
               (weight share + X reads) / per-CU load rate); a workgroup reads
-              X once per wave group, so at M = 64 X is as large as the weights
+              X once per wave group, so at M = 64 X is as large as the weights.
+              Decode tile kernel: rounds x (ring fill + (weights + M rows of
+              X per 64-k step) / its per-CU rate), its weights streamed
+              (non-temporal) at its own stream rate; a k split adds the
+              reduce pass
     reduce  = tile k split only: the reduce kernel reads the partial planes and
               writes Y, after the main kernel
     time    = max(compute, memory, per_cu, shortest launch) + reduce
@@ -105,6 +109,23 @@ def predict(op: str, M: int, N: int, K: int, machine_path: str = str(MACHINE)) -
     elif plan["kernel"] == "wide_tile":
         compute, memory, per_cu, reduce = _tile_launch(cal, cus, nmat, M, N, K, S,
                                                        plan["workgroups"], 2 * plan["tile_columns"])
+        t = max(compute, memory, per_cu, cal["launch_min_s"]) + reduce + gap
+    elif plan["kernel"] == "decode_tile":
+        # Each workgroup streams, per 64-k step of its split, 16 KiB of
+        # weights and M rows x 128 bytes of X (rows >= M move nothing);
+        # 64 MFMA rows of each operand per workgroup.
+        groups = plan["workgroups"]
+        kbs = math.ceil(math.ceil(K / 64) / S)
+        flops = 2.0 * 64 * 128 * kbs * 64 * groups
+        compute = math.ceil(groups / cus) * flops / groups / cal["small_m_flops_per_cu"]
+        wg_bytes = kbs * (16384.0 + min(M, 64) * 128.0)
+        per_cu = math.ceil(groups / cus) * (cal["decode_tile_fill_s"] +
+                                            wg_bytes / cal["decode_tile_bytes_per_cu_s"])
+        partials = 2.0 * plan["workspace_bytes"] if S > 1 else 0.0
+        nbytes = 2.0 * nmat * K * N + 2.0 * M * K + 2.0 * M * N + partials
+        memory = nbytes / cal["decode_tile_stream_bytes_per_s"]
+        # the split reduce: its own pass after the main kernel
+        reduce = cal["decode_tile_reduce_s"] if S > 1 else 0.0
         t = max(compute, memory, per_cu, cal["launch_min_s"]) + reduce + gap
     else:
         groups = plan["workgroups"]

@@ -55,9 +55,14 @@ def main() -> None:
         best = entries[0]["measured_us"]
         bucket = entries[0]["shape"]["M_bucket"]
         for e in entries:
-            s = e["schedule"]
-            # a setting is (column groups, splits); BM and the thread count
-            # follow from the shape
+            s = dict(e["schedule"])
+            # a setting is (column groups, splits) for M <= 64 (BN 0: the
+            # decode tile kernel; 32 G: the small-M kernel of width G) and
+            # the splits for the tile kernels, whose width the dispatcher
+            # picks per shape (BN 0 in the merged record); BM and the thread
+            # count follow from the shape
+            if s["BM"] == 256:
+                s["BN"] = 0
             key = (s["BN"], s["grain_size"])
             scores[(op, bucket)][key].append(e["measured_us"] / best)
             schedules[(op, bucket, key)] = s
@@ -80,9 +85,11 @@ def main() -> None:
             "llk-tune over the BASELINE shapes by make_db.py (one entry per operation and M "
             "bucket; relative_time = mean of time / best time over the bucket's shapes). Field "
             "meaning on this target: BM/BN = workgroup tile rows / columns per weight matrix "
-            "(small-M kernel: BN / 32 = column groups per workgroup); BK = k per step; VM/VN = "
-            "MFMA tile (small-M kernel v_mfma_f32_32x32x16_bf16, tile kernel "
-            "v_mfma_f32_16x16x32_bf16); vector_width = bf16 per lane operand; "
+            "(small-M kernel: BN / 32 = column groups per workgroup; BN 0: the decode tile "
+            "kernel for M <= 64, the width the dispatcher picks per shape for the tile kernels); "
+            "BK = k per step; VM/VN = MFMA tile (small-M and decode tile kernels "
+            "v_mfma_f32_32x32x16_bf16, tile kernels v_mfma_f32_16x16x32_bf16); "
+            "vector_width = bf16 per lane operand; "
             "num_threads = threads per workgroup; parallel_axis = grid decomposition; "
             "grain_size = k splits across workgroups (0 = chosen from the shape)."),
         "measured": measured,

@@ -212,7 +212,9 @@ size_t llk_swiglu_scratch_size(int64_t M, int64_t N, int64_t K);
 #define LLK_PLAN_OUT_F32 4u
 typedef struct llk_launch_plan {
   int kernel;                    /* 0 small-M bandwidth kernel, 1 MFMA tile kernel,
-                                    2 wide SwiGLU tile kernel (bf16 result) */
+                                    2 wide SwiGLU tile kernel (bf16 result),
+                                    3 decode tile kernel (M <= 64, K % 64 == 0,
+                                    aligned X: LLK_PLAN_X_ALIGNED) */
   int splits;                    /* k splits across workgroups (1 = none) */
   int group_width;               /* small-M kernel: 32-column groups per workgroup */
   int pad_x;                     /* tile kernel: X copied to a padded buffer first */
@@ -340,7 +342,9 @@ int llk_fill_normal_bf16(uint64_t seed, uint64_t stream, float sigma,
  * sent to the small-M kernel), "decode_splits" (force its k-split count,
  * 0 = cost model), "decode_target_wgs", "decode_min_kb",
  * "decode_group_width" (force the 32-column groups per small-M workgroup:
- * 1, 2, 4; 0 = cost model),
+ * 1, 2, 4; 0 = cost model; a forced width runs the small-M kernel),
+ * "decode_tile" (1: M <= 64 with K % 64 == 0 and 16-byte aligned X rows
+ * runs on the decode tile kernel; 0: always the small-M kernel),
  * "tile_splits" (force the tile kernel's k-split count, 0 = cost model),
  * "tile_wgs_per_wave", "tile_min_kb", "tile_tail_split" (1: the columns
  * of a partial last wave of tiles may run as a separate k-split launch;

@@ -3,8 +3,8 @@ gfx950 code object, loaded with hipModuleLoadData and resolved with
 hipModuleGetFunction (the reference's lookupOrCompile hands back the
 JIT-compiled entry of a key: JitCache.cpp:182-245).  The objects are built
 from the same sources as the library, so every launch path must give the
-library's own output bit for bit: small-M kernels with and without k
-splits, tile kernels with and without k splits, the wide SwiGLU kernel at
+library's own output bit for bit: the decode tile and small-M kernels
+with and without k splits, tile kernels with and without k splits, the wide SwiGLU kernel at
 both widths and with a k split, padded X and the K = 0 fill; two cases are
 also held to the oracle."""
 from __future__ import annotations
@@ -23,14 +23,18 @@ OUT = {"bf16": 0, "fp32": 2}
 
 # (operation, M, N, K, output, launch the dispatcher picks)
 CASES = [
-    ("fused_swiglu", 1, 1024, 4096, "bf16", "small-M, S = 8"),
-    ("fused_swiglu", 40, 640, 512, "fp32", "small-M, two row groups"),
+    ("fused_swiglu", 1, 1024, 4096, "bf16", "decode tile, S = 16"),
+    ("fused_swiglu", 40, 640, 512, "fp32", "decode tile, S = 4"),
+    ("fused_swiglu", 64, 1376, 512, "bf16", "decode tile (config 1)"),
+    ("fused_swiglu", 1, 1024, 4000, "bf16", "small-M, S = 8"),
+    ("fused_swiglu", 40, 640, 1000, "fp32", "small-M, two row groups, S = 8"),
     ("fused_swiglu", 300, 640, 1000, "bf16", "tile, S = 4, padded X"),
     ("fused_swiglu", 600, 1280, 512, "bf16", "wide tile, B = 7"),
     ("fused_swiglu", 2048, 11008, 512, "bf16", "wide tile, B = 11"),
     ("fused_swiglu", 255, 13824, 5120, "bf16", "wide tile, B = 7, S = 2 (config 5)"),
-    ("matmul", 1, 5120, 13824, "bf16", "small-M, S = 3"),
-    ("matmul", 64, 1024, 4096, "fp32", "small-M, S = 16"),
+    ("matmul", 1, 5120, 13824, "bf16", "decode tile, S = 6"),
+    ("matmul", 64, 1024, 4096, "fp32", "decode tile, S = 22"),
+    ("matmul", 64, 1024, 4000, "fp32", "small-M, S = 16"),
     ("matmul", 300, 640, 1000, "fp32", "tile, S = 4, padded X"),
     ("matmul", 1000, 1024, 512, "bf16", "tile, S = 2"),
 ]
@@ -48,6 +52,7 @@ def test_entry_matches_library_kernels(llk, gpu, op, M, N, K, out, what):
     print(f"case code object {op} M={M} N={N} K={K} {out} ({what})", flush=True)
     plan = llk.describe_launch(op, M, N, K, x_aligned=K % 64 == 0)
     assert (plan["kernel"] == "small_m") == what.startswith("small-M")
+    assert (plan["kernel"] == "decode_tile") == what.startswith("decode tile")
     assert (plan["kernel"] == "wide_tile") == what.startswith("wide")
     wide = re.search(r"B = (\d+)", what)
     if wide:

@@ -360,3 +360,46 @@ def test_small_m_kernels_no_scratch_and_pipelined_forms(skinny_asm):
     gemm_m64 = [f for f in forms if f[:5] == (1, 2, 4, 1, 2) and f[6] == 1]
     assert swiglu_m64 and all(f[8] == 1 for f in swiglu_m64), swiglu_m64
     assert gemm_m64 and all(f[8] == 0 for f in gemm_m64), gemm_m64
+
+
+def test_decode_tile_kernel_loop(skinny_asm):
+    """The decode tile kernel (every instantiation): no scratch; its K loop
+    (one 64-k step) holds exactly one vector-memory wait, vmcnt(6) -- the
+    wave's six loads of the next step may still be in flight -- then one
+    barrier, four non-temporal weight LDS-DMA loads and two X ones, each
+    right after its own M0 write and one wait state, and eight
+    v_mfma_f32_32x32x16_bf16."""
+    names = re.findall(r"^(_ZN10llk_gfx95018decode_tile_kernel\w+):", skinny_asm, re.M)
+    assert len(names) == 5, names  # SwiGLU bf16 / fp32, GEMM bf16 / fp16 / fp32
+    meta = dict(re.findall(r"\.name:\s+(_ZN10llk_gfx95018decode_tile_kernel\w+)\n"
+                           r"\s+\.private_segment_fixed_size:\s+(\d+)", skinny_asm))
+    assert sorted(meta) == sorted(names) and set(meta.values()) == {"0"}, meta
+    for name in names:
+        body = skinny_asm[skinny_asm.index(name + ":"):]
+        body = body[:body.index("s_endpgm")]
+        lines = [ln.split(";")[0].strip() for ln in body.split("\n")]
+        lines = [ln for ln in lines if ln]
+        labels = {ln[:-1]: i for i, ln in enumerate(lines) if ln.endswith(":")}
+        # loop regions: a header label to the last backward branch to it (the
+        # conditional X loads give the body more than one path back)
+        ends: dict[int, int] = {}
+        for i, ln in enumerate(lines):
+            m = re.match(r"^s_(?:cbranch_\w+|branch)\s+(\.LBB\d+_\d+)$", ln)
+            if m and m.group(1) in labels and labels[m.group(1)] < i:
+                ends[labels[m.group(1)]] = i
+        loop = [lines[h:e + 1] for h, e in ends.items()
+                if any("v_mfma" in b for b in lines[h:e + 1])]
+        assert len(loop) == 1, name
+        loop = loop[0]
+        assert sum("v_mfma_f32_32x32x16_bf16" in b for b in loop) == 8, name
+        vm = [re.search(r"vmcnt\((\d+)\)", b).group(1) for b in loop
+              if b.startswith("s_waitcnt") and "vmcnt" in b]
+        assert vm == ["6"], (name, vm)
+        assert sum(b == "s_barrier" for b in loop) == 1, name
+        loads = [i for i, b in enumerate(loop) if b.startswith("buffer_load") and b.endswith("lds")]
+        assert len(loads) == 6, name
+        assert sum(" nt lds" in loop[i] for i in loads) == 4, name
+        for i in loads:
+            assert loop[i - 2].startswith("s_mov_b32 m0,") and loop[i - 1] == "s_nop 0", \
+                (name, loop[i - 2:i + 1])
+        assert sum(b.startswith("s_mov_b32 m0,") for b in loop) == 6, name

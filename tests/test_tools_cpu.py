@@ -50,9 +50,9 @@ def test_compile_buckets_follow_shape_specialization(tmp_path):
     for m, b in zip((1, 4, 16, 64, 128), range(5)):
         assert f"@bucket_M{m}: llk.fused_swiglu M={m} N=512 K=256 -> bucket {b}" in r.stdout
     assert r.stdout.rstrip().endswith("Compilation successful")
-    # M <= 64: the small-M kernel; M = 128: a tile kernel (the wide SwiGLU one
-    # here: 5 tiles of 112 columns model below 4 of 128)
-    assert "kernel=small_m" in r.stdout and "kernel=swiglu_wide" in r.stdout
+    # M <= 64: the decode tile kernel; M = 128: a tile kernel (the wide
+    # SwiGLU one here: 5 tiles of 112 columns model below 4 of 128)
+    assert "kernel=decode_tile" in r.stdout and "kernel=swiglu_wide" in r.stdout
 
 
 @pytest.mark.parametrize("kw,msg", [
@@ -235,7 +235,13 @@ def test_describe_launch_configs():
     # config 5's SwiGLU at M = 1000: 112-column tiles, 496 of them
     p = llk.describe_launch("fused_swiglu", 1000, 13824, 5120)
     assert (p["kernel"], p["workgroups"], p["tile_columns"]) == ("wide_tile", 496, 112)
+    # config 4: the decode tile kernel, 64-column workgroups, unsplit
     p = llk.describe_launch("fused_swiglu", 8, 14336, 4096)
+    assert (p["kernel"], p["workgroups"], p["threads_per_workgroup"], p["splits"],
+            p["tile_columns"], p["workspace_bytes"], p["launches"]) == \
+        ("decode_tile", 224, 256, 1, 64, 0, 1)
+    # unaligned X rows: the small-M kernel
+    p = llk.describe_launch("fused_swiglu", 8, 14336, 4096, x_aligned=False)
     assert p["kernel"] == "small_m" and p["workgroups"] * p["threads_per_workgroup"] >= 256 * 256
     p = llk.describe_launch("matmul", 4096, 4096, 4096)
     assert (p["kernel"], p["workgroups"]) == ("tile", 256)
@@ -275,13 +281,54 @@ def test_tile_tail_split_plans():
             llk.set_tunable(name, old)
 
 
+def test_decode_tile_split_choices():
+    """The decode tile kernel's k splits for the BASELINE decode shapes:
+    config 4 and the config-5 SwiGLU unsplit (224 and 216 workgroups), the
+    config-5 down projection (40 n-blocks) in 6 splits, 240 workgroups in
+    one round; a narrow N spreads K over more splits; a forced count is
+    kept; unaligned X, `decode_tile` = 0 and a forced group width route to
+    the small-M kernel."""
+    plan = lambda op, M, N, K, **kw: (lambda p: (p["kernel"], p["splits"], p["workgroups"]))(  # noqa: E731
+        llk.describe_launch(op, M, N, K, **kw))
+    for M in (1, 8, 16, 64):
+        assert plan("fused_swiglu", M, 14336, 4096) == ("decode_tile", 1, 224)
+    for M in (1, 17):
+        assert plan("fused_swiglu", M, 13824, 5120) == ("decode_tile", 1, 216)
+    for M in (1, 17, 64):
+        assert plan("matmul", M, 5120, 13824) == ("decode_tile", 6, 240)
+    assert plan("fused_swiglu", 8, 128, 4096)[1] > 8
+    assert plan("fused_swiglu", 8, 14336, 4096, x_aligned=False)[0] == "small_m"
+    assert plan("fused_swiglu", 8, 14336, 4000)[0] == "small_m"  # K % 64 != 0
+    for name, value in (("decode_splits", 3), ("decode_tile", 0), ("decode_group_width", 2)):
+        old = llk.get_tunable(name)
+        llk.set_tunable(name, value)
+        try:
+            p = plan("fused_swiglu", 8, 14336, 4096)
+            assert p[0] == ("decode_tile" if name == "decode_splits" else "small_m"), (name, p)
+            if name == "decode_splits":
+                assert p[1:] == (3, 672)
+        finally:
+            llk.set_tunable(name, old)
+    assert llk.get_tunable("decode_tile") == 1
+
+
 def test_small_m_cost_model_choices():
-    """The small-M dispatcher's (width, splits) against llk-tune's measured
-    best on MI355X for the BASELINE decode shapes: config 1 (M=64, N=1376,
-    K=512: 8.27 us at width 1 unsplit; every split adds ~2.8 us), config 4
-    (width 2 unsplit, 224 workgroups), M=64 decode (width 2: 53.9 us vs 68.0
-    at width 1), the config-5 down projection (width 2, 3 splits: 240
-    workgroups in one round)."""
+    """The small-M dispatcher's (width, splits) -- for X the decode tile
+    kernel does not take, here with `decode_tile` = 0 -- against llk-tune's
+    measured best on MI355X for the BASELINE decode shapes: config 1 (M=64,
+    N=1376, K=512: 8.27 us at width 1 unsplit; every split adds ~2.8 us),
+    config 4 (width 2 unsplit, 224 workgroups), M=64 decode (width 2: 53.9
+    us vs 68.0 at width 1), the config-5 down projection (width 2, 3 splits:
+    240 workgroups in one round)."""
+    old_t = llk.get_tunable("decode_tile")
+    llk.set_tunable("decode_tile", 0)
+    try:
+        _small_m_choices()
+    finally:
+        llk.set_tunable("decode_tile", old_t)
+
+
+def _small_m_choices():
     plan = lambda op, M, N, K: (lambda p: (p["group_width"], p["splits"]))(  # noqa: E731
         llk.describe_launch(op, M, N, K))
     assert plan("fused_swiglu", 64, 1376, 512) == (1, 1)
@@ -308,9 +355,12 @@ def test_small_m_cost_model_choices():
 
 def test_tile_kernel_k_limit():
     """K beyond the tile kernel's 32-bit offsets is an error, not a launch;
-    the small-M kernel has no such limit."""
+    M <= 64 runs it on the decode tile kernel, and a K beyond that kernel's
+    32-bit offsets (a weight panel of 2 GiB) on the small-M kernel, which has
+    no such limit."""
     K = 1 << 22
     with pytest.raises(llk.LLKError, match="too large"):
         llk.describe_launch("fused_swiglu", 100, 256, K)
-    assert llk.describe_launch("fused_swiglu", 8, 256, K)["kernel"] == "small_m"
+    assert llk.describe_launch("fused_swiglu", 8, 256, K)["kernel"] == "decode_tile"
+    assert llk.describe_launch("fused_swiglu", 8, 256, 1 << 27)["kernel"] == "small_m"
     assert llk.describe_launch("fused_swiglu", 100, 256, K - 128)["kernel"] == "tile"
