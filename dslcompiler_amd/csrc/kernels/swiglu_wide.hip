@@ -56,6 +56,14 @@
 // staged whole in LDS (256 rows x 32 B bytes) and copied out in 16-byte
 // chunks with non-temporal stores.
 //
+// WNT (one m tile, M <= 256: every weight byte is read by one workgroup):
+// the weight loads are non-temporal, so the stream passes L2 without
+// evicting X (config 5's SwiGLU at M = 255: K loop 58.9 -> 52.2 us, launch
+// 84.6 -> 80.5 us in per-workgroup timestamps; 86.2 -> 79.1-80.4 us through
+// the library, the MLP 150.4 -> 138.5-140.1 us; with several m tiles, which
+// re-read the weight panels from L2, `nt` is slower: M = 1000 +3%, config 3
+// +4%; A/B on one box).
+//
 // Optional k split (SPLIT, config 5's SwiGLU at M = 255: 124 tiles of B = 7
 // x 2 splits = 248 workgroups where the 128-column kernel runs 108 x 2 =
 // 216): workgroup (tile, s) covers the 64-k blocks [s kbs, (s + 1) kbs) and
@@ -182,7 +190,7 @@ __device__ __forceinline__ void wide_tile_mn(const WideArgs& a, int tile, int& t
   }
 }
 
-template <int B, bool SPLIT>
+template <int B, bool SPLIT, bool WNT>
 __global__ __launch_bounds__(256, 1) void mfma_swiglu_wide_kernel(WideArgs a) {
   using Cfg = WideCfg<B>;
   constexpr int R = Cfg::R, C = Cfg::C, H0 = Cfg::H0, LW = Cfg::LW, LH = Cfg::LH;
@@ -261,7 +269,8 @@ __global__ __launch_bounds__(256, 1) void mfma_swiglu_wide_kernel(WideArgs a) {
   auto x_voff = [&](int blk, int i) { return x_off[i] + blk * 128; };
   // Prologue form (M0 write, wait state and load in one statement).
   auto pre_w = [&](int s, int k) {
-    dma16(k < LH ? rg : ru, w_voff(s, k), 0, w_m0(s & 3, k));
+    if constexpr (WNT) dma16_nt(k < LH ? rg : ru, w_voff(s, k), 0, w_m0(s & 3, k));
+    else dma16(k < LH ? rg : ru, w_voff(s, k), 0, w_m0(s & 3, k));
   };
   auto pre_x = [&](int blk, int i) { dma16(xrsrc, x_voff(blk, i), 0, x_m0(blk & 1, i)); };
 
@@ -343,7 +352,9 @@ __global__ __launch_bounds__(256, 1) void mfma_swiglu_wide_kernel(WideArgs a) {
   };
   auto issue_ld = [&](auto KSc, auto L, auto D, auto I) {
     constexpr int KS = decltype(KSc)::value, d = decltype(D)::value, idx = decltype(I)::value;
-    if constexpr (decltype(L)::value == 0)
+    if constexpr (decltype(L)::value == 0 && WNT)
+      dma16_m0_nt(idx < LH ? rg : ru, w_vo[idx % LH] + (g + KS + d) * 8192, 0);
+    else if constexpr (decltype(L)::value == 0)
       dma16_m0(idx < LH ? rg : ru, w_vo[idx % LH] + (g + KS + d) * 8192, 0);
     else
       dma16_m0(xrsrc, x_off[idx] + ((g >> 1) + (KS >> 1) + d) * 128, 0);
@@ -548,10 +559,10 @@ __global__ __launch_bounds__(256) void wide_reduce_kernel(WideArgs a) {
   store4<kOutBF16>(a.y, a.ldy, a.M, a.N, m, n, v, vec);
 }
 
-template <int B, bool SPLIT>
+template <int B, bool SPLIT, bool WNT>
 const char* wide_symbol() {
   static const std::string name = "_ZN10llk_gfx95023mfma_swiglu_wide_kernelI" + mangle_int(B) +
-                                  mangle_bool(SPLIT) + "EEvNS_8WideArgsE";
+                                  mangle_bool(SPLIT) + mangle_bool(WNT) + "EEvNS_8WideArgsE";
   return name.c_str();
 }
 
@@ -562,24 +573,28 @@ const char* wide_reduce_symbol() {
   return name.c_str();
 }
 
-template <int B, bool SPLIT>
+template <int B, bool SPLIT, bool WNT>
 static hipError_t launch_wide_kernel(const WideArgs& a, const llk::ModuleFns* mod,
                                      hipStream_t s) {
-  auto fn = mfma_swiglu_wide_kernel<B, SPLIT>;
+  auto fn = mfma_swiglu_wide_kernel<B, SPLIT, WNT>;
   if (!mod) {
     static std::atomic<uint64_t> lds_set{0};
     hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(fn), WideCfg<B>::kLds, lds_set);
     if (e != hipSuccess) return e;
   }
-  return launch_kernel(mod, reinterpret_cast<const void*>(fn), &wide_symbol<B, SPLIT>,
+  return launch_kernel(mod, reinterpret_cast<const void*>(fn), &wide_symbol<B, SPLIT, WNT>,
                        dim3(a.tiles_m * a.tiles_n * (SPLIT ? a.S : 1)), dim3(256),
                        WideCfg<B>::kLds, s, a);
 }
 
 template <int B>
 static hipError_t launch_wide_t(const WideArgs& a, const llk::ModuleFns* mod, hipStream_t s) {
-  if (a.S <= 1) return launch_wide_kernel<B, false>(a, mod, s);
-  hipError_t e = launch_wide_kernel<B, true>(a, mod, s);
+  const bool wnt = a.tiles_m == 1;
+  if (a.S <= 1)
+    return wnt ? launch_wide_kernel<B, false, true>(a, mod, s)
+               : launch_wide_kernel<B, false, false>(a, mod, s);
+  hipError_t e = wnt ? launch_wide_kernel<B, true, true>(a, mod, s)
+                     : launch_wide_kernel<B, true, false>(a, mod, s);
   if (e != hipSuccess) return e;
   const int64_t waves = (int64_t)a.tiles_m * a.tiles_n * 2 * B * 8;
   return launch_kernel(mod, reinterpret_cast<const void*>(wide_reduce_kernel<B>),

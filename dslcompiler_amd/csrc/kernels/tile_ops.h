@@ -1,6 +1,7 @@
-// tile_ops.h -- device building blocks shared by the MFMA tile kernels
-// (mfma_tile.hip, swiglu_wide.hip): wait counters, buffer resources, the
-// LDS-DMA loads, the in-place MFMA and the padding around it.
+// tile_ops.h -- device building blocks shared by the MFMA kernels
+// (mfma_tile.hip, swiglu_wide.hip, the decode tile kernel of
+// swiglu_decode.hip): wait counters, buffer resources, the LDS-DMA loads, the
+// in-place MFMA and the padding around it.
 #pragma once
 
 #include "common.h"
@@ -42,8 +43,12 @@ __device__ __forceinline__ void dma16(const u32x4& rsrc, int voff, int soff, uin
                :: "s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
 }
 // The same load, non-temporal (`nt`): for data each workgroup reads once
-// and no other workgroup reads again (a decode step's weights), so that it
-// streams past L2 rather than evicting what is reused there.
+// and no other workgroup reads again (weights when there is one m tile), so
+// that it streams past L2 rather than evicting what is reused there (X).
+// Measured per kernel: faster for the decode tile kernel and the wide SwiGLU
+// kernel's gathered 256-byte runs, slower for mfma_tile_kernel's 8 KiB
+// weight stages (k-split GEMM M = 200 / 255, SwiGLU M = 100: 6-16%), which
+// keep ordinary loads.
 __device__ __forceinline__ void dma16_nt(const u32x4& rsrc, int voff, int soff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
                :: "s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
@@ -61,6 +66,10 @@ __device__ __forceinline__ void set_m0(uint32_t lds) {
 }
 __device__ __forceinline__ void dma16_m0(const u32x4& rsrc, int voff, int soff) {
   asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" :: "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory");
+}
+__device__ __forceinline__ void dma16_m0_nt(const u32x4& rsrc, int voff, int soff) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen nt lds" :: "v"(voff), "s"(rsrc), "s"(soff)
                : "memory");
 }
 #pragma clang diagnostic pop

@@ -20,7 +20,7 @@ from dslcompiler_amd.cache import JitCache, KernelKey
 
 PKG = Path(llk.__file__).resolve().parent
 TILE = "_ZN10llk_gfx95016mfma_tile_kernelI"
-# config 3's whole tiles: mfma_tile_kernel<1, 0, true, false, false>(TileArgs)
+# the 128-column SwiGLU tiles: mfma_tile_kernel<1, 0, true, false>(TileArgs)
 CONFIG3 = TILE + "Li1ELi0ELb1ELb0EEEvNS_8TileArgsE"
 
 
@@ -46,9 +46,11 @@ def test_objects_hold_their_operations_kernels():
     assert {k[len(TILE):len(TILE) + 4] for k in sw if k.startswith(TILE)} == {"Li1E"}
     assert {k[len(TILE):len(TILE) + 4] for k in mm if k.startswith(TILE)} == {"Li0E"}
     # both operations' launchers: tile (5 / 7 instantiations), k-split
-    # reduce, small-M kernels (2 x 3 widths x 2 X paths x output types) and
-    # their reduce, X padding and the K = 0 fill; no tile form waits for
-    # another workgroup (every instantiation has four template arguments)
+    # reduce, wide SwiGLU tiles (2 widths x split x non-temporal weights),
+    # small-M kernels (2 x 3 widths x 2 X paths x output types) and their
+    # reduce, decode tile kernels (output types), X padding and the K = 0
+    # fill; no tile form waits for another workgroup (every instantiation has
+    # the four template arguments MODE, OUT, YVEC, SPLIT)
     def count(names, part):
         return sum(part in k for k in names)
     assert (count(sw, "mfma_tile_kernel"), count(mm, "mfma_tile_kernel")) == (5, 7)
@@ -56,7 +58,9 @@ def test_objects_hold_their_operations_kernels():
         if k.startswith(TILE):
             args = k[len(TILE):k.index("EEvNS_8TileArgsE")]
             assert len(re.findall(r"L[ib]\d+E", args)) == 4, k
+    assert (count(sw, "mfma_swiglu_wide_kernel"), count(mm, "mfma_swiglu_wide_kernel")) == (8, 0)
     assert (count(sw, "13skinny_kernel"), count(mm, "13skinny_kernel")) == (24, 36)
+    assert (count(sw, "decode_tile_kernel"), count(mm, "decode_tile_kernel")) == (2, 3)
     for names in (sw, mm):
         assert "_Z15pad_rows_kernelPKtliiPtl" in names
         assert "_Z16zero_rows_kernelPhllil" in names

@@ -118,6 +118,15 @@ def test_every_tile_instantiation_found(asm):
     assert len(ks) >= 10, sorted(ks)
 
 
+def test_tile_weight_loads_never_non_temporal(asm):
+    """The tile kernel's weight and X loads are ordinary ones in every form:
+    its weight panels stream fastest through L2 even when one workgroup reads
+    each byte (k-split GEMM M = 200 / 255 and SwiGLU M = 100 measured 6-16%
+    slower with `nt`)."""
+    for name, lines in kernels(asm).items():
+        assert not [b for b in lines if b.startswith("buffer_load") and " nt " in b], name
+
+
 def test_k_loop_is_768_in_place_mfmas_without_agpr_copies(asm):
     for name, lines in kernels(asm).items():
         body = [b for b in k_loop(lines) if is_insn(b)]
@@ -196,7 +205,8 @@ def test_wait_states_around_the_mfmas(asm):
 # without the k split (same K loop, register-order partial stores instead of
 # the SiLU epilogue).
 # ---------------------------------------------------------------------------
-WIDE = re.compile(r"^(_ZN10llk_gfx95023mfma_swiglu_wide_kernelILi(\d+)ELb([01])EE\w+):", re.M)
+WIDE = re.compile(r"^(_ZN10llk_gfx95023mfma_swiglu_wide_kernelILi(\d+)ELb([01])ELb([01])EE\w+):",
+                  re.M)
 # loads outstanding at the barriers of an even / odd stage (the refill
 # schedule of the kernel's header comment)
 WIDE_WAITS = {11: ("13", "11"), 7: ("10", "8")}
@@ -212,8 +222,9 @@ def wide_asm(tmp_path_factory) -> str:
     return out.read_text()
 
 
-def wide_kernels(asm: str) -> dict[tuple[int, int], list[str]]:
-    """(B, split) -> the kernel's instruction lines (as kernels())."""
+def wide_kernels(asm: str) -> dict[tuple[int, int, int], list[str]]:
+    """(B, split, non-temporal weights) -> the kernel's instruction lines (as
+    kernels())."""
     out = {}
     for m in WIDE.finditer(asm):
         body = asm[m.end():]
@@ -223,7 +234,7 @@ def wide_kernels(asm: str) -> dict[tuple[int, int], list[str]]:
             ln = ln.split(";")[0].strip()
             if ln and not ln.startswith(".") or re.match(r"^\.LBB\d+_\d+:", ln):
                 lines.append(ln)
-        out[(int(m.group(2)), int(m.group(3)))] = lines
+        out[(int(m.group(2)), int(m.group(3)), int(m.group(4)))] = lines
     return out
 
 
@@ -237,19 +248,20 @@ def _acc_regs(mfmas: list[str]) -> tuple[set[int], set[int]]:
 
 
 def test_wide_instantiations_and_no_scratch(wide_asm):
-    assert sorted(wide_kernels(wide_asm)) == [(7, 0), (7, 1), (11, 0), (11, 1)]
+    assert sorted(wide_kernels(wide_asm)) == [(b, sp, nt) for b in (7, 11) for sp in (0, 1)
+                                              for nt in (0, 1)]
     # no spills anywhere in the kernels (the epilogue once spilled AGPRs):
     # the metadata entry of each kernel, its name followed by its scratch size
     meta = re.findall(r"\.name:\s+(_ZN10llk_gfx95023mfma_swiglu_wide_kernel\w+)\n"
                       r"\s+\.private_segment_fixed_size:\s+(\d+)", wide_asm)
-    assert len(meta) == 4 and all(size == "0" for _, size in meta), meta
+    assert len(meta) == 8 and all(size == "0" for _, size in meta), meta
     for count in ("sgpr_spill_count", "vgpr_spill_count"):
         spills = re.findall(r"\." + count + r":\s+(\d+)", wide_asm)
         assert spills and all(n == "0" for n in spills), (count, spills)
 
 
 def test_wide_k_loop_in_place_mfmas(wide_asm):
-    for (Bw, _split), lines in wide_kernels(wide_asm).items():
+    for (Bw, _split, _nt), lines in wide_kernels(wide_asm).items():
         body = [b for b in k_loop(lines) if is_insn(b)]
         mf = [b for b in body if b.startswith(MFMA)]
         assert len(mf) == 4 * 8 * Bw, (Bw, len(mf))
@@ -269,7 +281,7 @@ def test_wide_k_loop_in_place_mfmas(wide_asm):
 
 
 def test_wide_k_loop_waits_and_m0(wide_asm):
-    for (Bw, _split), lines in wide_kernels(wide_asm).items():
+    for (Bw, _split, _nt), lines in wide_kernels(wide_asm).items():
         body = [b for b in k_loop(lines) if is_insn(b)]
         vm = [re.search(r"vmcnt\((\d+)\)", b).group(1) for b in body if "vmcnt" in b]
         even, odd = WIDE_WAITS[Bw]
@@ -286,8 +298,25 @@ def test_wide_k_loop_waits_and_m0(wide_asm):
             assert len(loads) == 1 and loads[0] >= a + 2, (Bw, insns[a:a + 4])
 
 
+def test_wide_weight_loads_non_temporal_for_one_m_tile(wide_asm):
+    """The WNT forms (one m tile: each weight byte read by one workgroup)
+    load every weight stage non-temporal and X as ordinary loads; the other
+    forms load nothing non-temporal."""
+    for (Bw, split, nt), lines in wide_kernels(wide_asm).items():
+        dma = [b for b in lines if b.startswith("buffer_load_dwordx4") and b.endswith(" lds")]
+        n_nt = sum(" nt " in b for b in dma)
+        if not nt:
+            assert n_nt == 0, (Bw, split)
+            continue
+        # a weight load's resource is the Wg or Wu one, X's is the third
+        rsrc = {}
+        for b in dma:
+            rsrc.setdefault(operands(b)[1], set()).add(" nt " in b)
+        assert sorted(map(sorted, rsrc.values())) == [[False], [True], [True]], (Bw, rsrc)
+
+
 def test_wide_wait_states_around_the_mfmas(wide_asm):
-    for (Bw, _split), lines in wide_kernels(wide_asm).items():
+    for (Bw, _split, _nt), lines in wide_kernels(wide_asm).items():
         insns = [b for b in lines if is_insn(b)]
         idx = [k for k, b in enumerate(insns) if b.startswith(MFMA)]
         first, last = idx[0], idx[-1]
@@ -312,7 +341,7 @@ def test_wide_wait_states_around_the_mfmas(wide_asm):
 
 
 def test_wide_no_valu_writes_mfma_operands_just_before(wide_asm):
-    for (Bw, _split), lines in wide_kernels(wide_asm).items():
+    for (Bw, _split, _nt), lines in wide_kernels(wide_asm).items():
         insns = [b for b in lines if is_insn(b)]
         for k, b in enumerate(insns):
             if not b.startswith(MFMA):
