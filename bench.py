@@ -207,13 +207,15 @@ def _unfused_swiglu(torch, F, x, w, gu, N):
     return F.silu(gu[:, :N]) * gu[:, N:]
 
 
-def bench_kernel_fn(torch, llk, M, K, N, calls=10):
+def bench_kernel_fn(torch, llk, M, K, N, calls=40, warm_s=0.05):
     """The reference-shaped KernelFn (llk_swiglu_kernel_fn, synchronous, raw
     row-major weights in device memory) on an M x K x N SwiGLU: us per call
     with the default per-call pack of Wg and Wu, and with packed weights
     reused (llk_kernel_fn_assume_immutable_weights); beside them the same
     shape through llk_swiglu_bf16 with packed handles; the difference of the
-    first two is the two packs (GB/s over their bytes read and written)."""
+    first two is the two packs (GB/s over their bytes read and written).
+    Each form is called for warm_s seconds before its `calls` timed calls
+    (the GPU's clock ramp)."""
     from dslcompiler_amd import cache as cmod
     g = torch.Generator(device="cuda")
     g.manual_seed(7)
@@ -222,7 +224,10 @@ def bench_kernel_fn(torch, llk, M, K, N, calls=10):
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
 
     def per_call(fn):
+        t_end = time.perf_counter() + warm_s
         fn()
+        while time.perf_counter() < t_end:
+            fn()
         torch.cuda.synchronize()
         t = time.perf_counter()
         for _ in range(calls):
@@ -240,7 +245,7 @@ def bench_kernel_fn(torch, llk, M, K, N, calls=10):
         llk.lib().llk_cache_clear(llk.lib().llk_kernel_fn_cache())
     pg, pu = llk.PackedWeights.from_device(wg), llk.PackedWeights.from_device(wu)
     out["swiglu_bf16_us"] = round(_time_loop(torch, lambda i: llk.fused_swiglu(x, pg, pu, out=y),
-                                             calls, 5) * 1e3, 1)
+                                             calls, 5, warm_s) * 1e3, 1)
     # the two packs' share of a call, and their rate over 2 x K x N x 2 bytes
     # read + the same written
     pack_us = out["pack_every_call_us"] - out["reuse_packed_us"]
