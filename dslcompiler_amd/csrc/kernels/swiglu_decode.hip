@@ -436,14 +436,29 @@ static int skinny_threads_w(int W) {
 // 45 us instead of 37 and 38.)  The kernel has no k parts inside a workgroup
 // and no partial sums in LDS.
 //
-// A step is 16 weight sub-blocks (16 KiB) + 8 KiB of X.  SwiGLU (NMAT 2): a
-// workgroup covers 64 columns (half an n-block) of Wg and Wu; GEMM (NMAT 1):
-// 128 columns (one n-block).  Wave w = (column group c = w & 1, m tile
-// h = w >> 1) accumulates acc[p] = 32 columns x 32 rows, p = 0, 1 (SwiGLU:
-// gate and up of the same columns, so the epilogue is register-local; GEMM:
-// column groups c and 2 + c).  With S > 1 workgroup (columns, s) covers the
-// 64-k blocks [s kbs, (s + 1) kbs) and writes fp32 partials in the layout of
+// A step is 16 weight sub-blocks (16 KiB) + 8 KiB of X per 64 rows.  SwiGLU
+// (NMAT 2): a workgroup covers 64 columns (half an n-block) of Wg and Wu;
+// GEMM (NMAT 1): 128 columns (one n-block).  Wave w = (column group
+// c = w & 1, m half h = w >> 1) accumulates acc[p][t] = 32 columns x 32 rows
+// (rows 32 (MT h + t) .. +32, t < MT), p = 0, 1 (SwiGLU: gate and up of the
+// same columns, so the epilogue is register-local; GEMM: column groups c and
+// 2 + c).  With S > 1 workgroup (columns, s) covers the 64-k blocks
+// [s kbs, (s + 1) kbs) and writes fp32 partials in the layout of
 // skinny_kernel's, which skinny_reduce_kernel adds in split order.
+//
+// MT (32-row MFMA tiles per wave: 1, 2, 4) sets the rows a workgroup holds,
+// 64 MT: MT = 1 for M <= 64 (decode), 2 and 4 for mid M (65..256 rows, one
+// m tile), where every weight byte is still read by one workgroup only --
+// the tile kernels need 256-row tiles and a k split to give 256 CUs work
+// there, and write fp32 partial planes for it.  Each step then carries 8 MT
+// KiB of X (from L2) beside the same 16 KiB of weights and 8 MT MFMAs per
+// wave; the ring keeps three slots (144 KiB at MT = 4).  Measured on config
+// 5's MLP (K = 5120, N = 13824): M = 65 and 128 take 86 and 100 us against
+// 114 and 126 us on the tile kernels, but at MT = 4 a step takes ~1.2 us
+// (the SwiGLU at M = 255: 97 us, against 74 us + 11 us of reduce for the
+// wide kernel's two k splits): per CU the loads in flight, not the MFMAs,
+// set the pace (about 34 KiB at once), and 32 KiB of X per step share them
+// with 16 KiB of weights -- so the dispatcher stops at 128 rows by default.
 struct DecTileArgs {
   const uint16_t* x;  // [M, K], row stride ldx
   const uint8_t* w0;  // packed (Wg, or B for the GEMM)
@@ -456,13 +471,20 @@ struct DecTileArgs {
   bool accumulate;  // GEMM only, S == 1: y += x w (the existing y read in its type)
 };
 
-constexpr int kDecSlots = 3;                   // ring slots (64-k steps)
-constexpr int kDecW = 16384, kDecSlot = 24576; // weights, then X (8 KiB), per slot
-constexpr int kDecLds = kDecSlots * kDecSlot;  // 72 KiB
+constexpr int kDecSlots = 3;  // ring slots (64-k steps)
+constexpr int kDecW = 16384;  // weights per slot, then X (8 KiB per 64 rows)
+constexpr int dec_slot_bytes(int MT) { return kDecW + 8192 * MT; }
+constexpr int dec_lds_bytes(int MT) { return kDecSlots * dec_slot_bytes(MT); }  // 72 / 96 / 144 KiB
+// 32-row MFMA tiles per wave for M rows (M <= 256).
+constexpr int dec_mt(int M) { return M <= 64 ? 1 : M <= 128 ? 2 : 4; }
 
-template <int NMAT, int OUT>
+template <int NMAT, int OUT, int MT>
 __global__ __launch_bounds__(256) void decode_tile_kernel(DecTileArgs a) {
+  static_assert(MT == 1 || MT == 2 || MT == 4, "64, 128 or 256 rows per workgroup");
   constexpr int kAhead = kDecSlots - 1;
+  constexpr int kDecSlot = dec_slot_bytes(MT);
+  constexpr int kXL = 2 * MT;       // X loads per wave and step (8 rows each)
+  constexpr int kLoads = 4 + kXL;   // loads per wave and step
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -496,14 +518,14 @@ __global__ __launch_bounds__(256) void decode_tile_kernel(DecTileArgs a) {
     w_vo[q] = (kq * 4 + n32) * kSubBytes + lane * 16;
     w_lds[q] = (uint32_t)(((p * 2 + c) * 4 + kq) * 1024);
   }
-  // This wave's X loads: rows 8 f .. 8 f + 7 for f = 2 wave + q, lane l
+  // This wave's X loads: rows 8 f .. 8 f + 7 for f = 2 MT wave + q, lane l
   // fetching physical chunk l & 7 of row 8 f + l / 8, i.e. logical chunk
   // (l & 7) ^ (row & 7).  Loads of rows >= M read zeros (no memory traffic)
   // but are issued all the same, so that every wave waits for one count.
-  int x_vo[2];
+  int x_vo[kXL];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int row = 8 * (wave * 2 + q) + (lane >> 3);
+  for (int q = 0; q < kXL; ++q) {
+    const int row = 8 * (wave * kXL + q) + (lane >> 3);
     x_vo[q] = (row * (int)a.ldx + (((lane & 7) ^ (row & 7)) * 8)) * 2;
   }
   const uint32_t lds0 = lds_addr(smem);
@@ -513,102 +535,162 @@ __global__ __launch_bounds__(256) void decode_tile_kernel(DecTileArgs a) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) dma16_nt(rw_mine, w_vo[q] + kb * kBlockBytes, 0, base + w_lds[q]);
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
-      dma16(rx, x_vo[q] + kb * 128, 0, base + kDecW + (uint32_t)(wave * 2 + q) * 1024);
+    for (int q = 0; q < kXL; ++q)
+      dma16(rx, x_vo[q] + kb * 128, 0, base + kDecW + (uint32_t)(wave * kXL + q) * 1024);
   };
   // Steps past the split's end read zeros (weights) or unused X into slots
   // no MFMA reads: the load count per step stays uniform.
 #pragma unroll
   for (int s = 0; s < kAhead; ++s) issue(s, s);
 
-  f32x16 acc[2];
+  f32x16 acc[2][MT];
 #pragma unroll
   for (int p = 0; p < 2; ++p)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[p][r] = 0.0f;
-  const uint8_t* const a_rd = smem + cg * 4096 + lane * 16;  // + slot + p * 8 KiB + kq KiB
-  const int xm = mh * 32 + (lane & 31);                       // the B operand's row
-  const uint8_t* const b_rd = smem + kDecW + xm * 128;
-  int slot = 0, fill = kAhead;
-  for (int kb = 0; kb < nkb; ++kb) {
-    wait_vmcnt<6 * (kAhead - 1)>();  // this wave's loads of step kb have landed
-    __syncthreads();                 // ... every wave's; slot `fill` (step kb - 1) is free
-    issue(kb + kAhead, fill);
-    fill = fill + 1 == kDecSlots ? 0 : fill + 1;
-    const int off = slot * kDecSlot;
-    bf16x8 A[2][4], Bx[4];
+    for (int t = 0; t < MT; ++t)
 #pragma unroll
-    for (int kq = 0; kq < 4; ++kq) {
-      Bx[kq] = *reinterpret_cast<const bf16x8*>(b_rd + off +
-                                                (((2 * kq + (lane >> 5)) ^ (xm & 7)) * 16));
+      for (int r = 0; r < 16; ++r) acc[p][t][r] = 0.0f;
+  const uint8_t* const a_rd = smem + cg * 4096 + lane * 16;  // + slot + p * 8 KiB + kq KiB
+  const int xm = mh * 32 * MT + (lane & 31);                  // the B operand's row (t = 0)
+  const uint8_t* const b_rd = smem + kDecW + xm * 128;        // + t * 4 KiB: tile t's rows
+  int slot = 0, fill = kAhead;
+  if constexpr (MT == 1) {
+    for (int kb = 0; kb < nkb; ++kb) {
+      wait_vmcnt<kLoads * (kAhead - 1)>();  // this wave's loads of step kb have landed
+      __syncthreads();                      // ... every wave's; slot `fill` (step kb - 1) is free
+      issue(kb + kAhead, fill);
+      fill = fill + 1 == kDecSlots ? 0 : fill + 1;
+      const int off = slot * kDecSlot;
+      bf16x8 A[2][4], Bx[4];
+#pragma unroll
+      for (int kq = 0; kq < 4; ++kq) {
+        Bx[kq] = *reinterpret_cast<const bf16x8*>(b_rd + off +
+                                                  (((2 * kq + (lane >> 5)) ^ (xm & 7)) * 16));
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+          A[p][kq] = *reinterpret_cast<const bf16x8*>(a_rd + off + p * 8192 + kq * 1024);
+      }
+#pragma unroll
+      for (int kq = 0; kq < 4; ++kq)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) acc[p][0] = mfma32(A[p][kq], Bx[kq], acc[p][0]);
+      slot = slot + 1 == kDecSlots ? 0 : slot + 1;
+    }
+  } else {
+    // 2 MT MFMAs per 16-k quarter kq, and the LDS serves 4 (2 + MT) KiB of
+    // operands per quarter to the workgroup's waves beside the ring's DMA
+    // writes: the operand reads of quarter kq + 1 are issued before the
+    // MFMAs of quarter kq (two register sets), and step kb + 1's barrier --
+    // after this wave's reads of step kb are done -- comes before step kb's
+    // last quarter, whose MFMAs then cover step kb + 1's first reads.
+    bf16x8 A[2][2], Bx[2][MT];
+    auto rd = [&](int off, int kq, int buf) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+        Bx[buf][t] = *reinterpret_cast<const bf16x8*>(
+            b_rd + off + t * 4096 + (((2 * kq + (lane >> 5)) ^ (xm & 7)) * 16));
 #pragma unroll
       for (int p = 0; p < 2; ++p)
-        A[p][kq] = *reinterpret_cast<const bf16x8*>(a_rd + off + p * 8192 + kq * 1024);
+        A[buf][p] = *reinterpret_cast<const bf16x8*>(a_rd + off + p * 8192 + kq * 1024);
+    };
+    auto mf = [&](int buf) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[p][t] = mfma32(A[buf][p], Bx[buf][t], acc[p][t]);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    wait_vmcnt<kLoads * (kAhead - 1)>();  // step 0 has landed (this wave's loads) ...
+    __syncthreads();                      // ... and every wave's
+    issue(kAhead, fill);
+    fill = 0;
+    rd(0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int kb = 0; kb < nkb; ++kb) {
+      const int off = slot * kDecSlot;
+      rd(off, 1, 1);
+      mf(0);
+      rd(off, 2, 0);
+      mf(1);
+      rd(off, 3, 1);
+      mf(0);
+      if (kb + 1 < nkb) {
+        wait_lgkmcnt0();                      // this wave's reads of step kb are done
+        wait_vmcnt<kLoads * (kAhead - 1)>();  // its loads of step kb + 1 have landed
+        __syncthreads();                      // every wave's; slot `fill` (step kb) is free
+        issue(kb + 1 + kAhead, fill);
+        fill = fill + 1 == kDecSlots ? 0 : fill + 1;
+        slot = slot + 1 == kDecSlots ? 0 : slot + 1;
+        rd(slot * kDecSlot, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      mf(1);
     }
-#pragma unroll
-    for (int kq = 0; kq < 4; ++kq)
-#pragma unroll
-      for (int p = 0; p < 2; ++p) acc[p] = mfma32(A[p][kq], Bx[kq], acc[p]);
-    slot = slot + 1 == kDecSlots ? 0 : slot + 1;
   }
   wait_vmcnt<0>();  // the trailing loads have landed before the workgroup ends
 
-  // acc[p] register r, lane l: row m = 32 h + l % 32, column 8 (r / 4) +
-  // 4 (l / 32) + r % 4 of the wave's 32-column group of operand p.
-  const int m = xm;
+  // acc[p][t] register r, lane l: row m = 32 (MT h + t) + l % 32, column
+  // 8 (r / 4) + 4 (l / 32) + r % 4 of the wave's 32-column group of operand p.
   const int n_col = NMAT == 2 ? grp * 64 + cg * 32 : nb * kPackN + cg * 32;
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const int n_off = 8 * g + 4 * (lane >> 5);
-    if (a.S > 1) {
-      if (m < a.rows) {
+  for (int t = 0; t < MT; ++t) {
+    const int m = xm + 32 * t;
+    if (MT > 1 && m >= a.rows) continue;  // rows past M's last 32-row group
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          const int mat = NMAT == 2 ? p : 0;
-          const int n = n_col + (NMAT == 2 ? 0 : p * 64) + n_off;
-          float* dst = a.part + (((size_t)split * NMAT + mat) * a.rows + m) * a.n_pad + n;
-          *reinterpret_cast<f32x4*>(dst) =
-              f32x4{acc[p][4 * g], acc[p][4 * g + 1], acc[p][4 * g + 2], acc[p][4 * g + 3]};
+    for (int g = 0; g < 4; ++g) {
+      const int n_off = 8 * g + 4 * (lane >> 5);
+      if (a.S > 1) {
+        if (m < a.rows) {
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            const int mat = NMAT == 2 ? p : 0;
+            const int n = n_col + (NMAT == 2 ? 0 : p * 64) + n_off;
+            float* dst = a.part + (((size_t)split * NMAT + mat) * a.rows + m) * a.n_pad + n;
+            *reinterpret_cast<f32x4*>(dst) = f32x4{acc[p][t][4 * g], acc[p][t][4 * g + 1],
+                                                   acc[p][t][4 * g + 2], acc[p][t][4 * g + 3]};
+          }
         }
-      }
-    } else if constexpr (NMAT == 2) {
-      float v[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) v[q] = swiglu_act(acc[0][4 * g + q], acc[1][4 * g + q]);
-      store4<OUT>(a.y, a.ldy, a.M, a.N, m, n_col + n_off, v, a.yvec);
-    } else {
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
+      } else if constexpr (NMAT == 2) {
         float v[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = acc[p][4 * g + q];
-        const int n = n_col + p * 64 + n_off;
-        if (a.accumulate) add_existing4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
-        store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
+        for (int q = 0; q < 4; ++q)
+          v[q] = swiglu_act(acc[0][t][4 * g + q], acc[1][t][4 * g + q]);
+        store4<OUT>(a.y, a.ldy, a.M, a.N, m, n_col + n_off, v, a.yvec);
+      } else {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] = acc[p][t][4 * g + q];
+          const int n = n_col + p * 64 + n_off;
+          if (a.accumulate) add_existing4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
+          store4<OUT>(a.y, a.ldy, a.M, a.N, m, n, v, a.yvec);
+        }
       }
     }
   }
 }
 
-template <int NMAT, int OUT>
+template <int NMAT, int OUT, int MT>
 const char* decode_tile_symbol() {
   static const std::string name = "_ZN10llk_gfx95018decode_tile_kernelI" + mangle_int(NMAT) +
-                                  mangle_int(OUT) + "EEvNS_11DecTileArgsE";
+                                  mangle_int(OUT) + mangle_int(MT) + "EEvNS_11DecTileArgsE";
   return name.c_str();
 }
 
-template <int NMAT, int OUT>
+template <int NMAT, int OUT, int MT>
 static hipError_t launch_decode_tile_t(const DecTileArgs& a, const llk::ModuleFns* mod,
                                        hipStream_t s) {
-  auto fn = decode_tile_kernel<NMAT, OUT>;
+  auto fn = decode_tile_kernel<NMAT, OUT, MT>;
+  constexpr int kLds = dec_lds_bytes(MT);
   if (!mod) {
     static std::atomic<uint64_t> lds_set{0};
-    hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(fn), kDecLds, lds_set);
+    hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(fn), kLds, lds_set);
     if (e != hipSuccess) return e;
   }
   const unsigned groups = (unsigned)((NMAT == 2 ? a.NB * 2 : a.NB) * a.S);
   hipError_t e = launch_kernel(mod, reinterpret_cast<const void*>(fn),
-                               &decode_tile_symbol<NMAT, OUT>, dim3(groups), dim3(256), kDecLds,
+                               &decode_tile_symbol<NMAT, OUT, MT>, dim3(groups), dim3(256), kLds,
                                s, a);
   if (e != hipSuccess || a.S == 1) return e;
   SkinnyArgs r{};
@@ -625,6 +707,14 @@ static hipError_t launch_decode_tile_t(const DecTileArgs& a, const llk::ModuleFn
   return launch_kernel(mod, reinterpret_cast<const void*>(skinny_reduce_kernel<NMAT, OUT>),
                        &skinny_reduce_symbol<NMAT, OUT>,
                        dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, r, a.rows);
+}
+
+template <int NMAT, int OUT>
+static hipError_t launch_decode_tile_mt(const DecTileArgs& a, int mt, const llk::ModuleFns* mod,
+                                        hipStream_t s) {
+  if (mt == 1) return launch_decode_tile_t<NMAT, OUT, 1>(a, mod, s);
+  if (mt == 2) return launch_decode_tile_t<NMAT, OUT, 2>(a, mod, s);
+  return launch_decode_tile_t<NMAT, OUT, 4>(a, mod, s);
 }
 
 }  // namespace llk_gfx950
@@ -693,14 +783,14 @@ hipError_t llk_launch_skinny(int mode, const uint16_t* x, int64_t ldx, const voi
   return hipErrorInvalidValue;
 }
 
-// Whether the decode tile kernel takes a shape: M <= 64, K a multiple of
+// Whether the decode tile kernel takes a shape: M <= 256, K a multiple of
 // 64, X rows 16-byte aligned (ldx % 8 == 0 and a 16-byte aligned base, the
-// caller's check), and the 32-bit buffer offsets: 64 rows of X plus the
-// trailing steps, and one weight panel plus them.
+// caller's check), and the 32-bit buffer offsets: the workgroup's 64 MT rows
+// of X plus the trailing steps, and one weight panel plus them.
 bool llk_decode_tile_fits(int M, int64_t K, int64_t ldx) {
-  if (M < 1 || M > 64 || K < 64 || K % 64 != 0 || ldx < K || ldx % 8 != 0) return false;
-  const int64_t KB = K / 64;
-  return 64 * ldx * 2 + (KB + 2) * 128 < ((int64_t)1 << 31) &&
+  if (M < 1 || M > 256 || K < 64 || K % 64 != 0 || ldx < K || ldx % 8 != 0) return false;
+  const int64_t KB = K / 64, rows = 64 * (int64_t)llk_gfx950::dec_mt(M);
+  return rows * ldx * 2 + (KB + 2) * 128 < ((int64_t)1 << 31) &&
          (KB + 2) * (int64_t)llk_gfx950::kBlockBytes < ((int64_t)1 << 31);
 }
 
@@ -736,17 +826,18 @@ hipError_t llk_launch_decode_tile(int mode, const uint16_t* x, int64_t ldx, cons
   a.yvec = yvec;
   a.accumulate = accumulate;
   if (a.S > 1 && (ws == nullptr || (int64_t)(a.S - 1) * a.kbs >= KB)) return hipErrorInvalidValue;
+  const int mt = dec_mt(M);
 #if !defined(LLK_CO_OP) || LLK_CO_OP == 1
   if (mode == 1) {
-    if (out == kOutBF16) return launch_decode_tile_t<2, kOutBF16>(a, mod, s);
-    if (out == kOutF32) return launch_decode_tile_t<2, kOutF32>(a, mod, s);
+    if (out == kOutBF16) return launch_decode_tile_mt<2, kOutBF16>(a, mt, mod, s);
+    if (out == kOutF32) return launch_decode_tile_mt<2, kOutF32>(a, mt, mod, s);
   }
 #endif
 #if !defined(LLK_CO_OP) || LLK_CO_OP == 0
   if (mode == 0) {
-    if (out == kOutBF16) return launch_decode_tile_t<1, kOutBF16>(a, mod, s);
-    if (out == kOutF32) return launch_decode_tile_t<1, kOutF32>(a, mod, s);
-    if (out == kOutF16) return launch_decode_tile_t<1, kOutF16>(a, mod, s);
+    if (out == kOutBF16) return launch_decode_tile_mt<1, kOutBF16>(a, mt, mod, s);
+    if (out == kOutF32) return launch_decode_tile_mt<1, kOutF32>(a, mt, mod, s);
+    if (out == kOutF16) return launch_decode_tile_mt<1, kOutF16>(a, mt, mod, s);
   }
 #endif
   return hipErrorInvalidValue;

@@ -609,8 +609,8 @@ int decode_tile_splits(int nmat, int64_t M, int64_t KB, int64_t NB, int64_t forc
 // and, for a padded X, shorter row chunks.
 // accumulate (GEMM, C += A B): the tile path takes the partial planes at any
 // S (the reduce adds C) and no tail split.
-Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const llk_tensor2d* x,
-                 size_t max_ws = SIZE_MAX, bool accumulate = false, bool out_bf16 = true) {
+Plan plan_launch_base(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB,
+                      const llk_tensor2d* x, size_t max_ws, bool accumulate, bool out_bf16) {
   Plan p;
   llk::ScheduleEntry se;
   const bool have_db = db_entry(nmat, M, &se);
@@ -703,6 +703,41 @@ Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const l
     if (p.ws_bytes <= max_ws || p.S == 1) break;
   }
   return p;
+}
+
+// Mid M (64 < M <= midm_max_m, at most 256; 128 by default): the decode
+// tile kernel's 128- and 256-row forms when K is a multiple of 64 and X
+// rows are 16-byte aligned -- one m tile, so every weight byte is read by
+// one workgroup, with k splits from the forced `decode_splits`, else the
+// schedule DB entry's grain_size, else the decode tile model (config 5's MLP
+// at M = 128: the SwiGLU's 216 workgroups unsplit, the down projection's 40
+// in 6 splits); otherwise the tile kernels.  With X unknown (sizing), the
+// larger of the two workspaces.
+Plan plan_launch(int nmat, int64_t M, int64_t K, int64_t KB, int64_t NB, const llk_tensor2d* x,
+                 size_t max_ws = SIZE_MAX, bool accumulate = false, bool out_bf16 = true) {
+  if (M > 64 && M <= std::min<int64_t>(256, llk::tunable("midm_max_m")) &&
+      llk::tunable("decode_tile") != 0 && llk_decode_tile_fits((int)M, K, x ? x->stride0 : K)) {
+    int64_t forced = llk::tunable("decode_splits");
+    llk::ScheduleEntry se;
+    if (forced <= 0 && db_entry(nmat, M, &se) && se.grain_size > 0) forced = se.grain_size;
+    int s = decode_tile_splits(nmat, M, KB, NB, forced);
+    size_t ws = llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), s);
+    while (ws > max_ws && s > 1) ws = llk_skinny_workspace_bytes(nmat, (int)M, (int)(NB * 128), --s);
+    if (x && x_vec_ok(x)) {
+      Plan p;
+      p.skinny = true;
+      p.dtile = true;
+      p.S = s;
+      p.ws_bytes = ws;
+      return p;
+    }
+    if (!x) {
+      Plan p = plan_launch_base(nmat, M, K, KB, NB, x, max_ws, accumulate, out_bf16);
+      p.ws_bytes = std::max(p.ws_bytes, ws);
+      return p;
+    }
+  }
+  return plan_launch_base(nmat, M, K, KB, NB, x, max_ws, accumulate, out_bf16);
 }
 
 // K == 0: the reference's verifiers accept an empty reduction

@@ -21,7 +21,14 @@ struct Knob {
 //                    small-M kernel of that width.
 // decode_tile:       1 = M <= 64 with K a multiple of 64 and 16-byte aligned
 //                    X rows runs on the decode tile kernel (LDS-DMA ring);
-//                    0 = always the small-M kernel.
+//                    0 = always the small-M kernel (and no mid-M form).
+// midm_max_m:        largest M (<= 256) above 64 that runs on the decode
+//                    tile kernel's 128- and 256-row forms (K a multiple of
+//                    64, 16-byte aligned X rows) instead of the tile
+//                    kernels; 64 or less = never.  128 by default: the
+//                    256-row form re-reads 32 KiB of X per 64-k step beside
+//                    16 KiB of weights and loses to the tile kernels (config
+//                    5 MLP at M = 200 / 255: 146 / 156 us against 140 / 143).
 // tile_splits:       force the tile kernel's k-split count (0 = cost model).
 // tile_wgs_per_wave: workgroups the tile kernel runs at once (1 per CU).
 // tile_min_kb:       fewest 64-k steps per tile-kernel split.
@@ -42,6 +49,7 @@ Knob g_knobs[] = {
     {"decode_min_kb", {2}},
     {"decode_group_width", {0}},
     {"decode_tile", {1}},
+    {"midm_max_m", {128}},
     {"tile_splits", {0}},
     {"tile_wgs_per_wave", {256}},
     {"tile_min_kb", {4}},

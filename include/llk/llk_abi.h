@@ -345,6 +345,9 @@ int llk_fill_normal_bf16(uint64_t seed, uint64_t stream, float sigma,
  * 1, 2, 4; 0 = cost model; a forced width runs the small-M kernel),
  * "decode_tile" (1: M <= 64 with K % 64 == 0 and 16-byte aligned X rows
  * runs on the decode tile kernel; 0: always the small-M kernel),
+ * "midm_max_m" (largest M above 64, at most 256, that runs on the decode
+ * tile kernel's 128- and 256-row forms when K % 64 == 0 and X rows are
+ * 16-byte aligned; default 128; 64 or less: the tile kernels from M = 65 on),
  * "tile_splits" (force the tile kernel's k-split count, 0 = cost model),
  * "tile_wgs_per_wave", "tile_min_kb", "tile_tail_split" (1: the columns
  * of a partial last wave of tiles may run as a separate k-split launch;

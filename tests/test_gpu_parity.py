@@ -62,8 +62,9 @@ def test_swiglu_reference_shapes(llk, gpu, orc, M, N, K):
 
 @pytest.mark.parametrize("M", [1, 8, 16, 17, 33, 64, 65, 255, 256, 257, 300])
 def test_swiglu_m_sweep(llk, gpu, orc, M):
-    """Covers the decode kernel (M <= 64, 1..4 MFMA column groups) and the
-    prefill tile kernel (M > 64), including ragged M edge tiles."""
+    """Covers the decode kernels (M <= 64), the decode tile kernel's 128-row
+    form (M = 65) and the prefill tile kernels (M > 128), including ragged M
+    edge tiles."""
     print(f"case swiglu m-sweep M={M} K=576 N=392", flush=True)
     x, wg, wu = swiglu_inputs(M, 576, 392, seed=7)
     _check_swiglu(llk, gpu, orc, x, wg, wu, f"M{M}")

@@ -60,11 +60,12 @@ def _wide_and_tile(llk, gpu, x, wg, wu, B, x_stride=None):
     N = wg.shape[1]
     pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
     xd = to_dev(gpu, x, x_stride)
-    with _tunables(llk, tile_wide=B, tile_splits=1):
+    # midm_max_m = 64: rows 65..128 stay on the tile kernels
+    with _tunables(llk, tile_wide=B, tile_splits=1, midm_max_m=64):
         plan = llk.describe_launch("fused_swiglu", M, N, K, x_aligned=x_stride is None and K % 64 == 0)
         assert (plan["kernel"], plan["tile_columns"], plan["splits"]) == ("wide_tile", 16 * B, 1), plan
         yw = from_dev(llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.bfloat16))
-    with _tunables(llk, tile_wide=0, tile_splits=1):
+    with _tunables(llk, tile_wide=0, tile_splits=1, midm_max_m=64):
         plan = llk.describe_launch("fused_swiglu", M, N, K)
         assert (plan["kernel"], plan["splits"]) == ("tile", 1), plan
         yt = from_dev(llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.bfloat16))

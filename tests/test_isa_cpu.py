@@ -392,14 +392,17 @@ def test_small_m_kernels_no_scratch_and_pipelined_forms(skinny_asm):
 
 
 def test_decode_tile_kernel_loop(skinny_asm):
-    """The decode tile kernel (every instantiation): no scratch; its K loop
-    (one 64-k step) holds exactly one vector-memory wait, vmcnt(6) -- the
-    wave's six loads of the next step may still be in flight -- then one
-    barrier, four non-temporal weight LDS-DMA loads and two X ones, each
-    right after its own M0 write and one wait state, and eight
-    v_mfma_f32_32x32x16_bf16."""
+    """The decode tile kernel (every instantiation, MT = 1, 2, 4 32-row MFMA
+    tiles per wave): no scratch; its K loop (one 64-k step) holds exactly one
+    vector-memory wait, vmcnt(4 + 2 MT) -- the wave's loads of the next step
+    may still be in flight -- then one barrier, four non-temporal weight
+    LDS-DMA loads and 2 MT X ones, each right after its own M0 write and one
+    wait state, and 8 MT v_mfma_f32_32x32x16_bf16."""
     names = re.findall(r"^(_ZN10llk_gfx95018decode_tile_kernel\w+):", skinny_asm, re.M)
-    assert len(names) == 5, names  # SwiGLU bf16 / fp32, GEMM bf16 / fp16 / fp32
+    # (SwiGLU bf16 / fp32, GEMM bf16 / fp16 / fp32) x MT
+    assert len(names) == 15, names
+    mts = [int(re.search(r"decode_tile_kernelILi\d+ELi\d+ELi(\d+)E", n).group(1)) for n in names]
+    assert sorted(mts) == [1] * 5 + [2] * 5 + [4] * 5, mts
     meta = dict(re.findall(r"\.name:\s+(_ZN10llk_gfx95018decode_tile_kernel\w+)\n"
                            r"\s+\.private_segment_fixed_size:\s+(\d+)", skinny_asm))
     assert sorted(meta) == sorted(names) and set(meta.values()) == {"0"}, meta
@@ -420,15 +423,16 @@ def test_decode_tile_kernel_loop(skinny_asm):
                 if any("v_mfma" in b for b in lines[h:e + 1])]
         assert len(loop) == 1, name
         loop = loop[0]
-        assert sum("v_mfma_f32_32x32x16_bf16" in b for b in loop) == 8, name
+        mt = int(re.search(r"decode_tile_kernelILi\d+ELi\d+ELi(\d+)E", name).group(1))
+        assert sum("v_mfma_f32_32x32x16_bf16" in b for b in loop) == 8 * mt, name
         vm = [re.search(r"vmcnt\((\d+)\)", b).group(1) for b in loop
               if b.startswith("s_waitcnt") and "vmcnt" in b]
-        assert vm == ["6"], (name, vm)
+        assert vm == [str(4 + 2 * mt)], (name, vm)
         assert sum(b == "s_barrier" for b in loop) == 1, name
         loads = [i for i, b in enumerate(loop) if b.startswith("buffer_load") and b.endswith("lds")]
-        assert len(loads) == 6, name
+        assert len(loads) == 4 + 2 * mt, name
         assert sum(" nt lds" in loop[i] for i in loads) == 4, name
         for i in loads:
             assert loop[i - 2].startswith("s_mov_b32 m0,") and loop[i - 1] == "s_nop 0", \
                 (name, loop[i - 2:i + 1])
-        assert sum(b.startswith("s_mov_b32 m0,") for b in loop) == 6, name
+        assert sum(b.startswith("s_mov_b32 m0,") for b in loop) == 4 + 2 * mt, name
