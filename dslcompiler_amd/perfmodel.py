@@ -113,12 +113,14 @@ def predict(op: str, M: int, N: int, K: int, machine_path: str = str(MACHINE)) -
     elif plan["kernel"] == "decode_tile":
         # Each workgroup streams, per 64-k step of its split, 16 KiB of
         # weights and M rows x 128 bytes of X (rows >= M move nothing);
-        # 64 MFMA rows of each operand per workgroup.
+        # 128 MFMA columns and 64 MT rows per workgroup (MT = 1 for M <= 64,
+        # 2 up to 128 rows, 4 up to 256: the mid-M forms).
         groups = plan["workgroups"]
+        rows = 64 * (1 if M <= 64 else 2 if M <= 128 else 4)
         kbs = math.ceil(math.ceil(K / 64) / S)
-        flops = 2.0 * 64 * 128 * kbs * 64 * groups
+        flops = 2.0 * rows * 128 * kbs * 64 * groups
         compute = math.ceil(groups / cus) * flops / groups / cal["small_m_flops_per_cu"]
-        wg_bytes = kbs * (16384.0 + min(M, 64) * 128.0)
+        wg_bytes = kbs * (16384.0 + min(M, rows) * 128.0)
         per_cu = math.ceil(groups / cus) * (cal["decode_tile_fill_s"] +
                                             wg_bytes / cal["decode_tile_bytes_per_cu_s"])
         partials = 2.0 * plan["workspace_bytes"] if S > 1 else 0.0
