@@ -50,10 +50,12 @@ PAIRS = [
     ((255, 5120, 13824, None), (100, 1000, 500, 1003)),
     ((8, 13824, 5120, None), (3, 4096, 384, None)),       # small-M k split; then unsplit
     ((9000, 4000, 256, None), (300, 4000, 256, 4008)),    # padded X beyond the array: chunks
+    ((128, 2048, 1000, None), (70, 1024, 600, None)),     # mid M (decode tile, 128 rows), k splits
 ]
 
 
-@pytest.mark.parametrize("pair", PAIRS, ids=["tile-split", "small-m-split", "pad-chunks"])
+@pytest.mark.parametrize("pair", PAIRS, ids=["tile-split", "small-m-split", "pad-chunks",
+                                             "mid-m-split"])
 def test_noalloc_matches_existing_entry(llk, gpu, orc, pair):
     for M, K, N, xs in pair:
         print(f"case noalloc M={M} K={K} N={N} x_stride={xs}", flush=True)
