@@ -38,6 +38,8 @@ DECODE = dict(K=4096, N=14336)
 DECODE_M = (1, 8, 16, 64)
 MLP = dict(K=5120, N=13824)
 MLP_M = (1, 17, 255, 1000, 4097)
+# Mid M between config 5's rows (the decode tile kernel's 128-row form), reported apart.
+MLP_MID_M = (65, 128)
 # Every timed workload first runs its --warmup launches, then keeps launching
 # until this much time has passed since the first one: the GPU needs ~35 ms of
 # load to reach its steady clock (the first 50 prefill launches average
@@ -456,6 +458,7 @@ def main() -> None:
         extra["gemm_4096"] = {"us": round(gem["ms"] * 1e3, 1), "tflops": round(gem["tflops"], 1),
                               "mfma_frac": round(gem["tflops"] / PEAK_BF16_TFLOPS, 4)}
         extra["mlp_k5120_n13824"] = bench_mlp(torch, llk, a.steps, a.warmup)
+        extra["mlp_k5120_n13824_mid_m"] = bench_mlp(torch, llk, a.steps, a.warmup, MLP_MID_M)
         extra["vendor_hipblaslt"] = bench_vendor(torch, max(10, a.steps // 2), a.warmup)
         g16 = bench_gemm(torch, llk, max(10, a.steps // 2), a.warmup, torch.bfloat16)
         extra["gemm_4096_bf16_out"] = {"us": round(g16["ms"] * 1e3, 1),

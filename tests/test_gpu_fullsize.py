@@ -88,11 +88,12 @@ def test_config2_gemm_4096(llk, gpu, orc):
     assert np.max(np.abs(c[:1] - c64)) < 1e-4
 
 
-@pytest.mark.parametrize("M", [1, 17, 255, 1000, 4097])
+@pytest.mark.parametrize("M", [1, 17, 65, 128, 255, 1000, 4097])
 def test_config5_mlp(llk, gpu, orc, M):
     """Config 5: SwiGLU (K=5120, N=13824) then Z = Y Wd, Wd [13824, 5120];
-    ragged M; 1% of X scaled x20; bf16 out.  Each stage against the oracle on
-    every row; Z against the oracle applied to the GPU's own Y."""
+    ragged M (65 and 128: the mid-M forms, between config 5's rows); 1% of X
+    scaled x20; bf16 out.  Each stage against the oracle on every row; Z
+    against the oracle applied to the GPU's own Y."""
     print(f"case config5 M={M}", flush=True)
     K, N = 5120, 13824
     x, wg, wu = swiglu_inputs(M, K, N, seed=42)
