@@ -16,8 +16,10 @@
 // applies, else the small-M kernel's width, and splits from the cost
 // models), the same kernel at k splits S in {1, 2, 3, 4, 6, 8}, then the
 // small-M kernel at 32-column groups per workgroup G in {1, 2, 4} x S in
-// {auto, 1, 2, 3, 4, 6, 8}; tile kernels: S in {auto, 1, 2, 3, 4, 6, 8, 12,
-// 16} (at least 4 k-steps of 64 per split).  Each is timed with HIP events
+// {auto, 1, 2, 3, 4, 6, 8}; mid M (M > 64 where the dispatcher takes the
+// decode tile kernel's 128- or 256-row form): that kernel at S in {auto, 1,
+// 2, 3, 4, 6, 8}; tile kernels: S in {auto, 1, 2, 3, 4, 6, 8, 12, 16} (at
+// least 4 k-steps of 64 per split).  Each is timed with HIP events
 // (best of 3 windows of --measure-ms after a warm-up); the --top fastest
 // are written as schedule_db.json records in the reference schema with this
 // target's field meaning (BN = 32 G for the small-M kernel, 0 for the
@@ -90,6 +92,12 @@ int main(int argc, char** argv) {
   const int bucket = llk_classify_m(M);
   const bool small = M <= 64;
   const int64_t KB = (K + 63) / 64;
+  // Mid M: the dispatcher's own plan for this shape (aligned X) is the
+  // decode tile kernel; its k splits follow decode_splits.
+  llk_launch_plan own{};
+  check_llk(llk_describe_launch(swiglu ? 0 : 3, M, N, K, 1, &own), "describe");
+  const bool midm = !small && own.kernel == 3;
+  const bool dsplits = small || midm;  // candidates set decode_splits, not tile_splits
   int copies = (int)copies_opt;
   if (copies <= 0) {
     const double wbytes = 2.0 * nmat * (double)K * N;
@@ -108,7 +116,7 @@ int main(int argc, char** argv) {
   check_llk(llk_get_tunable("tile_splits", &saved_ts), "tunable");
   auto apply = [&](const Candidate& c) {
     check_llk(llk_set_tunable("decode_group_width", small ? c.G : saved_g), "tunable");
-    check_llk(llk_set_tunable(small ? "decode_splits" : "tile_splits", c.S), "tunable");
+    check_llk(llk_set_tunable(dsplits ? "decode_splits" : "tile_splits", c.S), "tunable");
   };
   auto restore = [&]() {
     (void)llk_set_tunable("decode_group_width", saved_g);
@@ -122,6 +130,9 @@ int main(int argc, char** argv) {
     for (int g : gs)
       for (int s : small_s)
         if (s <= KB) cands.push_back({g, s});
+  } else if (midm) {
+    for (int s : small_s)
+      if (s <= KB) cands.push_back({0, s});
   } else {
     for (int s : tile_s)
       if (s == 0 || s == 1 || KB / s >= 4) cands.push_back({0, s});
@@ -143,7 +154,8 @@ int main(int argc, char** argv) {
   }
   cands.swap(uniq);
   std::printf("M=%lld (bucket %d) N=%lld K=%lld op=%s kernel=%s\n", (long long)M, bucket,
-              (long long)N, (long long)K, op.c_str(), small ? "small_m" : "mfma_tile");
+              (long long)N, (long long)K, op.c_str(),
+              small ? "small_m" : midm ? "decode_tile (mid M)" : "mfma_tile");
   std::printf("Generated %zu candidate launches\n", cands.size());
 
   if (!dry) {
@@ -242,7 +254,10 @@ int main(int argc, char** argv) {
   for (int i = 0; i < count; ++i) {
     const auto& c = cands[i];
     const bool sm = c.plan.kernel == 0 || c.plan.kernel == 3;  // small-M or decode tile
-    const int64_t BM = c.plan.kernel == 0 ? (M <= 32 ? 32 : 64) : sm ? 64 : 256;
+    // BM: rows per workgroup (the decode tile kernel: 64, or 128 / 256 at mid M)
+    const int64_t BM = c.plan.kernel == 0   ? (M <= 32 ? 32 : 64)
+                       : c.plan.kernel == 3 ? (M <= 64 ? 64 : M <= 128 ? 128 : 256)
+                                            : 256;
     // BN 0 / grain_size 0: the dispatcher chooses for each shape (for M <= 64
     // the decode tile kernel where it applies, else the small-M kernel's
     // width); VM x VN is the MFMA tile (small-M and decode tile kernels

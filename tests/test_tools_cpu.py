@@ -184,6 +184,24 @@ def test_tune_dry_run_writes_loadable_db(tmp_path):
     assert sel.BN == e["schedule"]["BN"] and sel.grain_size == e["schedule"]["grain_size"]
 
 
+def test_tune_mid_m_candidates(tmp_path):
+    """Mid M (the dispatcher's plan is the decode tile kernel's 128-row
+    form): llk-tune's candidates are that kernel at decode_splits S, its
+    records BM = 128 rows, BN = 0 (the decode tile kernel), grain_size = S;
+    the same shape with midm_max_m at 64 would be a tile-kernel shape."""
+    out = tmp_path / "tune.json"
+    r = subprocess.run([str(BIN / "llk-tune"), "--op=fused_swiglu", "--M=100", "--N=13824",
+                        "--K=5120", "--dry-run", f"-o={out}", "--top=7"],
+                       capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    assert "kernel=decode_tile (mid M)" in r.stdout
+    assert "Generated 7 candidate launches" in r.stdout
+    entries = json.loads(out.read_text())["entries"]
+    assert [e["schedule"]["grain_size"] for e in entries] == [0, 1, 2, 3, 4, 6, 8]
+    assert all(e["schedule"]["BM"] == 128 and e["schedule"]["BN"] == 0 for e in entries)
+    assert all(e["shape"]["M_bucket"] == 4 for e in entries)
+
+
 def _db(tmp_path, entries):
     p = tmp_path / "db.json"
     p.write_text(json.dumps({"version": 1, "entries": entries}))
