@@ -168,3 +168,42 @@ def test_routing_and_agreement_with_tile_kernels(llk, gpu, orc):
                                out_f32=True)["kernel"] == "tile"
     yf_un = _swiglu(llk, gpu, x, pg, pu, gpu.float32, x_stride=K + 3)
     assert_parity(yf_un, yf_ref, "unaligned X on the tile kernel")
+
+
+def _random_cases(n=16, seed=2027):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        out.append(dict(op=str(rng.choice(["swiglu", "gemm"])), M=int(rng.integers(65, 257)),
+                        K=64 * int(rng.integers(1, 33)), N=int(rng.integers(1, 1300)),
+                        pad=8 * int(rng.integers(0, 5)), splits=int(rng.choice([0, 0, 2, 3, 7])),
+                        seed=int(rng.integers(0, 1 << 30))))
+    return out
+
+
+@pytest.mark.parametrize("c", _random_cases(), ids=lambda c: f"{c['op']}-M{c['M']}-K{c['K']}-N{c['N']}")
+def test_random_mid_m(llk, gpu, orc, c):
+    """Seeded random mid-M shapes (K a multiple of 64, X strides a multiple
+    of 8 elements) on the decode tile kernel, automatic or forced k splits,
+    against the oracle; the bf16 result is the rounding of the fp32 one."""
+    print(f"case mid-M random {c}", flush=True)
+    M, K, N = c["M"], c["K"], c["N"]
+    s = 1.0 / np.sqrt(K)
+    x = normal_bf16(c["seed"], 0, (M, K))
+    w0 = normal_bf16(c["seed"], 1, (K, N), s)
+    w1 = normal_bf16(c["seed"], 2, (K, N), s)
+    xd = to_dev(gpu, x, K + c["pad"] if c["pad"] else None)
+    p0, p1 = llk.PackedWeights.from_host(w0), llk.PackedWeights.from_host(w1)
+    with _Tunable(llk, "decode_splits", c["splits"]):
+        op = "fused_swiglu" if c["op"] == "swiglu" else "matmul"
+        assert llk.describe_launch(op, M, N, K)["kernel"] == "decode_tile"
+        if c["op"] == "swiglu":
+            yf = from_dev(llk.fused_swiglu(xd, p0, p1, out_dtype=gpu.float32))
+            yb = from_dev(llk.fused_swiglu(xd, p0, p1, out_dtype=gpu.bfloat16))
+            ref, _ = orc.swiglu(x, w0, w1)
+        else:
+            yf = from_dev(llk.matmul(xd, p0, out_dtype=gpu.float32))
+            yb = from_dev(llk.matmul(xd, p0, out_dtype=gpu.bfloat16))
+            ref, _ = orc.gemm(x, w0)
+    assert_parity(yf, ref, f"mid-M random {c}")
+    assert np.array_equal(yb, to_bf16_bits(yf))
