@@ -212,10 +212,12 @@ def _unfused_swiglu(torch, F, x, w, gu, N):
 def bench_kernel_fn(torch, llk, M, K, N, calls=40, warm_s=0.05):
     """The reference-shaped KernelFn (llk_swiglu_kernel_fn, synchronous, raw
     row-major weights in device memory) on an M x K x N SwiGLU: us per call
-    with the default per-call pack of Wg and Wu, and with packed weights
-    reused (llk_kernel_fn_assume_immutable_weights); beside them the same
-    shape through llk_swiglu_bf16 with packed handles; the difference of the
-    first two is the two packs (GB/s over their bytes read and written).
+    reading the weights at every call (the default: the row-major decode
+    tile kernel at M <= 128, else a per-call pack of Wg and Wu), and with
+    packed weights reused (llk_kernel_fn_assume_immutable_weights); beside
+    them the same shape through llk_swiglu_bf16 with packed handles; with the
+    per-call pack, the difference of the first two is the two packs (GB/s
+    over their bytes read and written).
     Each form is called for warm_s seconds before its `calls` timed calls
     (the GPU's clock ramp)."""
     from dslcompiler_amd import cache as cmod
@@ -238,7 +240,12 @@ def bench_kernel_fn(torch, llk, M, K, N, calls=40, warm_s=0.05):
         return (time.perf_counter() - t) / calls * 1e6
 
     out = {}
-    out["pack_every_call_us"] = round(per_call(lambda: cmod.swiglu_kernel_fn(x, wg, wu, y, y)), 1)
+    # weights read at every call: straight from the row-major buffers where
+    # the decode tile kernel takes the shape (M <= 128), else packed per call
+    plan = llk.describe_launch("fused_swiglu", M, N, K)
+    out["fresh_weights_path"] = ("row-major decode tile" if plan["kernel"] == "decode_tile" and M <= 128
+                                 else "pack per call")
+    out["fresh_weights_us"] = round(per_call(lambda: cmod.swiglu_kernel_fn(x, wg, wu, y, y)), 1)
     old = cmod.kernel_fn_assume_immutable_weights(True)
     try:
         out["reuse_packed_us"] = round(per_call(lambda: cmod.swiglu_kernel_fn(x, wg, wu, y, y)), 1)
@@ -248,11 +255,12 @@ def bench_kernel_fn(torch, llk, M, K, N, calls=40, warm_s=0.05):
     pg, pu = llk.PackedWeights.from_device(wg), llk.PackedWeights.from_device(wu)
     out["swiglu_bf16_us"] = round(_time_loop(torch, lambda i: llk.fused_swiglu(x, pg, pu, out=y),
                                              calls, 5, warm_s) * 1e3, 1)
-    # the two packs' share of a call, and their rate over 2 x K x N x 2 bytes
-    # read + the same written
-    pack_us = out["pack_every_call_us"] - out["reuse_packed_us"]
-    out["packs_us"] = round(pack_us, 1)
-    out["packs_gbs"] = round(2 * 2.0 * 2 * K * N / max(pack_us, 1e-3) / 1e3, 1)
+    if out["fresh_weights_path"] == "pack per call":
+        # the two packs' share of a call, and their rate over 2 x K x N x 2
+        # bytes read + the same written
+        pack_us = out["fresh_weights_us"] - out["reuse_packed_us"]
+        out["packs_us"] = round(pack_us, 1)
+        out["packs_gbs"] = round(2 * 2.0 * 2 * K * N / max(pack_us, 1e-3) / 1e3, 1)
     return out
 
 

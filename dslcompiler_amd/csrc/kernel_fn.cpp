@@ -4,10 +4,12 @@
 //
 // The reference's JIT'd function reads wg and wu on every call
 // (swiglu_vector_avx2.cpp:278-285 passes the caller's buffers straight
-// through), so by default so does this one: each call packs wg and wu into
-// the MFMA operand layout on the device (one pack launch per matrix, into a
-// per-device buffer the library owns) and then runs the same kernels as
-// llk_swiglu_bf16.  A caller whose weight buffers never change may opt into
+// through), so by default so does this one.  Device-resident weights with
+// 16-byte aligned rows at most 128 rows of X go straight to the decode tile
+// kernel's row-major form (the same launch and bits as the packed path);
+// otherwise each call packs wg and wu into the MFMA operand layout on the
+// device (one pack launch per matrix, into a per-device buffer the library
+// owns) and then runs the same kernels as llk_swiglu_bf16.  A caller whose weight buffers never change may opt into
 // reusing packed handles across calls (llk_kernel_fn_assume_immutable_
 // weights): they are then resolved through the L4 weight level of a
 // per-device cache (WeightKey = address, shape, BK: JitCache.h:143-146,
@@ -43,6 +45,10 @@ int swiglu_with_module(const llk_tensor2d* x, const llk_packed_weights* wg,
 int gemm_with_module(const llk_tensor2d* a, const llk_packed_weights* b, llk_tensor2d* c,
                      int c_dtype, llk_kernel_context* ctx, const ModuleFns* mod,
                      bool accumulate);
+int rowmajor_with_module(int mode, const llk_tensor2d* x, const llk_tensor2d* wg,
+                         const llk_tensor2d* wu, llk_tensor2d* y, int out_dtype,
+                         llk_kernel_context* ctx, const ModuleFns* mod, bool accumulate,
+                         bool* taken);
 // L4 get-or-pack as a counted reference (kernel_cache.cpp).
 int cache_get_shared(llk_jit_cache* c, const llk_tensor2d* w, int64_t bk, int on_device,
                      unsigned flags, std::shared_ptr<llk_packed_weights>* out);
@@ -174,37 +180,6 @@ int memref_call(int op, int out_dtype, const ModuleFns* mod, llk_memref2d* x, ll
   const size_t ye = elem_bytes(out_dtype);
   hipStream_t s = nullptr;
 
-  // Weights.
-  const int nw = swiglu ? 2 : 1;
-  llk_memref2d* wm[2] = {wg, wu};
-  const llk_packed_weights* pw[2] = {nullptr, nullptr};
-  std::shared_ptr<llk_packed_weights> held[2];  // references kept to the end of the call
-  if (g_immutable.load(std::memory_order_relaxed)) {
-    llk_jit_cache* cache = nullptr;
-    if ((rc = device_cache(d, &cache))) return rc;
-    for (int i = 0; i < nw; ++i) {
-      const llk_tensor2d t = weight_tensor(*wm[i]);
-      rc = cache_get_shared(cache, &t, kBK, is_host_only(t.data) ? 0 : 1, 0, &held[i]);
-      if (rc) return status(rc);
-      pw[i] = held[i].get();
-    }
-  } else {
-    size_t off[2] = {0, 0}, total = 0;
-    for (int i = 0; i < nw; ++i) {
-      off[i] = total;
-      total += (llk_pack_device_bytes(wm[i]->size0, wm[i]->size1) + 255) / 256 * 256;
-    }
-    if ((rc = ensure(&d.wstage, &d.wstage_bytes, total, "KernelFn: packed-weight buffer")))
-      return rc;
-    for (int i = 0; i < nw; ++i) {
-      const llk_tensor2d t = weight_tensor(*wm[i]);
-      rc = pack_into(&t, kBK, !is_host_only(t.data), static_cast<uint8_t*>(d.wstage) + off[i], s,
-                     mod, &d.view[i]);
-      if (rc) return status(rc);
-      pw[i] = d.view[i];
-    }
-  }
-
   // X and the result: in place when the GPU can address them, else through
   // dense device copies.
   llk_tensor2d xt{memref_data(*x, 2), M, K, x->stride0, 1};
@@ -235,11 +210,59 @@ int memref_call(int op, int out_dtype, const ModuleFns* mod, llk_memref2d* x, ll
     if (e != hipSuccess) return fail(LLK_ERR_HIP, hipGetErrorString(e));
   }
   llk_kernel_context ctx{nullptr, 0, s};  // null stream, library workspace
-  rc = swiglu ? swiglu_with_module(&xt, pw[0], pw[1], &yt, out_dtype, &ctx, mod)
-              : gemm_with_module(&xt, pw[0], &yt, out_dtype, &ctx, mod, true);
-  if (rc) {
+  auto bail = [&](int code) {
     (void)hipStreamSynchronize(s);  // nothing queued outlives the call
-    return status(rc);
+    return status(code);
+  };
+  bool direct = false;  // launched on the caller's row-major weights
+  // Weights.  Read on every call (the default): device-resident weights
+  // go straight to the decode tile kernel where it takes the shape (at most
+  // 128 rows; rowmajor_with_module), else they are packed into the MFMA
+  // operand layout first.
+  const int nw = swiglu ? 2 : 1;
+  llk_memref2d* wm[2] = {wg, wu};
+  const llk_packed_weights* pw[2] = {nullptr, nullptr};
+  std::shared_ptr<llk_packed_weights> held[2];  // references kept to the end of the call
+  if (g_immutable.load(std::memory_order_relaxed)) {
+    llk_jit_cache* cache = nullptr;
+    if ((rc = device_cache(d, &cache))) return bail(rc);
+    for (int i = 0; i < nw; ++i) {
+      const llk_tensor2d t = weight_tensor(*wm[i]);
+      rc = cache_get_shared(cache, &t, kBK, is_host_only(t.data) ? 0 : 1, 0, &held[i]);
+      if (rc) return bail(rc);
+      pw[i] = held[i].get();
+    }
+  } else if (!is_host_only(memref_data(*wg, 2)) &&
+             (!swiglu || !is_host_only(memref_data(*wu, 2)))) {
+    const llk_tensor2d wgt = weight_tensor(*wg);
+    const llk_tensor2d wut = swiglu ? weight_tensor(*wu) : wgt;
+    bool taken = false;
+    rc = rowmajor_with_module(swiglu ? 1 : 0, &xt, &wgt, swiglu ? &wut : nullptr, &yt, out_dtype,
+                              &ctx, mod, !swiglu, &taken);
+    if (rc) return bail(rc);
+    direct = taken;
+  }
+  if (!direct && pw[0] == nullptr) {
+    size_t off[2] = {0, 0}, total = 0;
+    for (int i = 0; i < nw; ++i) {
+      off[i] = total;
+      total += (llk_pack_device_bytes(wm[i]->size0, wm[i]->size1) + 255) / 256 * 256;
+    }
+    if ((rc = ensure(&d.wstage, &d.wstage_bytes, total, "KernelFn: packed-weight buffer")))
+      return bail(rc);
+    for (int i = 0; i < nw; ++i) {
+      const llk_tensor2d t = weight_tensor(*wm[i]);
+      rc = pack_into(&t, kBK, !is_host_only(t.data), static_cast<uint8_t*>(d.wstage) + off[i], s,
+                     mod, &d.view[i]);
+      if (rc) return bail(rc);
+      pw[i] = d.view[i];
+    }
+  }
+
+  if (!direct) {
+    rc = swiglu ? swiglu_with_module(&xt, pw[0], pw[1], &yt, out_dtype, &ctx, mod)
+                : gemm_with_module(&xt, pw[0], &yt, out_dtype, &ctx, mod, true);
+    if (rc) return bail(rc);
   }
   if (y_host)
     e = hipMemcpy2DAsync(y_user, (size_t)result->stride0 * ye, yt.data, (size_t)N * ye,

@@ -469,6 +469,9 @@ struct DecTileArgs {
   int M, N, KB, NB, S, kbs, n_pad, rows;
   bool yvec;
   bool accumulate;  // GEMM only, S == 1: y += x w (the existing y read in its type)
+  // The row-major form (RM): w0 / w1 are bf16 [K, N] with rows of ldw0 /
+  // ldw1 elements instead of packed payloads.
+  int64_t ldw0, ldw1;
 };
 
 constexpr int kDecSlots = 3;  // ring slots (64-k steps)
@@ -478,7 +481,7 @@ constexpr int dec_lds_bytes(int MT) { return kDecSlots * dec_slot_bytes(MT); }  
 // 32-row MFMA tiles per wave for M rows (M <= 256).
 constexpr int dec_mt(int M) { return M <= 64 ? 1 : M <= 128 ? 2 : 4; }
 
-template <int NMAT, int OUT, int MT>
+template <int NMAT, int OUT, int MT, bool RM>
 __global__ __launch_bounds__(256) void decode_tile_kernel(DecTileArgs a) {
   static_assert(MT == 1 || MT == 2 || MT == 4, "64, 128 or 256 rows per workgroup");
   constexpr int kAhead = kDecSlots - 1;
@@ -496,28 +499,61 @@ __global__ __launch_bounds__(256) void decode_tile_kernel(DecTileArgs a) {
   const int kb0 = split * a.kbs;
   const int nkb = min(a.KB - kb0, a.kbs);
 
-  // Weight resources: this n-block's panel from 64-k block kb0 (loads past
-  // the panel read zero); X from column 64 kb0, up to row M.
-  const int64_t panel = (int64_t)a.KB * kBlockBytes;
-  const int64_t woff = (int64_t)nb * panel + (int64_t)kb0 * kBlockBytes;
-  const int wbytes = (int)(panel - (int64_t)kb0 * kBlockBytes);
-  const u32x4 rw_lo = buffer_rsrc(a.w0 + woff, wbytes);
-  const u32x4 rw_hi = buffer_rsrc((NMAT == 2 ? a.w1 : a.w0) + woff, wbytes);
-  const u32x4 rx = buffer_rsrc(a.x + (size_t)kb0 * 64,
-                               (int)((int64_t)a.M * a.ldx * 2 - (int64_t)kb0 * 128));
-  // This wave's weight loads: sub-blocks i = 4 wave + q of the step, i.e.
-  // operand p = i >> 3, k quarter (i >> 1) & 3, column group c = i & 1 --
-  // packed 32-column group 2 (grp & 1) + c of matrix p (SwiGLU) or 2 p + c
-  // (GEMM) -- placed at ((p * 2 + c) * 4 + kq) KiB of the slot.
+  // Weight resources and this wave's four loads per 64-k step (offset of
+  // step kb: w_vo[q] + kb * w_step, LDS place: w_lds[q] in the slot).
+  u32x4 rw_lo, rw_hi;
   int w_vo[4];
   uint32_t w_lds[4];
+  int w_step;
+  if constexpr (!RM) {
+    // Packed: this n-block's panel from 64-k block kb0 (loads past the panel
+    // read zero).  Sub-blocks i = 4 wave + q of the step, i.e. operand
+    // p = i >> 3, k quarter (i >> 1) & 3, column group c = i & 1 -- packed
+    // 32-column group 2 (grp & 1) + c of matrix p (SwiGLU) or 2 p + c
+    // (GEMM) -- placed at ((p * 2 + c) * 4 + kq) KiB of the slot.
+    const int64_t panel = (int64_t)a.KB * kBlockBytes;
+    const int64_t woff = (int64_t)nb * panel + (int64_t)kb0 * kBlockBytes;
+    const int wbytes = (int)(panel - (int64_t)kb0 * kBlockBytes);
+    rw_lo = buffer_rsrc(a.w0 + woff, wbytes);
+    rw_hi = buffer_rsrc((NMAT == 2 ? a.w1 : a.w0) + woff, wbytes);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int i = wave * 4 + q, p = i >> 3, kq = (i >> 1) & 3, c = i & 1;
-    const int n32 = NMAT == 2 ? 2 * (grp & 1) + c : 2 * p + c;
-    w_vo[q] = (kq * 4 + n32) * kSubBytes + lane * 16;
-    w_lds[q] = (uint32_t)(((p * 2 + c) * 4 + kq) * 1024);
+    for (int q = 0; q < 4; ++q) {
+      const int i = wave * 4 + q, p = i >> 3, kq = (i >> 1) & 3, c = i & 1;
+      const int n32 = NMAT == 2 ? 2 * (grp & 1) + c : 2 * p + c;
+      w_vo[q] = (kq * 4 + n32) * kSubBytes + lane * 16;
+      w_lds[q] = (uint32_t)(((p * 2 + c) * 4 + kq) * 1024);
+    }
+    w_step = kBlockBytes;
+  } else {
+    // Row-major: slab p of the slot (8 KiB: 64 k rows x 64 columns, 128 bytes
+    // a row) holds matrix p's 64 columns of this workgroup (SwiGLU) or its
+    // columns 64 p .. +64 (GEMM).  Load i = 4 wave + q fetches slab i >> 3,
+    // rows 8 (i & 7) .. +8, lane l row 8 (i & 7) + l / 8 and 16-byte chunk
+    // l & 7 of the LDS row, which holds the row's chunk (l & 7) ^ 4 (i & 1):
+    // rows 8 .. 15 of each 16 keep their 64-byte halves swapped, so that an
+    // A operand's two half-waves (rows k and k + 8) read different banks.
+    // Resources reach from row 64 kb0 to the matrix's last element: rows
+    // past K and columns of a slab starting at or past N read zero.
+    const int K = a.KB * 64;
+    auto slab = [&](const uint8_t* w, int64_t ldw, int ncol) {
+      const int64_t left = ((int64_t)(K - kb0 * 64 - 1) * ldw + (a.N - ncol)) * 2;
+      return buffer_rsrc(w + ((int64_t)kb0 * 64 * ldw + ncol) * 2, ncol < a.N ? (int)left : 0);
+    };
+    const int n0 = NMAT == 2 ? grp * 64 : nb * kPackN;
+    rw_lo = slab(a.w0, a.ldw0, n0);
+    rw_hi = NMAT == 2 ? slab(a.w1, a.ldw1, n0) : slab(a.w0, a.ldw0, n0 + 64);
+    const int64_t ldw = NMAT == 2 && wave >= 2 ? a.ldw1 : a.ldw0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = wave * 4 + q;
+      const int r = (i & 7) * 8 + (lane >> 3);
+      w_vo[q] = (int)((r * ldw + (((lane & 7) ^ ((i & 1) * 4)) * 8)) * 2);
+      w_lds[q] = (uint32_t)((i >> 3) * 8192 + (i & 7) * 1024);
+    }
+    w_step = (int)(64 * ldw * 2);
   }
+  const u32x4 rx = buffer_rsrc(a.x + (size_t)kb0 * 64,
+                               (int)((int64_t)a.M * a.ldx * 2 - (int64_t)kb0 * 128));
   // This wave's X loads: rows 8 f .. 8 f + 7 for f = 2 MT wave + q, lane l
   // fetching physical chunk l & 7 of row 8 f + l / 8, i.e. logical chunk
   // (l & 7) ^ (row & 7).  Loads of rows >= M read zeros (no memory traffic)
@@ -533,7 +569,7 @@ __global__ __launch_bounds__(256) void decode_tile_kernel(DecTileArgs a) {
   auto issue = [&](int kb, int slot) {
     const uint32_t base = lds0 + (uint32_t)(slot * kDecSlot);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dma16_nt(rw_mine, w_vo[q] + kb * kBlockBytes, 0, base + w_lds[q]);
+    for (int q = 0; q < 4; ++q) dma16_nt(rw_mine, w_vo[q] + kb * w_step, 0, base + w_lds[q]);
 #pragma unroll
     for (int q = 0; q < kXL; ++q)
       dma16(rx, x_vo[q] + kb * 128, 0, base + kDecW + (uint32_t)(wave * kXL + q) * 1024);
@@ -551,6 +587,27 @@ __global__ __launch_bounds__(256) void decode_tile_kernel(DecTileArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[p][t][r] = 0.0f;
   const uint8_t* const a_rd = smem + cg * 4096 + lane * 16;  // + slot + p * 8 KiB + kq KiB
+  // RM: lane l's A operand -- k = 16 kq + 8 (l / 32) + 0..7 of column
+  // n = 32 cg + l % 32 -- gathered from the slab's rows (element (k, n) at
+  // k * 128 + 2 n, the 16-byte chunk n / 8 swapped with its partner 4 away
+  // in rows 8 .. 15 of every 16, i.e. for l >= 32).
+  const int a_n = 32 * cg + (lane & 31);
+  const uint16_t* const a_rm = reinterpret_cast<const uint16_t*>(smem) + (lane >> 5) * 8 * 64 +
+                               (((a_n >> 3) ^ ((lane >> 5) * 4)) * 8 + (a_n & 7));
+  auto rd_a = [&](int off, int p, int kq) -> bf16x8 {
+    if constexpr (!RM) {
+      return *reinterpret_cast<const bf16x8*>(a_rd + off + p * 8192 + kq * 1024);
+    } else {
+      // eight 16-bit loads into the halves of four registers (ds_read_u16_d16
+      // and _d16_hi), all issued before the MFMAs wait for them
+      const uint16_t* const src = a_rm + (off + p * 8192) / 2 + kq * 16 * 64;
+      typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+      u16x8 v;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = src[j * 64];
+      return __builtin_bit_cast(bf16x8, v);
+    }
+  };
   const int xm = mh * 32 * MT + (lane & 31);                  // the B operand's row (t = 0)
   const uint8_t* const b_rd = smem + kDecW + xm * 128;        // + t * 4 KiB: tile t's rows
   int slot = 0, fill = kAhead;
@@ -568,7 +625,7 @@ __global__ __launch_bounds__(256) void decode_tile_kernel(DecTileArgs a) {
                                                   (((2 * kq + (lane >> 5)) ^ (xm & 7)) * 16));
 #pragma unroll
         for (int p = 0; p < 2; ++p)
-          A[p][kq] = *reinterpret_cast<const bf16x8*>(a_rd + off + p * 8192 + kq * 1024);
+          A[p][kq] = rd_a(off, p, kq);
       }
 #pragma unroll
       for (int kq = 0; kq < 4; ++kq)
@@ -591,7 +648,7 @@ __global__ __launch_bounds__(256) void decode_tile_kernel(DecTileArgs a) {
             b_rd + off + t * 4096 + (((2 * kq + (lane >> 5)) ^ (xm & 7)) * 16));
 #pragma unroll
       for (int p = 0; p < 2; ++p)
-        A[buf][p] = *reinterpret_cast<const bf16x8*>(a_rd + off + p * 8192 + kq * 1024);
+        A[buf][p] = rd_a(off, p, kq);
     };
     auto mf = [&](int buf) {
 #pragma unroll
@@ -671,17 +728,18 @@ __global__ __launch_bounds__(256) void decode_tile_kernel(DecTileArgs a) {
   }
 }
 
-template <int NMAT, int OUT, int MT>
+template <int NMAT, int OUT, int MT, bool RM>
 const char* decode_tile_symbol() {
   static const std::string name = "_ZN10llk_gfx95018decode_tile_kernelI" + mangle_int(NMAT) +
-                                  mangle_int(OUT) + mangle_int(MT) + "EEvNS_11DecTileArgsE";
+                                  mangle_int(OUT) + mangle_int(MT) + mangle_bool(RM) +
+                                  "EEvNS_11DecTileArgsE";
   return name.c_str();
 }
 
-template <int NMAT, int OUT, int MT>
+template <int NMAT, int OUT, int MT, bool RM>
 static hipError_t launch_decode_tile_t(const DecTileArgs& a, const llk::ModuleFns* mod,
                                        hipStream_t s) {
-  auto fn = decode_tile_kernel<NMAT, OUT, MT>;
+  auto fn = decode_tile_kernel<NMAT, OUT, MT, RM>;
   constexpr int kLds = dec_lds_bytes(MT);
   if (!mod) {
     static std::atomic<uint64_t> lds_set{0};
@@ -690,7 +748,7 @@ static hipError_t launch_decode_tile_t(const DecTileArgs& a, const llk::ModuleFn
   }
   const unsigned groups = (unsigned)((NMAT == 2 ? a.NB * 2 : a.NB) * a.S);
   hipError_t e = launch_kernel(mod, reinterpret_cast<const void*>(fn),
-                               &decode_tile_symbol<NMAT, OUT, MT>, dim3(groups), dim3(256), kLds,
+                               &decode_tile_symbol<NMAT, OUT, MT, RM>, dim3(groups), dim3(256), kLds,
                                s, a);
   if (e != hipSuccess || a.S == 1) return e;
   SkinnyArgs r{};
@@ -712,9 +770,18 @@ static hipError_t launch_decode_tile_t(const DecTileArgs& a, const llk::ModuleFn
 template <int NMAT, int OUT>
 static hipError_t launch_decode_tile_mt(const DecTileArgs& a, int mt, const llk::ModuleFns* mod,
                                         hipStream_t s) {
-  if (mt == 1) return launch_decode_tile_t<NMAT, OUT, 1>(a, mod, s);
-  if (mt == 2) return launch_decode_tile_t<NMAT, OUT, 2>(a, mod, s);
-  return launch_decode_tile_t<NMAT, OUT, 4>(a, mod, s);
+  if (mt == 1) return launch_decode_tile_t<NMAT, OUT, 1, false>(a, mod, s);
+  if (mt == 2) return launch_decode_tile_t<NMAT, OUT, 2, false>(a, mod, s);
+  return launch_decode_tile_t<NMAT, OUT, 4, false>(a, mod, s);
+}
+
+// The row-major form exists for 64 and 128 rows (MT = 1, 2).
+template <int NMAT, int OUT>
+static hipError_t launch_decode_rowmajor_mt(const DecTileArgs& a, int mt,
+                                            const llk::ModuleFns* mod, hipStream_t s) {
+  if (mt == 1) return launch_decode_tile_t<NMAT, OUT, 1, true>(a, mod, s);
+  if (mt == 2) return launch_decode_tile_t<NMAT, OUT, 2, true>(a, mod, s);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace llk_gfx950
@@ -794,6 +861,16 @@ bool llk_decode_tile_fits(int M, int64_t K, int64_t ldx) {
          (KB + 2) * (int64_t)llk_gfx950::kBlockBytes < ((int64_t)1 << 31);
 }
 
+// Whether the row-major form takes a shape (beside llk_decode_tile_fits):
+// at most 128 rows, each weight matrix bf16 [K, N] with 16-byte aligned rows
+// of ldw >= N elements, and K + 128 rows of it within 32-bit offsets.
+bool llk_decode_rowmajor_fits(int M, int64_t K, int64_t ldx, const void* w, int64_t ldw,
+                              int64_t N) {
+  return M <= 128 && llk_decode_tile_fits(M, K, ldx) && w != nullptr &&
+         reinterpret_cast<uintptr_t>(w) % 16 == 0 && ldw % 8 == 0 && ldw >= N &&
+         (K + 128) * ldw * 2 < ((int64_t)1 << 31);
+}
+
 // Internal: the decode tile kernel.  mode 1 = SwiGLU (w0 = Wg, w1 = Wu),
 // mode 0 = GEMM (w0 = B); llk_decode_tile_fits(M, 64 * KB, ldx) must hold.
 // S > 1 splits K over S workgroups of kbs = ceil(KB / S) blocks (every split
@@ -838,6 +915,59 @@ hipError_t llk_launch_decode_tile(int mode, const uint16_t* x, int64_t ldx, cons
     if (out == kOutBF16) return launch_decode_tile_mt<1, kOutBF16>(a, mt, mod, s);
     if (out == kOutF32) return launch_decode_tile_mt<1, kOutF32>(a, mt, mod, s);
     if (out == kOutF16) return launch_decode_tile_mt<1, kOutF16>(a, mt, mod, s);
+  }
+#endif
+  return hipErrorInvalidValue;
+}
+
+// Internal: the decode tile kernel reading row-major weights (no packed
+// payload): w0 / w1 are bf16 [K, N] with rows of ldw0 / ldw1 elements,
+// llk_decode_rowmajor_fits must hold for each; otherwise as
+// llk_launch_decode_tile (grid, k splits, workspace and results: the same
+// MFMA operands in the same order, so the same bits as the packed form).
+hipError_t llk_launch_decode_rowmajor(int mode, const uint16_t* x, int64_t ldx,
+                                      const uint16_t* w0, int64_t ldw0, const uint16_t* w1,
+                                      int64_t ldw1, void* y, int64_t ldy, int M, int N, int K,
+                                      int S, void* ws, int out, bool yvec, bool accumulate,
+                                      const llk::ModuleFns* mod, hipStream_t s) {
+  using namespace llk_gfx950;
+  if (N < 1 || !llk_decode_rowmajor_fits(M, K, ldx, w0, ldw0, N) ||
+      (mode == 1 && !llk_decode_rowmajor_fits(M, K, ldx, w1, ldw1, N)) ||
+      (accumulate && mode != 0))
+    return hipErrorInvalidValue;
+  DecTileArgs a{};
+  a.x = x;
+  a.w0 = reinterpret_cast<const uint8_t*>(w0);
+  a.w1 = reinterpret_cast<const uint8_t*>(mode == 1 ? w1 : w0);
+  a.ldw0 = ldw0;
+  a.ldw1 = mode == 1 ? ldw1 : ldw0;
+  a.y = y;
+  a.part = static_cast<float*>(ws);
+  a.ldx = ldx;
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.KB = K / 64;
+  a.NB = (N + kPackN - 1) / kPackN;
+  a.S = S < 1 ? 1 : S;
+  a.kbs = (a.KB + a.S - 1) / a.S;
+  a.n_pad = a.NB * kPackN;
+  a.rows = skinny_rows(M);
+  a.yvec = yvec;
+  a.accumulate = accumulate;
+  if (a.S > 1 && (ws == nullptr || (int64_t)(a.S - 1) * a.kbs >= a.KB)) return hipErrorInvalidValue;
+  const int mt = dec_mt(M);
+#if !defined(LLK_CO_OP) || LLK_CO_OP == 1
+  if (mode == 1) {
+    if (out == kOutBF16) return launch_decode_rowmajor_mt<2, kOutBF16>(a, mt, mod, s);
+    if (out == kOutF32) return launch_decode_rowmajor_mt<2, kOutF32>(a, mt, mod, s);
+  }
+#endif
+#if !defined(LLK_CO_OP) || LLK_CO_OP == 0
+  if (mode == 0) {
+    if (out == kOutBF16) return launch_decode_rowmajor_mt<1, kOutBF16>(a, mt, mod, s);
+    if (out == kOutF32) return launch_decode_rowmajor_mt<1, kOutF32>(a, mt, mod, s);
+    if (out == kOutF16) return launch_decode_rowmajor_mt<1, kOutF16>(a, mt, mod, s);
   }
 #endif
   return hipErrorInvalidValue;

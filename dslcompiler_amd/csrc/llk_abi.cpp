@@ -54,6 +54,13 @@ hipError_t llk_launch_decode_tile(int mode, const uint16_t* x, int64_t ldx, cons
                                   const void* w1, void* y, int64_t ldy, int M, int N, int KB,
                                   int NB, int S, void* ws, int out, bool yvec, bool accumulate,
                                   const llk::ModuleFns* mod, hipStream_t s);
+bool llk_decode_rowmajor_fits(int M, int64_t K, int64_t ldx, const void* w, int64_t ldw,
+                              int64_t N);
+hipError_t llk_launch_decode_rowmajor(int mode, const uint16_t* x, int64_t ldx,
+                                      const uint16_t* w0, int64_t ldw0, const uint16_t* w1,
+                                      int64_t ldw1, void* y, int64_t ldy, int M, int N, int K,
+                                      int S, void* ws, int out, bool yvec, bool accumulate,
+                                      const llk::ModuleFns* mod, hipStream_t s);
 hipError_t llk_launch_pad_rows(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* out,
                                int64_t ldo, const llk::ModuleFns* mod, hipStream_t s);
 hipError_t llk_launch_pack(const uint16_t* w, int64_t ld, int K, int N, int KB, int NB, void* out,
@@ -1506,6 +1513,48 @@ int pack_into(const llk_tensor2d* w, int64_t bk, bool w_on_device, void* dst, hi
   e = hipMemcpyAsync(dst, staging.data(), v->dev_bytes, hipMemcpyHostToDevice, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);  // staging is freed on return
   return e == hipSuccess ? LLK_OK : fail_hip(e, "upload of packed weights");
+}
+
+// Row-major weights straight into the decode tile kernel, for the
+// KernelFn path (kernel_fn.cpp), which otherwise packs the caller's weights
+// on every call: x, wg (and wu for SwiGLU, mode 1; GEMM: mode 0, accumulate
+// adds the existing y) and y in device memory, weights bf16 [K, N].  Taken
+// (*taken = true) only where the dispatcher's plan for the same shape and X
+// is the decode tile kernel with at most 128 rows and the weights' rows
+// suit its loads (llk_decode_rowmajor_fits); then it launches that plan --
+// same grid, k splits and MFMA operands -- so the result equals the packed
+// path's bit for bit.  Otherwise nothing is launched and the caller packs.
+int rowmajor_with_module(int mode, const llk_tensor2d* x, const llk_tensor2d* wg,
+                         const llk_tensor2d* wu, llk_tensor2d* y, int out_dtype,
+                         llk_kernel_context* ctx, const ModuleFns* mod, bool accumulate,
+                         bool* taken) {
+  *taken = false;
+  const int64_t M = x->dim0, K = x->dim1, N = wg->dim1;
+  if (M < 1 || M > 128 || N < 1 || K < 1 || y->dim0 != M || y->dim1 != N) return LLK_OK;
+  if (wg->stride1 != 1 || (mode == 1 && (!wu || wu->stride1 != 1 || wu->dim1 != N))) return LLK_OK;
+  const int nmat = mode == 1 ? 2 : 1;
+  const int64_t KB = llk::deviceBlocksK(K), NB = llk::deviceBlocksN(N);
+  const Plan p = plan_launch(nmat, M, K, KB, NB, x, SIZE_MAX, accumulate, out_dtype == LLK_BF16);
+  if (!p.dtile || !x_vec_ok(x) ||
+      !llk_decode_rowmajor_fits((int)M, K, x->stride0, wg->data, wg->stride0, N) ||
+      (mode == 1 && !llk_decode_rowmajor_fits((int)M, K, x->stride0, wu->data, wu->stride0, N)))
+    return LLK_OK;
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  void* ws = nullptr;
+  Workspace* held = nullptr;
+  if ((rc = get_workspace(dev, p.ws_bytes, ctx, &ws, &held))) return rc;
+  *taken = true;
+  hipStream_t s = stream_of(ctx);
+  const hipError_t e = llk_launch_decode_rowmajor(
+      mode, static_cast<const uint16_t*>(x->data), x->stride0,
+      static_cast<const uint16_t*>(wg->data), wg->stride0,
+      mode == 1 ? static_cast<const uint16_t*>(wu->data) : nullptr, mode == 1 ? wu->stride0 : 0,
+      y->data, y->stride0, (int)M, (int)N, (int)K, p.S, ws, out_dtype, y_vec_ok(y, out_dtype),
+      accumulate, mod, s);
+  release_workspace(dev, held, s);
+  return e == hipSuccess ? LLK_OK : fail_hip(e, "decode tile kernel (row-major weights)");
 }
 
 // The SwiGLU and GEMM entry points with the kernels of a loaded code object

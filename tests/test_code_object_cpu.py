@@ -49,7 +49,8 @@ def test_objects_hold_their_operations_kernels():
     # reduce, wide SwiGLU tiles (2 widths x split x non-temporal weights),
     # small-M kernels (2 x 3 widths x 2 X paths x output types) and their
     # reduce, decode tile kernels (output types x 64-, 128- and 256-row
-    # forms), X padding and the K = 0
+    # forms on the packed payload, 64- and 128-row forms on row-major
+    # weights), X padding and the K = 0
     # fill; no tile form waits for another workgroup (every instantiation has
     # the four template arguments MODE, OUT, YVEC, SPLIT)
     def count(names, part):
@@ -61,7 +62,7 @@ def test_objects_hold_their_operations_kernels():
             assert len(re.findall(r"L[ib]\d+E", args)) == 4, k
     assert (count(sw, "mfma_swiglu_wide_kernel"), count(mm, "mfma_swiglu_wide_kernel")) == (8, 0)
     assert (count(sw, "13skinny_kernel"), count(mm, "13skinny_kernel")) == (24, 36)
-    assert (count(sw, "decode_tile_kernel"), count(mm, "decode_tile_kernel")) == (6, 9)
+    assert (count(sw, "decode_tile_kernel"), count(mm, "decode_tile_kernel")) == (10, 15)
     for names in (sw, mm):
         assert "_Z15pad_rows_kernelPKtliiPtl" in names
         assert "_Z16zero_rows_kernelPhllil" in names

@@ -20,7 +20,7 @@ import threading
 import numpy as np
 import pytest
 
-from common import assert_parity, assert_parity_bf16, swiglu_inputs
+from common import assert_parity, assert_parity_bf16, normal_bf16, swiglu_inputs
 from gpu_util import from_dev, to_dev
 
 pytestmark = pytest.mark.gpu
@@ -53,8 +53,9 @@ def test_memref_is_56_bytes():
 
 @pytest.mark.parametrize("M,K,N", [(8, 1024, 768), (300, 576, 392)])
 def test_kernel_fn_device_operands(llk, gpu, orc, M, K, N):
-    """Device operands used in place; by default the weights are packed on
-    every call (the L4 level is not consulted) and repeated calls give the
+    """Device operands used in place; by default the weights are read at
+    every call (M = 8: straight from the row-major buffers; M = 300: packed
+    per call), the L4 level is not consulted, and repeated calls give the
     same bits."""
     print(f"case kernel_fn device M={M} K={K} N={N}", flush=True)
     x, wg, wu = swiglu_inputs(M, K, N, seed=M + 5)
@@ -70,7 +71,7 @@ def test_kernel_fn_device_operands(llk, gpu, orc, M, K, N):
     y.fill_(float("nan"))
     _call(llk, mx, mg, mu, my)
     assert np.array_equal(from_dev(y), got1)
-    assert _l4(llk) == l4_0, "weights packed per call, not through L4"
+    assert _l4(llk) == l4_0, "weights read per call, not through L4"
 
 
 def test_kernel_fn_sees_weights_rewritten_in_place(llk, gpu, orc):
@@ -263,3 +264,59 @@ func.func @swiglu(%x: tensor<{M}x{K}xbf16>, %wg: tensor<{K}x{N}xbf16>, %wu: tens
     fn(xd, wgd, wud, y, y)
     assert_parity_bf16(from_dev(y), orc.swiglu(x, wg, wu)[0], "string-keyed KernelFn")
     jc.close()
+
+
+@pytest.mark.parametrize("M,K,N,ldw", [(1, 1024, 768, 768), (8, 2048, 1000, 1008),
+                                       (33, 640, 600, 603), (64, 4096, 512, 512),
+                                       (100, 1280, 1376, 1376), (128, 576, 392, 400),
+                                       (129, 576, 392, 392)])
+def test_kernel_fn_rowmajor_matches_packed(llk, gpu, orc, M, K, N, ldw):
+    """Device weights and at most 128 rows of X: the KernelFn reads the
+    caller's row-major weights (rows of ldw elements, ldw % 8 == 0) straight
+    into the decode tile kernel, without a pack; its result equals
+    llk_swiglu_bf16's on packed weights bit for bit (the same launch) and the
+    oracle to the bar.  A stride the row-major loads cannot take (ldw % 8 !=
+    0) and M > 128 pack first, with the same result."""
+    print(f"case kernel_fn row-major M={M} K={K} N={N} ldw={ldw}", flush=True)
+    x, wg, wu = swiglu_inputs(M, K, N, seed=M + K)
+    xd = to_dev(gpu, x)
+    wgd, wud = to_dev(gpu, wg, ldw), to_dev(gpu, wu, ldw)
+    y = gpu.full((M, N), float("nan"), dtype=gpu.bfloat16, device="cuda")
+    mx, my = _memref(xd.data_ptr(), M, K, K), _memref(y.data_ptr(), M, N, N)
+    mg, mu = _memref(wgd.data_ptr(), K, N, ldw), _memref(wud.data_ptr(), K, N, ldw)
+    _call(llk, mx, mg, mu, my)
+    got = from_dev(y)
+    pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
+    packed = from_dev(llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.bfloat16))
+    assert np.array_equal(got, packed), "KernelFn differs from the packed path"
+    assert_parity_bf16(got, orc.swiglu(x, wg, wu)[0], f"KernelFn row-major M={M}")
+
+
+@pytest.mark.parametrize("M,S", [(8, 0), (40, 3), (100, 0)])
+def test_kernel_fn_rowmajor_matmul_entry(llk, gpu, orc, M, S):
+    """The object-code level's matmul KernelFn (fp32 key, result = init + x
+    wg) on device weights (row-major, no pack) and on host weights (packed
+    per call): the same bits, on the oracle's bar; with the decode tile
+    kernel's k split forced (S = 3: the reduce adds init)."""
+    print(f"case kernel_fn row-major matmul M={M} S={S}", flush=True)
+    K, N = 1536, 700
+    a = normal_bf16(91, M, (M, K))
+    b = normal_bf16(91, K, (K, N), 1.0 / np.sqrt(K))
+    ad, bd = to_dev(gpu, a), to_dev(gpu, b)
+    b_host = np.ascontiguousarray(b)
+    jc = llk.JitCache()
+    mm = jc.lookup_or_compile(llk.KernelKey(operation=3, isa=7, N=N, K=K, output_type=2))
+    init = gpu.randn((M, N), dtype=gpu.float32, device="cuda")
+    old = llk.get_tunable("decode_splits")
+    llk.set_tunable("decode_splits", S)
+    try:
+        c_dev = gpu.full((M, N), float("nan"), dtype=gpu.float32, device="cuda")
+        mm(ad, bd, None, init, c_dev)
+        c_host = gpu.full((M, N), float("nan"), dtype=gpu.float32, device="cuda")
+        mm(ad, b_host, None, init, c_host)
+    finally:
+        llk.set_tunable("decode_splits", old)
+        jc.close()
+    assert np.array_equal(from_dev(c_dev), from_dev(c_host))
+    ref, _ = orc.gemm(a, b)
+    assert_parity(from_dev(c_dev), ref + from_dev(init), f"matmul KernelFn row-major M={M}")

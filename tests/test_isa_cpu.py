@@ -392,17 +392,22 @@ def test_small_m_kernels_no_scratch_and_pipelined_forms(skinny_asm):
 
 
 def test_decode_tile_kernel_loop(skinny_asm):
-    """The decode tile kernel (every instantiation, MT = 1, 2, 4 32-row MFMA
-    tiles per wave): no scratch; its K loop (one 64-k step) holds exactly one
-    vector-memory wait, vmcnt(4 + 2 MT) -- the wave's loads of the next step
-    may still be in flight -- then one barrier, four non-temporal weight
-    LDS-DMA loads and 2 MT X ones, each right after its own M0 write and one
-    wait state, and 8 MT v_mfma_f32_32x32x16_bf16."""
+    """The decode tile kernel (every instantiation: MT = 1, 2, 4 32-row MFMA
+    tiles per wave on the packed payload, MT = 1, 2 on row-major weights):
+    no scratch; its K loop (one 64-k step; the loop region with the barrier)
+    holds exactly one vector-memory wait, vmcnt(4 + 2 MT) -- the wave's loads
+    of the next step may still be in flight -- then one barrier, four
+    non-temporal weight LDS-DMA loads and 2 MT X ones, each right after its
+    own M0 write and one wait state, and 8 MT v_mfma_f32_32x32x16_bf16; the
+    packed forms read each A operand as one 16-byte LDS load, the row-major
+    ones gather it from eight rows (64 ds_read_u16 per step)."""
     names = re.findall(r"^(_ZN10llk_gfx95018decode_tile_kernel\w+):", skinny_asm, re.M)
-    # (SwiGLU bf16 / fp32, GEMM bf16 / fp16 / fp32) x MT
-    assert len(names) == 15, names
-    mts = [int(re.search(r"decode_tile_kernelILi\d+ELi\d+ELi(\d+)E", n).group(1)) for n in names]
-    assert sorted(mts) == [1] * 5 + [2] * 5 + [4] * 5, mts
+    form = r"decode_tile_kernelILi\d+ELi\d+ELi(\d+)ELb(\d)E"
+    # (SwiGLU bf16 / fp32, GEMM bf16 / fp16 / fp32) x (MT 1, 2, 4 packed; 1, 2 row-major)
+    assert len(names) == 25, names
+    forms = sorted((int(re.search(form, n).group(1)), int(re.search(form, n).group(2)))
+                   for n in names)
+    assert forms == sorted([(mt, 0) for mt in (1, 2, 4)] * 5 + [(mt, 1) for mt in (1, 2)] * 5), forms
     meta = dict(re.findall(r"\.name:\s+(_ZN10llk_gfx95018decode_tile_kernel\w+)\n"
                            r"\s+\.private_segment_fixed_size:\s+(\d+)", skinny_asm))
     assert sorted(meta) == sorted(names) and set(meta.values()) == {"0"}, meta
@@ -420,11 +425,14 @@ def test_decode_tile_kernel_loop(skinny_asm):
             if m and m.group(1) in labels and labels[m.group(1)] < i:
                 ends[labels[m.group(1)]] = i
         loop = [lines[h:e + 1] for h, e in ends.items()
-                if any("v_mfma" in b for b in lines[h:e + 1])]
+                if any("v_mfma" in b for b in lines[h:e + 1])
+                and any(b == "s_barrier" for b in lines[h:e + 1])]
         assert len(loop) == 1, name
         loop = loop[0]
-        mt = int(re.search(r"decode_tile_kernelILi\d+ELi\d+ELi(\d+)E", name).group(1))
+        mt, rm = (int(v) for v in re.search(form, name).groups())
         assert sum("v_mfma_f32_32x32x16_bf16" in b for b in loop) == 8 * mt, name
+        u16 = sum(b.startswith("ds_read_u16") for b in loop)
+        assert u16 == (64 if rm else 0), (name, u16)
         vm = [re.search(r"vmcnt\((\d+)\)", b).group(1) for b in loop
               if b.startswith("s_waitcnt") and "vmcnt" in b]
         assert vm == [str(4 + 2 * mt)], (name, vm)
