@@ -320,3 +320,28 @@ def test_kernel_fn_rowmajor_matmul_entry(llk, gpu, orc, M, S):
     assert np.array_equal(from_dev(c_dev), from_dev(c_host))
     ref, _ = orc.gemm(a, b)
     assert_parity(from_dev(c_dev), ref + from_dev(init), f"matmul KernelFn row-major M={M}")
+
+
+@pytest.mark.parametrize("M,S", [(24, 5), (96, 3)])
+def test_kernel_fn_rowmajor_split_matches_packed(llk, gpu, orc, M, S):
+    """A forced k split on the row-major path (partial planes and the
+    split-order reduce) gives the packed path's bits at the same split."""
+    print(f"case kernel_fn row-major split M={M} S={S}", flush=True)
+    K, N = 1280, 720
+    x, wg, wu = swiglu_inputs(M, K, N, seed=M + S)
+    xd, wgd, wud = to_dev(gpu, x), to_dev(gpu, wg), to_dev(gpu, wu)
+    y = gpu.full((M, N), float("nan"), dtype=gpu.bfloat16, device="cuda")
+    mx, my = _memref(xd.data_ptr(), M, K, K), _memref(y.data_ptr(), M, N, N)
+    mg, mu = _memref(wgd.data_ptr(), K, N, N), _memref(wud.data_ptr(), K, N, N)
+    pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
+    old = llk.get_tunable("decode_splits")
+    llk.set_tunable("decode_splits", S)
+    try:
+        assert llk.describe_launch("fused_swiglu", M, N, K)["splits"] == S
+        _call(llk, mx, mg, mu, my)
+        got = from_dev(y)
+        packed = from_dev(llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.bfloat16))
+    finally:
+        llk.set_tunable("decode_splits", old)
+    assert np.array_equal(got, packed)
+    assert_parity_bf16(got, orc.swiglu(x, wg, wu)[0], f"KernelFn row-major M={M} S={S}")
