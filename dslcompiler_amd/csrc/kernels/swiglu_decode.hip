@@ -528,10 +528,11 @@ __global__ __launch_bounds__(256) void decode_tile_kernel(DecTileArgs a) {
     // Row-major: slab p of the slot (8 KiB: 64 k rows x 64 columns, 128 bytes
     // a row) holds matrix p's 64 columns of this workgroup (SwiGLU) or its
     // columns 64 p .. +64 (GEMM).  Load i = 4 wave + q fetches slab i >> 3,
-    // rows 8 (i & 7) .. +8, lane l row 8 (i & 7) + l / 8 and 16-byte chunk
-    // l & 7 of the LDS row, which holds the row's chunk (l & 7) ^ 4 (i & 1):
-    // rows 8 .. 15 of each 16 keep their 64-byte halves swapped, so that an
-    // A operand's two half-waves (rows k and k + 8) read different banks.
+    // rows 8 (i & 7) .. +8, lane l row r = 8 (i & 7) + l / 8 and 16-byte
+    // chunk l & 7 of the LDS row, which holds the row's chunk (l & 7) ^ sw(r),
+    // sw(r) = 4 (bit 1 of r ^ bit 3 of r): the row's 64-byte halves swapped
+    // where the two bits differ, so that the transposed reads of an A
+    // operand (rows k .. k + 3 in each half-wave) meet 64 distinct banks.
     // Resources reach from row 64 kb0 to the matrix's last element: rows
     // past K and columns of a slab starting at or past N read zero.
     const int K = a.KB * 64;
@@ -547,7 +548,8 @@ __global__ __launch_bounds__(256) void decode_tile_kernel(DecTileArgs a) {
     for (int q = 0; q < 4; ++q) {
       const int i = wave * 4 + q;
       const int r = (i & 7) * 8 + (lane >> 3);
-      w_vo[q] = (int)((r * ldw + (((lane & 7) ^ ((i & 1) * 4)) * 8)) * 2);
+      const int sw = 4 * (((lane >> 4) ^ i) & 1);  // bits 1 and 3 of r
+      w_vo[q] = (int)((r * ldw + (((lane & 7) ^ sw) * 8)) * 2);
       w_lds[q] = (uint32_t)((i >> 3) * 8192 + (i & 7) * 1024);
     }
     w_step = (int)(64 * ldw * 2);
@@ -588,24 +590,27 @@ __global__ __launch_bounds__(256) void decode_tile_kernel(DecTileArgs a) {
       for (int r = 0; r < 16; ++r) acc[p][t][r] = 0.0f;
   const uint8_t* const a_rd = smem + cg * 4096 + lane * 16;  // + slot + p * 8 KiB + kq KiB
   // RM: lane l's A operand -- k = 16 kq + 8 (l / 32) + 0..7 of column
-  // n = 32 cg + l % 32 -- gathered from the slab's rows (element (k, n) at
-  // k * 128 + 2 n, the 16-byte chunk n / 8 swapped with its partner 4 away
-  // in rows 8 .. 15 of every 16, i.e. for l >= 32).
-  const int a_n = 32 * cg + (lane & 31);
-  const uint16_t* const a_rm = reinterpret_cast<const uint16_t*>(smem) + (lane >> 5) * 8 * 64 +
-                               (((a_n >> 3) ^ ((lane >> 5) * 4)) * 8 + (a_n & 7));
+  // n = 32 cg + l % 32 -- is two transposed reads (ds_read_b64_tr_b16, k
+  // + 0..3 and + 4..7).  Such a read gives lane i of each 16-lane group, as
+  // element j, element i % 4 of the 8 bytes named by the group's lane
+  // i / 4 + 4 j; so the group's lane 4 j + c names row k + j, columns
+  // n0 + 4 c .. + 3 (n0 = 32 cg + 16 (g & 1), g = l / 16), and lane i
+  // receives column n0 + i at rows k .. k + 3 (element (k, n) of a slab at
+  // k * 128 + 2 n, its 16-byte chunk XOR sw(k) as loaded).
+  const int a_g = lane >> 4, a_j = (lane >> 2) & 3, a_c = lane & 3;
+  const int a_chunk = (4 * cg + 2 * (a_g & 1) + (a_c >> 1)) ^ (4 * ((a_j >> 1) ^ (a_g >> 1)));
+  const uint16_t* const a_rm = reinterpret_cast<const uint16_t*>(smem) +
+                               (8 * (a_g >> 1) + a_j) * 64 + a_chunk * 8 + 4 * (a_c & 1);
   auto rd_a = [&](int off, int p, int kq) -> bf16x8 {
     if constexpr (!RM) {
       return *reinterpret_cast<const bf16x8*>(a_rd + off + p * 8192 + kq * 1024);
     } else {
-      // eight 16-bit loads into the halves of four registers (ds_read_u16_d16
-      // and _d16_hi), all issued before the MFMAs wait for them
+      typedef short v4i16 __attribute__((ext_vector_type(4)));
+      typedef __attribute__((address_space(3))) v4i16* lds_v4i16;
       const uint16_t* const src = a_rm + (off + p * 8192) / 2 + kq * 16 * 64;
-      typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
-      u16x8 v;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = src[j * 64];
-      return __builtin_bit_cast(bf16x8, v);
+      const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16)(src));
+      const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16)(src + 4 * 64));
+      return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     }
   };
   const int xm = mh * 32 * MT + (lane & 31);                  // the B operand's row (t = 0)

@@ -400,7 +400,7 @@ def test_decode_tile_kernel_loop(skinny_asm):
     non-temporal weight LDS-DMA loads and 2 MT X ones, each right after its
     own M0 write and one wait state, and 8 MT v_mfma_f32_32x32x16_bf16; the
     packed forms read each A operand as one 16-byte LDS load, the row-major
-    ones gather it from eight rows (64 ds_read_u16 per step)."""
+    ones as two transposed 8-byte reads (16 ds_read_b64_tr_b16 per step)."""
     names = re.findall(r"^(_ZN10llk_gfx95018decode_tile_kernel\w+):", skinny_asm, re.M)
     form = r"decode_tile_kernelILi\d+ELi\d+ELi(\d+)ELb(\d)E"
     # (SwiGLU bf16 / fp32, GEMM bf16 / fp16 / fp32) x (MT 1, 2, 4 packed; 1, 2 row-major)
@@ -431,8 +431,9 @@ def test_decode_tile_kernel_loop(skinny_asm):
         loop = loop[0]
         mt, rm = (int(v) for v in re.search(form, name).groups())
         assert sum("v_mfma_f32_32x32x16_bf16" in b for b in loop) == 8 * mt, name
-        u16 = sum(b.startswith("ds_read_u16") for b in loop)
-        assert u16 == (64 if rm else 0), (name, u16)
+        tr = sum(b.startswith("ds_read_b64_tr_b16") for b in loop)
+        assert tr == (16 if rm else 0), (name, tr)
+        assert not any(b.startswith("ds_read_u16") for b in loop), name
         vm = [re.search(r"vmcnt\((\d+)\)", b).group(1) for b in loop
               if b.startswith("s_waitcnt") and "vmcnt" in b]
         assert vm == [str(4 + 2 * mt)], (name, vm)
