@@ -209,11 +209,28 @@ def _unfused_swiglu(torch, F, x, w, gu, N):
     return F.silu(gu[:, :N]) * gu[:, N:]
 
 
+def native_kernel_fn_us(M, K, N):
+    """us per synchronous llk_swiglu_kernel_fn call timed from C by
+    `llk-bench --kernel-fn` (a child process, row-major device weights, one
+    weight set as below, wall clock per call, best of 3 windows): the call
+    without the Python ctypes wrapper's per-call work."""
+    import subprocess
+    exe = ROOT / "dslcompiler_amd" / "bin" / "llk-bench"
+    r = subprocess.run([str(exe), f"--M={M}", f"--N={N}", f"--K={K}", "--kernel-fn",
+                        "--warmup-ms=100", "--measure-ms=200", "--reps=3"],
+                       capture_output=True, text=True, timeout=120)
+    m = re.search(r"\(([0-9.]+) ms/iter", r.stdout)
+    if r.returncode != 0 or not m:
+        return {"error": (r.stderr or r.stdout).strip()[-300:]}
+    return round(float(m.group(1)) * 1e3, 1)
+
+
 def bench_kernel_fn(torch, llk, M, K, N, calls=40, warm_s=0.05):
     """The reference-shaped KernelFn (llk_swiglu_kernel_fn, synchronous, raw
     row-major weights in device memory) on an M x K x N SwiGLU: us per call
     reading the weights at every call (the default: the row-major decode
-    tile kernel at M <= 128, else a per-call pack of Wg and Wu), and with
+    tile kernel at M <= 128, else a per-call pack of Wg and Wu) through the
+    Python wrapper and from C (native_kernel_fn_us), and with
     packed weights reused (llk_kernel_fn_assume_immutable_weights); beside
     them the same shape through llk_swiglu_bf16 with packed handles; with the
     per-call pack, the difference of the first two is the two packs (GB/s
@@ -246,6 +263,7 @@ def bench_kernel_fn(torch, llk, M, K, N, calls=40, warm_s=0.05):
     out["fresh_weights_path"] = ("row-major decode tile" if plan["kernel"] == "decode_tile" and M <= 128
                                  else "pack per call")
     out["fresh_weights_us"] = round(per_call(lambda: cmod.swiglu_kernel_fn(x, wg, wu, y, y)), 1)
+    out["fresh_weights_native_us"] = native_kernel_fn_us(M, K, N)
     old = cmod.kernel_fn_assume_immutable_weights(True)
     try:
         out["reuse_packed_us"] = round(per_call(lambda: cmod.swiglu_kernel_fn(x, wg, wu, y, y)), 1)

@@ -28,6 +28,19 @@ def test_llk_bench_runs(gpu):
     assert m and float(m.group(1)) > 0 and float(m.group(2)) > 0, r.stdout
 
 
+def test_llk_bench_kernel_fn_runs(gpu):
+    """llk-bench --kernel-fn: synchronous llk_swiglu_kernel_fn calls on
+    row-major device weights, timed by wall clock."""
+    print("case llk-bench --kernel-fn", flush=True)
+    r = subprocess.run([str(BIN / "llk-bench"), "--M=8", "--N=1408", "--K=1024", "--kernel-fn",
+                        "--warmup-ms=20", "--measure-ms=20", "--reps=2", "--copies=2"],
+                       capture_output=True, text=True, timeout=100)
+    assert r.returncode == 0, r.stderr
+    m = re.search(r"Best: ([0-9.]+) GFLOPS \(([0-9.]+) ms/iter, 2 reps\)", r.stdout)
+    assert m and float(m.group(1)) > 0 and float(m.group(2)) > 0, r.stdout
+    assert "llk_swiglu_kernel_fn: synchronous calls, wall clock per call" in r.stdout
+
+
 def test_llk_tune_measures_and_writes_db(gpu, tmp_path):
     print("case llk-tune", flush=True)
     out = tmp_path / "tune.json"

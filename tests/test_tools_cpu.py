@@ -111,11 +111,23 @@ def test_bench_options_in_llvm_cl_forms(args):
     assert "kernel=swiglu_wide splits=1" in r.stdout and "workgroups=504" in r.stdout
 
 
+def test_bench_kernel_fn_option():
+    """llk-bench --kernel-fn (timing llk_swiglu_kernel_fn by wall clock per
+    call, as the reference's harness times its function) parses with the
+    other options; the dry run names it."""
+    r = _tool("llk-bench", "-M", "8", "-N", "14336", "-K", "4096", "--kernel-fn", "--dry-run")
+    assert r.returncode == 0, r.stderr
+    assert "M=8 N=14336 K=4096" in r.stdout and r.stdout.split("\n")[0].endswith("kernel-fn")
+    assert "kernel=decode_tile" in r.stdout
+
+
 @pytest.mark.parametrize("tool,args,msg", [
     ("llk-bench", ["--bogus"], "Unknown command line argument '--bogus'"),
     ("llk-bench", ["--threads=2", "-x"], "Unknown command line argument '-x'"),
     ("llk-bench", ["-M"], "for the -M option: requires a value!"),
     ("llk-bench", ["-M", "12x"], "'12x' value invalid for integer argument"),
+    ("llk-bench", ["--kernel-fn", "--op=matmul"], "--kernel-fn: llk_swiglu_kernel_fn computes"),
+    ("llk-bench", ["--kernel-fn", "--out=f32"], "--kernel-fn: llk_swiglu_kernel_fn computes"),
     ("llk-tune", ["--dry-run=maybe"], "invalid value for boolean argument"),
     ("llk-tune", ["--threads=8", "--dry-run"], "Unknown command line argument '--threads=8'"),
     ("llk-compile", [], "Not enough positional command line arguments"),
