@@ -10,8 +10,10 @@
 // hipErrorNotFound, which the C ABI reports as a status.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <string>
 
 namespace llk {
@@ -23,6 +25,15 @@ hipFunction_t module_function(const ModuleFns* m, const char* symbol);
 
 namespace llk_gfx950 {
 
+// Completion event bound to this thread's launches while set (by a library
+// call that holds a workspace, for the duration of its launches): each
+// launch names it as the kernel's stop event (hipExtLaunchKernel /
+// hipExtModuleLaunchKernel), so after the call it completes with the last
+// of them.  Unlike hipEventRecord, which enqueues a marker packet of its own
+// that the stream's next kernel waits behind (~6 us on MI355X), the event
+// rides on the kernel's own dispatch.
+inline thread_local hipEvent_t t_launch_done = nullptr;
+
 // Launches with the host stub `stub` when mod is null, else the function
 // `symbol()` of the loaded object.  args are the kernel's parameters, by
 // value, in order.  Returns the launch call's own status, so an error left
@@ -32,11 +43,22 @@ template <class... Args>
 hipError_t launch_kernel(const llk::ModuleFns* mod, const void* stub, const char* (*symbol)(),
                          dim3 grid, dim3 block, unsigned lds, hipStream_t s, Args... args) {
   void* params[] = {static_cast<void*>(&args)...};
-  if (!mod) return hipLaunchKernel(stub, grid, block, params, lds, s);
+  hipEvent_t done = t_launch_done;
+  if (!mod)
+    return done ? hipExtLaunchKernel(stub, grid, block, params, lds, s, nullptr, done, 0)
+                : hipLaunchKernel(stub, grid, block, params, lds, s);
   hipFunction_t f = llk::module_function(mod, symbol());
   if (!f) return hipErrorNotFound;
-  return hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, lds, s,
-                               params, nullptr);
+  // hipExtModuleLaunchKernel takes the grid in work-items (32-bit)
+  const uint64_t gx = (uint64_t)grid.x * block.x, gy = (uint64_t)grid.y * block.y,
+                 gz = (uint64_t)grid.z * block.z;
+  if (!done || gx > UINT32_MAX || gy > UINT32_MAX || gz > UINT32_MAX) {
+    const hipError_t e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y,
+                                               block.z, lds, s, params, nullptr);
+    return e == hipSuccess && done ? hipEventRecord(done, s) : e;
+  }
+  return hipExtModuleLaunchKernel(f, (uint32_t)gx, (uint32_t)gy, (uint32_t)gz, block.x, block.y,
+                                  block.z, lds, s, params, nullptr, nullptr, done, 0);
 }
 
 // Pieces of mangled names: a template argument of type int or bool.

@@ -18,6 +18,7 @@
 #include <string>
 #include <vector>
 
+#include "kernels/launch.h"
 #include "packed_weights.h"
 #include "runtime/kernel_key.h"
 #include "runtime/packed_layout.h"
@@ -92,7 +93,7 @@ constexpr int kMaxDevices = 64;
 struct Workspace {
   void* ptr = nullptr;
   size_t bytes = 0;
-  hipEvent_t done = nullptr;  // recorded on the stream after the last call that used it
+  hipEvent_t done = nullptr;  // completes after the last call that used it (see bind)
   bool pinned = false;        // used under graph capture: a graph may name it, never freed
   int busy = 0;               // calls between get_workspace and release_workspace
   uint64_t tick = 0;          // last use, for LRU eviction
@@ -221,8 +222,9 @@ bool evict_one_workspace(DeviceState& st, const Workspace* keep) {
 // The library keeps at most `max_workspaces` of them per device (tunable,
 // default 16): a new stream (or thread, on the per-thread default stream)
 // beyond that evicts the least recently used idle one.  A buffer is freed
-// (on eviction, on growth, or by llk_workspace_trim) only after the event
-// recorded behind the last call that used it has completed, so work still
+// (on eviction, on growth, or by llk_workspace_trim) only after its event,
+// which completes with the last kernel of the last call that used it, has
+// completed (BindDone: the event rides on the launches themselves), so work still
 // queued on a stream -- even one destroyed since -- never loses its
 // buffer; a workspace that a call used while its stream was capturing a
 // graph is pinned instead (the graph names it) and is never freed.  Growth
@@ -300,18 +302,44 @@ int get_workspace(int dev, size_t need, llk_kernel_context* ctx, void** out, Wor
   return LLK_OK;
 }
 
+// Binds a held workspace's `done` event to the calling thread's launches
+// from construction to end(): launch_kernel names it as each kernel's stop
+// event, so it completes with the call's last kernel.  Not when `s` is
+// capturing a graph (an event under capture would be a graph node, not a
+// point the host can wait for): release_workspace then pins the workspace.
+class BindDone {
+ public:
+  BindDone(Workspace* w, hipStream_t s) : prev_(llk_gfx950::t_launch_done) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (w && hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) {
+      llk_gfx950::t_launch_done = w->done;
+      bound_ = true;
+    }
+  }
+  ~BindDone() { end(); }
+  void end() { llk_gfx950::t_launch_done = prev_; }
+  bool bound() const { return bound_; }
+  BindDone(const BindDone&) = delete;
+  BindDone& operator=(const BindDone&) = delete;
+
+ private:
+  hipEvent_t prev_;
+  bool bound_ = false;
+};
+
 // Gives back a workspace from get_workspace once the call's launches are
-// enqueued on `s`: records its `done` event there, or pins it when `s` is
-// capturing a graph (an event recorded under capture would be a graph node,
-// not a point the host can wait for).
-void release_workspace(int dev, Workspace* w, hipStream_t s) {
+// enqueued on `s`.  `bound`: its `done` event rode on those launches
+// (BindDone); otherwise it is recorded on `s` now, or the workspace is
+// pinned when `s` is capturing a graph.
+void release_workspace(int dev, Workspace* w, hipStream_t s, bool bound = false) {
   if (!w) return;
   DeviceState& st = g_dev[dev];
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   // Pinned too when the capture state or the record cannot be had: no event
   // then marks this call's end, so the buffer must outlive it.
-  bool pin = hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone;
-  if (!pin && hipEventRecord(w->done, s) != hipSuccess) pin = true;
+  bool pin = !bound &&
+             (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone);
+  if (!bound && !pin && hipEventRecord(w->done, s) != hipSuccess) pin = true;
   if (pin) (void)hipGetLastError();  // a failed query leaves no error for the next call
   std::lock_guard<std::mutex> lk(st.mu);
   if (pin) w->pinned = true;
@@ -784,9 +812,11 @@ int run_contraction(int mode, const llk_tensor2d* x, const llk_packed_weights* w
   int rc = get_workspace(dev, p.ws_bytes, ctx, &ws, &held);
   if (rc) return rc;
   hipStream_t s = stream_of(ctx);
+  BindDone bind(held, s);
   rc = launch_contraction(mode, x, w0, w1, y, out_dtype, p, static_cast<uint8_t*>(ws), s, what,
                           mod, accumulate);
-  release_workspace(dev, held, s);
+  bind.end();
+  release_workspace(dev, held, s, bind.bound());
   return rc;
 }
 
@@ -1547,13 +1577,15 @@ int rowmajor_with_module(int mode, const llk_tensor2d* x, const llk_tensor2d* wg
   if ((rc = get_workspace(dev, p.ws_bytes, ctx, &ws, &held))) return rc;
   *taken = true;
   hipStream_t s = stream_of(ctx);
+  BindDone bind(held, s);
   const hipError_t e = llk_launch_decode_rowmajor(
       mode, static_cast<const uint16_t*>(x->data), x->stride0,
       static_cast<const uint16_t*>(wg->data), wg->stride0,
       mode == 1 ? static_cast<const uint16_t*>(wu->data) : nullptr, mode == 1 ? wu->stride0 : 0,
       y->data, y->stride0, (int)M, (int)N, (int)K, p.S, ws, out_dtype, y_vec_ok(y, out_dtype),
       accumulate, mod, s);
-  release_workspace(dev, held, s);
+  bind.end();
+  release_workspace(dev, held, s, bind.bound());
   return e == hipSuccess ? LLK_OK : fail_hip(e, "decode tile kernel (row-major weights)");
 }
 
