@@ -229,8 +229,9 @@ def bench_kernel_fn(torch, llk, M, K, N, calls=40, warm_s=0.05):
     """The reference-shaped KernelFn (llk_swiglu_kernel_fn, synchronous, raw
     row-major weights in device memory) on an M x K x N SwiGLU: us per call
     reading the weights at every call (the default: the row-major decode
-    tile kernel at M <= 128, else a per-call pack of Wg and Wu) through the
-    Python wrapper and from C (native_kernel_fn_us), and with
+    tile kernel at M <= 128, the 128-column tile kernel's row-major form
+    above, else a per-call pack of Wg and Wu) through the Python wrapper and
+    from C (native_kernel_fn_us), and with
     packed weights reused (llk_kernel_fn_assume_immutable_weights); beside
     them the same shape through llk_swiglu_bf16 with packed handles; with the
     per-call pack, the difference of the first two is the two packs (GB/s
@@ -257,11 +258,13 @@ def bench_kernel_fn(torch, llk, M, K, N, calls=40, warm_s=0.05):
         return (time.perf_counter() - t) / calls * 1e6
 
     out = {}
-    # weights read at every call: straight from the row-major buffers where
-    # the decode tile kernel takes the shape (M <= 128), else packed per call
+    # weights read at every call: straight from the row-major buffers --
+    # the decode tile kernel's form up to 128 rows, the 128-column tile
+    # kernel's above (K % 64 == 0, N % 8 == 0) -- else packed per call
     plan = llk.describe_launch("fused_swiglu", M, N, K)
-    out["fresh_weights_path"] = ("row-major decode tile" if plan["kernel"] == "decode_tile" and M <= 128
-                                 else "pack per call")
+    out["fresh_weights_path"] = (
+        "row-major decode tile" if plan["kernel"] == "decode_tile" and M <= 128
+        else "row-major tile (128-column)" if K % 64 == 0 and N % 8 == 0 else "pack per call")
     out["fresh_weights_us"] = round(per_call(lambda: cmod.swiglu_kernel_fn(x, wg, wu, y, y)), 1)
     out["fresh_weights_native_us"] = native_kernel_fn_us(M, K, N)
     old = cmod.kernel_fn_assume_immutable_weights(True)

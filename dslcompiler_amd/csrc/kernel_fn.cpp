@@ -5,11 +5,13 @@
 // The reference's JIT'd function reads wg and wu on every call
 // (swiglu_vector_avx2.cpp:278-285 passes the caller's buffers straight
 // through), so by default so does this one.  Device-resident weights with
-// 16-byte aligned rows at most 128 rows of X go straight to the decode tile
-// kernel's row-major form (the same launch and bits as the packed path);
-// otherwise each call packs wg and wu into the MFMA operand layout on the
-// device (one pack launch per matrix, into a per-device buffer the library
-// owns) and then runs the same kernels as llk_swiglu_bf16.  A caller whose weight buffers never change may opt into
+// 16-byte aligned rows go straight to a row-major form of the kernels --
+// the decode tile kernel's at most 128 rows of X (the same launch and bits
+// as the packed path), the SwiGLU's 128-column tile kernel's above (its
+// plan and bits; K a multiple of 64, N of 8); otherwise each call packs wg
+// and wu into the MFMA operand layout on the device (one pack launch per
+// matrix, into a per-device buffer the library owns) and then runs the same
+// kernels as llk_swiglu_bf16.  A caller whose weight buffers never change may opt into
 // reusing packed handles across calls (llk_kernel_fn_assume_immutable_
 // weights): they are then resolved through the L4 weight level of a
 // per-device cache (WeightKey = address, shape, BK: JitCache.h:143-146,
@@ -216,8 +218,9 @@ int memref_call(int op, int out_dtype, const ModuleFns* mod, llk_memref2d* x, ll
   };
   bool direct = false;  // launched on the caller's row-major weights
   // Weights.  Read on every call (the default): device-resident weights
-  // go straight to the decode tile kernel where it takes the shape (at most
-  // 128 rows; rowmajor_with_module), else they are packed into the MFMA
+  // go straight to the kernels where their row-major forms take the shape
+  // (rowmajor_with_module: the decode tile kernel up to 128 rows; above, the
+  // SwiGLU's 128-column tile kernel), else they are packed into the MFMA
   // operand layout first.
   const int nw = swiglu ? 2 : 1;
   llk_memref2d* wm[2] = {wg, wu};

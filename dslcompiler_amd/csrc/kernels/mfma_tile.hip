@@ -99,6 +99,10 @@ struct TileArgs {
   // partial planes (S >= 1), which keeps the tile kernel's epilogue, and its
   // registers, those of C = A B.
   int accumulate;
+  // The row-major form (mfma_tile_rm_kernel, fused SwiGLU): w0 / w1 are the
+  // caller's bf16 [K, N] matrices with rows of ldw0 / ldw1 elements instead
+  // of packed payloads.
+  int64_t ldw0, ldw1;
 };
 
 constexpr int kThreads = 256;
@@ -127,8 +131,13 @@ __device__ __forceinline__ void acc_fence(f32x4 (&acc)[8][8]) {
 // OUT: output element type (kOutBF16, kOutF16 (GEMM only), kOutF32).
 // YVEC: Y rows allow a 4-element vector store (aligned base, ldy % 4 == 0).
 // SPLIT: store raw fp32 partial accumulators of k split s (see TileArgs).
-template <int MODE, int OUT, bool YVEC, bool SPLIT>
-__global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
+// RM: the weights are the caller's row-major matrices (TileArgs::ldw0/1),
+// loaded and read as described at the weight stream below; everything else
+// -- MFMAs, their operands' values and order, epilogue -- is the packed
+// form's, so both give the same bits.
+template <int MODE, int OUT, bool YVEC, bool SPLIT, bool RM>
+__device__ __forceinline__ void tile_body(TileArgs a) {
+  static_assert(!RM || MODE == 1, "the row-major form is the fused SwiGLU's");
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
   const int lane = threadIdx.x & 63;
@@ -174,18 +183,44 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   // operand read (lane group g reading chunk 4h + g of each) land on 16
   // distinct 16-byte bank groups.  Wave w fills rows w*64 .. +64.
   const int wslot = wave >> 1;
-  const uint8_t* wpanel;
-  if (MODE == 1) {
-    wpanel = (wslot ? a.w1 : a.w0) + (size_t)tn * a.KB * kBlockBytes;
+  u32x4 wrsrc;
+  int w_voff = lane * 16;
+  // Row-major weights (RM): slot half h of a stage holds matrix h's (Wg,
+  // Wu) 32 k rows x 128 columns of this tile, 256 bytes a row, row r at
+  // 256 r, its 16-byte chunk c at c ^ sw(r), sw(r) = 2 ((r & 3) | ((r >> 1)
+  // & 4)).  Load i (0..7) of a half brings rows 4 i .. +4 (lane l: row
+  // 4 i + l / 16, chunk position l % 16), whole 128-byte lines; wave w
+  // issues loads 4 (w & 1) .. +4 of half w >> 1 (offset w_rm[i] + stage *
+  // w_step).  The resource reaches from row 64 kb0 to the matrix's last
+  // element: rows past K read zero.
+  int w_rm[4] = {0, 0, 0, 0};
+  int w_step = 0;
+  if constexpr (!RM) {
+    const uint8_t* wpanel;
+    if (MODE == 1) {
+      wpanel = (wslot ? a.w1 : a.w0) + (size_t)tn * a.KB * kBlockBytes;
+    } else {
+      // An odd NB leaves the last tile without a second block; its wave pair
+      // streams block 0 instead and the results (n >= N) are never stored.
+      const int nb = 2 * tn + wslot;
+      wpanel = a.w0 + (size_t)(nb < a.NB ? nb : 0) * a.KB * kBlockBytes;
+    }
+    wpanel += (size_t)kb0 * kBlockBytes + (wave & 1) * 4 * kSubBytes;
+    wrsrc = buffer_rsrc(wpanel, nkb * kBlockBytes);
   } else {
-    // An odd NB leaves the last tile without a second block; its wave pair
-    // streams block 0 instead and the results (n >= N) are never stored.
-    const int nb = 2 * tn + wslot;
-    wpanel = a.w0 + (size_t)(nb < a.NB ? nb : 0) * a.KB * kBlockBytes;
+    const int64_t ldw = wslot ? a.ldw1 : a.ldw0;
+    const int ncol = tn * 128;
+    const int64_t left = ((int64_t)(a.KB * 64 - kb0 * 64 - 1) * ldw + (a.N - ncol)) * 2;
+    wrsrc = buffer_rsrc((wslot ? a.w1 : a.w0) + ((int64_t)kb0 * 64 * ldw + ncol) * 2,
+                        ncol < a.N ? (int)left : 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * ((wave & 1) * 4 + i) + (lane >> 4);
+      const int sw = 2 * ((r & 3) | ((r >> 1) & 4));
+      w_rm[i] = (int)((r * ldw + (((lane & 15) ^ sw) * 8)) * 2);
+    }
+    w_step = (int)(32 * ldw * 2);
   }
-  wpanel += (size_t)kb0 * kBlockBytes + (wave & 1) * 4 * kSubBytes;
-  const u32x4 wrsrc = buffer_rsrc(wpanel, nkb * kBlockBytes);
-  const int w_voff = lane * 16;
 
   // The X resource starts at row m0, column 64 kb0, and ends at row M:
   // rows >= M read zero.
@@ -202,7 +237,10 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   // Load i (0..3) of this wave's share of weight stage t into ring slot wb.
   auto dma_w = [&](int t, int wb, int i) {
     const uint8_t* st = smem + wb * kWStageBytes + (wave * 4) * kSubBytes;
-    dma16(wrsrc, w_voff, t * 8 * kSubBytes + i * kSubBytes, lds_addr(st + i * kSubBytes));
+    if constexpr (RM)
+      dma16(wrsrc, w_rm[i] + t * w_step, 0, lds_addr(st + i * kSubBytes));
+    else
+      dma16(wrsrc, w_voff, t * 8 * kSubBytes + i * kSubBytes, lds_addr(st + i * kSubBytes));
   };
   // Load i (0..7) of this wave's share of X block u into ring slot xb.
   auto dma_x = [&](int u, int xb, int i) {
@@ -228,7 +266,12 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   auto rw_m0 = [&](int wb, int i) {
     set_m0(lds_addr(smem + wb * kWStageBytes + (wave * 4 + i) * kSubBytes));
   };
-  auto rw_ld = [&](int s, int i) { dma16_m0(wrsrc, w_voff + s * 8 * kSubBytes, i * kSubBytes); };
+  auto rw_ld = [&](int s, int i) {
+    if constexpr (RM)
+      dma16_m0(wrsrc, w_rm[i] + s * w_step, 0);
+    else
+      dma16_m0(wrsrc, w_voff + s * 8 * kSubBytes, i * kSubBytes);
+  };
   // Refill load i (0..7) of X block u into ring slot xb.
   auto rx_m0 = [&](int xb, int i) {
     set_m0(lds_addr(smem + kXRingOff + xb * kXBlockBytes + (wave * 8 + i) * kSubBytes));
@@ -251,8 +294,33 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
     const int nn = (MODE == 1) ? wn * 64 + 16 * (i & 3) : 16 * i;
     return slot * 8 * kSubBytes + (nn >> 5) * kSubBytes + ((nn >> 4) & 1) * 256 + a_lane;
   };
+  // RM: A operand i is two transposed reads (ds_read_b64_tr_b16, k + 0..3
+  // and + 4..7 of lane l's 8 k = 8 (l / 16) ..).  Such a read gives lane i'
+  // of each 16-lane group, as element j, element i' % 4 of the 8 bytes named
+  // by the group's lane i' / 4 + 4 j; so the group's lane 4 j + c names row
+  // 8 (l / 16) + j (+ 4), columns nn + 4 c .. + 3 of the half, and lane i'
+  // receives column nn + i' at four consecutive k.  With nn = 16 q, the
+  // chunk (2 q + c / 2) ^ sw(row) = 2 (q ^ s) + c / 2, s = j | 4 ((l / 16) &
+  // 1): one address per q % 4 (q = 4 wn + i % 4), the rest immediate.
+  int a_rm[4] = {0, 0, 0, 0};
+  if constexpr (RM) {
+    const int g = lane >> 4, j = (lane >> 2) & 3, c = lane & 3;
+    const int s = j | (4 * (g & 1));
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      a_rm[q] = (8 * g + j) * 256 + ((4 * wn + q) ^ s) * 32 + (c >> 1) * 16 + (c & 1) * 8;
+  }
   auto rd_a = [&](int wb, int i) {
-    return *reinterpret_cast<const bf16x8*>(smem + wb * kWStageBytes + a_off(i));
+    if constexpr (RM) {
+      typedef short v4i16 __attribute__((ext_vector_type(4)));
+      typedef __attribute__((address_space(3))) v4i16* lds_v4i16;
+      const uint8_t* const p = smem + wb * kWStageBytes + (i >> 2) * 8192 + a_rm[i & 3];
+      const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16)(p));
+      const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16)(p + 1024));
+      return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    } else {
+      return *reinterpret_cast<const bf16x8*>(smem + wb * kWStageBytes + a_off(i));
+    }
   };
   auto rd_b = [&](int xb, int h, int j) {
     return *reinterpret_cast<const bf16x8*>(smem + kXRingOff + xb * kXBlockBytes +
@@ -515,6 +583,17 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   }
 }
 
+template <int MODE, int OUT, bool YVEC, bool SPLIT>
+__global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
+  tile_body<MODE, OUT, YVEC, SPLIT, false>(a);
+}
+
+// The fused SwiGLU on the caller's row-major weights (TileArgs::ldw0/1).
+template <int MODE, int OUT, bool YVEC, bool SPLIT>
+__global__ __launch_bounds__(kThreads, 1) void mfma_tile_rm_kernel(TileArgs a) {
+  tile_body<MODE, OUT, YVEC, SPLIT, true>(a);
+}
+
 // Sums the S partial planes of each output element in split order (fixed,
 // so results are reproducible) and applies the epilogue.  One thread per
 // 4 consecutive n of a row.
@@ -554,11 +633,12 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(TileArgs a) {
 // library's own kernels).  A build of one operation's code object
 // (LLK_CO_OP: 1 SwiGLU, 0 GEMM) instantiates that operation's kernels only.
 // ---------------------------------------------------------------------------
-template <int MODE, int OUT, bool YVEC, bool SPLIT>
+template <int MODE, int OUT, bool YVEC, bool SPLIT, bool RM = false>
 const char* tile_symbol() {
-  static const std::string name = "_ZN10llk_gfx95016mfma_tile_kernelI" + mangle_int(MODE) +
-                                  mangle_int(OUT) + mangle_bool(YVEC) + mangle_bool(SPLIT) +
-                                  "EEvNS_8TileArgsE";
+  static const std::string name =
+      std::string(RM ? "_ZN10llk_gfx95019mfma_tile_rm_kernelI" : "_ZN10llk_gfx95016mfma_tile_kernelI") +
+      mangle_int(MODE) + mangle_int(OUT) + mangle_bool(YVEC) + mangle_bool(SPLIT) +
+      "EEvNS_8TileArgsE";
   return name.c_str();
 }
 
@@ -569,9 +649,13 @@ const char* split_reduce_symbol() {
   return name.c_str();
 }
 
-template <int MODE, int OUT, bool YVEC, bool SPLIT>
+template <int MODE, int OUT, bool YVEC, bool SPLIT, bool RM = false>
 static hipError_t launch_tile_t(const TileArgs& a, const llk::ModuleFns* mod, hipStream_t s) {
-  auto fn = mfma_tile_kernel<MODE, OUT, YVEC, SPLIT>;
+  void (*fn)(TileArgs);
+  if constexpr (RM)
+    fn = mfma_tile_rm_kernel<MODE, OUT, YVEC, SPLIT>;
+  else
+    fn = mfma_tile_kernel<MODE, OUT, YVEC, SPLIT>;
   if (!mod) {
     static std::atomic<uint64_t> lds_set{0};  // devices configured, per instantiation
     hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(fn), kLdsBytes, lds_set);
@@ -580,14 +664,14 @@ static hipError_t launch_tile_t(const TileArgs& a, const llk::ModuleFns* mod, hi
   const int tiles = a.tiles_m * a.tiles_n;
   dim3 grid(tiles * (SPLIT ? a.S : 1)), block(kThreads);
   return launch_kernel(mod, reinterpret_cast<const void*>(fn),
-                       &tile_symbol<MODE, OUT, YVEC, SPLIT>, grid, block, kLdsBytes, s, a);
+                       &tile_symbol<MODE, OUT, YVEC, SPLIT, RM>, grid, block, kLdsBytes, s, a);
 }
 
-template <int MODE, int OUT, bool YVEC>
+template <int MODE, int OUT, bool YVEC, bool RM = false>
 static hipError_t launch_t(const TileArgs& a, const llk::ModuleFns* mod, hipStream_t s) {
-  if (a.S <= 1 && !a.accumulate) return launch_tile_t<MODE, OUT, YVEC, false>(a, mod, s);
+  if (a.S <= 1 && !a.accumulate) return launch_tile_t<MODE, OUT, YVEC, false, RM>(a, mod, s);
   // Partials are fp32 planes with 16-byte aligned rows: one instantiation.
-  hipError_t e = launch_tile_t<MODE, kOutF32, true, true>(a, mod, s);
+  hipError_t e = launch_tile_t<MODE, kOutF32, true, true, RM>(a, mod, s);
   if (e != hipSuccess) return e;
   const int64_t threads = (int64_t)a.M * ((a.N + 3) / 4);
   return launch_kernel(mod, reinterpret_cast<const void*>(split_reduce_kernel<MODE, OUT, YVEC>),
@@ -660,6 +744,7 @@ hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void*
   a.n_pad = NB * 128;
   a.part = static_cast<float*>(part);
   a.accumulate = accumulate ? 1 : 0;
+  a.ldw0 = a.ldw1 = 0;
   if (a.S > 1 && (part == nullptr || (int64_t)(a.S - 1) * a.kbs >= KB)) return hipErrorInvalidValue;
   if (accumulate && (mode != 0 || part == nullptr)) return hipErrorInvalidValue;
 #if !defined(LLK_CO_OP) || LLK_CO_OP == 1
@@ -669,4 +754,60 @@ hipError_t llk_launch_tile(int mode, const uint16_t* x, int64_t ldx, const void*
   if (mode == 0) return launch_mode<0>(a, out, yvec, mod, s);
 #endif
   return hipErrorInvalidValue;
+}
+
+// Whether the row-major tile form takes a [K, N] weight matrix at w (row
+// stride ldw elements) with X of row stride ldx: K a multiple of 64, N and
+// ldw multiples of 8 (16-byte chunks wholly inside or outside a row),
+// 16-byte aligned rows, and every offset the kernel forms (up to K + 128
+// rows) within 32 bits.
+bool llk_tile_rowmajor_fits(int M, int64_t K, int64_t ldx, const void* w, int64_t ldw,
+                            int64_t N) {
+  return M > 0 && K > 0 && K % 64 == 0 && N > 0 && N % 8 == 0 && ldw % 8 == 0 && ldw >= N &&
+         reinterpret_cast<uintptr_t>(w) % 16 == 0 && ldx % 8 == 0 && ldx >= K &&
+         (K + 128) * ldw * 2 < ((int64_t)1 << 31) && llk_tile_x_fits(M, ldx);
+}
+
+// Internal.  The fused SwiGLU (bf16 result) on row-major bf16 weights wg /
+// wu ([K, N], row strides ldwg / ldwu; llk_tile_rowmajor_fits for both) and
+// x as for llk_launch_tile with K = 64 KB: the same grid, k splits and
+// partial planes as llk_launch_tile(1, ...) with NB = ceil(N / 128), and the
+// same bits.
+hipError_t llk_launch_tile_rowmajor(const uint16_t* x, int64_t ldx, const uint16_t* wg,
+                                    int64_t ldwg, const uint16_t* wu, int64_t ldwu, void* y,
+                                    int64_t ldy, int M, int N, int K, int S, void* part,
+                                    bool yvec, const llk::ModuleFns* mod, hipStream_t s) {
+  using namespace llk_gfx950;
+  if (!llk_tile_rowmajor_fits(M, K, ldx, wg, ldwg, N) ||
+      !llk_tile_rowmajor_fits(M, K, ldx, wu, ldwu, N))
+    return hipErrorInvalidValue;
+  TileArgs a;
+  a.x = x;
+  a.w0 = reinterpret_cast<const uint8_t*>(wg);
+  a.w1 = reinterpret_cast<const uint8_t*>(wu);
+  a.y = y;
+  a.ldx = ldx;
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.KB = K / 64;
+  a.NB = (N + 127) / 128;
+  a.tiles_m = (M + kTileM - 1) / kTileM;
+  a.tiles_n = a.NB;
+  a.group_m = 8;
+  a.S = S > 1 ? S : 1;
+  a.kbs = (a.KB + a.S - 1) / a.S;
+  a.n_pad = a.NB * 128;
+  a.part = static_cast<float*>(part);
+  a.accumulate = 0;
+  a.ldw0 = ldwg;
+  a.ldw1 = ldwu;
+  if (a.S > 1 && (part == nullptr || (int64_t)(a.S - 1) * a.kbs >= a.KB))
+    return hipErrorInvalidValue;
+#if !defined(LLK_CO_OP) || LLK_CO_OP == 1
+  return yvec ? launch_t<1, kOutBF16, true, true>(a, mod, s)
+              : launch_t<1, kOutBF16, false, true>(a, mod, s);
+#else
+  return hipErrorInvalidValue;
+#endif
 }

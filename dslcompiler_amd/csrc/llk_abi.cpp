@@ -62,6 +62,11 @@ hipError_t llk_launch_decode_rowmajor(int mode, const uint16_t* x, int64_t ldx,
                                       int64_t ldw1, void* y, int64_t ldy, int M, int N, int K,
                                       int S, void* ws, int out, bool yvec, bool accumulate,
                                       const llk::ModuleFns* mod, hipStream_t s);
+bool llk_tile_rowmajor_fits(int M, int64_t K, int64_t ldx, const void* w, int64_t ldw, int64_t N);
+hipError_t llk_launch_tile_rowmajor(const uint16_t* x, int64_t ldx, const uint16_t* wg,
+                                    int64_t ldwg, const uint16_t* wu, int64_t ldwu, void* y,
+                                    int64_t ldy, int M, int N, int K, int S, void* part,
+                                    bool yvec, const llk::ModuleFns* mod, hipStream_t s);
 hipError_t llk_launch_pad_rows(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* out,
                                int64_t ldo, const llk::ModuleFns* mod, hipStream_t s);
 hipError_t llk_launch_pack(const uint16_t* w, int64_t ld, int K, int N, int KB, int NB, void* out,
@@ -1545,48 +1550,93 @@ int pack_into(const llk_tensor2d* w, int64_t bk, bool w_on_device, void* dst, hi
   return e == hipSuccess ? LLK_OK : fail_hip(e, "upload of packed weights");
 }
 
-// Row-major weights straight into the decode tile kernel, for the
-// KernelFn path (kernel_fn.cpp), which otherwise packs the caller's weights
-// on every call: x, wg (and wu for SwiGLU, mode 1; GEMM: mode 0, accumulate
-// adds the existing y) and y in device memory, weights bf16 [K, N].  Taken
-// (*taken = true) only where the dispatcher's plan for the same shape and X
-// is the decode tile kernel with at most 128 rows and the weights' rows
-// suit its loads (llk_decode_rowmajor_fits); then it launches that plan --
-// same grid, k splits and MFMA operands -- so the result equals the packed
-// path's bit for bit.  Otherwise nothing is launched and the caller packs.
+// Row-major weights straight into the kernels, for the KernelFn path
+// (kernel_fn.cpp), which otherwise packs the caller's weights on every call:
+// x, wg (and wu for SwiGLU, mode 1; GEMM: mode 0, accumulate adds the
+// existing y) and y in device memory, weights bf16 [K, N].  Taken (*taken =
+// true) where
+//  * the dispatcher's plan for the shape and X is the decode tile kernel
+//    with at most 128 rows and the weights' rows suit its loads
+//    (llk_decode_rowmajor_fits): that plan, with the same grid, k splits and
+//    MFMA operands, so the result equals the packed path's bit for bit;
+//  * otherwise, for the fused SwiGLU with a bf16 result on the tile path
+//    (X aligned, K a multiple of 64, llk_tile_rowmajor_fits): the 128-column
+//    tile kernel's row-major form with that kernel's plan -- k splits, and
+//    the unsplit head columns launched first where the plan splits only the
+//    tail (a column offset into the weights and Y) -- never the wide tiles,
+//    whose unsplit and equal-split bits are the 128-column kernel's anyway.
+// Otherwise nothing is launched and the caller packs.
 int rowmajor_with_module(int mode, const llk_tensor2d* x, const llk_tensor2d* wg,
                          const llk_tensor2d* wu, llk_tensor2d* y, int out_dtype,
                          llk_kernel_context* ctx, const ModuleFns* mod, bool accumulate,
                          bool* taken) {
   *taken = false;
+  if (llk::tunable("kernel_fn_rowmajor") == 0) return LLK_OK;
   const int64_t M = x->dim0, K = x->dim1, N = wg->dim1;
-  if (M < 1 || M > 128 || N < 1 || K < 1 || y->dim0 != M || y->dim1 != N) return LLK_OK;
+  if (M < 1 || N < 1 || K < 1 || y->dim0 != M || y->dim1 != N || !x_vec_ok(x)) return LLK_OK;
   if (wg->stride1 != 1 || (mode == 1 && (!wu || wu->stride1 != 1 || wu->dim1 != N))) return LLK_OK;
   const int nmat = mode == 1 ? 2 : 1;
   const int64_t KB = llk::deviceBlocksK(K), NB = llk::deviceBlocksN(N);
   const Plan p = plan_launch(nmat, M, K, KB, NB, x, SIZE_MAX, accumulate, out_dtype == LLK_BF16);
-  if (!p.dtile || !x_vec_ok(x) ||
-      !llk_decode_rowmajor_fits((int)M, K, x->stride0, wg->data, wg->stride0, N) ||
-      (mode == 1 && !llk_decode_rowmajor_fits((int)M, K, x->stride0, wu->data, wu->stride0, N)))
+  auto fits = [&](bool (*f)(int, int64_t, int64_t, const void*, int64_t, int64_t)) {
+    return f((int)M, K, x->stride0, wg->data, wg->stride0, N) &&
+           (mode != 1 || f((int)M, K, x->stride0, wu->data, wu->stride0, N));
+  };
+  int S = p.S;
+  size_t ws_bytes = p.ws_bytes;
+  bool tile = false;
+  int64_t head_cols = 0;  // tile form: columns of the unsplit head launch
+  if (p.dtile && M <= 128) {
+    if (!fits(&llk_decode_rowmajor_fits)) return LLK_OK;
+  } else if (!p.skinny && mode == 1 && out_dtype == LLK_BF16 && !accumulate && !p.pad &&
+             p.chunk >= M && fits(&llk_tile_rowmajor_fits)) {
+    llk::ScheduleEntry se;
+    const bool have_db = db_entry(nmat, M, &se);
+    const TilePlan tp = tile_plan(nmat, M, KB, NB, have_db ? se.grain_size : 0);
+    S = tp.S;
+    head_cols = std::min<int64_t>(tp.head_nb * 128, N);
+    ws_bytes = llk_tile_split_bytes(1, (int)M, (int)(NB - tp.head_nb), S, false);
+    tile = true;
+  } else {
     return LLK_OK;
+  }
   int dev = -1;
   int rc = current_device(&dev);
   if (rc) return rc;
   void* ws = nullptr;
   Workspace* held = nullptr;
-  if ((rc = get_workspace(dev, p.ws_bytes, ctx, &ws, &held))) return rc;
+  if ((rc = get_workspace(dev, ws_bytes, ctx, &ws, &held))) return rc;
   *taken = true;
   hipStream_t s = stream_of(ctx);
   BindDone bind(held, s);
-  const hipError_t e = llk_launch_decode_rowmajor(
-      mode, static_cast<const uint16_t*>(x->data), x->stride0,
-      static_cast<const uint16_t*>(wg->data), wg->stride0,
-      mode == 1 ? static_cast<const uint16_t*>(wu->data) : nullptr, mode == 1 ? wu->stride0 : 0,
-      y->data, y->stride0, (int)M, (int)N, (int)K, p.S, ws, out_dtype, y_vec_ok(y, out_dtype),
-      accumulate, mod, s);
+  const uint16_t* const xd = static_cast<const uint16_t*>(x->data);
+  const uint16_t* const wgd = static_cast<const uint16_t*>(wg->data);
+  const uint16_t* const wud = mode == 1 ? static_cast<const uint16_t*>(wu->data) : nullptr;
+  hipError_t e = hipSuccess;
+  if (tile) {
+    // head columns unsplit, then the rest with the plan's splits (offsets of
+    // 128-column multiples keep every row 16-byte aligned)
+    const bool yv = y_vec_ok(y, out_dtype);
+    if (head_cols > 0)
+      e = llk_launch_tile_rowmajor(xd, x->stride0, wgd, wg->stride0, wud, wu->stride0, y->data,
+                                   y->stride0, (int)M, (int)head_cols, (int)K, 1, nullptr, yv,
+                                   mod, s);
+    if (e == hipSuccess && head_cols < N)
+      e = llk_launch_tile_rowmajor(xd, x->stride0, wgd + head_cols, wg->stride0, wud + head_cols,
+                                   wu->stride0, static_cast<uint16_t*>(y->data) + head_cols,
+                                   y->stride0, (int)M, (int)(N - head_cols), (int)K,
+                                   S, ws, yv, mod, s);
+  } else {
+    e = llk_launch_decode_rowmajor(mode, xd, x->stride0, wgd, wg->stride0, wud,
+                                   mode == 1 ? wu->stride0 : 0, y->data, y->stride0, (int)M, (int)N,
+                                   (int)K, S, ws, out_dtype, y_vec_ok(y, out_dtype), accumulate,
+                                   mod, s);
+  }
   bind.end();
   release_workspace(dev, held, s, bind.bound());
-  return e == hipSuccess ? LLK_OK : fail_hip(e, "decode tile kernel (row-major weights)");
+  return e == hipSuccess ? LLK_OK
+                         : fail_hip(e, tile ? "tile kernel (row-major weights)"
+                                            : "decode tile kernel (row-major weights)");
 }
 
 // The SwiGLU and GEMM entry points with the kernels of a loaded code object

@@ -38,6 +38,11 @@ struct Knob {
 //                    take the wide tile kernel (16 B columns per matrix, B = 7
 //                    or 11) where its whole waves beat the 128-column tile;
 //                    0 = never; 7 or 11 = that width whenever it applies.
+// kernel_fn_rowmajor: 1 = the KernelFn entries read device weights with
+//                    aligned rows straight into the kernels' row-major forms
+//                    (the decode tile kernel's up to 128 rows, the SwiGLU's
+//                    128-column tile kernel's above); 0 = they pack the
+//                    weights on every call.
 // max_workspaces:    library-owned workspaces kept per device (one per
 //                    stream, or per thread on the per-thread default
 //                    stream); beyond it the least recently used idle one is
@@ -55,6 +60,7 @@ Knob g_knobs[] = {
     {"tile_min_kb", {4}},
     {"tile_tail_split", {1}},
     {"tile_wide", {1}},
+    {"kernel_fn_rowmajor", {1}},
     {"max_workspaces", {16}},
 };
 

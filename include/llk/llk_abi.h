@@ -351,8 +351,12 @@ int llk_fill_normal_bf16(uint64_t seed, uint64_t stream, float sigma,
  * "tile_splits" (force the tile kernel's k-split count, 0 = cost model),
  * "tile_wgs_per_wave", "tile_min_kb", "tile_tail_split" (1: the columns
  * of a partial last wave of tiles may run as a separate k-split launch;
- * 0: never; a forced "tile_splits" also turns it off), "max_workspaces"
- * (library-owned workspaces kept per device, see llk_workspace_stats).
+ * 0: never; a forced "tile_splits" also turns it off), "tile_wide" (1:
+ * the cost model may take the wide SwiGLU tiles; 0: never; 7 or 11: that
+ * width), "kernel_fn_rowmajor" (1: the KernelFn entries read device weights
+ * with aligned rows straight into the kernels' row-major forms; 0: they
+ * pack the weights on every call), "max_workspaces" (library-owned
+ * workspaces kept per device, see llk_workspace_stats).
  * Returns LLK_OK or LLK_ERR_INVALID_ARGUMENT for an unknown name. */
 int llk_set_tunable(const char* name, int64_t value);
 int llk_get_tunable(const char* name, int64_t* value);
@@ -575,10 +579,14 @@ size_t llk_cache_size(const llk_jit_cache* c);
  * (JitCache.h:79-109): bf16 x [M, K], raw row-major bf16 wg, wu [K, N],
  * init and result [M, N] (callers pass init == result; init is only
  * shape-checked), result = bf16(SiLU(x wg) * (x wu)).  Like the JIT'd
- * function, every call reads wg and wu as they are at the call: they are
- * packed into the MFMA operand layout on the device (one pack launch per
- * matrix into a buffer the library owns per device), so a caller may
- * rewrite a weight buffer in place or reuse its address between calls.
+ * function, every call reads wg and wu as they are at the call, so a caller
+ * may rewrite a weight buffer in place or reuse its address between calls:
+ * device-resident weights with 16-byte aligned rows (row stride a multiple
+ * of 8) go straight to the kernels' row-major forms -- the decode tile
+ * kernel's for at most 128 rows of X, the 128-column tile kernel's above
+ * (K a multiple of 64, N of 8) -- and other weights are packed into the
+ * MFMA operand layout on the device first (one pack launch per matrix into
+ * a buffer the library owns per device).
  * Operands may be device memory (used in place) or host memory (staged
  * through device buffers).  Runs on the null stream and returns when the
  * result is written, like the reference's JIT'd function.  Calls on one

@@ -175,6 +175,9 @@ def test_tunables(llk):
     llk.set_tunable("decode_splits", 3)
     assert llk.get_tunable("decode_splits") == 3
     llk.set_tunable("decode_splits", 0)
+    # the header's knobs, at their documented defaults
+    assert [llk.get_tunable(k) for k in ("midm_max_m", "tile_tail_split", "tile_wide",
+                                         "kernel_fn_rowmajor", "max_workspaces")] == [128, 1, 1, 1, 16]
     with pytest.raises(llk.LLKError, match="unknown tunable"):
         llk.set_tunable("no_such_knob", 1)
     with pytest.raises(llk.LLKError):

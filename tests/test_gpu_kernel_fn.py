@@ -345,3 +345,113 @@ def test_kernel_fn_rowmajor_split_matches_packed(llk, gpu, orc, M, S):
         llk.set_tunable("decode_splits", old)
     assert np.array_equal(got, packed)
     assert_parity_bf16(got, orc.swiglu(x, wg, wu)[0], f"KernelFn row-major M={M} S={S}")
+
+
+@pytest.fixture
+def tile_knobs(llk):
+    """Sets dispatcher knobs for one test and restores them after it."""
+    saved = {}
+
+    def set_(**kw):
+        for k, v in kw.items():
+            saved.setdefault(k, llk.get_tunable(k))
+            llk.set_tunable(k, v)
+    yield set_
+    for k, v in saved.items():
+        llk.set_tunable(k, v)
+
+
+@pytest.mark.parametrize("M,K,N,ldw,wide", [
+    (129, 576, 392, 392, True), (200, 1024, 1000, 1000, True), (257, 640, 1400, 1400, True),
+    (300, 2048, 1408, 1416, True), (600, 1024, 1000, 1000, False), (2304, 1024, 4096, 4096, False)])
+def test_kernel_fn_rowmajor_tile_matches_packed(llk, gpu, orc, tile_knobs, M, K, N, ldw, wide):
+    """Above 128 rows, device weights with K % 64 == 0 and N % 8 == 0: the
+    KernelFn runs the 128-column tile kernel's row-major form on the
+    caller's [K, N] weights (rows of ldw elements), with that kernel's plan
+    -- k splits, and at M = 2304 x N = 4096 an unsplit head of 28 n-blocks
+    and a 2-way split tail.  Its result equals llk_swiglu_bf16's on packed
+    weights bit for bit: against the 128-column kernel's own plan, and (wide)
+    against the default plan, whose wide tiles give the same bits at the
+    same split count; and the oracle to the bar."""
+    print(f"case kernel_fn row-major tile M={M} K={K} N={N} ldw={ldw}", flush=True)
+    if not wide:
+        tile_knobs(tile_wide=0)
+    x, wg, wu = swiglu_inputs(M, K, N, seed=M + N)
+    xd = to_dev(gpu, x)
+    wgd, wud = to_dev(gpu, wg, ldw), to_dev(gpu, wu, ldw)
+    y = gpu.full((M, N), float("nan"), dtype=gpu.bfloat16, device="cuda")
+    mx, my = _memref(xd.data_ptr(), M, K, K), _memref(y.data_ptr(), M, N, N)
+    mg, mu = _memref(wgd.data_ptr(), K, N, ldw), _memref(wud.data_ptr(), K, N, ldw)
+    _call(llk, mx, mg, mu, my)
+    got = from_dev(y)
+    pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
+    packed = from_dev(llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.bfloat16))
+    assert np.array_equal(got, packed), "KernelFn differs from the packed path"
+    if M * N <= 600 * 1408:
+        assert_parity_bf16(got, orc.swiglu(x, wg, wu)[0], f"KernelFn row-major tile M={M}")
+
+
+@pytest.mark.parametrize("M", [64, 300])
+def test_kernel_fn_rowmajor_off_packs(llk, gpu, orc, tile_knobs, M):
+    """kernel_fn_rowmajor = 0: the KernelFn packs the weights on every call
+    instead, with the same bits as the row-major forms (the 128-column plan
+    on both sides at M = 300)."""
+    print(f"case kernel_fn row-major off M={M}", flush=True)
+    K, N = 1024, 1000
+    tile_knobs(tile_wide=0)
+    x, wg, wu = swiglu_inputs(M, K, N, seed=M + 5)
+    xd, wgd, wud = to_dev(gpu, x), to_dev(gpu, wg), to_dev(gpu, wu)
+    mx, mg, mu = (_memref(xd.data_ptr(), M, K, K), _memref(wgd.data_ptr(), K, N, N),
+                  _memref(wud.data_ptr(), K, N, N))
+    outs = []
+    for on in (1, 0):
+        tile_knobs(kernel_fn_rowmajor=on)
+        y = gpu.full((M, N), float("nan"), dtype=gpu.bfloat16, device="cuda")
+        _call(llk, mx, mg, mu, _memref(y.data_ptr(), M, N, N))
+        outs.append(from_dev(y))
+    assert np.array_equal(outs[0], outs[1])
+    assert_parity_bf16(outs[1], orc.swiglu(x, wg, wu)[0], f"KernelFn packed M={M}")
+
+
+@pytest.mark.parametrize("M,S", [(300, 3), (520, 7)])
+def test_kernel_fn_rowmajor_tile_split_matches_packed(llk, gpu, orc, tile_knobs, M, S):
+    """A forced k split on the row-major tile path (partial planes, the
+    split-order reduce) gives the packed 128-column kernel's bits at the
+    same split."""
+    print(f"case kernel_fn row-major tile split M={M} S={S}", flush=True)
+    K, N = 1280, 720
+    tile_knobs(tile_wide=0, tile_splits=S)
+    assert llk.describe_launch("fused_swiglu", M, N, K)["splits"] == S
+    x, wg, wu = swiglu_inputs(M, K, N, seed=M + S)
+    xd, wgd, wud = to_dev(gpu, x), to_dev(gpu, wg), to_dev(gpu, wu)
+    y = gpu.full((M, N), float("nan"), dtype=gpu.bfloat16, device="cuda")
+    mx, my = _memref(xd.data_ptr(), M, K, K), _memref(y.data_ptr(), M, N, N)
+    mg, mu = _memref(wgd.data_ptr(), K, N, N), _memref(wud.data_ptr(), K, N, N)
+    _call(llk, mx, mg, mu, my)
+    got = from_dev(y)
+    pg, pu = llk.PackedWeights.from_host(wg), llk.PackedWeights.from_host(wu)
+    packed = from_dev(llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.bfloat16))
+    assert np.array_equal(got, packed)
+    assert_parity_bf16(got, orc.swiglu(x, wg, wu)[0], f"KernelFn row-major tile M={M} S={S}")
+
+
+def test_kernel_fn_rowmajor_tile_config3(llk, gpu):
+    """Config 3 at full size (M = 2048, K = 4096, N = 11008) through the
+    KernelFn on row-major device weights: bit for bit llk_swiglu_bf16's
+    result on packed weights (the wide kernel, unsplit, whose bits are the
+    128-column kernel's)."""
+    print("case kernel_fn row-major tile config 3", flush=True)
+    M, K, N = 2048, 4096, 11008
+    g = gpu.Generator(device="cuda")
+    g.manual_seed(3)
+    xd = gpu.randn((M, K), generator=g, device="cuda").to(gpu.bfloat16)
+    wgd = (gpu.randn((K, N), generator=g, device="cuda") / 64).to(gpu.bfloat16)
+    wud = (gpu.randn((K, N), generator=g, device="cuda") / 64).to(gpu.bfloat16)
+    y = gpu.full((M, N), float("nan"), dtype=gpu.bfloat16, device="cuda")
+    mx, my = _memref(xd.data_ptr(), M, K, K), _memref(y.data_ptr(), M, N, N)
+    mg, mu = _memref(wgd.data_ptr(), K, N, N), _memref(wud.data_ptr(), K, N, N)
+    _call(llk, mx, mg, mu, my)
+    pg, pu = llk.PackedWeights.from_device(wgd), llk.PackedWeights.from_device(wud)
+    ref = llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.bfloat16)
+    assert gpu.equal(y, ref)
+    assert not gpu.isnan(y.float()).any()

@@ -39,7 +39,10 @@ sys.path.insert(0, str(ROOT))
 from dslcompiler_amd import build as B  # noqa: E402
 
 MFMA = "v_mfma_f32_16x16x32_bf16"
-KERNEL = re.compile(r"^(_ZN10llk_gfx95016mfma_tile_kernel\w+):", re.M)
+# the tile kernel and its row-major form (mfma_tile_rm_kernel: the caller's
+# [K, N] weights, A operands by transposed LDS reads); every check below
+# holds for both
+KERNEL = re.compile(r"^(_ZN10llk_gfx950(?:16mfma_tile_kernel|19mfma_tile_rm_kernel)\w+):", re.M)
 
 
 @pytest.fixture(scope="module")
@@ -115,7 +118,22 @@ def test_every_tile_instantiation_found(asm):
     ks = kernels(asm)
     # SwiGLU (bf16/fp32 out, both Y vector forms, split partials) and GEMM
     # (bf16/fp16/fp32 out, both forms, split partials)
-    assert len(ks) >= 10, sorted(ks)
+    assert len([k for k in ks if "16mfma_tile_kernel" in k]) == 12, sorted(ks)
+    # row-major SwiGLU: bf16 out in both Y forms, split partials
+    assert sorted(k[len("_ZN10llk_gfx95019mfma_tile_rm_kernelI"):].split("EE")[0]
+                  for k in ks if "rm_kernel" in k) == [
+        "Li1ELi0ELb0ELb0", "Li1ELi0ELb1ELb0", "Li1ELi2ELb1ELb1"], sorted(ks)
+
+
+def test_k_loop_operand_reads(asm):
+    """Per twelve-stage loop body: 96 B-operand reads of 16 bytes; the A
+    operands (8 per stage) as 96 more 16-byte reads from the packed payload,
+    or, in the row-major form, as 192 transposed 8-byte reads."""
+    for name, lines in kernels(asm).items():
+        body = [b for b in k_loop(lines) if is_insn(b)]
+        b128 = sum(b.startswith("ds_read_b128") for b in body)
+        tr = sum(b.startswith("ds_read_b64_tr_b16") for b in body)
+        assert (b128, tr) == ((96, 192) if "rm_kernel" in name else (192, 0)), (name, b128, tr)
 
 
 def test_tile_weight_loads_never_non_temporal(asm):
