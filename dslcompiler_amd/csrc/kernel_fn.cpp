@@ -7,8 +7,9 @@
 // through), so by default so does this one.  Device-resident weights with
 // 16-byte aligned rows go straight to a row-major form of the kernels --
 // the decode tile kernel's at most 128 rows of X (the same launch and bits
-// as the packed path), the SwiGLU's 128-column tile kernel's above (its
-// plan and bits; K a multiple of 64, N of 8); otherwise each call packs wg
+// as the packed path), the tile kernel's above (the SwiGLU's 128-column
+// plan, the matmul's accumulating plan, and their bits; K a multiple of 64,
+// N of 8); otherwise each call packs wg
 // and wu into the MFMA operand layout on the device (one pack launch per
 // matrix, into a per-device buffer the library owns) and then runs the same
 // kernels as llk_swiglu_bf16.  A caller whose weight buffers never change may opt into
@@ -220,7 +221,7 @@ int memref_call(int op, int out_dtype, const ModuleFns* mod, llk_memref2d* x, ll
   // Weights.  Read on every call (the default): device-resident weights
   // go straight to the kernels where their row-major forms take the shape
   // (rowmajor_with_module: the decode tile kernel up to 128 rows; above, the
-  // SwiGLU's 128-column tile kernel), else they are packed into the MFMA
+  // tile kernel), else they are packed into the MFMA
   // operand layout first.
   const int nw = swiglu ? 2 : 1;
   llk_memref2d* wm[2] = {wg, wu};

@@ -137,7 +137,6 @@ __device__ __forceinline__ void acc_fence(f32x4 (&acc)[8][8]) {
 // form's, so both give the same bits.
 template <int MODE, int OUT, bool YVEC, bool SPLIT, bool RM>
 __device__ __forceinline__ void tile_body(TileArgs a) {
-  static_assert(!RM || MODE == 1, "the row-major form is the fused SwiGLU's");
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
   const int lane = threadIdx.x & 63;
@@ -185,8 +184,9 @@ __device__ __forceinline__ void tile_body(TileArgs a) {
   const int wslot = wave >> 1;
   u32x4 wrsrc;
   int w_voff = lane * 16;
-  // Row-major weights (RM): slot half h of a stage holds matrix h's (Wg,
-  // Wu) 32 k rows x 128 columns of this tile, 256 bytes a row, row r at
+  // Row-major weights (RM): slot half h of a stage holds 32 k rows x 128
+  // columns -- SwiGLU: this tile's columns of matrix h (Wg, Wu); GEMM:
+  // n-block 2 tn + h of B (past N: zeros) -- 256 bytes a row, row r at
   // 256 r, its 16-byte chunk c at c ^ sw(r), sw(r) = 2 ((r & 3) | ((r >> 1)
   // & 4)).  Load i (0..7) of a half brings rows 4 i .. +4 (lane l: row
   // 4 i + l / 16, chunk position l % 16), whole 128-byte lines; wave w
@@ -208,10 +208,11 @@ __device__ __forceinline__ void tile_body(TileArgs a) {
     wpanel += (size_t)kb0 * kBlockBytes + (wave & 1) * 4 * kSubBytes;
     wrsrc = buffer_rsrc(wpanel, nkb * kBlockBytes);
   } else {
-    const int64_t ldw = wslot ? a.ldw1 : a.ldw0;
-    const int ncol = tn * 128;
+    const int64_t ldw = MODE == 1 && wslot ? a.ldw1 : a.ldw0;
+    const uint8_t* const wmat = MODE == 1 && wslot ? a.w1 : a.w0;
+    const int ncol = (MODE == 1 ? tn : 2 * tn + wslot) * 128;
     const int64_t left = ((int64_t)(a.KB * 64 - kb0 * 64 - 1) * ldw + (a.N - ncol)) * 2;
-    wrsrc = buffer_rsrc((wslot ? a.w1 : a.w0) + ((int64_t)kb0 * 64 * ldw + ncol) * 2,
+    wrsrc = buffer_rsrc(wmat + ((int64_t)kb0 * 64 * ldw + (ncol < a.N ? ncol : 0)) * 2,
                         ncol < a.N ? (int)left : 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -301,20 +302,24 @@ __device__ __forceinline__ void tile_body(TileArgs a) {
   // 8 (l / 16) + j (+ 4), columns nn + 4 c .. + 3 of the half, and lane i'
   // receives column nn + i' at four consecutive k.  With nn = 16 q, the
   // chunk (2 q + c / 2) ^ sw(row) = 2 (q ^ s) + c / 2, s = j | 4 ((l / 16) &
-  // 1): one address per q % 4 (q = 4 wn + i % 4), the rest immediate.
-  int a_rm[4] = {0, 0, 0, 0};
+  // 1): one address per q of the wave (SwiGLU: q = 4 wn + i % 4 in half
+  // i / 4; GEMM: q = i in half wn), the rest immediate.
+  constexpr int kQ = MODE == 1 ? 4 : 8;
+  int a_rm[kQ] = {};
   if constexpr (RM) {
     const int g = lane >> 4, j = (lane >> 2) & 3, c = lane & 3;
     const int s = j | (4 * (g & 1));
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      a_rm[q] = (8 * g + j) * 256 + ((4 * wn + q) ^ s) * 32 + (c >> 1) * 16 + (c & 1) * 8;
+    for (int q = 0; q < kQ; ++q)
+      a_rm[q] = (MODE == 1 ? 0 : wn * 8192) + (8 * g + j) * 256 +
+                ((MODE == 1 ? 4 * wn + q : q) ^ s) * 32 + (c >> 1) * 16 + (c & 1) * 8;
   }
   auto rd_a = [&](int wb, int i) {
     if constexpr (RM) {
       typedef short v4i16 __attribute__((ext_vector_type(4)));
       typedef __attribute__((address_space(3))) v4i16* lds_v4i16;
-      const uint8_t* const p = smem + wb * kWStageBytes + (i >> 2) * 8192 + a_rm[i & 3];
+      const uint8_t* const p = smem + wb * kWStageBytes +
+                               (MODE == 1 ? (i >> 2) * 8192 + a_rm[i & 3] : a_rm[i]);
       const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16)(p));
       const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16)(p + 1024));
       return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -588,7 +593,8 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_tile_kernel(TileArgs a) {
   tile_body<MODE, OUT, YVEC, SPLIT, false>(a);
 }
 
-// The fused SwiGLU on the caller's row-major weights (TileArgs::ldw0/1).
+// The fused SwiGLU or the GEMM on the caller's row-major weights
+// (TileArgs::ldw0/1).
 template <int MODE, int OUT, bool YVEC, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 1) void mfma_tile_rm_kernel(TileArgs a) {
   tile_body<MODE, OUT, YVEC, SPLIT, true>(a);
@@ -667,9 +673,10 @@ static hipError_t launch_tile_t(const TileArgs& a, const llk::ModuleFns* mod, hi
                        &tile_symbol<MODE, OUT, YVEC, SPLIT, RM>, grid, block, kLdsBytes, s, a);
 }
 
+// A k-split (or accumulating) launch: the tile kernel's fp32 partial planes,
+// then split_reduce_kernel.
 template <int MODE, int OUT, bool YVEC, bool RM = false>
-static hipError_t launch_t(const TileArgs& a, const llk::ModuleFns* mod, hipStream_t s) {
-  if (a.S <= 1 && !a.accumulate) return launch_tile_t<MODE, OUT, YVEC, false, RM>(a, mod, s);
+static hipError_t launch_split(const TileArgs& a, const llk::ModuleFns* mod, hipStream_t s) {
   // Partials are fp32 planes with 16-byte aligned rows: one instantiation.
   hipError_t e = launch_tile_t<MODE, kOutF32, true, true, RM>(a, mod, s);
   if (e != hipSuccess) return e;
@@ -677,6 +684,12 @@ static hipError_t launch_t(const TileArgs& a, const llk::ModuleFns* mod, hipStre
   return launch_kernel(mod, reinterpret_cast<const void*>(split_reduce_kernel<MODE, OUT, YVEC>),
                        &split_reduce_symbol<MODE, OUT, YVEC>,
                        dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a);
+}
+
+template <int MODE, int OUT, bool YVEC, bool RM = false>
+static hipError_t launch_t(const TileArgs& a, const llk::ModuleFns* mod, hipStream_t s) {
+  if (a.S <= 1 && !a.accumulate) return launch_tile_t<MODE, OUT, YVEC, false, RM>(a, mod, s);
+  return launch_split<MODE, OUT, YVEC, RM>(a, mod, s);
 }
 
 template <int MODE, int OUT>
@@ -768,23 +781,26 @@ bool llk_tile_rowmajor_fits(int M, int64_t K, int64_t ldx, const void* w, int64_
          (K + 128) * ldw * 2 < ((int64_t)1 << 31) && llk_tile_x_fits(M, ldx);
 }
 
-// Internal.  The fused SwiGLU (bf16 result) on row-major bf16 weights wg /
-// wu ([K, N], row strides ldwg / ldwu; llk_tile_rowmajor_fits for both) and
-// x as for llk_launch_tile with K = 64 KB: the same grid, k splits and
-// partial planes as llk_launch_tile(1, ...) with NB = ceil(N / 128), and the
-// same bits.
-hipError_t llk_launch_tile_rowmajor(const uint16_t* x, int64_t ldx, const uint16_t* wg,
-                                    int64_t ldwg, const uint16_t* wu, int64_t ldwu, void* y,
-                                    int64_t ldy, int M, int N, int K, int S, void* part,
-                                    bool yvec, const llk::ModuleFns* mod, hipStream_t s) {
+// Internal.  On row-major bf16 weights ([K, N], row strides ldw0 / ldw1;
+// llk_tile_rowmajor_fits for each) and x as for llk_launch_tile with
+// K = 64 KB: mode 1, the fused SwiGLU with a bf16 result (w0 = Wg, w1 =
+// Wu); mode 0, the accumulating GEMM y += x w0 (bf16, fp16 or fp32 y; part
+// holds the planes at S >= 1).  The same grid, k splits and partial planes
+// as llk_launch_tile(mode, ...) with NB = ceil(N / 128), and the same bits.
+hipError_t llk_launch_tile_rowmajor(int mode, const uint16_t* x, int64_t ldx, const uint16_t* w0,
+                                    int64_t ldw0, const uint16_t* w1, int64_t ldw1, void* y,
+                                    int64_t ldy, int M, int N, int K, int S, void* part, int out,
+                                    bool yvec, bool accumulate, const llk::ModuleFns* mod,
+                                    hipStream_t s) {
   using namespace llk_gfx950;
-  if (!llk_tile_rowmajor_fits(M, K, ldx, wg, ldwg, N) ||
-      !llk_tile_rowmajor_fits(M, K, ldx, wu, ldwu, N))
+  if (mode == 1 ? (out != kOutBF16 || accumulate || !llk_tile_rowmajor_fits(M, K, ldx, w1, ldw1, N))
+                : (mode != 0 || !accumulate || part == nullptr))
     return hipErrorInvalidValue;
+  if (!llk_tile_rowmajor_fits(M, K, ldx, w0, ldw0, N)) return hipErrorInvalidValue;
   TileArgs a;
   a.x = x;
-  a.w0 = reinterpret_cast<const uint8_t*>(wg);
-  a.w1 = reinterpret_cast<const uint8_t*>(wu);
+  a.w0 = reinterpret_cast<const uint8_t*>(w0);
+  a.w1 = reinterpret_cast<const uint8_t*>(w1);
   a.y = y;
   a.ldx = ldx;
   a.ldy = ldy;
@@ -793,21 +809,34 @@ hipError_t llk_launch_tile_rowmajor(const uint16_t* x, int64_t ldx, const uint16
   a.KB = K / 64;
   a.NB = (N + 127) / 128;
   a.tiles_m = (M + kTileM - 1) / kTileM;
-  a.tiles_n = a.NB;
+  a.tiles_n = mode == 1 ? a.NB : (a.NB + 1) / 2;
   a.group_m = 8;
   a.S = S > 1 ? S : 1;
   a.kbs = (a.KB + a.S - 1) / a.S;
   a.n_pad = a.NB * 128;
   a.part = static_cast<float*>(part);
-  a.accumulate = 0;
-  a.ldw0 = ldwg;
-  a.ldw1 = ldwu;
+  a.accumulate = accumulate ? 1 : 0;
+  a.ldw0 = ldw0;
+  a.ldw1 = ldw1;
   if (a.S > 1 && (part == nullptr || (int64_t)(a.S - 1) * a.kbs >= a.KB))
     return hipErrorInvalidValue;
 #if !defined(LLK_CO_OP) || LLK_CO_OP == 1
-  return yvec ? launch_t<1, kOutBF16, true, true>(a, mod, s)
-              : launch_t<1, kOutBF16, false, true>(a, mod, s);
-#else
-  return hipErrorInvalidValue;
+  if (mode == 1)
+    return yvec ? launch_t<1, kOutBF16, true, true>(a, mod, s)
+                : launch_t<1, kOutBF16, false, true>(a, mod, s);
 #endif
+#if !defined(LLK_CO_OP) || LLK_CO_OP == 0
+  if (mode == 0) {  // accumulating: the planes and the reduce, which reads y
+    if (out == kOutBF16)
+      return yvec ? launch_split<0, kOutBF16, true, true>(a, mod, s)
+                  : launch_split<0, kOutBF16, false, true>(a, mod, s);
+    if (out == kOutF16)
+      return yvec ? launch_split<0, kOutF16, true, true>(a, mod, s)
+                  : launch_split<0, kOutF16, false, true>(a, mod, s);
+    if (out == kOutF32)
+      return yvec ? launch_split<0, kOutF32, true, true>(a, mod, s)
+                  : launch_split<0, kOutF32, false, true>(a, mod, s);
+  }
+#endif
+  return hipErrorInvalidValue;
 }

@@ -63,10 +63,11 @@ hipError_t llk_launch_decode_rowmajor(int mode, const uint16_t* x, int64_t ldx,
                                       int S, void* ws, int out, bool yvec, bool accumulate,
                                       const llk::ModuleFns* mod, hipStream_t s);
 bool llk_tile_rowmajor_fits(int M, int64_t K, int64_t ldx, const void* w, int64_t ldw, int64_t N);
-hipError_t llk_launch_tile_rowmajor(const uint16_t* x, int64_t ldx, const uint16_t* wg,
-                                    int64_t ldwg, const uint16_t* wu, int64_t ldwu, void* y,
-                                    int64_t ldy, int M, int N, int K, int S, void* part,
-                                    bool yvec, const llk::ModuleFns* mod, hipStream_t s);
+hipError_t llk_launch_tile_rowmajor(int mode, const uint16_t* x, int64_t ldx, const uint16_t* w0,
+                                    int64_t ldw0, const uint16_t* w1, int64_t ldw1, void* y,
+                                    int64_t ldy, int M, int N, int K, int S, void* part, int out,
+                                    bool yvec, bool accumulate, const llk::ModuleFns* mod,
+                                    hipStream_t s);
 hipError_t llk_launch_pad_rows(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* out,
                                int64_t ldo, const llk::ModuleFns* mod, hipStream_t s);
 hipError_t llk_launch_pack(const uint16_t* w, int64_t ld, int K, int N, int KB, int NB, void* out,
@@ -1559,12 +1560,14 @@ int pack_into(const llk_tensor2d* w, int64_t bk, bool w_on_device, void* dst, hi
 //    with at most 128 rows and the weights' rows suit its loads
 //    (llk_decode_rowmajor_fits): that plan, with the same grid, k splits and
 //    MFMA operands, so the result equals the packed path's bit for bit;
-//  * otherwise, for the fused SwiGLU with a bf16 result on the tile path
-//    (X aligned, K a multiple of 64, llk_tile_rowmajor_fits): the 128-column
-//    tile kernel's row-major form with that kernel's plan -- k splits, and
-//    the unsplit head columns launched first where the plan splits only the
-//    tail (a column offset into the weights and Y) -- never the wide tiles,
-//    whose unsplit and equal-split bits are the 128-column kernel's anyway.
+//  * otherwise, on the tile path (X aligned, K a multiple of 64,
+//    llk_tile_rowmajor_fits), the tile kernel's row-major form: for the
+//    fused SwiGLU with a bf16 result, the 128-column kernel's plan -- k
+//    splits, and the unsplit head columns launched first where the plan
+//    splits only the tail (a column offset into the weights and Y) -- never
+//    the wide tiles, whose unsplit and equal-split bits are the 128-column
+//    kernel's anyway; for the accumulating GEMM, the plan itself (k-split
+//    planes, the reduce adding y).
 // Otherwise nothing is launched and the caller packs.
 int rowmajor_with_module(int mode, const llk_tensor2d* x, const llk_tensor2d* wg,
                          const llk_tensor2d* wu, llk_tensor2d* y, int out_dtype,
@@ -1597,6 +1600,10 @@ int rowmajor_with_module(int mode, const llk_tensor2d* x, const llk_tensor2d* wg
     head_cols = std::min<int64_t>(tp.head_nb * 128, N);
     ws_bytes = llk_tile_split_bytes(1, (int)M, (int)(NB - tp.head_nb), S, false);
     tile = true;
+  } else if (!p.skinny && mode == 0 && accumulate && !p.pad && p.chunk >= M && p.head_nb == 0 &&
+             fits(&llk_tile_rowmajor_fits)) {
+    ws_bytes = llk_tile_split_bytes(0, (int)M, (int)NB, S, true);
+    tile = true;
   } else {
     return LLK_OK;
   }
@@ -1617,15 +1624,17 @@ int rowmajor_with_module(int mode, const llk_tensor2d* x, const llk_tensor2d* wg
     // head columns unsplit, then the rest with the plan's splits (offsets of
     // 128-column multiples keep every row 16-byte aligned)
     const bool yv = y_vec_ok(y, out_dtype);
+    const int64_t ldu = mode == 1 ? wu->stride0 : 0;
     if (head_cols > 0)
-      e = llk_launch_tile_rowmajor(xd, x->stride0, wgd, wg->stride0, wud, wu->stride0, y->data,
-                                   y->stride0, (int)M, (int)head_cols, (int)K, 1, nullptr, yv,
-                                   mod, s);
+      e = llk_launch_tile_rowmajor(1, xd, x->stride0, wgd, wg->stride0, wud, ldu, y->data,
+                                   y->stride0, (int)M, (int)head_cols, (int)K, 1, nullptr,
+                                   out_dtype, yv, false, mod, s);
     if (e == hipSuccess && head_cols < N)
-      e = llk_launch_tile_rowmajor(xd, x->stride0, wgd + head_cols, wg->stride0, wud + head_cols,
-                                   wu->stride0, static_cast<uint16_t*>(y->data) + head_cols,
-                                   y->stride0, (int)M, (int)(N - head_cols), (int)K,
-                                   S, ws, yv, mod, s);
+      e = llk_launch_tile_rowmajor(
+          mode, xd, x->stride0, wgd + head_cols, wg->stride0,
+          mode == 1 ? wud + head_cols : nullptr, ldu,
+          static_cast<uint8_t*>(y->data) + head_cols * (int64_t)dtype_size(out_dtype), y->stride0,
+          (int)M, (int)(N - head_cols), (int)K, S, ws, out_dtype, yv, accumulate, mod, s);
   } else {
     e = llk_launch_decode_rowmajor(mode, xd, x->stride0, wgd, wg->stride0, wud,
                                    mode == 1 ? wu->stride0 : 0, y->data, y->stride0, (int)M, (int)N,

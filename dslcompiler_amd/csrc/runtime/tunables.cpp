@@ -40,9 +40,9 @@ struct Knob {
 //                    0 = never; 7 or 11 = that width whenever it applies.
 // kernel_fn_rowmajor: 1 = the KernelFn entries read device weights with
 //                    aligned rows straight into the kernels' row-major forms
-//                    (the decode tile kernel's up to 128 rows, the SwiGLU's
-//                    128-column tile kernel's above); 0 = they pack the
-//                    weights on every call.
+//                    (the decode tile kernel's up to 128 rows, the tile
+//                    kernel's above: SwiGLU and the accumulating matmul);
+//                    0 = they pack the weights on every call.
 // max_workspaces:    library-owned workspaces kept per device (one per
 //                    stream, or per thread on the per-thread default
 //                    stream); beyond it the least recently used idle one is

@@ -353,7 +353,8 @@ int llk_fill_normal_bf16(uint64_t seed, uint64_t stream, float sigma,
  * of a partial last wave of tiles may run as a separate k-split launch;
  * 0: never; a forced "tile_splits" also turns it off), "tile_wide" (1:
  * the cost model may take the wide SwiGLU tiles; 0: never; 7 or 11: that
- * width), "kernel_fn_rowmajor" (1: the KernelFn entries read device weights
+ * width), "kernel_fn_rowmajor" (1: the KernelFn entries -- SwiGLU and, from
+ * the object-code level, matmul -- read device weights
  * with aligned rows straight into the kernels' row-major forms; 0: they
  * pack the weights on every call), "max_workspaces" (library-owned
  * workspaces kept per device, see llk_workspace_stats).
@@ -583,8 +584,8 @@ size_t llk_cache_size(const llk_jit_cache* c);
  * may rewrite a weight buffer in place or reuse its address between calls:
  * device-resident weights with 16-byte aligned rows (row stride a multiple
  * of 8) go straight to the kernels' row-major forms -- the decode tile
- * kernel's for at most 128 rows of X, the 128-column tile kernel's above
- * (K a multiple of 64, N of 8) -- and other weights are packed into the
+ * kernel's for at most 128 rows of X, the tile kernel's above (K a
+ * multiple of 64, N of 8) -- and other weights are packed into the
  * MFMA operand layout on the device first (one pack launch per matrix into
  * a buffer the library owns per device).
  * Operands may be device memory (used in place) or host memory (staged

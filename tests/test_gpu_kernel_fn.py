@@ -292,12 +292,14 @@ def test_kernel_fn_rowmajor_matches_packed(llk, gpu, orc, M, K, N, ldw):
     assert_parity_bf16(got, orc.swiglu(x, wg, wu)[0], f"KernelFn row-major M={M}")
 
 
-@pytest.mark.parametrize("M,S", [(8, 0), (40, 3), (100, 0)])
+@pytest.mark.parametrize("M,S", [(8, 0), (40, 3), (100, 0), (200, 0), (600, 0), (300, 5)])
 def test_kernel_fn_rowmajor_matmul_entry(llk, gpu, orc, M, S):
     """The object-code level's matmul KernelFn (fp32 key, result = init + x
-    wg) on device weights (row-major, no pack) and on host weights (packed
-    per call): the same bits, on the oracle's bar; with the decode tile
-    kernel's k split forced (S = 3: the reduce adds init)."""
+    wg) on device weights (row-major, no pack: the decode tile kernel's form
+    up to 128 rows, the tile kernel's accumulating form above) and on host
+    weights (packed per call): the same bits, on the oracle's bar; with a k
+    split forced (S = 3 on the decode tile kernel, 5 on the tile kernel: the
+    reduce adds init)."""
     print(f"case kernel_fn row-major matmul M={M} S={S}", flush=True)
     K, N = 1536, 700
     a = normal_bf16(91, M, (M, K))
@@ -307,15 +309,16 @@ def test_kernel_fn_rowmajor_matmul_entry(llk, gpu, orc, M, S):
     jc = llk.JitCache()
     mm = jc.lookup_or_compile(llk.KernelKey(operation=3, isa=7, N=N, K=K, output_type=2))
     init = gpu.randn((M, N), dtype=gpu.float32, device="cuda")
-    old = llk.get_tunable("decode_splits")
-    llk.set_tunable("decode_splits", S)
+    knob = "decode_splits" if M <= 128 else "tile_splits"
+    old = llk.get_tunable(knob)
+    llk.set_tunable(knob, S)
     try:
         c_dev = gpu.full((M, N), float("nan"), dtype=gpu.float32, device="cuda")
         mm(ad, bd, None, init, c_dev)
         c_host = gpu.full((M, N), float("nan"), dtype=gpu.float32, device="cuda")
         mm(ad, b_host, None, init, c_host)
     finally:
-        llk.set_tunable("decode_splits", old)
+        llk.set_tunable(knob, old)
         jc.close()
     assert np.array_equal(from_dev(c_dev), from_dev(c_host))
     ref, _ = orc.gemm(a, b)
