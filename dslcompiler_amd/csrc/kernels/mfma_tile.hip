@@ -783,8 +783,8 @@ bool llk_tile_rowmajor_fits(int M, int64_t K, int64_t ldx, const void* w, int64_
 
 // Internal.  On row-major bf16 weights ([K, N], row strides ldw0 / ldw1;
 // llk_tile_rowmajor_fits for each) and x as for llk_launch_tile with
-// K = 64 KB: mode 1, the fused SwiGLU with a bf16 result (w0 = Wg, w1 =
-// Wu); mode 0, the accumulating GEMM y += x w0 (bf16, fp16 or fp32 y; part
+// K = 64 KB: mode 1, the fused SwiGLU with a bf16 or fp32 result (w0 = Wg,
+// w1 = Wu); mode 0, the accumulating GEMM y += x w0 (bf16, fp16 or fp32 y; part
 // holds the planes at S >= 1).  The same grid, k splits and partial planes
 // as llk_launch_tile(mode, ...) with NB = ceil(N / 128), and the same bits.
 hipError_t llk_launch_tile_rowmajor(int mode, const uint16_t* x, int64_t ldx, const uint16_t* w0,
@@ -793,7 +793,8 @@ hipError_t llk_launch_tile_rowmajor(int mode, const uint16_t* x, int64_t ldx, co
                                     bool yvec, bool accumulate, const llk::ModuleFns* mod,
                                     hipStream_t s) {
   using namespace llk_gfx950;
-  if (mode == 1 ? (out != kOutBF16 || accumulate || !llk_tile_rowmajor_fits(M, K, ldx, w1, ldw1, N))
+  if (mode == 1 ? ((out != kOutBF16 && out != kOutF32) || accumulate ||
+                   !llk_tile_rowmajor_fits(M, K, ldx, w1, ldw1, N))
                 : (mode != 0 || !accumulate || part == nullptr))
     return hipErrorInvalidValue;
   if (!llk_tile_rowmajor_fits(M, K, ldx, w0, ldw0, N)) return hipErrorInvalidValue;
@@ -821,9 +822,12 @@ hipError_t llk_launch_tile_rowmajor(int mode, const uint16_t* x, int64_t ldx, co
   if (a.S > 1 && (part == nullptr || (int64_t)(a.S - 1) * a.kbs >= a.KB))
     return hipErrorInvalidValue;
 #if !defined(LLK_CO_OP) || LLK_CO_OP == 1
-  if (mode == 1)
+  if (mode == 1 && out == kOutBF16)
     return yvec ? launch_t<1, kOutBF16, true, true>(a, mod, s)
                 : launch_t<1, kOutBF16, false, true>(a, mod, s);
+  if (mode == 1)
+    return yvec ? launch_t<1, kOutF32, true, true>(a, mod, s)
+                : launch_t<1, kOutF32, false, true>(a, mod, s);
 #endif
 #if !defined(LLK_CO_OP) || LLK_CO_OP == 0
   if (mode == 0) {  // accumulating: the planes and the reduce, which reads y

@@ -1562,7 +1562,7 @@ int pack_into(const llk_tensor2d* w, int64_t bk, bool w_on_device, void* dst, hi
 //    MFMA operands, so the result equals the packed path's bit for bit;
 //  * otherwise, on the tile path (X aligned, K a multiple of 64,
 //    llk_tile_rowmajor_fits), the tile kernel's row-major form: for the
-//    fused SwiGLU with a bf16 result, the 128-column kernel's plan -- k
+//    fused SwiGLU (bf16 or fp32 result), the 128-column kernel's plan -- k
 //    splits, and the unsplit head columns launched first where the plan
 //    splits only the tail (a column offset into the weights and Y) -- never
 //    the wide tiles, whose unsplit and equal-split bits are the 128-column
@@ -1591,8 +1591,8 @@ int rowmajor_with_module(int mode, const llk_tensor2d* x, const llk_tensor2d* wg
   int64_t head_cols = 0;  // tile form: columns of the unsplit head launch
   if (p.dtile && M <= 128) {
     if (!fits(&llk_decode_rowmajor_fits)) return LLK_OK;
-  } else if (!p.skinny && mode == 1 && out_dtype == LLK_BF16 && !accumulate && !p.pad &&
-             p.chunk >= M && fits(&llk_tile_rowmajor_fits)) {
+  } else if (!p.skinny && mode == 1 && (out_dtype == LLK_BF16 || out_dtype == LLK_FP32) &&
+             !accumulate && !p.pad && p.chunk >= M && fits(&llk_tile_rowmajor_fits)) {
     llk::ScheduleEntry se;
     const bool have_db = db_entry(nmat, M, &se);
     const TilePlan tp = tile_plan(nmat, M, KB, NB, have_db ? se.grain_size : 0);

@@ -458,3 +458,26 @@ def test_kernel_fn_rowmajor_tile_config3(llk, gpu):
     ref = llk.fused_swiglu(xd, pg, pu, out_dtype=gpu.bfloat16)
     assert gpu.equal(y, ref)
     assert not gpu.isnan(y.float()).any()
+
+
+@pytest.mark.parametrize("M", [100, 300])
+def test_object_code_swiglu_fp32_rowmajor(llk, gpu, orc, M):
+    """The object-code level's SwiGLU entry with an fp32 result key on device
+    weights (row-major: the decode tile kernel's form at M = 100, the tile
+    kernel's at M = 300) and on host weights (packed per call): the same
+    bits, and the oracle's fp32 result to the bar."""
+    print(f"case object-code SwiGLU fp32 row-major M={M}", flush=True)
+    K, N = 1024, 720
+    x, wg, wu = swiglu_inputs(M, K, N, seed=M + 11)
+    xd, wgd, wud = to_dev(gpu, x), to_dev(gpu, wg), to_dev(gpu, wu)
+    jc = llk.JitCache()
+    try:
+        fn = jc.lookup_or_compile(llk.KernelKey(operation=0, isa=7, N=N, K=K, output_type=2))
+        y_dev = gpu.full((M, N), float("nan"), dtype=gpu.float32, device="cuda")
+        fn(xd, wgd, wud, y_dev, y_dev)
+        y_host = gpu.full((M, N), float("nan"), dtype=gpu.float32, device="cuda")
+        fn(xd, np.ascontiguousarray(wg), np.ascontiguousarray(wu), y_host, y_host)
+    finally:
+        jc.close()
+    assert np.array_equal(from_dev(y_dev), from_dev(y_host))
+    assert_parity(from_dev(y_dev), orc.swiglu(x, wg, wu)[0], f"SwiGLU fp32 KernelFn M={M}")

@@ -119,11 +119,12 @@ def test_every_tile_instantiation_found(asm):
     # SwiGLU (bf16/fp32 out, both Y vector forms, split partials) and GEMM
     # (bf16/fp16/fp32 out, both forms, split partials)
     assert len([k for k in ks if "16mfma_tile_kernel" in k]) == 12, sorted(ks)
-    # row-major: SwiGLU bf16 out in both Y forms and split partials; the
-    # accumulating GEMM's split partials
+    # row-major: SwiGLU bf16 and fp32 out in both Y forms and split
+    # partials; the accumulating GEMM's split partials
     assert sorted(k[len("_ZN10llk_gfx95019mfma_tile_rm_kernelI"):].split("EE")[0]
                   for k in ks if "rm_kernel" in k) == [
-        "Li0ELi2ELb1ELb1", "Li1ELi0ELb0ELb0", "Li1ELi0ELb1ELb0", "Li1ELi2ELb1ELb1"], sorted(ks)
+        "Li0ELi2ELb1ELb1", "Li1ELi0ELb0ELb0", "Li1ELi0ELb1ELb0", "Li1ELi2ELb0ELb0",
+        "Li1ELi2ELb1ELb0", "Li1ELi2ELb1ELb1"], sorted(ks)
 
 
 def test_k_loop_operand_reads(asm):
