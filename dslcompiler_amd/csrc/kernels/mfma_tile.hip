@@ -63,6 +63,14 @@
 // X must be padded to whole 64-k steps with 16-byte aligned rows (the host
 // copies it into a padded buffer otherwise); rows >= M read as zero through
 // the buffer resource's range check.
+//
+// Row-major form (mfma_tile_rm_kernel, the same body with RM = true): the
+// weights are the caller's bf16 [K, N] matrices instead of a packed payload
+// -- each stage's 32 k rows x 128 columns per half come in as 256-byte rows
+// with XOR-swizzled 16-byte chunks, and each A operand is two transposed
+// LDS reads (ds_read_b64_tr_b16) -- for the KernelFn entries, which read the
+// caller's weights at every call.  The MFMAs see the same operands in the
+// same order, so results equal the packed form's bit for bit.
 #include <type_traits>
 
 #include "common.h"
