@@ -702,7 +702,7 @@ __global__ __launch_bounds__(256) void decode_tile_kernel(DecTileArgs a) {
     for (int g = 0; g < 4; ++g) {
       const int n_off = 8 * g + 4 * (lane >> 5);
       if (a.S > 1) {
-        if (m < a.rows) {
+        if (m < a.M) {  // the reduce reads rows < M only
 #pragma unroll
           for (int p = 0; p < 2; ++p) {
             const int mat = NMAT == 2 ? p : 0;
