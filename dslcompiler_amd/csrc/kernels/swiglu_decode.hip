@@ -249,7 +249,7 @@ __global__ __launch_bounds__(KS * G * 64) void skinny_kernel(SkinnyArgs a) {
     const int m = t * 32 + (ln & 31);
     const int n = (eg >> 2) * kPackN + (eg & 3) * 32 + 8 * g + 4 * (ln >> 5);
     if (a.S > 1) {
-      if (n < a.n_pad) {
+      if (n < a.n_pad && m < a.M) {  // the reduce reads rows < M only
 #pragma unroll
         for (int p = 0; p < NMAT; ++p) {
           float* dst = a.part + (((size_t)split * NMAT + p) * (MT * 32) + m) * a.n_pad + n;
